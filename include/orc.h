@@ -1,0 +1,167 @@
+/*
+ * orc.h — C ABI of the MI355X (gfx950) kernels behind ORACLE's
+ * speculative-decoding hot path.
+ *
+ * The reference (Titouan935/oracle-engine) has no FFI: its hot path is the C++
+ * API of core/gguf_parser.hpp, core/ops.hpp, core/model.hpp and
+ * core/sampler.hpp, linked statically. Each entry point below names the
+ * reference function or loop it replaces (file:line in the reference tree).
+ * The C++ host in oracle-engine_amd/host keeps that C++ API and calls only
+ * these functions.
+ *
+ * Conventions
+ *  - Every function returns 0 on success or a negative ORC_E_* code; the
+ *    message of the last error on the calling thread is orc_last_error().
+ *  - Pointers named d_* are device (HBM) pointers; h_* are host pointers.
+ *  - All kernels are stream-ordered on `stream` (NULL = the library's default
+ *    stream created by orc_init). Nothing allocates in a kernel entry point.
+ *  - Floating-point data is fp32; quantized weights are raw GGML blocks exactly
+ *    as stored in the GGUF file (type ids as in core/gguf_parser.hpp:9-24).
+ *  - Matrices follow GGUF: a weight with shape [n_in, n_out] is n_out rows of
+ *    n_in elements, rows contiguous; activations X are [n_tok][ldx] row-major.
+ */
+#ifndef ORC_H
+#define ORC_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* error codes */
+#define ORC_OK 0
+#define ORC_E_INVALID (-1)     /* bad argument (shape, type, pointer) */
+#define ORC_E_UNSUPPORTED (-2) /* quantization type or shape not supported */
+#define ORC_E_HIP (-3)         /* a HIP runtime call failed */
+#define ORC_E_NOINIT (-4)      /* orc_init was not called */
+
+/* GGML type ids (core/gguf_parser.hpp:9-24) */
+#define ORC_F32 0
+#define ORC_F16 1
+#define ORC_Q4_0 2
+#define ORC_Q8_0 8
+#define ORC_Q4_K 12
+#define ORC_Q6_K 14
+
+typedef void* orc_stream_t; /* a hipStream_t */
+typedef void* orc_graph_t;  /* an instantiated hipGraphExec_t */
+typedef void* orc_event_t;  /* a hipEvent_t */
+
+/* ── runtime ─────────────────────────────────────────────────────────────── */
+/* Select `device`, create the default stream. Replaces nothing in the
+ * reference (CPU-only); called once by the host before any other entry point. */
+int orc_init(int device);
+int orc_shutdown(void);
+const char* orc_last_error(void);
+/* Device name, compute-unit count and HBM bytes (for reports). */
+int orc_device_info(char* name, int name_cap, int* n_cu, size_t* hbm_bytes);
+
+int orc_malloc(void** d_ptr, size_t bytes);
+int orc_free(void* d_ptr);
+int orc_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes, orc_stream_t stream);
+int orc_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, orc_stream_t stream);
+int orc_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes, orc_stream_t stream);
+/* Fill with a byte value using a kernel (graph-capture safe). */
+int orc_fill(void* d_dst, int byte_value, size_t bytes, orc_stream_t stream);
+/* Allocate device memory and copy `bytes` raw GGUF bytes into it, unchanged.
+ * Replaces the RAM preload of the data section (core/gguf_parser.cpp:112-138). */
+int orc_upload(const void* h_src, size_t bytes, void** d_ptr);
+int orc_stream_create(orc_stream_t* stream);
+int orc_stream_destroy(orc_stream_t stream);
+int orc_stream_sync(orc_stream_t stream);
+int orc_device_sync(void);
+/* Stream capture into a replayable graph (one decode step / one verify round). */
+int orc_graph_begin(orc_stream_t stream);
+int orc_graph_end(orc_stream_t stream, orc_graph_t* graph);
+int orc_graph_launch(orc_graph_t graph, orc_stream_t stream);
+int orc_graph_destroy(orc_graph_t graph);
+int orc_event_create(orc_event_t* ev);
+int orc_event_destroy(orc_event_t ev);
+int orc_event_record(orc_event_t ev, orc_stream_t stream);
+int orc_event_elapsed_ms(orc_event_t start, orc_event_t stop, float* ms);
+
+/* ── quant codecs ────────────────────────────────────────────────────────── */
+/* Bytes of one row of n_el elements of `type` (core/gguf_parser.cpp:61-75). */
+int64_t orc_row_bytes(int type, int64_t n_el);
+/* Dequantize n_el contiguous elements to fp32, bit-exact with the reference
+ * codecs: fp16/Q4_0/Q8_0/Q4_K/Q6_K (core/gguf_parser.cpp:1002-1154,
+ * dequantize_into :420-441). */
+int orc_dequant(int type, const void* d_w, int64_t n_el, float* d_y, orc_stream_t stream);
+/* Embedding gather: y[t][:] = dequant(row ids[t] of an [n_in, n_rows] table);
+ * ids outside [0, n_rows) read row 0 (model.cpp:352-358, 549-558 +
+ * dequantize_row gguf_parser.cpp:443-482). ids is a device array. */
+int orc_embed(int type, const void* d_table, int n_in, int n_rows, const int32_t* d_ids, int n_tok, float* d_y,
+              int ldy, orc_stream_t stream);
+
+/* ── quantized GEMV / GEMM ──────────────────────────────────────────────── */
+/* Y[t][j] = dot(X[t], dequant(W[j])) for t < n_tok, j < n_out, fp32
+ * accumulation. n_tok = 1 is the decode GEMV (gemv_q / gemv_q_range,
+ * core/gguf_parser.cpp:868-911); n_tok > 1 is the verify / prefill GEMM
+ * (gemm_q, core/gguf_parser.cpp:919-997). The per-(token,row) reduction order
+ * does not depend on n_tok, so the verify pass is bit-identical to n_tok
+ * separate GEMVs. Supported types: Q4_0, Q8_0, Q4_K, Q6_K. */
+int orc_gemm(int type, const void* d_w, int n_tok, int n_out, int n_in, const float* d_x, int ldx, float* d_y,
+             int ldy, orc_stream_t stream);
+static inline int orc_gemv(int type, const void* d_w, int n_out, int n_in, const float* d_x, float* d_y,
+                           orc_stream_t stream) {
+    return orc_gemm(type, d_w, 1, n_out, n_in, d_x, n_in, d_y, n_out, stream);
+}
+
+/* Fused multi-output GEMM: up to 3 weight matrices of one type sharing X and
+ * n_in (e.g. Q|K|V, or gate|up), with an optional RMSNorm prologue applied to
+ * each X row (ops::rmsnorm, core/ops.cpp:149-195, eps as given) and one of the
+ * epilogues below. Replaces the projection sequences of Model::forward
+ * (model.cpp:366-388, 449-473) and forward_prefill (model.cpp:565-581,
+ * 629-643). */
+#define ORC_EPI_STORE 0  /* y = W·x (+ bias)                          */
+#define ORC_EPI_ACCUM 1  /* y += W·x   (residual add, model.cpp:444,473) */
+#define ORC_EPI_SWIGLU 2 /* seg0 = gate, seg1 = up: y0 = silu(g) * u   */
+typedef struct {
+    const void* d_w;    /* weight rows */
+    int n_out;          /* rows */
+    float* d_y;         /* output column base; element (t, j) at d_y[t*ldy + j] */
+    const float* d_bias;/* optional per-row bias (Qwen2 QKV bias, model.cpp:384-388) */
+} orc_seg;
+int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_tok, int n_in, const float* d_x, int ldx, int ldy,
+                   const float* d_norm_w, float eps, int epilogue, orc_stream_t stream);
+
+/* ── elementwise / attention ─────────────────────────────────────────────── */
+/* out[t] = rmsnorm(x[t]) for n_rows rows of n (ops::rmsnorm, ops.cpp:149-195). */
+int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_rows, float eps, orc_stream_t stream);
+/* RoPE (rotate-half pairs (i, i+hd/2), theta = pos / base^(2i/hd),
+ * ops::rope ops.cpp:440-485) on the q and k columns of n_tok QKV rows laid out
+ * [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)] with row stride ldqkv, then
+ * store k and v of token t at KV position start_pos + t (model.cpp:401-408,
+ * 595-602). The cos/sin table d_rope is [max_pos][hd/2] pairs of floats built
+ * on the host with the reference's float powf/cosf/sinf, so angles are
+ * bit-identical. KV cache layout: [n_kv][ctx][hd] fp32 per layer. */
+int orc_rope_kv_store(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim, int start_pos,
+                      const float* d_rope, float* d_kcache, float* d_vcache, int ctx, orc_stream_t stream);
+/* Causal GQA attention for n_tok query tokens at positions start_pos..,
+ * each attending to KV positions [0, start_pos + t] (model.cpp:410-435,
+ * 604-626). q rows have stride ldq, output rows stride ldo. Scale
+ * 1/sqrt(head_dim), softmax with max subtraction. Split over KV chunks with
+ * an online-softmax merge; d_work needs orc_attn_workspace() bytes. */
+size_t orc_attn_workspace(int n_tok, int n_heads, int head_dim, int max_pos);
+int orc_attn_gqa(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv, int head_dim, int start_pos,
+                 const float* d_kcache, const float* d_vcache, int ctx, float* d_out, int ldo, void* d_work,
+                 orc_stream_t stream);
+
+/* ── argmax, sampling, acceptance ────────────────────────────────────────── */
+/* out[r] = first index of the maximum of row r (ops::argmax ops.cpp:490-497,
+ * bench_engine.cpp:82-88). d_work needs orc_argmax_workspace() bytes. */
+size_t orc_argmax_workspace(int n_rows, int n);
+int orc_argmax(const float* d_x, int n_rows, int n, int ld, int32_t* d_out, void* d_work, orc_stream_t stream);
+
+/* Greedy acceptance of one batched verify round (bench_engine.cpp:337-355):
+ * given the verify logits argmax ids tgt[0..n_draft] and the draft ids
+ * d_draft[0..n_draft-1], writes out[0] = a (number accepted), out[1] = the
+ * next token (first mismatch, or the bonus tgt[n_draft] when all match). */
+int orc_spec_accept_greedy(const int32_t* d_tgt_ids, const int32_t* d_draft_ids, int n_draft, int32_t* d_out,
+                           orc_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,735 @@
+// Quantized GEMV / GEMM on raw GGML blocks (gfx950), plus the bit-exact
+// dequant codecs and the embedding gather.
+//
+// Replaces gemv_q / gemv_q_range / gemm_q / dequantize_row
+// (core/gguf_parser.cpp:443-482, 496-997) and the fp16 + block codecs
+// (:1002-1154).
+//
+// GEMM design (one kernel family; n_tok = 1 is the decode GEMV):
+//  * A 256-thread workgroup owns a tile of weight rows. Lanes are split into
+//    groups of LPR lanes; each group owns ROWS rows and walks their row bytes
+//    in "units" (a type-specific slice of a block: 16 B of Q4_K nibbles, a
+//    64-value quarter of a Q6_K superblock, one Q8_0/Q4_0 block). Consecutive
+//    lanes take consecutive units, so a wavefront's loads cover contiguous
+//    row bytes; blocks are read straight from the as-uploaded GGUF bytes with
+//    (possibly unaligned) 128-bit loads.
+//  * The activations of all n_tok tokens for one K tile are staged in LDS
+//    (fp32, with 4 floats of padding every 32/64 values so that the lanes of
+//    a group hit distinct banks), together with per-16-value sums of x used
+//    for the Q4_K minimum term and the Q6_K/Q4_0 code offsets.
+//  * Each weight code is decoded once per row and applied to every token held
+//    in LDS; accumulation is fp32. A lane's partial sum depends only on the
+//    units it owns, and the group reduction is a fixed xor-butterfly, so the
+//    result for a (token, row) pair is bit-identical for every n_tok: the
+//    (k+1)-token verify pass equals k+1 separate decode GEMVs.
+//  * Optional RMSNorm prologue on X and store / accumulate / SwiGLU epilogues
+//    fuse the surrounding transformer ops into the projection launches.
+#include "orc_internal.hpp"
+
+#include <algorithm>
+
+namespace orc {
+
+// ── per-type geometry ────────────────────────────────────────────────────────
+template <int QT> struct QTr;
+template <> struct QTr<ORC_Q8_0> { static constexpr int BLK_EL = 32, BLK_B = 34, UPB = 1, PP = 32; };
+template <> struct QTr<ORC_Q4_0> { static constexpr int BLK_EL = 32, BLK_B = 18, UPB = 1, PP = 32; };
+template <> struct QTr<ORC_Q4_K> { static constexpr int BLK_EL = 256, BLK_B = 144, UPB = 8, PP = 64; };
+template <> struct QTr<ORC_Q6_K> { static constexpr int BLK_EL = 256, BLK_B = 210, UPB = 4, PP = 64; };
+
+template <int PP> __device__ __forceinline__ int padx(int k) { return k + 4 * (k / PP); }
+
+// Q4_K 6-bit (scale, min) of sub-block `is` from the 12 scale bytes held in
+// three dwords (core/gguf_parser.cpp:1085-1093).
+__device__ __forceinline__ void q4k_scale_min(int is, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
+                                              uint32_t& mn) {
+    if (is < 4) {
+        sc = (s0 >> (8 * is)) & 63u;
+        mn = (s1 >> (8 * is)) & 63u;
+    } else {
+        const int k = 8 * (is - 4);
+        const uint32_t b8 = (s2 >> k) & 0xFFu;
+        sc = (b8 & 0xFu) | (((s0 >> k) & 0xFFu) >> 6 << 4);
+        mn = (b8 >> 4) | (((s1 >> k) & 0xFFu) >> 6 << 4);
+    }
+}
+
+// Σ_{i<16} w[i] * x[i] with x read from LDS as 4 float4 (sequential FMA chain).
+__device__ __forceinline__ float dot16(const float* w, const float* xl) {
+    const float4* x4 = (const float4*)xl;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float4 v = x4[i];
+        s = __builtin_fmaf(w[4 * i + 0], v.x, s);
+        s = __builtin_fmaf(w[4 * i + 1], v.y, s);
+        s = __builtin_fmaf(w[4 * i + 2], v.z, s);
+        s = __builtin_fmaf(w[4 * i + 3], v.w, s);
+    }
+    return s;
+}
+
+// Unpack 4 dwords of codes into 16 floats, byte k of dword i -> w[4i+k].
+__device__ __forceinline__ void bytes_to_f(const uint32_t (&q)[4], float* w) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[4 * i + k] = ubyte_f(q[i], k);
+}
+
+struct UnitCtx {
+    const float* xs;  // LDS x, token 0, at tile element 0 (padded layout)
+    int xs_stride;    // floats between tokens
+    const float* sx;  // LDS per-16 sums of x, token 0
+    int sx_stride;
+    int k0;           // first element of the tile
+};
+
+// ── per-type unit dot products over ROWS rows and NT tokens ──────────────────
+template <int QT, int NT, int ROWS> struct UnitDot;
+
+template <int NT, int ROWS> struct UnitDot<ORC_Q4_K, NT, ROWS> {
+    // unit u: superblock u/8, 16-byte nibble chunk c = u%8 of that superblock.
+    // Chunk c holds values 64j+16h+[0,16) (low nibbles, sub-block 2j) and
+    // 64j+32+16h+[0,16) (high nibbles, sub-block 2j+1), j = c/2, h = c%2.
+    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
+                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
+        const int b = u >> 3, ch = u & 7, j = ch >> 1, h = ch & 1;
+        u32x4 hdr[ROWS], qv[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if (ok[r]) {
+                const uint8_t* blk = rows[r] + (size_t)b * 144;
+                hdr[r] = ld16(blk);
+                qv[r] = ld16(blk + 16 + 16 * ch);
+            }
+        const int eA = b * 256 + 64 * j + 16 * h - c.k0, eB = eA + 32;
+        const int pA = padx<64>(eA), pB = padx<64>(eB);
+        float dA[ROWS], mA[ROWS], dB[ROWS], mB[ROWS];
+        float wa[ROWS][16], wb[ROWS][16];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            if (!ok[r]) continue;
+            const float d = h2f(hdr[r].x & 0xFFFFu), dmin = h2f(hdr[r].x >> 16);
+            uint32_t s0, m0, s1, m1;
+            q4k_scale_min(2 * j, hdr[r].y, hdr[r].z, hdr[r].w, s0, m0);
+            q4k_scale_min(2 * j + 1, hdr[r].y, hdr[r].z, hdr[r].w, s1, m1);
+            dA[r] = d * (float)s0; mA[r] = dmin * (float)m0;
+            dB[r] = d * (float)s1; mB[r] = dmin * (float)m1;
+            uint32_t lo[4] = {qv[r].x & 0x0F0F0F0Fu, qv[r].y & 0x0F0F0F0Fu, qv[r].z & 0x0F0F0F0Fu, qv[r].w & 0x0F0F0F0Fu};
+            uint32_t hi[4] = {(qv[r].x >> 4) & 0x0F0F0F0Fu, (qv[r].y >> 4) & 0x0F0F0F0Fu, (qv[r].z >> 4) & 0x0F0F0F0Fu,
+                              (qv[r].w >> 4) & 0x0F0F0F0Fu};
+            bytes_to_f(lo, wa[r]);
+            bytes_to_f(hi, wb[r]);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float* xt = c.xs + t * c.xs_stride;
+            const float sxA = c.sx[t * c.sx_stride + eA / 16], sxB = c.sx[t * c.sx_stride + eB / 16];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                if (!ok[r]) continue;
+                const float sA = dot16(wa[r], xt + pA), sB = dot16(wb[r], xt + pB);
+                acc[r][t] += dA[r] * sA - mA[r] * sxA + dB[r] * sB - mB[r] * sxB;
+            }
+        }
+    }
+};
+
+template <int NT, int ROWS> struct UnitDot<ORC_Q6_K, NT, ROWS> {
+    // unit u: superblock u/4, quarter v = u%4: half hh = v/2, l0 = 16*(v%2).
+    // Group g (0..3) holds values 128hh+32g+l0+[0,16) with scale sc[8hh+2g+v%2].
+    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
+                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
+        const int b = u >> 2, v = u & 3, hh = v >> 1, odd = v & 1, l0 = 16 * odd;
+        u32x4 qa[ROWS], qb[ROWS], qh[ROWS];
+        u32x2 sc[ROWS];
+        uint32_t dh[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if (ok[r]) {
+                const uint8_t* blk = rows[r] + (size_t)b * 210;
+                qa[r] = ld16(blk + 64 * hh + l0);
+                qb[r] = ld16(blk + 64 * hh + 32 + l0);
+                qh[r] = ld16(blk + 128 + 32 * hh + l0);
+                sc[r] = ld8(blk + 192 + 8 * hh);
+                dh[r] = ld2(blk + 208);
+            }
+        const int e0 = b * 256 + 128 * hh + l0 - c.k0;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float w[ROWS][16], sg[ROWS];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                if (!ok[r]) continue;
+                const int si = 2 * g + odd;  // byte index inside the 8 scale bytes
+                const uint32_t sw = si < 4 ? sc[r].x : sc[r].y;
+                const int8_t s8 = (int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
+                sg[r] = h2f(dh[r]) * (float)s8;
+                uint32_t qq[4];
+                const uint32_t a4[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w};
+                const uint32_t b4[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+                const uint32_t h4[4] = {qh[r].x, qh[r].y, qh[r].z, qh[r].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t nib, hb;
+                    if (g == 0) { nib = a4[i] & 0x0F0F0F0Fu; hb = (h4[i] << 4) & 0x30303030u; }
+                    else if (g == 1) { nib = b4[i] & 0x0F0F0F0Fu; hb = (h4[i] << 2) & 0x30303030u; }
+                    else if (g == 2) { nib = (a4[i] >> 4) & 0x0F0F0F0Fu; hb = h4[i] & 0x30303030u; }
+                    else { nib = (b4[i] >> 4) & 0x0F0F0F0Fu; hb = (h4[i] >> 2) & 0x30303030u; }
+                    qq[i] = nib | hb;
+                }
+                bytes_to_f(qq, w[r]);
+            }
+            const int eg = e0 + 32 * g;
+            const int pg = padx<64>(eg);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float* xt = c.xs + t * c.xs_stride;
+                const float sxg = c.sx[t * c.sx_stride + eg / 16];
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    if (!ok[r]) continue;
+                    // codes are stored +32: Σ (q-32) x = Σ q x - 32 Σ x
+                    const float s = dot16(w[r], xt + pg);
+                    acc[r][t] += sg[r] * (s - 32.f * sxg);
+                }
+            }
+        }
+    }
+};
+
+template <int NT, int ROWS> struct UnitDot<ORC_Q8_0, NT, ROWS> {
+    // unit u: block u (fp16 d + 32 int8 codes), acc += d * Σ q x.
+    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
+                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
+        u32x4 q0[ROWS], q1[ROWS];
+        uint32_t dh[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if (ok[r]) {
+                const uint8_t* blk = rows[r] + (size_t)u * 34;
+                dh[r] = ld2(blk);
+                q0[r] = ld16(blk + 2);
+                q1[r] = ld16(blk + 18);
+            }
+        const int e0 = u * 32 - c.k0;
+        const int p0 = padx<32>(e0);
+        float w[ROWS][32], d[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            if (!ok[r]) continue;
+            d[r] = h2f(dh[r]);
+            const uint32_t qq[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) w[r][4 * i + k] = (float)(int8_t)((qq[i] >> (8 * k)) & 0xFFu);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float* xt = c.xs + t * c.xs_stride + p0;
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                if (!ok[r]) continue;
+                const float s = dot16(w[r], xt) + 0.f;
+                const float s2 = dot16(w[r] + 16, xt + 16);
+                acc[r][t] += d[r] * (s + s2);
+            }
+        }
+    }
+};
+
+template <int NT, int ROWS> struct UnitDot<ORC_Q4_0, NT, ROWS> {
+    // unit u: block u (fp16 d + 16 bytes: low nibble -> value l, high -> l+16),
+    // codes stored +8.
+    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
+                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
+        u32x4 qv[ROWS];
+        uint32_t dh[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if (ok[r]) {
+                const uint8_t* blk = rows[r] + (size_t)u * 18;
+                dh[r] = ld2(blk);
+                qv[r] = ld16(blk + 2);
+            }
+        const int e0 = u * 32 - c.k0;
+        const int p0 = padx<32>(e0);
+        float wl[ROWS][16], wh[ROWS][16], d[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            if (!ok[r]) continue;
+            d[r] = h2f(dh[r]);
+            uint32_t lo[4] = {qv[r].x & 0x0F0F0F0Fu, qv[r].y & 0x0F0F0F0Fu, qv[r].z & 0x0F0F0F0Fu, qv[r].w & 0x0F0F0F0Fu};
+            uint32_t hi[4] = {(qv[r].x >> 4) & 0x0F0F0F0Fu, (qv[r].y >> 4) & 0x0F0F0F0Fu, (qv[r].z >> 4) & 0x0F0F0F0Fu,
+                              (qv[r].w >> 4) & 0x0F0F0F0Fu};
+            bytes_to_f(lo, wl[r]);
+            bytes_to_f(hi, wh[r]);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float* xt = c.xs + t * c.xs_stride + p0;
+            const float sxs = c.sx[t * c.sx_stride + e0 / 16] + c.sx[t * c.sx_stride + e0 / 16 + 1];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                if (!ok[r]) continue;
+                const float s = dot16(wl[r], xt) + dot16(wh[r], xt + 16);
+                acc[r][t] += d[r] * (s - 8.f * sxs);
+            }
+        }
+    }
+};
+
+// ── the GEMM kernel ──────────────────────────────────────────────────────────
+struct GemmParams {
+    const uint8_t* w[3];
+    float* y[3];
+    const float* bias[3];
+    int rows[3];
+    int n_seg;
+    int tile_rows_total;  // rows (or gate/up pairs) covered by the grid
+    int n_in;
+    int units_per_row;
+    uint64_t row_bytes;
+    const float* x;
+    int ldx, ldy, n_tok;
+    const float* norm_w;
+    float eps;
+    int epi;
+    int kt_el;     // K tile in elements (multiple of the block size)
+    int n_ktiles;
+};
+
+constexpr int kWG = 256;
+
+template <int QT, int NT, int LPR, int ROWS>
+__global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
+    using T = QTr<QT>;
+    extern __shared__ float smem[];
+    constexpr int G = 64 / LPR;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane % LPR, group = wave * G + lane / LPR;
+    const int xs_stride = padx<T::PP>(p.kt_el) + 4;
+    const int sx_stride = p.kt_el / 16;
+    float* xs = smem;
+    float* sx = smem + NT * xs_stride;
+    float* red = sx + NT * sx_stride;  // 8 floats of reduction scratch + NT inverse RMS
+
+    // rows owned by this lane group
+    const uint8_t* rows[ROWS];
+    bool ok[ROWS];
+    float* yout[ROWS];
+    const float* bias[ROWS];
+    const int base = (blockIdx.x * 4 * G + group) * ROWS;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        int seg = 0, j;
+        if (p.epi == ORC_EPI_SWIGLU) {  // slot 0 = gate row, slot 1 = up row of the same index
+            j = base / ROWS;
+            seg = r;
+            ok[r] = j < p.rows[0];
+        } else {
+            j = base + r;
+            ok[r] = j < p.tile_rows_total;
+            while (seg + 1 < p.n_seg && j >= p.rows[seg]) { j -= p.rows[seg]; ++seg; }
+        }
+        rows[r] = p.w[seg] + (size_t)(ok[r] ? j : 0) * p.row_bytes;
+        yout[r] = p.y[seg] + j;
+        bias[r] = p.bias[seg] ? p.bias[seg] + j : nullptr;
+    }
+
+    // optional RMSNorm prologue: inverse RMS per token, same reduction for any n_tok
+    float* inv = red + 8;
+    if (p.norm_w) {
+        for (int t = 0; t < NT; ++t) {
+            const float4* xr = (const float4*)(p.x + (size_t)t * p.ldx);
+            float ss = 0.f;
+            for (int i = tid; i < p.n_in / 4; i += kWG) {
+                float4 v = xr[i];
+                ss = __builtin_fmaf(v.x, v.x, ss);
+                ss = __builtin_fmaf(v.y, v.y, ss);
+                ss = __builtin_fmaf(v.z, v.z, ss);
+                ss = __builtin_fmaf(v.w, v.w, ss);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            if (lane == 0) red[wave] = ss;
+            __syncthreads();
+            if (tid == 0) inv[t] = 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)p.n_in + p.eps);
+            __syncthreads();
+        }
+    }
+
+    float acc[ROWS][NT];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[r][t] = 0.f;
+
+    const int units_per_tile = p.kt_el / T::BLK_EL * T::UPB;
+    for (int kt = 0; kt < p.n_ktiles; ++kt) {
+        const int k0 = kt * p.kt_el;
+        const int kn = min(p.kt_el, p.n_in - k0);
+        if (kt) __syncthreads();
+        // stage x (normalized when requested) into padded LDS
+        const int q4 = kn / 4;
+        for (int i = tid; i < NT * q4; i += kWG) {
+            const int t = i / q4, k = 4 * (i - t * q4);
+            float4 v = *(const float4*)(p.x + (size_t)t * p.ldx + k0 + k);
+            if (p.norm_w) {
+                const float s = inv[t];
+                const float4 w = *(const float4*)(p.norm_w + k0 + k);
+                v.x = (v.x * s) * w.x; v.y = (v.y * s) * w.y; v.z = (v.z * s) * w.z; v.w = (v.w * s) * w.w;
+            }
+            *(float4*)(xs + t * xs_stride + padx<T::PP>(k)) = v;
+        }
+        __syncthreads();
+        const int n16 = kn / 16;
+        for (int i = tid; i < NT * n16; i += kWG) {
+            const int t = i / n16, g = i - t * n16;
+            const float* src = xs + t * xs_stride + padx<T::PP>(16 * g);
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) s += src[k];
+            sx[t * sx_stride + g] = s;
+        }
+        __syncthreads();
+        UnitCtx c{xs, xs_stride, sx, sx_stride, k0};
+        const int u0 = kt * units_per_tile;
+        const int u1 = min(p.units_per_row, u0 + units_per_tile);
+        for (int u = u0 + li; u < u1; u += LPR) UnitDot<QT, NT, ROWS>::run(rows, ok, u, c, acc);
+    }
+
+    // group reduction (fixed xor butterfly) and epilogue
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float v = acc[r][t];
+#pragma unroll
+            for (int o = LPR / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+            acc[r][t] = v;
+        }
+    if (li != 0) return;
+    if (p.epi == ORC_EPI_SWIGLU) {
+        if (!ok[0]) return;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float g = acc[0][t], u = acc[1][t];
+            yout[0][(size_t)t * p.ldy] = (g / (1.f + expf(-g))) * u;
+        }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        if (!ok[r]) continue;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float v = acc[r][t];
+            if (bias[r]) v += *bias[r];
+            float* dst = yout[r] + (size_t)t * p.ldy;
+            if (p.epi == ORC_EPI_ACCUM) *dst += v;
+            else *dst = v;
+        }
+    }
+}
+
+// ── host-side launch ────────────────────────────────────────────────────────
+static int units_per_block(int type) {
+    switch (type) {
+        case ORC_Q8_0: case ORC_Q4_0: return 1;
+        case ORC_Q4_K: return 8;
+        case ORC_Q6_K: return 4;
+        default: return 0;
+    }
+}
+static int block_elems(int type) { return type == ORC_Q4_K || type == ORC_Q6_K ? 256 : 32; }
+
+// Lanes per row group: a function of (type, n_in) only, never of n_tok, so
+// every token sees the same reduction order.
+static int choose_lpr(int units) {
+    if (units >= 256) return 64;
+    if (units >= 96) return 32;
+    if (units >= 32) return 16;
+    return 8;
+}
+
+constexpr int kRows = 2;
+constexpr size_t kLdsBudget = 64 * 1024;
+
+template <int QT, int NT>
+static int launch_nt(const GemmParams& p0, int lpr, hipStream_t s) {
+    GemmParams p = p0;
+    const int G = 64 / lpr;
+    const int tile = 4 * G * kRows;
+    const int n_items = p.epi == ORC_EPI_SWIGLU ? p.rows[0] * kRows : p.tile_rows_total;
+    const int grid = (n_items + tile - 1) / tile;
+    const int PP = QTr<QT>::PP;
+    // K tile: as many whole blocks as fit the LDS budget, in units a multiple of lpr
+    const int be = QTr<QT>::BLK_EL, upb = QTr<QT>::UPB;
+    auto lds_for = [&](int kt) {
+        return (size_t)NT * ((kt + 4 * (kt / PP) + 4) + kt / 16) * 4 + (8 + 16) * 4;
+    };
+    int kt = (p.n_in + be - 1) / be * be;
+    if (lds_for(kt) > kLdsBudget) {
+        const int blk_step = std::max(1, lpr / upb);  // blocks per step so units stay a multiple of lpr
+        int nb = kLdsBudget / lds_for(be);
+        nb = std::max(blk_step, nb / blk_step * blk_step);
+        kt = nb * be;
+        while (kt > be * blk_step && lds_for(kt) > kLdsBudget) kt -= be * blk_step;
+    }
+    p.kt_el = kt;
+    p.n_ktiles = (p.n_in + kt - 1) / kt;
+    const size_t lds = lds_for(kt);
+    switch (lpr) {
+#define L(LPR_) case LPR_: hipLaunchKernelGGL((k_gemm<QT, NT, LPR_, kRows>), dim3(grid), dim3(kWG), lds, s, p); break;
+        L(8) L(16) L(32) L(64)
+#undef L
+        default: return set_error(ORC_E_INVALID, "bad lpr");
+    }
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+template <int QT>
+static int launch_type(const GemmParams& p, int lpr, hipStream_t s) {
+    switch (p.n_tok) {
+        case 1: return launch_nt<QT, 1>(p, lpr, s);
+        case 2: return launch_nt<QT, 2>(p, lpr, s);
+        case 3: return launch_nt<QT, 3>(p, lpr, s);
+        case 4: return launch_nt<QT, 4>(p, lpr, s);
+        case 5: return launch_nt<QT, 5>(p, lpr, s);
+        case 6: return launch_nt<QT, 6>(p, lpr, s);
+        case 7: return launch_nt<QT, 7>(p, lpr, s);
+        case 8: return launch_nt<QT, 8>(p, lpr, s);
+        case 9: return launch_nt<QT, 9>(p, lpr, s);
+        default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..9");
+    }
+}
+
+static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
+    const int upb = units_per_block(type);
+    p.units_per_row = p.n_in / block_elems(type) * upb;
+    const int lpr = choose_lpr(p.units_per_row);
+    // tokens are processed in chunks of at most 9; chunking never changes a
+    // (token,row) result because the reduction order is independent of n_tok
+    const int total = p.n_tok;
+    for (int t0 = 0; t0 < total; t0 += 9) {
+        GemmParams q = p;
+        q.n_tok = std::min(9, total - t0);
+        q.x = p.x + (size_t)t0 * p.ldx;
+        for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
+        int rc;
+        switch (type) {
+            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, lpr, s); break;
+            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, lpr, s); break;
+            case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, lpr, s); break;
+            case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, lpr, s); break;
+            default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
+        }
+        if (rc) return rc;
+    }
+    return ORC_OK;
+}
+
+}  // namespace orc
+
+using namespace orc;
+
+extern "C" int64_t orc_row_bytes(int type, int64_t n) {
+    switch (type) {
+        case ORC_F32: return n * 4;
+        case ORC_F16: return n * 2;
+        case ORC_Q4_0: return n % 32 ? -1 : n / 32 * 18;
+        case ORC_Q8_0: return n % 32 ? -1 : n / 32 * 34;
+        case ORC_Q4_K: return n % 256 ? -1 : n / 256 * 144;
+        case ORC_Q6_K: return n % 256 ? -1 : n / 256 * 210;
+        default: return -1;
+    }
+}
+
+static int check_gemm_shape(int type, int n_tok, int n_in, const float* x, int ldx, int ldy, const void* w) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0)
+        return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
+    if (n_tok < 1 || n_in <= 0 || n_in % block_elems(type))
+        return set_error(ORC_E_INVALID, "gemm: n_in must be a positive multiple of the block size");
+    if (!x || !w || ldx < n_in || ldx % 4 || ldy < 1)
+        return set_error(ORC_E_INVALID, "gemm: bad pointers or strides (ldx >= n_in, ldx % 4 == 0)");
+    if (((uintptr_t)x & 15) != 0) return set_error(ORC_E_INVALID, "gemm: x must be 16-byte aligned");
+    return ORC_OK;
+}
+
+extern "C" int orc_gemm(int type, const void* d_w, int n_tok, int n_out, int n_in, const float* d_x, int ldx,
+                        float* d_y, int ldy, orc_stream_t stream) {
+    if (int rc = check_gemm_shape(type, n_tok, n_in, d_x, ldx, ldy, d_w)) return rc;
+    if (n_out <= 0 || !d_y || (n_tok > 1 && ldy < n_out)) return set_error(ORC_E_INVALID, "gemm: bad output");
+    GemmParams p{};
+    p.w[0] = (const uint8_t*)d_w;
+    p.y[0] = d_y;
+    p.rows[0] = n_out;
+    p.n_seg = 1;
+    p.tile_rows_total = n_out;
+    p.n_in = n_in;
+    p.row_bytes = (uint64_t)orc_row_bytes(type, n_in);
+    p.x = d_x;
+    p.ldx = ldx;
+    p.ldy = ldy;
+    p.n_tok = n_tok;
+    p.epi = ORC_EPI_STORE;
+    return gemm_dispatch(p, type, resolve_stream(stream));
+}
+
+extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_tok, int n_in, const float* d_x,
+                              int ldx, int ldy, const float* d_norm_w, float eps, int epilogue, orc_stream_t stream) {
+    if (int rc = check_gemm_shape(type, n_tok, n_in, d_x, ldx, ldy, segs ? segs[0].d_w : nullptr)) return rc;
+    if (n_segs < 1 || n_segs > 3) return set_error(ORC_E_INVALID, "gemm_fused: 1..3 segments");
+    if (epilogue == ORC_EPI_SWIGLU && (n_segs != 2 || segs[0].n_out != segs[1].n_out))
+        return set_error(ORC_E_INVALID, "gemm_fused: SwiGLU needs gate and up segments of equal rows");
+    if (epilogue < ORC_EPI_STORE || epilogue > ORC_EPI_SWIGLU) return set_error(ORC_E_INVALID, "bad epilogue");
+    if (d_norm_w && ((uintptr_t)d_norm_w & 15)) return set_error(ORC_E_INVALID, "norm weights must be 16-byte aligned");
+    GemmParams p{};
+    int total = 0;
+    for (int i = 0; i < n_segs; ++i) {
+        if (!segs[i].d_w || !segs[i].d_y || segs[i].n_out <= 0) return set_error(ORC_E_INVALID, "gemm_fused: bad segment");
+        p.w[i] = (const uint8_t*)segs[i].d_w;
+        p.y[i] = segs[i].d_y;
+        p.bias[i] = segs[i].d_bias;
+        p.rows[i] = segs[i].n_out;
+        total += segs[i].n_out;
+    }
+    p.n_seg = n_segs;
+    p.tile_rows_total = total;
+    p.n_in = n_in;
+    p.row_bytes = (uint64_t)orc_row_bytes(type, n_in);
+    p.x = d_x;
+    p.ldx = ldx;
+    p.ldy = ldy;
+    p.n_tok = n_tok;
+    p.norm_w = d_norm_w;
+    p.eps = eps;
+    p.epi = epilogue;
+    return gemm_dispatch(p, type, resolve_stream(stream));
+}
+
+// ── bit-exact dequant (core/gguf_parser.cpp:1029-1154) ───────────────────────
+namespace orc {
+// One thread per 32 consecutive output values; rounding exactly as the
+// reference build: Q4_0/Q8_0/F16 one product or exact conversion, Q4_K
+// fma(d*sc, q, -(dmin*m)) (the reference's d1*q - m1f contracts to one FMA),
+// Q6_K (d*sc)*q with two roundings.
+__device__ __forceinline__ void dequant32(int type, const uint8_t* w, int64_t g, float* out) {
+    switch (type) {
+        case ORC_F32:
+            for (int i = 0; i < 32; ++i) out[i] = ((const float*)w)[g * 32 + i];
+            break;
+        case ORC_F16:
+            for (int i = 0; i < 32; ++i) out[i] = h2f(ld2(w + (g * 32 + i) * 2));
+            break;
+        case ORC_Q8_0: {
+            const uint8_t* b = w + g * 34;
+            const float d = h2f(ld2(b));
+            for (int i = 0; i < 32; ++i) out[i] = d * (float)(int8_t)b[2 + i];
+            break;
+        }
+        case ORC_Q4_0: {
+            const uint8_t* b = w + g * 18;
+            const float d = h2f(ld2(b));
+            for (int l = 0; l < 16; ++l) {
+                out[l] = d * (float)((int)(b[2 + l] & 0xF) - 8);
+                out[l + 16] = d * (float)((int)(b[2 + l] >> 4) - 8);
+            }
+            break;
+        }
+        case ORC_Q4_K: {  // 32 values = one sub-block
+            const int64_t sb = g >> 3;
+            const int s = (int)(g & 7), j = s >> 1, hi = s & 1;
+            const uint8_t* b = w + sb * 144;
+            const float d = h2f(ld2(b)), dmin = h2f(ld2(b + 2));
+            uint32_t sc, mn;
+            q4k_scale_min(s, ld4(b + 4), ld4(b + 8), ld4(b + 12), sc, mn);
+            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+            const uint8_t* qs = b + 16 + 32 * j;
+            for (int l = 0; l < 32; ++l) {
+                const uint32_t q = hi ? (qs[l] >> 4) : (qs[l] & 0xF);
+                out[l] = __builtin_fmaf(d1, (float)q, -m1);
+            }
+            break;
+        }
+        case ORC_Q6_K: {  // 32 values = values 128hh+32gg+[0,32) of superblock sb
+            const int64_t sb = g >> 3;
+            const int s = (int)(g & 7), hh = s >> 2, gg = s & 3;
+            const uint8_t* b = w + sb * 210;
+            const uint8_t* ql = b + 64 * hh;
+            const uint8_t* qh = b + 128 + 32 * hh;
+            const int8_t* sc = (const int8_t*)(b + 192 + 8 * hh);
+            const float d = h2f(ld2(b + 208));
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                int q;
+                if (gg == 0) q = (ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4);
+                else if (gg == 1) q = (ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4);
+                else if (gg == 2) q = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4);
+                else q = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4);
+                out[l] = (d * (float)sc[is + 2 * gg]) * (float)(q - 32);
+            }
+            break;
+        }
+    }
+}
+
+__global__ void k_dequant(int type, const uint8_t* w, int64_t n_groups, float* y) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_groups) return;
+    float v[32];
+    dequant32(type, w, g, v);
+    float4* o = (float4*)(y + g * 32);
+    for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+__global__ void k_embed(int type, const uint8_t* table, int n_in, int n_rows, uint64_t row_bytes, const int32_t* ids,
+                        float* y, int ldy) {
+    const int t = blockIdx.y;
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g * 32 >= n_in) return;
+    int id = ids[t];
+    if (id < 0 || id >= n_rows) id = 0;
+    float v[32];
+    dequant32(type, table + (uint64_t)id * row_bytes, g, v);
+    float4* o = (float4*)(y + (size_t)t * ldy + g * 32);
+    for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+}  // namespace orc
+
+static bool dq_type_ok(int t) {
+    return t == ORC_F32 || t == ORC_F16 || t == ORC_Q4_0 || t == ORC_Q8_0 || t == ORC_Q4_K || t == ORC_Q6_K;
+}
+
+extern "C" int orc_dequant(int type, const void* d_w, int64_t n_el, float* d_y, orc_stream_t stream) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!dq_type_ok(type)) return set_error(ORC_E_UNSUPPORTED, "dequant: unsupported type " + std::to_string(type));
+    const int be = (type == ORC_Q4_K || type == ORC_Q6_K) ? 256 : 32;
+    if (n_el <= 0 || n_el % be || !d_w || !d_y) return set_error(ORC_E_INVALID, "dequant: bad size or pointer");
+    if ((uintptr_t)d_y & 15) return set_error(ORC_E_INVALID, "dequant: output must be 16-byte aligned");
+    const int64_t groups = n_el / 32;
+    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, resolve_stream(stream), type,
+                       (const uint8_t*)d_w, groups, d_y);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_embed(int type, const void* d_table, int n_in, int n_rows, const int32_t* d_ids, int n_tok,
+                         float* d_y, int ldy, orc_stream_t stream) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!dq_type_ok(type)) return set_error(ORC_E_UNSUPPORTED, "embed: unsupported type " + std::to_string(type));
+    const int be = (type == ORC_Q4_K || type == ORC_Q6_K) ? 256 : 32;
+    if (n_in <= 0 || n_in % be || n_rows <= 0 || n_tok < 0 || ldy < n_in || ldy % 4 || !d_table || !d_ids || !d_y)
+        return set_error(ORC_E_INVALID, "embed: bad arguments");
+    if (n_tok == 0) return ORC_OK;
+    const int groups = n_in / 32;
+    hipLaunchKernelGGL(k_embed, dim3((groups + 63) / 64, n_tok), dim3(64), 0, resolve_stream(stream), type,
+                       (const uint8_t*)d_table, n_in, n_rows, (uint64_t)orc_row_bytes(type, n_in), d_ids, d_y, ldy);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}

@@ -1,0 +1,50 @@
+// Internal helpers shared by the HIP translation units of liborc_hip.so.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/orc.h"
+
+namespace orc {
+
+// Error plumbing: the C ABI returns codes; the message is kept per thread.
+int set_error(int code, const std::string& msg);
+hipStream_t resolve_stream(orc_stream_t s);
+bool initialized();
+
+#define ORC_HIP_CHECK(expr)                                                                       \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            return ::orc::set_error(ORC_E_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define ORC_LAUNCH_CHECK() ORC_HIP_CHECK(hipGetLastError())
+
+// ── device helpers ───────────────────────────────────────────────────────────
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Exact IEEE half -> float (the hardware conversion is exact for all inputs,
+// including subnormals, as the reference's fp16() is).
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;
+}
+
+// Unaligned loads: gfx950 under HSA runs in unaligned-access mode, so these
+// compile to single global_load_dword{,x2,x4} at any byte alignment.
+typedef u32x4 __attribute__((aligned(1))) u32x4_u;
+typedef u32x2 __attribute__((aligned(1))) u32x2_u;
+typedef uint32_t __attribute__((aligned(1))) u32_u;
+typedef uint16_t __attribute__((aligned(1))) u16_u;
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return *(const u32x4_u*)p; }
+__device__ __forceinline__ u32x2 ld8(const uint8_t* p) { return *(const u32x2_u*)p; }
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *(const u32_u*)p; }
+__device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const u16_u*)p; }
+
+// Byte k of w as float; the compiler emits one v_cvt_f32_ubyte{k}.
+__device__ __forceinline__ float ubyte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
+
+}  // namespace orc

@@ -1,0 +1,322 @@
+// Transformer elementwise ops, GQA attention over the device KV cache, argmax
+// and greedy acceptance (gfx950).
+//
+// Replaces ops::rmsnorm / ops::rope / ops::softmax / ops::argmax
+// (core/ops.cpp:149-195, 386-497), the KV store and per-head attention loops
+// of Model::forward (core/model.cpp:401-435) and Model::forward_prefill
+// (core/model.cpp:595-626), and the acceptance step of the batched spec loop
+// (benchmark/bench_engine.cpp:337-355).
+#include "orc_internal.hpp"
+
+#include <cfloat>
+
+namespace orc {
+
+// ── RMSNorm: one workgroup per row, the same reduction as the GEMM prologue ───
+__global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float4* xr = (const float4*)(x + (size_t)blockIdx.x * n);
+    float ss = 0.f;
+    for (int i = tid; i < n / 4; i += 256) {
+        float4 v = xr[i];
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    const float s = 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)n + eps);
+    float4* o4 = (float4*)(out + (size_t)blockIdx.x * n);
+    const float4* w4 = (const float4*)w;
+    for (int i = tid; i < n / 4; i += 256) {
+        float4 v = xr[i], g = w4[i];
+        o4[i] = make_float4((v.x * s) * g.x, (v.y * s) * g.y, (v.z * s) * g.z, (v.w * s) * g.w);
+    }
+}
+
+// ── RoPE on q,k + KV store. One workgroup per token. ─────────────────────────
+// rope table: [pos][half] of (cos, sin); KV cache per layer: [n_kv][ctx][hd].
+__global__ __launch_bounds__(256) void k_rope_kv(float* qkv, int ldqkv, int n_heads, int n_kv, int hd, int start_pos,
+                                                 const float2* rope, float* kc, float* vc, int ctx) {
+    const int t = blockIdx.x, pos = start_pos + t, half = hd / 2;
+    float* row = qkv + (size_t)t * ldqkv;
+    const float2* cs = rope + (size_t)pos * half;
+    const int nrot = (n_heads + n_kv) * half;
+    for (int i = threadIdx.x; i < nrot; i += blockDim.x) {
+        const int h = i / half, k = i - h * half;
+        float* v = row + h * hd;  // q heads then k heads are contiguous
+        const float2 c = cs[k];
+        const float a = v[k], b = v[k + half];
+        v[k] = a * c.x - b * c.y;
+        v[k + half] = a * c.y + b * c.x;
+    }
+    __syncthreads();
+    const float* kr = row + n_heads * hd;
+    const float* vr = kr + n_kv * hd;
+    for (int i = threadIdx.x; i < n_kv * hd; i += blockDim.x) {
+        const int g = i / hd, k = i - g * hd;
+        const size_t o = ((size_t)g * ctx + pos) * hd + k;
+        kc[o] = kr[i];
+        vc[o] = vr[i];
+    }
+}
+
+// ── GQA attention, split over KV chunks ──────────────────────────────────────
+// Grid (chunk, kv head). A workgroup stages its KV chunk in LDS once and
+// serves every query row of the group: n_gqa heads x n_tok tokens, processed
+// in batches of RB rows. Per row it writes the chunk-local max m, sum l and
+// unnormalized output O; k_attn_combine merges chunks (online softmax).
+constexpr int kCH = 32, kRB = 16;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_partial(const float* q, int ldq, int n_tok, int n_heads, int n_kv,
+                                                      int start_pos, const float* kc, const float* vc, int ctx,
+                                                      float* work) {
+    __shared__ float Ks[kCH][HD + 4];
+    __shared__ float Vs[kCH][HD];
+    __shared__ float Qs[kRB][HD];
+    __shared__ float Ps[kRB][kCH];
+    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int gqa = n_heads / n_kv;
+    const int p0 = c * kCH;
+    const int pmax = start_pos + n_tok - 1;
+    const int np = min(kCH, pmax + 1 - p0);
+    const float scale = 1.f / sqrtf((float)HD);
+    const float* kg = kc + ((size_t)g * ctx + p0) * HD;
+    const float* vg = vc + ((size_t)g * ctx + p0) * HD;
+    for (int i = tid; i < kCH * HD / 4; i += 256) {
+        const int p = i / (HD / 4), k = 4 * (i - p * (HD / 4));
+        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+        if (p < np) {
+            kv = *(const float4*)(kg + (size_t)p * HD + k);
+            vv = *(const float4*)(vg + (size_t)p * HD + k);
+        }
+        *(float4*)&Ks[p][k] = kv;
+        *(float4*)&Vs[p][k] = vv;
+    }
+    const int nqr = gqa * n_tok;
+    for (int rb = 0; rb < nqr; rb += kRB) {
+        __syncthreads();
+        for (int i = tid; i < kRB * HD; i += 256) {
+            const int r = i / HD, k = i - r * HD, qr = rb + r;
+            float v = 0.f;
+            if (qr < nqr) {
+                const int t = qr / gqa, h = g * gqa + (qr - t * gqa);
+                v = q[(size_t)t * ldq + h * HD + k];
+            }
+            Qs[r][k] = v;
+        }
+        __syncthreads();
+        for (int i = tid; i < kRB * kCH; i += 256) {
+            const int r = i / kCH, p = i - r * kCH, qr = rb + r;
+            float s = -INFINITY;
+            if (qr < nqr && p < np && p0 + p <= start_pos + qr / gqa) {
+                float d = 0.f;
+#pragma unroll 8
+                for (int k = 0; k < HD; k += 4) {
+                    const float4 a = *(const float4*)&Qs[r][k], b = *(const float4*)&Ks[p][k];
+                    d = __builtin_fmaf(a.x, b.x, d);
+                    d = __builtin_fmaf(a.y, b.y, d);
+                    d = __builtin_fmaf(a.z, b.z, d);
+                    d = __builtin_fmaf(a.w, b.w, d);
+                }
+                s = d * scale;
+            }
+            Ps[r][p] = s;
+        }
+        __syncthreads();
+        // row softmax pieces: 32 lanes per row, 8 rows per pass over 256 threads
+        {
+            const int r = tid >> 5, p = tid & 31;
+            for (int rr = r; rr < kRB; rr += 8) {
+                float s = Ps[rr][p];
+                float m = s;
+#pragma unroll
+                for (int o = 16; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 32));
+                const float e = (m == -INFINITY) ? 0.f : expf(s - m);
+                float l = e;
+#pragma unroll
+                for (int o = 16; o >= 1; o >>= 1) l += __shfl_xor(l, o, 32);
+                Ps[rr][p] = e;
+                const int qr = rb + rr;
+                if (p == 0 && qr < nqr) {
+                    const int t = qr / gqa, h = g * gqa + (qr - t * gqa);
+                    float* w = work + (((size_t)c * n_heads + h) * n_tok + t) * (HD + 2);
+                    w[HD] = m;
+                    w[HD + 1] = l;
+                }
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < kRB * HD; i += 256) {
+            const int r = i / HD, k = i - r * HD, qr = rb + r;
+            if (qr >= nqr) continue;
+            float o = 0.f;
+            for (int p = 0; p < np; ++p) o = __builtin_fmaf(Ps[r][p], Vs[p][k], o);
+            const int t = qr / gqa, h = g * gqa + (qr - t * gqa);
+            work[(((size_t)c * n_heads + h) * n_tok + t) * (HD + 2) + k] = o;
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, int start_pos, const float* work,
+                                                     float* out, int ldo) {
+    const int h = blockIdx.x, t = blockIdx.y, k = threadIdx.x;
+    const int nch = (start_pos + t) / kCH + 1;  // chunks that hold positions <= start_pos + t
+    float M = -INFINITY;
+    for (int c = 0; c < nch; ++c) {
+        const float* w = work + (((size_t)c * n_heads + h) * n_tok + t) * (HD + 2);
+        if (w[HD + 1] > 0.f) M = fmaxf(M, w[HD]);
+    }
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < nch; ++c) {
+        const float* w = work + (((size_t)c * n_heads + h) * n_tok + t) * (HD + 2);
+        const float l = w[HD + 1];
+        if (!(l > 0.f)) continue;
+        const float f = expf(w[HD] - M);
+        L = __builtin_fmaf(l, f, L);
+        O = __builtin_fmaf(w[k], f, O);
+    }
+    out[(size_t)t * ldo + h * HD + k] = O / L;
+}
+
+// ── argmax (first index of the maximum) ──────────────────────────────────────
+constexpr int kArgBlock = 1024;  // elements per stage-1 workgroup slice x 4
+
+struct VI { float v; int i; };
+__device__ __forceinline__ VI vi_max(VI a, VI b) {
+    // larger value wins; equal values -> lower index (the reference scans
+    // left to right with a strict '>')
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+__device__ __forceinline__ VI wave_vi_max(VI a) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        VI b{__shfl_xor(a.v, o, 64), __shfl_xor(a.i, o, 64)};
+        a = vi_max(a, b);
+    }
+    return a;
+}
+
+__global__ __launch_bounds__(256) void k_argmax1(const float* x, int n, int ld, int n_slices, VI* part) {
+    __shared__ VI red[4];
+    const int row = blockIdx.y, s = blockIdx.x, tid = threadIdx.x;
+    const float* xr = x + (size_t)row * ld;
+    const int per = (n + n_slices - 1) / n_slices;
+    const int b = s * per, e = min(n, b + per);
+    VI best{-INFINITY, 0x7FFFFFFF};
+    for (int i = b + tid; i < e; i += 256) best = vi_max(best, VI{xr[i], i});
+    best = wave_vi_max(best);
+    if ((tid & 63) == 0) red[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) part[(size_t)row * n_slices + s] = vi_max(vi_max(red[0], red[1]), vi_max(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(64) void k_argmax2(const VI* part, int n_slices, int32_t* out) {
+    const int row = blockIdx.x;
+    VI best{-INFINITY, 0x7FFFFFFF};
+    for (int i = threadIdx.x; i < n_slices; i += 64) best = vi_max(best, part[(size_t)row * n_slices + i]);
+    best = wave_vi_max(best);
+    if (threadIdx.x == 0) out[row] = best.i == 0x7FFFFFFF ? 0 : best.i;
+}
+
+__global__ void k_accept_greedy(const int32_t* tgt, const int32_t* dft, int n_draft, int32_t* out) {
+    if (threadIdx.x != 0) return;
+    int a = 0;
+    while (a < n_draft && tgt[a] == dft[a]) ++a;
+    out[0] = a;
+    out[1] = tgt[a];
+}
+
+}  // namespace orc
+
+using namespace orc;
+
+extern "C" int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_rows, float eps,
+                           orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n <= 0 || n % 4 || n_rows < 0 || !d_out || !d_x || !d_w) return set_error(ORC_E_INVALID, "rmsnorm: bad args");
+    if (((uintptr_t)d_out | (uintptr_t)d_x | (uintptr_t)d_w) & 15)
+        return set_error(ORC_E_INVALID, "rmsnorm: pointers must be 16-byte aligned");
+    if (!n_rows) return ORC_OK;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(n_rows), dim3(256), 0, resolve_stream(s), d_out, d_x, d_w, n, eps);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_rope_kv_store(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
+                                 int start_pos, const float* d_rope, float* d_kc, float* d_vc, int ctx,
+                                 orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n_tok < 0 || n_heads <= 0 || n_kv <= 0 || head_dim <= 0 || head_dim % 2 || start_pos < 0 ||
+        start_pos + n_tok > ctx || ldqkv < (n_heads + 2 * n_kv) * head_dim || !d_qkv || !d_rope || !d_kc || !d_vc)
+        return set_error(ORC_E_INVALID, "rope_kv_store: bad args (positions must fit the context)");
+    if (!n_tok) return ORC_OK;
+    hipLaunchKernelGGL(k_rope_kv, dim3(n_tok), dim3(256), 0, resolve_stream(s), d_qkv, ldqkv, n_heads, n_kv, head_dim,
+                       start_pos, (const float2*)d_rope, d_kc, d_vc, ctx);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" size_t orc_attn_workspace(int n_tok, int n_heads, int head_dim, int max_pos) {
+    const size_t nch = (size_t)(max_pos + kCH - 1) / kCH;
+    return nch * (size_t)n_heads * (size_t)n_tok * (size_t)(head_dim + 2) * sizeof(float);
+}
+
+extern "C" int orc_attn_gqa(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv, int head_dim, int start_pos,
+                            const float* d_kc, const float* d_vc, int ctx, float* d_out, int ldo, void* d_work,
+                            orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || start_pos < 0 || start_pos + n_tok > ctx ||
+        !d_q || !d_kc || !d_vc || !d_out || !d_work || ldq % 4 || ((uintptr_t)d_q & 15))
+        return set_error(ORC_E_INVALID, "attn_gqa: bad args");
+    if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_gqa: head_dim must be 64 or 128");
+    const int nch = (start_pos + n_tok + kCH - 1) / kCH;
+    hipStream_t st = resolve_stream(s);
+    if (head_dim == 64) {
+        hipLaunchKernelGGL(k_attn_partial<64>, dim3(nch, n_kv), dim3(256), 0, st, d_q, ldq, n_tok, n_heads, n_kv,
+                           start_pos, d_kc, d_vc, ctx, (float*)d_work);
+        ORC_LAUNCH_CHECK();
+        hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_heads, n_tok), dim3(64), 0, st, n_tok, n_heads, start_pos,
+                           (const float*)d_work, d_out, ldo);
+    } else {
+        hipLaunchKernelGGL(k_attn_partial<128>, dim3(nch, n_kv), dim3(256), 0, st, d_q, ldq, n_tok, n_heads, n_kv,
+                           start_pos, d_kc, d_vc, ctx, (float*)d_work);
+        ORC_LAUNCH_CHECK();
+        hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_heads, n_tok), dim3(128), 0, st, n_tok, n_heads, start_pos,
+                           (const float*)d_work, d_out, ldo);
+    }
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+static int argmax_slices(int n) { return std::max(1, std::min(256, (n + kArgBlock - 1) / kArgBlock)); }
+
+extern "C" size_t orc_argmax_workspace(int n_rows, int n) { return (size_t)n_rows * argmax_slices(n) * sizeof(VI); }
+
+extern "C" int orc_argmax(const float* d_x, int n_rows, int n, int ld, int32_t* d_out, void* d_work, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n <= 0 || n_rows <= 0 || ld < n || !d_x || !d_out || !d_work) return set_error(ORC_E_INVALID, "argmax: bad args");
+    const int ns = argmax_slices(n);
+    hipStream_t st = resolve_stream(s);
+    hipLaunchKernelGGL(k_argmax1, dim3(ns, n_rows), dim3(256), 0, st, d_x, n, ld, ns, (VI*)d_work);
+    ORC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_argmax2, dim3(n_rows), dim3(64), 0, st, (const VI*)d_work, ns, d_out);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_spec_accept_greedy(const int32_t* d_tgt, const int32_t* d_dft, int n_draft, int32_t* d_out,
+                                      orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n_draft < 0 || !d_tgt || !d_out || (n_draft && !d_dft)) return set_error(ORC_E_INVALID, "accept: bad args");
+    hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64), 0, resolve_stream(s), d_tgt, d_dft, n_draft, d_out);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}

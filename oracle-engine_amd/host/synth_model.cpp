@@ -1,0 +1,190 @@
+#include "synth_model.hpp"
+#include "gguf_writer.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <map>
+
+namespace orc {
+
+static inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static uint64_t tensor_key(uint64_t seed, const std::string& name) {
+    uint64_t h = 0xCBF29CE484222325ull ^ mix64(seed);
+    for (unsigned char c : name) h = (h ^ c) * 0x100000001B3ull;
+    return mix64(h);
+}
+
+static inline float normal_at(uint64_t key, uint64_t i, float sigma) {
+    uint64_t r = mix64(key + (i + 1) * 0x9E3779B97F4A7C15ull);
+    double u1 = ((double)(r >> 32) + 0.5) * (1.0 / 4294967296.0);
+    double u2 = ((double)(r & 0xFFFFFFFFull) + 0.5) * (1.0 / 4294967296.0);
+    double z = std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+    return (float)(sigma * z);
+}
+
+float synth_weight(uint64_t seed, const std::string& tensor, uint64_t i) {
+    return normal_at(tensor_key(seed, tensor), i, 0.02f);
+}
+
+static SynthSpec tiny(const std::string& name) {
+    SynthSpec s;
+    s.name = name;
+    s.n_layers = 2; s.d_model = 512; s.n_heads = 8; s.n_kv_heads = 2; s.head_dim = 64;
+    s.ffn = 1024; s.vocab = 2048; s.seed = 7;
+    return s;
+}
+
+bool synth_preset(const std::string& name, SynthSpec& s) {
+    using T = GGMLType;
+    if (name == "c1") {  // Llama-3.2-1B shape, all Q8_0, tied
+        s = SynthSpec{}; s.name = name; s.arch = "llama";
+        s.n_layers = 16; s.d_model = 2048; s.n_heads = 32; s.n_kv_heads = 8; s.head_dim = 64;
+        s.ffn = 8192; s.vocab = 128256; s.rope_theta = 500000.f; s.tied = true; s.seed = 101;
+        s.t_default = s.t_attn_v = s.t_ffn_down = s.t_embd = T::Q8_0;
+        return true;
+    }
+    if (name == "c2" || name == "c3d") {  // Llama-3.2-3B shape, Q4_K_M mix, tied (head = token_embd Q6_K)
+        s = SynthSpec{}; s.name = name; s.arch = "llama";
+        s.n_layers = 28; s.d_model = 3072; s.n_heads = 24; s.n_kv_heads = 8; s.head_dim = 128;
+        s.ffn = 8192; s.vocab = 128256; s.rope_theta = 500000.f; s.tied = true; s.seed = 202;
+        s.t_default = T::Q4_K; s.t_attn_v = T::Q6_K; s.t_ffn_down = T::Q6_K; s.t_embd = T::Q6_K;
+        if (name == "c3d") {  // draft: the target's float layers 0..7 and head, all Q8_0
+            s.n_layers = 8; s.tied = false; s.head_from_embd = true;
+            s.t_default = s.t_attn_v = s.t_ffn_down = s.t_embd = s.t_output = T::Q8_0;
+        }
+        return true;
+    }
+    if (name == "c4" || name == "c5") {  // Qwen2.5-7B shape, QKV bias, untied
+        s = SynthSpec{}; s.name = name; s.arch = "qwen2";
+        s.n_layers = 28; s.d_model = 3584; s.n_heads = 28; s.n_kv_heads = 4; s.head_dim = 128;
+        s.ffn = 18944; s.vocab = 152064; s.rope_theta = 1000000.f; s.rms_eps = 1e-6f;
+        s.tied = false; s.qkv_bias = true; s.seed = 404;
+        if (name == "c4") {
+            s.t_default = T::Q4_K; s.t_attn_v = T::Q6_K; s.t_ffn_down = T::Q6_K;
+            s.t_embd = T::Q4_K; s.t_output = T::Q6_K;
+        } else {
+            s.t_default = s.t_attn_v = s.t_ffn_down = s.t_embd = s.t_output = T::Q6_K;
+        }
+        return true;
+    }
+    if (name == "c4d") {  // Qwen2.5-0.5B shape draft, Q8_0, tied
+        s = SynthSpec{}; s.name = name; s.arch = "qwen2";
+        s.n_layers = 24; s.d_model = 896; s.n_heads = 14; s.n_kv_heads = 2; s.head_dim = 64;
+        s.ffn = 4864; s.vocab = 152064; s.rope_theta = 1000000.f; s.rms_eps = 1e-6f;
+        s.tied = true; s.qkv_bias = true; s.seed = 505;
+        s.t_default = s.t_attn_v = s.t_ffn_down = s.t_embd = T::Q8_0;
+        return true;
+    }
+    // Small models for parity tests (the reference runs them in seconds).
+    if (name == "t-q8") { s = tiny(name); return true; }
+    if (name == "t-q40") {
+        s = tiny(name); s.t_default = s.t_attn_v = s.t_ffn_down = s.t_embd = T::Q4_0; return true;
+    }
+    if (name == "t-q4k" || name == "t-q4k-d") {  // Q4_K_M-style mix; -d: 1-layer Q8_0 draft of it
+        s = tiny("t-q4k");
+        s.t_default = T::Q4_K; s.t_attn_v = T::Q6_K; s.t_ffn_down = T::Q6_K; s.t_embd = T::Q6_K;
+        if (name == "t-q4k-d") {
+            s.name = name; s.n_layers = 1; s.tied = false; s.head_from_embd = true;
+            s.t_default = s.t_attn_v = s.t_ffn_down = s.t_embd = s.t_output = T::Q8_0;
+        }
+        return true;
+    }
+    if (name == "t-q6k") {
+        s = tiny(name); s.tied = false;
+        s.t_default = s.t_attn_v = s.t_ffn_down = s.t_embd = s.t_output = T::Q6_K; return true;
+    }
+    if (name == "t-qwen") {  // qwen2 arch: biases, untied Q4_K embedding + Q6_K head
+        s = tiny(name); s.arch = "qwen2"; s.qkv_bias = true; s.tied = false; s.rope_theta = 1000000.f;
+        s.n_heads = 8; s.n_kv_heads = 4; s.rms_eps = 1e-6f;
+        s.t_default = T::Q4_K; s.t_attn_v = T::Q6_K; s.t_ffn_down = T::Q6_K;
+        s.t_embd = T::Q4_K; s.t_output = T::Q6_K; return true;
+    }
+    if (name == "t-qwen-d") {  // independent 1-layer Q8_0 draft for t-qwen (stochastic spec tests)
+        s = tiny(name); s.arch = "qwen2"; s.qkv_bias = true; s.tied = true; s.rope_theta = 1000000.f;
+        s.n_layers = 1; s.d_model = 256; s.n_heads = 4; s.n_kv_heads = 2; s.ffn = 512; s.seed = 9;
+        s.rms_eps = 1e-6f; return true;
+    }
+    return false;
+}
+
+std::vector<std::string> synth_preset_names() {
+    return {"c1", "c2", "c3d", "c4", "c4d", "c5", "t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen",
+            "t-qwen-d"};
+}
+
+bool synth_write(const SynthSpec& s, const std::string& path, bool verbose) {
+    GGUFWriter w;
+    const std::string a = s.arch;
+    w.add_str("general.architecture", a);
+    w.add_str("general.name", "orc-synthetic-" + s.name);
+    w.add_u32(a + ".block_count", (uint32_t)s.n_layers);
+    w.add_u32(a + ".context_length", 131072);
+    w.add_u32(a + ".embedding_length", (uint32_t)s.d_model);
+    w.add_u32(a + ".feed_forward_length", (uint32_t)s.ffn);
+    w.add_u32(a + ".attention.head_count", (uint32_t)s.n_heads);
+    w.add_u32(a + ".attention.head_count_kv", (uint32_t)s.n_kv_heads);
+    w.add_u32(a + ".attention.key_length", (uint32_t)s.head_dim);
+    w.add_u32(a + ".attention.value_length", (uint32_t)s.head_dim);
+    w.add_f32(a + ".rope.freq_base", s.rope_theta);
+    w.add_f32(a + ".attention.layer_norm_rms_epsilon", s.rms_eps);
+    w.add_u32(a + ".vocab_size", (uint32_t)s.vocab);
+
+    const uint64_t seed = s.seed;
+    const int D = s.d_model, NQ = s.n_heads * s.head_dim, NKV = s.n_kv_heads * s.head_dim, FF = s.ffn;
+
+    // A quantized matrix [n_in, n_out] whose floats come from stream `src`.
+    auto matrix = [&](const std::string& name, const std::string& src, int n_in, int n_out, GGMLType t) {
+        w.add_tensor(name, {(uint64_t)n_in, (uint64_t)n_out}, t,
+                     [seed, src, n_in, t](int64_t r0, int64_t r1, uint8_t* dst) {
+                         const uint64_t key = tensor_key(seed, src);
+                         const uint64_t rb = row_bytes(t, n_in);
+#pragma omp parallel for schedule(dynamic, 16)
+                         for (int64_t r = r0; r < r1; ++r) {
+                             std::vector<float> row(n_in);
+                             for (int i = 0; i < n_in; ++i) row[i] = normal_at(key, (uint64_t)r * n_in + i, 0.02f);
+                             quantize_any(t, row.data(), n_in, dst + (r - r0) * rb);
+                         }
+                     });
+    };
+    auto ones = [&](const std::string& name, int n) {
+        w.add_tensor(name, {(uint64_t)n}, GGMLType::F32, [n](int64_t, int64_t, uint8_t* dst) {
+            for (int i = 0; i < n; ++i) { float one = 1.f; std::memcpy(dst + 4 * i, &one, 4); }
+        });
+    };
+    auto bias = [&](const std::string& name, int n) {
+        w.add_tensor(name, {(uint64_t)n}, GGMLType::F32, [seed, name, n](int64_t, int64_t, uint8_t* dst) {
+            const uint64_t key = tensor_key(seed, name);
+            for (int i = 0; i < n; ++i) { float v = normal_at(key, (uint64_t)i, 0.02f); std::memcpy(dst + 4 * i, &v, 4); }
+        });
+    };
+
+    matrix("token_embd.weight", "token_embd.weight", D, s.vocab, s.t_embd);
+    for (int l = 0; l < s.n_layers; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        ones(b + "attn_norm.weight", D);
+        matrix(b + "attn_q.weight", b + "attn_q.weight", D, NQ, s.t_default);
+        matrix(b + "attn_k.weight", b + "attn_k.weight", D, NKV, s.t_default);
+        matrix(b + "attn_v.weight", b + "attn_v.weight", D, NKV, s.t_attn_v);
+        if (s.qkv_bias) {
+            bias(b + "attn_q.bias", NQ);
+            bias(b + "attn_k.bias", NKV);
+            bias(b + "attn_v.bias", NKV);
+        }
+        matrix(b + "attn_output.weight", b + "attn_output.weight", NQ, D, s.t_default);
+        ones(b + "ffn_norm.weight", D);
+        matrix(b + "ffn_gate.weight", b + "ffn_gate.weight", D, FF, s.t_default);
+        matrix(b + "ffn_up.weight", b + "ffn_up.weight", D, FF, s.t_default);
+        matrix(b + "ffn_down.weight", b + "ffn_down.weight", FF, D, s.t_ffn_down);
+    }
+    ones("output_norm.weight", D);
+    if (!s.tied)
+        matrix("output.weight", s.head_from_embd ? "token_embd.weight" : "output.weight", D, s.vocab, s.t_output);
+    return w.write(path, verbose);
+}
+
+}  // namespace orc

@@ -1,0 +1,151 @@
+"""ctypes binding of the C ABI in include/orc.h (liborc_hip.so) and of the
+host C API in include/oracle_host.h (liboracle_host.so).
+
+Used by tests/, bench.py and __graft_entry__.py. Loading fails loudly when the
+HIP library has not been built: there is no CPU fallback on the product path.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(PKG, "lib")
+HIP_LIB = os.path.join(LIB_DIR, "liborc_hip.so")
+HOST_LIB = os.path.join(LIB_DIR, "liboracle_host.so")
+BIN_DIR = os.path.join(PKG, "bin")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+EPI_STORE, EPI_ACCUM, EPI_SWIGLU = 0, 1, 2
+
+_vp = C.c_void_p
+_fp = C.POINTER(C.c_float)
+_ip = C.POINTER(C.c_int32)
+
+
+class OrcError(RuntimeError):
+    pass
+
+
+class Seg(C.Structure):
+    _fields_ = [("d_w", _vp), ("n_out", C.c_int), ("d_y", _vp), ("d_bias", _vp)]
+
+
+# (name, restype, argtypes) for every entry point declared in include/orc.h
+ABI = [
+    ("orc_init", C.c_int, [C.c_int]),
+    ("orc_shutdown", C.c_int, []),
+    ("orc_last_error", C.c_char_p, []),
+    ("orc_device_info", C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_size_t)]),
+    ("orc_malloc", C.c_int, [C.POINTER(_vp), C.c_size_t]),
+    ("orc_free", C.c_int, [_vp]),
+    ("orc_memcpy_h2d", C.c_int, [_vp, _vp, C.c_size_t, _vp]),
+    ("orc_memcpy_d2h", C.c_int, [_vp, _vp, C.c_size_t, _vp]),
+    ("orc_memcpy_d2d", C.c_int, [_vp, _vp, C.c_size_t, _vp]),
+    ("orc_fill", C.c_int, [_vp, C.c_int, C.c_size_t, _vp]),
+    ("orc_upload", C.c_int, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    ("orc_stream_create", C.c_int, [C.POINTER(_vp)]),
+    ("orc_stream_destroy", C.c_int, [_vp]),
+    ("orc_stream_sync", C.c_int, [_vp]),
+    ("orc_device_sync", C.c_int, []),
+    ("orc_graph_begin", C.c_int, [_vp]),
+    ("orc_graph_end", C.c_int, [_vp, C.POINTER(_vp)]),
+    ("orc_graph_launch", C.c_int, [_vp, _vp]),
+    ("orc_graph_destroy", C.c_int, [_vp]),
+    ("orc_event_create", C.c_int, [C.POINTER(_vp)]),
+    ("orc_event_destroy", C.c_int, [_vp]),
+    ("orc_event_record", C.c_int, [_vp, _vp]),
+    ("orc_event_elapsed_ms", C.c_int, [_vp, _vp, C.POINTER(C.c_float)]),
+    ("orc_row_bytes", C.c_int64, [C.c_int, C.c_int64]),
+    ("orc_dequant", C.c_int, [C.c_int, _vp, C.c_int64, _vp, _vp]),
+    ("orc_embed", C.c_int, [C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp]),
+    ("orc_gemm", C.c_int, [C.c_int, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp]),
+    ("orc_gemm_fused", C.c_int, [C.c_int, C.POINTER(Seg), C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
+                                 C.c_float, C.c_int, _vp]),
+    ("orc_rmsnorm", C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_float, _vp]),
+    ("orc_rope_kv_store", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp,
+                                    C.c_int, _vp]),
+    ("orc_attn_workspace", C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int]),
+    ("orc_attn_gqa", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp,
+                               C.c_int, _vp, _vp]),
+    ("orc_argmax_workspace", C.c_size_t, [C.c_int, C.c_int]),
+    ("orc_argmax", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
+    ("orc_spec_accept_greedy", C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
+]
+
+
+def load_hip_lib(path=HIP_LIB):
+    if not os.path.exists(path):
+        raise OrcError(f"{path} is missing: build it with __graft_entry__.build() (no CPU fallback exists)")
+    lib = C.CDLL(path, mode=C.RTLD_GLOBAL)
+    for name, res, args in ABI:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+class Device:
+    """The HIP library plus small helpers for device buffers."""
+
+    def __init__(self, device=0):
+        self.L = load_hip_lib()
+        self.check(self.L.orc_init(device))
+
+    def check(self, rc):
+        if rc != 0:
+            raise OrcError(f"orc error {rc}: {self.L.orc_last_error().decode()}")
+        return rc
+
+    def info(self):
+        name = C.create_string_buffer(256)
+        cu = C.c_int()
+        hbm = C.c_size_t()
+        self.check(self.L.orc_device_info(name, 256, C.byref(cu), C.byref(hbm)))
+        return name.value.decode(), cu.value, hbm.value
+
+    def alloc(self, nbytes):
+        p = _vp()
+        self.check(self.L.orc_malloc(C.byref(p), max(int(nbytes), 1)))
+        return DBuf(self, p.value, int(nbytes))
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = self.alloc(arr.nbytes)
+        b.write(arr)
+        return b
+
+    def sync(self):
+        self.check(self.L.orc_device_sync())
+
+
+class DBuf:
+    def __init__(self, dev, ptr, nbytes):
+        self.dev, self.ptr, self.nbytes = dev, ptr, nbytes
+
+    def write(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        self.dev.check(self.dev.L.orc_memcpy_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes, None))
+
+    def read(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype)
+        self.dev.check(self.dev.L.orc_memcpy_d2h(out.ctypes.data, self.ptr + offset, out.nbytes, None))
+        return out
+
+    def at(self, offset):
+        return self.ptr + offset
+
+    def free(self):
+        if self.ptr:
+            self.dev.L.orc_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

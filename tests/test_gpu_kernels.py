@@ -1,0 +1,248 @@
+"""Parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars: dequant bit-exact; GEMV within 2e-6 of sum|w*x| of the float64 result
+and 1e-3 relative (norm-wise) of the oracle's fp32 gemv; the n-token GEMM
+bit-identical to n separate GEMVs; elementwise ops within 1e-6 relative.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from conftest import rand_blocks
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [ol.Q4_K, ol.Q6_K, ol.Q8_0, ol.Q4_0]
+_libm = C.CDLL("libm.so.6")
+_libm.powf.restype = C.c_float
+_libm.powf.argtypes = [C.c_float, C.c_float]
+_libm.cosf.restype = C.c_float
+_libm.cosf.argtypes = [C.c_float]
+_libm.sinf.restype = C.c_float
+_libm.sinf.argtypes = [C.c_float]
+
+
+def rope_table(max_pos, hd, base):
+    """cos/sin pairs with the reference's float powf/cosf/sinf (ops.cpp:461-466)."""
+    half = hd // 2
+    t = np.zeros((max_pos, half, 2), np.float32)
+    inv = [np.float32(_libm.powf(C.c_float(base), C.c_float(np.float32(2 * i) / np.float32(hd)))) for i in range(half)]
+    for p in range(max_pos):
+        for i in range(half):
+            th = np.float32(np.float32(p) / inv[i])
+            t[p, i, 0] = _libm.cosf(C.c_float(th))
+            t[p, i, 1] = _libm.sinf(C.c_float(th))
+    return t
+
+
+@pytest.mark.parametrize("qt", TYPES + [ol.F16])
+def test_dequant_bitexact(dev, oracle, qt):
+    print(f"[gpu] dequant type={qt}", flush=True)
+    rng = np.random.default_rng(qt)
+    n = 256 * 40
+    raw = rand_blocks(qt, n, rng)
+    want = oracle.dequant(qt, raw, n)
+    dw, dy = dev.upload(raw), dev.alloc(n * 4)
+    dev.check(dev.L.orc_dequant(qt, dw.ptr, n, dy.ptr, None))
+    got = dy.read(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_fp16_exhaustive(dev, oracle):
+    print("[gpu] fp16 sweep", flush=True)
+    raw = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.uint8)
+    want = oracle.dequant(ol.F16, raw, 65536)
+    dw, dy = dev.upload(raw), dev.alloc(65536 * 4)
+    dev.check(dev.L.orc_dequant(ol.F16, dw.ptr, 65536, dy.ptr, None))
+    got = dy.read(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _gemm(dev, qt, w_dev, n_tok, n_out, n_in, X):
+    dx = dev.upload(np.ascontiguousarray(X, np.float32))
+    dy = dev.alloc(n_tok * n_out * 4)
+    dev.check(dev.L.orc_gemm(qt, w_dev.ptr, n_tok, n_out, n_in, dx.ptr, n_in, dy.ptr, n_out, None))
+    return dy.read(np.float32).reshape(n_tok, n_out)
+
+
+SHAPES = [(ol.Q4_K, 515, 3072), (ol.Q4_K, 64, 3584), (ol.Q6_K, 301, 3072), (ol.Q6_K, 130, 8192),
+          (ol.Q8_0, 700, 896), (ol.Q8_0, 129, 2048), (ol.Q4_0, 257, 2048), (ol.Q6_K, 40, 18944)]
+
+
+@pytest.mark.parametrize("qt,n_out,n_in", SHAPES)
+def test_gemv_vs_exact(dev, oracle, qt, n_out, n_in):
+    print(f"[gpu] gemv type={qt} {n_out}x{n_in}", flush=True)
+    rng = np.random.default_rng(n_out * 7 + n_in)
+    raw = rand_blocks(qt, n_out * n_in, rng)
+    x = rng.uniform(-1, 1, n_in).astype(np.float32)
+    got = _gemm(dev, qt, dev.upload(raw), 1, n_out, n_in, x[None])[0]
+    W = oracle.dequant(qt, raw, n_out * n_in).reshape(n_out, n_in).astype(np.float64)
+    exact = W @ x.astype(np.float64)
+    scale = np.abs(W) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(got - exact) <= 2e-6 * scale + 1e-30), np.max(np.abs(got - exact) / scale)
+    ref = oracle.gemv(qt, raw, n_out, n_in, x)  # fp32 restatement of gemv_q
+    assert np.linalg.norm(got - ref) <= 1e-3 * np.linalg.norm(ref)
+
+
+@pytest.mark.parametrize("qt,n_out,n_in", [(ol.Q4_K, 200, 3072), (ol.Q6_K, 77, 8192), (ol.Q8_0, 90, 896),
+                                           (ol.Q4_0, 33, 2048), (ol.Q6_K, 24, 18944)])
+def test_gemm_batch_invariant(dev, qt, n_out, n_in):
+    """verify(n)[t] is bit-identical to the decode GEMV of token t, n = 1..12."""
+    print(f"[gpu] gemm invariance type={qt} {n_out}x{n_in}", flush=True)
+    rng = np.random.default_rng(3)
+    raw = rand_blocks(qt, n_out * n_in, rng)
+    wd = dev.upload(raw)
+    X = rng.normal(0, 1, (12, n_in)).astype(np.float32)
+    single = np.stack([_gemm(dev, qt, wd, 1, n_out, n_in, X[t:t + 1])[0] for t in range(12)])
+    for nt in (2, 5, 7, 9, 12):
+        got = _gemm(dev, qt, wd, nt, n_out, n_in, X[:nt])
+        assert np.array_equal(got.view(np.uint32), single[:nt].view(np.uint32)), nt
+
+
+def test_gemm_fused_epilogues(dev):
+    print("[gpu] fused epilogues", flush=True)
+    import orc
+
+    rng = np.random.default_rng(11)
+    n_in, nq, nk, ff = 512, 256, 128, 384
+    wq, wk, wv = (dev.upload(rand_blocks(ol.Q4_K, n * n_in, rng)) for n in (nq, nk, nk))
+    bq = dev.upload(rng.normal(0, 0.1, nq).astype(np.float32))
+    normw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
+    dnorm = dev.upload(normw)
+    for nt in (1, 4):
+        X = rng.normal(0, 1, (nt, n_in)).astype(np.float32)
+        dx = dev.upload(X)
+        # reference composition: rmsnorm kernel, then plain GEMMs, bias on the host
+        dxn = dev.alloc(X.nbytes)
+        dev.check(dev.L.orc_rmsnorm(dxn.ptr, dx.ptr, dnorm.ptr, n_in, nt, C.c_float(1e-5), None))
+        Xn = dxn.read(np.float32).reshape(nt, n_in)
+        ref = [_gemm(dev, ol.Q4_K, w, nt, n, n_in, Xn) for w, n in ((wq, nq), (wk, nk), (wv, nk))]
+        ref[0] = ref[0] + bq.read(np.float32)[None]
+        ld = nq + 2 * nk
+        dy = dev.alloc(nt * ld * 4)
+        segs = (orc.Seg * 3)(orc.Seg(wq.ptr, nq, dy.ptr, bq.ptr), orc.Seg(wk.ptr, nk, dy.ptr + nq * 4, None),
+                             orc.Seg(wv.ptr, nk, dy.ptr + (nq + nk) * 4, None))
+        dev.check(dev.L.orc_gemm_fused(ol.Q4_K, segs, 3, nt, n_in, dx.ptr, n_in, ld, dnorm.ptr, C.c_float(1e-5),
+                                       orc.EPI_STORE, None))
+        Y = dy.read(np.float32).reshape(nt, ld)
+        assert np.array_equal(Y[:, :nq], ref[0])
+        assert np.array_equal(Y[:, nq:nq + nk], ref[1])
+        assert np.array_equal(Y[:, nq + nk:], ref[2])
+        # SwiGLU: silu(gate) * up
+        wg, wu = (dev.upload(rand_blocks(ol.Q6_K, ff * n_in, rng)) for _ in range(2))
+        g = _gemm(dev, ol.Q6_K, wg, nt, ff, n_in, X)
+        u = _gemm(dev, ol.Q6_K, wu, nt, ff, n_in, X)
+        dh = dev.alloc(nt * ff * 4)
+        segs2 = (orc.Seg * 2)(orc.Seg(wg.ptr, ff, dh.ptr, None), orc.Seg(wu.ptr, ff, None, None))
+        segs2[1].d_y = dh.ptr
+        dev.check(dev.L.orc_gemm_fused(ol.Q6_K, segs2, 2, nt, n_in, dx.ptr, n_in, ff, None, C.c_float(0),
+                                       orc.EPI_SWIGLU, None))
+        h = dh.read(np.float32).reshape(nt, ff)
+        want = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
+        assert np.allclose(h, want, rtol=1e-5, atol=1e-6)
+        # residual accumulate
+        res = rng.normal(0, 1, (nt, nk)).astype(np.float32)
+        dr = dev.upload(res)
+        segs3 = (orc.Seg * 1)(orc.Seg(wk.ptr, nk, dr.ptr, None))
+        dev.check(dev.L.orc_gemm_fused(ol.Q4_K, segs3, 1, nt, n_in, dx.ptr, n_in, nk, None, C.c_float(0),
+                                       orc.EPI_ACCUM, None))
+        plain = _gemm(dev, ol.Q4_K, wk, nt, nk, n_in, X)
+        assert np.array_equal(dr.read(np.float32).reshape(nt, nk), res + plain)
+
+
+def test_rmsnorm(dev, oracle):
+    rng = np.random.default_rng(5)
+    for n in (896, 2048, 3072, 3584):
+        x = rng.normal(0, 2, (3, n)).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        dx, dw, dy = dev.upload(x), dev.upload(w), dev.alloc(x.nbytes)
+        dev.check(dev.L.orc_rmsnorm(dy.ptr, dx.ptr, dw.ptr, n, 3, C.c_float(1e-5), None))
+        got = dy.read(np.float32).reshape(3, n)
+        for r in range(3):
+            assert np.allclose(got[r], oracle.rmsnorm(x[r], w), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("H,KVH,hd,base", [(24, 8, 128, 500000.0), (28, 4, 128, 1e6), (14, 2, 64, 1e6)])
+def test_rope_kv_store(dev, oracle, H, KVH, hd, base):
+    print(f"[gpu] rope H={H} KVH={KVH} hd={hd}", flush=True)
+    rng = np.random.default_rng(H)
+    ctx, nt, sp = 64, 5, 37
+    ld = (H + 2 * KVH) * hd
+    qkv = rng.normal(0, 1, (nt, ld)).astype(np.float32)
+    tab = rope_table(ctx, hd, base)
+    dq, dt = dev.upload(qkv), dev.upload(tab)
+    kc, vc = dev.alloc(KVH * ctx * hd * 4), dev.alloc(KVH * ctx * hd * 4)
+    dev.check(dev.L.orc_rope_kv_store(dq.ptr, ld, nt, H, KVH, hd, sp, dt.ptr, kc.ptr, vc.ptr, ctx, None))
+    got = dq.read(np.float32).reshape(nt, ld)
+    K = kc.read(np.float32).reshape(KVH, ctx, hd)
+    V = vc.read(np.float32).reshape(KVH, ctx, hd)
+    for t in range(nt):
+        q, k = oracle.rope(qkv[t, :H * hd], qkv[t, H * hd:(H + KVH) * hd], H, KVH, hd, sp + t, base)
+        assert np.allclose(got[t, :H * hd], q, rtol=1e-5, atol=2e-6)
+        assert np.allclose(got[t, H * hd:(H + KVH) * hd], k, rtol=1e-5, atol=2e-6)
+        assert np.array_equal(K[:, sp + t, :].reshape(-1), got[t, H * hd:(H + KVH) * hd])
+        assert np.array_equal(V[:, sp + t, :].reshape(-1), qkv[t, (H + KVH) * hd:])
+
+
+@pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 0, 1), (24, 8, 128, 200, 1), (24, 8, 128, 127, 5),
+                                            (28, 4, 128, 700, 7), (14, 2, 64, 31, 9), (32, 8, 64, 1000, 1)])
+def test_attention(dev, oracle, H, KVH, hd, sp, nt):
+    print(f"[gpu] attention H={H} KVH={KVH} hd={hd} sp={sp} nt={nt}", flush=True)
+    rng = np.random.default_rng(sp + nt)
+    ctx = sp + nt + 3
+    K = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    V = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    Q = rng.normal(0, 1, (nt, H * hd)).astype(np.float32)
+    dK, dV, dQ = dev.upload(K), dev.upload(V), dev.upload(Q)
+    dO = dev.alloc(nt * H * hd * 4)
+    ws = dev.alloc(dev.L.orc_attn_workspace(nt, H, hd, ctx))
+    dev.check(dev.L.orc_attn_gqa(dQ.ptr, H * hd, nt, H, KVH, hd, sp, dK.ptr, dV.ptr, ctx, dO.ptr, H * hd, ws.ptr,
+                                 None))
+    got = dO.read(np.float32).reshape(nt, H * hd)
+    kc = K.transpose(1, 0, 2).reshape(ctx, KVH * hd)  # oracle layout [pos][kv*hd]
+    vc = V.transpose(1, 0, 2).reshape(ctx, KVH * hd)
+    for t in range(nt):
+        want = oracle.attention(Q[t], kc, vc, H, KVH, hd, sp + t)
+        assert np.allclose(got[t], want, rtol=1e-5, atol=2e-6), np.abs(got[t] - want).max()
+
+
+def test_argmax_first_index(dev, oracle):
+    rng = np.random.default_rng(9)
+    rows, n = 6, 128256
+    x = rng.normal(0, 1, (rows, n)).astype(np.float32)
+    x[1, 5] = x[1, 99999] = 50.0          # tie: first index wins
+    x[2, :] = 1.0                          # all equal -> 0
+    x[3, n - 1] = 77.0                     # maximum at the end
+    x[4, 0] = 77.0                         # maximum at the start
+    dx, do = dev.upload(x), dev.alloc(rows * 4)
+    ws = dev.alloc(dev.L.orc_argmax_workspace(rows, n))
+    dev.check(dev.L.orc_argmax(dx.ptr, rows, n, n, do.ptr, ws.ptr, None))
+    got = do.read(np.int32)
+    assert list(got) == [oracle.argmax(x[r]) for r in range(rows)]
+    assert got[1] == 5 and got[2] == 0 and got[3] == n - 1 and got[4] == 0
+
+
+def test_accept_greedy(dev):
+    cases = [([5, 6, 7, 8, 9], [5, 6, 7, 8], 4, 9), ([5, 6, 7, 8, 9], [5, 1, 7, 8], 1, 6),
+             ([3, 6, 7, 8, 9], [5, 6, 7, 8], 0, 3), ([1, 2], [1], 1, 2)]
+    for tgt, dft, a, nxt in cases:
+        dt, dd, do = dev.upload(np.array(tgt, np.int32)), dev.upload(np.array(dft, np.int32)), dev.alloc(8)
+        dev.check(dev.L.orc_spec_accept_greedy(dt.ptr, dd.ptr, len(dft), do.ptr, None))
+        assert list(do.read(np.int32)) == [a, nxt]
+
+
+def test_error_paths(dev):
+    """Bad shapes and unsupported types are rejected before any launch."""
+    import orc
+
+    d = dev.alloc(4096)
+    assert dev.L.orc_gemm(13, d.ptr, 1, 4, 256, d.ptr, 256, d.ptr, 4, None) == -2  # Q5_K unsupported
+    assert dev.L.orc_gemm(ol.Q4_K, d.ptr, 1, 4, 100, d.ptr, 100, d.ptr, 4, None) == -1  # n_in not a block multiple
+    assert dev.L.orc_rope_kv_store(d.ptr, 1024, 2, 4, 2, 64, 63, d.ptr, d.ptr, d.ptr, 64, None) == -1  # past ctx
+    assert b"ctx" in dev.L.orc_last_error() or b"context" in dev.L.orc_last_error()
+    with pytest.raises(orc.OrcError):
+        dev.check(dev.L.orc_dequant(13, d.ptr, 256, d.ptr, None))
