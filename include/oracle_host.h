@@ -1,0 +1,50 @@
+/*
+ * oracle_host.h — C API of the C++ host (liboracle_host.so) that mirrors the
+ * reference's Model / harness API on top of orc.h. It exists so that
+ * non-C++ callers (the Python tests and bench.py, a ctypes/cgo binding) can
+ * drive whole decode loops; C++ callers use host/model.hpp and host/spec.hpp
+ * directly. Every entry point names the reference API it exposes.
+ */
+#ifndef ORACLE_HOST_H
+#define ORACLE_HOST_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct orch_model orch_model;
+
+/* Model::load (core/model.cpp:17-96); ctx_len 0 keeps the reference's 512. */
+orch_model* orch_load(const char* gguf_path, int ctx_len);
+void orch_free(orch_model* m);
+/* Message of the last failure (load or call), "" if none. */
+const char* orch_error(const orch_model* m);
+/* cfg[0..9] = n_vocab, n_layers, n_heads, n_kv_heads, embed_dim, ffn_hidden,
+ * head_dim, ctx_len, has_qkv_bias, tied_head (ModelConfig, core/model.hpp:10-27). */
+int orch_cfg(const orch_model* m, int32_t* cfg, float* rope_freq);
+/* Model::reset (core/model.hpp:92). */
+int orch_reset(orch_model* m);
+/* Model::forward (core/model.cpp:340-495); logits may be NULL (no LM head). */
+int orch_forward(orch_model* m, int32_t token, int pos, float* logits);
+/* Model::forward_prefill / forward_batch (core/model.cpp:510-674); logits
+ * [n][n_vocab] may be NULL. */
+int orch_forward_batch(orch_model* m, const int32_t* tokens, int n, int start_pos, float* logits);
+/* Harness greedy decode (benchmark/bench_engine.cpp:221-243): if prefill,
+ * reset + batched prefill of n_prompt-1 tokens; then n_gen argmax steps.
+ * Returns tokens written (<0 on error). */
+int orch_greedy(orch_model* m, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out, int prefill);
+/* Harness speculative greedy decode (benchmark/bench_engine.cpp:285-363)
+ * with draft length k; stats[0..3] = accepted, proposed, target passes,
+ * rounds. Returns tokens written. */
+int orch_spec_greedy(orch_model* tgt, orch_model* dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
+                     int32_t* out, int64_t* stats, int prefill);
+/* Quantized weight bytes one decode step streams (layers + LM head if logits). */
+double orch_weight_bytes(const orch_model* m, int logits);
+/* Block the host until all device work of the library has finished. */
+int orch_sync(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

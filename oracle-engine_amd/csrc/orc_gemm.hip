@@ -302,26 +302,36 @@ struct GemmParams {
 };
 
 constexpr int kWG = 256;
+constexpr int kMaxNT = 5;  // tokens per launch; larger batches are chunked (results unchanged)
 
-template <int QT, int NT, int LPR, int ROWS>
+// KS waves share one row group (split-K across waves): a group is LPR lanes in
+// each of KS waves, KS*LPR lanes in all, lane li owning units li, li+KS*LPR, ...
+// The butterfly over LPR lanes and the fixed-order sum over the KS waves make
+// the reduction order a function of (LPR, KS) only.
+template <int QT, int NT, int LPR, int KS, int ROWS>
 __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
     using T = QTr<QT>;
     extern __shared__ float smem[];
-    constexpr int G = 64 / LPR;
+    constexpr int G = 64 / LPR;     // groups per wave
+    constexpr int GR = 4 / KS;      // wave rows
+    constexpr int LT = KS * LPR;    // lanes per group
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int li = lane % LPR, group = wave * G + lane / LPR;
+    const int wsub = wave % KS, wrow = wave / KS;
+    const int li = wsub * LPR + lane % LPR, gl = wrow * G + lane / LPR;
     const int xs_stride = padx<T::PP>(p.kt_el) + 4;
     const int sx_stride = p.kt_el / 16;
     float* xs = smem;
     float* sx = smem + NT * xs_stride;
-    float* red = sx + NT * sx_stride;  // 8 floats of reduction scratch + NT inverse RMS
+    float* red = sx + NT * sx_stride;  // 8 floats of reduction scratch, 8 inverse RMS, then KS partials
+    float* inv = red + 8;
+    float* part = red + 16;
 
     // rows owned by this lane group
     const uint8_t* rows[ROWS];
     bool ok[ROWS];
     float* yout[ROWS];
     const float* bias[ROWS];
-    const int base = (blockIdx.x * 4 * G + group) * ROWS;
+    const int base = (blockIdx.x * GR * G + gl) * ROWS;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         int seg = 0, j;
@@ -340,7 +350,6 @@ __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
     }
 
     // optional RMSNorm prologue: inverse RMS per token, same reduction for any n_tok
-    float* inv = red + 8;
     if (p.norm_w) {
         for (int t = 0; t < NT; ++t) {
             const float4* xr = (const float4*)(p.x + (size_t)t * p.ldx);
@@ -398,10 +407,11 @@ __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
         UnitCtx c{xs, xs_stride, sx, sx_stride, k0};
         const int u0 = kt * units_per_tile;
         const int u1 = min(p.units_per_row, u0 + units_per_tile);
-        for (int u = u0 + li; u < u1; u += LPR) UnitDot<QT, NT, ROWS>::run(rows, ok, u, c, acc);
+#pragma unroll 2
+        for (int u = u0 + li; u < u1; u += LT) UnitDot<QT, NT, ROWS>::run(rows, ok, u, c, acc);
     }
 
-    // group reduction (fixed xor butterfly) and epilogue
+    // reduction: xor butterfly over the LPR lanes of a wave, then the KS waves in fixed order
 #pragma unroll
     for (int r = 0; r < ROWS; ++r)
 #pragma unroll
@@ -411,7 +421,25 @@ __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
             for (int o = LPR / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
             acc[r][t] = v;
         }
-    if (li != 0) return;
+    if (KS > 1) {
+        const int slot = (gl * ROWS) * NT;
+        if (lane % LPR == 0)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) part[(wsub * GR * G * ROWS) * NT + slot + r * NT + t] = acc[r][t];
+        __syncthreads();
+        if (wsub != 0) return;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int o = slot + r * NT + t, st = GR * G * ROWS * NT;
+                if (KS == 2) acc[r][t] = part[o] + part[st + o];
+                else acc[r][t] = (part[o] + part[st + o]) + (part[2 * st + o] + part[3 * st + o]);
+            }
+    }
+    if (lane % LPR != 0) return;
     if (p.epi == ORC_EPI_SWIGLU) {
         if (!ok[0]) return;
 #pragma unroll
@@ -446,86 +474,110 @@ static int units_per_block(int type) {
 }
 static int block_elems(int type) { return type == ORC_Q4_K || type == ORC_Q6_K ? 256 : 32; }
 
-// Lanes per row group: a function of (type, n_in) only, never of n_tok, so
-// every token sees the same reduction order.
-static int choose_lpr(int units) {
-    if (units >= 256) return 64;
-    if (units >= 96) return 32;
-    if (units >= 32) return 16;
-    return 8;
+constexpr int kRows = 2;
+size_t g_lds_budget = 64 * 1024;  // set from the device limit at first use
+
+static size_t lds_bytes(int type, int nt, int kt, int ks, int lpr) {
+    const int PP = (type == ORC_Q4_K || type == ORC_Q6_K) ? 64 : 32;
+    const size_t part = (size_t)ks * (4 / ks) * (64 / lpr) * kRows * nt;
+    return (size_t)nt * ((kt + 4 * (kt / PP) + 4) + kt / 16) * 4 + (16 + part) * 4;
 }
 
-constexpr int kRows = 2;
-constexpr size_t kLdsBudget = 64 * 1024;
+struct GemmShape { int lpr, ks; };
+
+// Lanes per row group (LPR) and waves per group (KS) depend on (type, n_in,
+// n_out) only, never on n_tok, so every token sees the same reduction order.
+// Narrow matrices get more lanes per row (more workgroups in flight); the
+// smallest K tile (KS*LPR units for kMaxNT tokens) must fit the LDS budget.
+static GemmShape choose_shape(int type, int units, int n_out) {
+    const int el_per_unit = block_elems(type) / units_per_block(type);
+    int cap = 64;
+    while (cap > 8 && lds_bytes(type, kMaxNT, cap * el_per_unit, 1, 64) > g_lds_budget) cap /= 2;
+    int lt;
+    if (n_out >= 12288) lt = units >= 96 ? 32 : units >= 32 ? 16 : 8;  // many rows: 1 wave per group
+    else {
+        lt = 8;
+        while (lt * 2 <= units && lt * 2 <= 64) lt *= 2;  // up to one unit per lane
+    }
+    lt = std::min(lt, cap);
+    GemmShape g;
+    if (n_out >= 12288 || lt < 16) { g.ks = 1; g.lpr = std::min(lt, 32); }
+    else if (lt == 16) { g.ks = 2; g.lpr = 8; }
+    else { g.ks = 4; g.lpr = lt / 4; }
+    return g;
+}
 
 template <int QT, int NT>
-static int launch_nt(const GemmParams& p0, int lpr, hipStream_t s) {
+static int launch_nt(const GemmParams& p0, GemmShape sh, hipStream_t s) {
     GemmParams p = p0;
-    const int G = 64 / lpr;
-    const int tile = 4 * G * kRows;
+    const int lpr = sh.lpr, ks = sh.ks;
+    const int tile = (4 / ks) * (64 / lpr) * kRows;
     const int n_items = p.epi == ORC_EPI_SWIGLU ? p.rows[0] * kRows : p.tile_rows_total;
     const int grid = (n_items + tile - 1) / tile;
-    const int PP = QTr<QT>::PP;
-    // K tile: as many whole blocks as fit the LDS budget, in units a multiple of lpr
+    // K tile: as many whole blocks as fit, units per tile a multiple of KS*LPR
     const int be = QTr<QT>::BLK_EL, upb = QTr<QT>::UPB;
-    auto lds_for = [&](int kt) {
-        return (size_t)NT * ((kt + 4 * (kt / PP) + 4) + kt / 16) * 4 + (8 + 16) * 4;
-    };
+    const int type = QT;
     int kt = (p.n_in + be - 1) / be * be;
-    if (lds_for(kt) > kLdsBudget) {
-        const int blk_step = std::max(1, lpr / upb);  // blocks per step so units stay a multiple of lpr
-        int nb = kLdsBudget / lds_for(be);
-        nb = std::max(blk_step, nb / blk_step * blk_step);
-        kt = nb * be;
-        while (kt > be * blk_step && lds_for(kt) > kLdsBudget) kt -= be * blk_step;
+    if (lds_bytes(type, NT, kt, ks, lpr) > g_lds_budget) {
+        const int blk_step = std::max(1, ks * lpr / upb);
+        kt = blk_step * be;
+        while (kt + blk_step * be < p.n_in && lds_bytes(type, NT, kt + blk_step * be, ks, lpr) <= g_lds_budget)
+            kt += blk_step * be;
     }
     p.kt_el = kt;
     p.n_ktiles = (p.n_in + kt - 1) / kt;
-    const size_t lds = lds_for(kt);
-    switch (lpr) {
-#define L(LPR_) case LPR_: hipLaunchKernelGGL((k_gemm<QT, NT, LPR_, kRows>), dim3(grid), dim3(kWG), lds, s, p); break;
-        L(8) L(16) L(32) L(64)
-#undef L
-        default: return set_error(ORC_E_INVALID, "bad lpr");
+    const size_t lds = lds_bytes(type, NT, kt, ks, lpr);
+    if (lds > g_lds_budget) return set_error(ORC_E_UNSUPPORTED, "gemm: K tile does not fit LDS");
+#define L(LPR_, KS_)                                                                                  \
+    if (lpr == LPR_ && ks == KS_) {                                                                   \
+        hipLaunchKernelGGL((k_gemm<QT, NT, LPR_, KS_, kRows>), dim3(grid), dim3(kWG), lds, s, p);     \
+        ORC_LAUNCH_CHECK();                                                                           \
+        return ORC_OK;                                                                                \
     }
-    ORC_LAUNCH_CHECK();
-    return ORC_OK;
+    L(8, 1) L(16, 1) L(32, 1) L(8, 2) L(8, 4) L(16, 4)
+#undef L
+    return set_error(ORC_E_INVALID, "gemm: no kernel for this shape");
 }
 
 template <int QT>
-static int launch_type(const GemmParams& p, int lpr, hipStream_t s) {
+static int launch_type(const GemmParams& p, GemmShape sh, hipStream_t s) {
     switch (p.n_tok) {
-        case 1: return launch_nt<QT, 1>(p, lpr, s);
-        case 2: return launch_nt<QT, 2>(p, lpr, s);
-        case 3: return launch_nt<QT, 3>(p, lpr, s);
-        case 4: return launch_nt<QT, 4>(p, lpr, s);
-        case 5: return launch_nt<QT, 5>(p, lpr, s);
-        case 6: return launch_nt<QT, 6>(p, lpr, s);
-        case 7: return launch_nt<QT, 7>(p, lpr, s);
-        case 8: return launch_nt<QT, 8>(p, lpr, s);
-        case 9: return launch_nt<QT, 9>(p, lpr, s);
-        default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..9");
+        case 1: return launch_nt<QT, 1>(p, sh, s);
+        case 2: return launch_nt<QT, 2>(p, sh, s);
+        case 3: return launch_nt<QT, 3>(p, sh, s);
+        case 4: return launch_nt<QT, 4>(p, sh, s);
+        case 5: return launch_nt<QT, 5>(p, sh, s);
+        default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..5");
     }
 }
 
 static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
+    static bool lds_init = false;
+    if (!lds_init) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
+            g_lds_budget = std::min<size_t>((size_t)v, 160 * 1024);
+        lds_init = true;
+    }
     const int upb = units_per_block(type);
     p.units_per_row = p.n_in / block_elems(type) * upb;
-    const int lpr = choose_lpr(p.units_per_row);
-    // tokens are processed in chunks of at most 9; chunking never changes a
+    const int n_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.tile_rows_total;
+    const GemmShape sh = choose_shape(type, p.units_per_row, n_out);
+    // tokens are processed in chunks of at most kMaxNT; chunking never changes a
     // (token,row) result because the reduction order is independent of n_tok
     const int total = p.n_tok;
-    for (int t0 = 0; t0 < total; t0 += 9) {
+    for (int t0 = 0; t0 < total; t0 += kMaxNT) {
         GemmParams q = p;
-        q.n_tok = std::min(9, total - t0);
+        q.n_tok = std::min(kMaxNT, total - t0);
         q.x = p.x + (size_t)t0 * p.ldx;
         for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
         int rc;
         switch (type) {
-            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, lpr, s); break;
-            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, lpr, s); break;
-            case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, lpr, s); break;
-            case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, lpr, s); break;
+            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, sh, s); break;
+            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, sh, s); break;
+            case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, sh, s); break;
+            case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, sh, s); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
         }
         if (rc) return rc;

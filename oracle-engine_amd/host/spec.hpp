@@ -1,0 +1,39 @@
+// Decode loops on the device: greedy decode with the reference harness
+// protocol (benchmark/bench_engine.cpp:221-243) and speculative greedy
+// decode with one batched (k+1)-token verify per round
+// (benchmark/bench_engine.cpp:300-356). Token ids are produced and consumed
+// on the device; per round only the verify argmax ids and the accepted count
+// cross to the host.
+#pragma once
+#include "model.hpp"
+
+#include <cstdint>
+#include <vector>
+
+struct SpecStats {
+    long accepted = 0, proposed = 0, passes = 0, rounds = 0;
+};
+
+// Device scratch reused across calls (no allocation in the decode loops).
+class DecodeSession {
+public:
+    explicit DecodeSession(int max_tokens = 4096, int max_k = 16);
+    ~DecodeSession();
+    DecodeSession(const DecodeSession&) = delete;
+    DecodeSession& operator=(const DecodeSession&) = delete;
+
+    // Batched prefill of prompt[0 .. n_prompt-2] into the model's KV cache.
+    int prefill(Model& m, const int32_t* prompt, int n_prompt);
+    // n_gen greedy tokens after a prefilled prompt; returns tokens written or <0.
+    int greedy(Model& m, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out);
+    // Speculative greedy with draft length k after both models are prefilled.
+    int spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k, int32_t* out,
+                    SpecStats* st);
+
+private:
+    int max_tokens_, max_k_;
+    int32_t* d_hist_ = nullptr;  // greedy token chain
+    int32_t* d_vin_ = nullptr;   // [next, d0 .. d_{k-1}]
+    int32_t* d_tgt_ = nullptr;   // verify argmax ids
+    int32_t* d_acc_ = nullptr;   // accepted count, next token
+};

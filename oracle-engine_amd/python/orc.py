@@ -149,3 +149,106 @@ class DBuf:
             self.free()
         except Exception:
             pass
+
+
+# ── host API (include/oracle_host.h) ─────────────────────────────────────────
+HOST_ABI = [
+    ("orch_load", _vp, [C.c_char_p, C.c_int]),
+    ("orch_free", None, [_vp]),
+    ("orch_error", C.c_char_p, [_vp]),
+    ("orch_cfg", C.c_int, [_vp, _ip, _fp]),
+    ("orch_reset", C.c_int, [_vp]),
+    ("orch_forward", C.c_int, [_vp, C.c_int32, C.c_int, _fp]),
+    ("orch_forward_batch", C.c_int, [_vp, _ip, C.c_int, C.c_int, _fp]),
+    ("orch_greedy", C.c_int, [_vp, _ip, C.c_int, C.c_int, _ip, C.c_int]),
+    ("orch_spec_greedy", C.c_int, [_vp, _vp, _ip, C.c_int, C.c_int, C.c_int, _ip, C.POINTER(C.c_int64), C.c_int]),
+    ("orch_weight_bytes", C.c_double, [_vp, C.c_int]),
+    ("orch_sync", C.c_int, []),
+]
+
+_host = None
+
+
+def load_host_lib(path=HOST_LIB):
+    global _host
+    if _host is None:
+        load_hip_lib()  # resolves liborc_hip.so first (and fails loudly if missing)
+        if not os.path.exists(path):
+            raise OrcError(f"{path} is missing: build it with __graft_entry__.build()")
+        lib = C.CDLL(path)
+        for name, res, args in HOST_ABI:
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _host = lib
+    return _host
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, np.int32)
+
+
+class Model:
+    """Device-resident model (Model API of core/model.hpp) through liboracle_host."""
+
+    def __init__(self, path, ctx_len=0):
+        self.L = load_host_lib()
+        self.h = self.L.orch_load(str(path).encode(), int(ctx_len))
+        if not self.h:
+            raise OrcError(f"cannot load {path}: {self.L.orch_error(None).decode()}")
+        cfg = np.zeros(10, np.int32)
+        rope = C.c_float()
+        self.L.orch_cfg(self.h, cfg.ctypes.data_as(_ip), C.byref(rope))
+        (self.n_vocab, self.n_layers, self.n_heads, self.n_kv_heads, self.embed_dim, self.ffn, self.head_dim,
+         self.ctx_len, self.has_bias, self.tied) = (int(v) for v in cfg)
+        self.rope = rope.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.orch_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc < 0:
+            raise OrcError(f"host error {rc}: {self.L.orch_error(self.h).decode()}")
+        return rc
+
+    def reset(self):
+        self._check(self.L.orch_reset(self.h))
+
+    def forward(self, tok, pos, logits=True):
+        out = np.empty(self.n_vocab, np.float32) if logits else None
+        self._check(self.L.orch_forward(self.h, int(tok), int(pos), out.ctypes.data_as(_fp) if logits else None))
+        return out
+
+    def forward_batch(self, toks, start_pos, logits=True):
+        toks = _i32(toks)
+        out = np.empty((toks.size, self.n_vocab), np.float32) if logits else None
+        self._check(self.L.orch_forward_batch(self.h, toks.ctypes.data_as(_ip), toks.size, int(start_pos),
+                                              out.ctypes.data_as(_fp) if logits else None))
+        return out
+
+    def greedy(self, prompt, n_gen, prefill=True):
+        prompt = _i32(prompt)
+        out = np.empty(n_gen, np.int32)
+        n = self._check(self.L.orch_greedy(self.h, prompt.ctypes.data_as(_ip), prompt.size, n_gen,
+                                           out.ctypes.data_as(_ip), int(prefill)))
+        return out[:n]
+
+    def spec_greedy(self, draft, prompt, n_gen, k, prefill=True):
+        prompt = _i32(prompt)
+        out = np.empty(n_gen + k + 2, np.int32)
+        st = np.zeros(4, np.int64)
+        n = self._check(self.L.orch_spec_greedy(self.h, draft.h, prompt.ctypes.data_as(_ip), prompt.size, n_gen, k,
+                                                out.ctypes.data_as(_ip), st.ctypes.data_as(C.POINTER(C.c_int64)),
+                                                int(prefill)))
+        return out[:n], {"accepted": int(st[0]), "proposed": int(st[1]), "passes": int(st[2]), "rounds": int(st[3])}
+
+    def weight_bytes(self, logits=True):
+        return self.L.orch_weight_bytes(self.h, int(logits))

@@ -1,0 +1,347 @@
+"""Pins the CPU oracle (oracle/orc_oracle.c) before it is trusted as the
+checker: against the reference's own outputs (tests/golden/ref_fixtures.npz,
+written by tests/golden/make_golden.py from the reference compiled from its
+sources) and against closed forms / invariants chosen so that a plausible
+mistake (dropped term, wrong index or sign, wrong rounding order) fails.
+CPU only."""
+import hashlib
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from conftest import GOLDEN, SYNTH, rand_blocks
+
+FIX = np.load(os.path.join(GOLDEN, "ref_fixtures.npz"))
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return FIX
+
+
+def test_models_regenerate_identically(models_dir):
+    for m in ("t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen", "t-qwen-d"):
+        h = hashlib.sha256(open(models_dir / f"{m}.gguf", "rb").read()).hexdigest()
+        assert h == bytes(FIX[f"sha/{m}"]).decode(), m
+
+
+# ── codecs ───────────────────────────────────────────────────────────────────
+@pytest.mark.parametrize("name,qt", [("q4_0", ol.Q4_0), ("q4_k", ol.Q4_K), ("q6_k", ol.Q6_K)])
+def test_dequant_matches_reference_hooks(oracle, name, qt):
+    raw = FIX[f"dq/{name}/raw"]
+    want = FIX[f"dq/{name}/out"]
+    got = oracle.dequant(qt, raw, want.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_rows_match_reference(oracle, models_dir):
+    import gguf_read
+
+    for key in [k for k in FIX.files if k.startswith("dqrow/")]:
+        _, m, t = key.split("/", 2)
+        tt, shape, off = gguf_read.tensors(str(models_dir / f"{m}.gguf"))[t]
+        rb = ol.row_bytes(tt, shape[0])
+        raw = np.fromfile(models_dir / f"{m}.gguf", np.uint8, count=4 * rb, offset=off + 3 * rb)
+        got = oracle.dequant(tt, raw, 4 * shape[0])
+        assert np.array_equal(got.view(np.uint32), FIX[key].view(np.uint32)), key
+
+
+def test_fp16_closed_form(oracle):
+    """All 65536 halves equal the IEEE conversion (numpy) bit for bit."""
+    raw = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.dequant(ol.F16, raw.view(np.uint8), 65536)
+    want = raw.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _f16(raw, off):
+    return raw[:, off:off + 2].copy().view(np.float16).astype(np.float32).reshape(-1)
+
+
+def test_q8_0_q4_0_closed_form(oracle):
+    rng = np.random.default_rng(1)
+    raw = rand_blocks(ol.Q8_0, 32 * 64, rng).reshape(-1, 34)
+    want = (_f16(raw, 0)[:, None] * raw[:, 2:].view(np.int8).astype(np.float32)).reshape(-1)
+    assert np.array_equal(oracle.dequant(ol.Q8_0, raw.reshape(-1), want.size), want)
+    raw = rand_blocks(ol.Q4_0, 32 * 64, rng).reshape(-1, 18)
+    q = raw[:, 2:].astype(np.int32)
+    codes = np.concatenate([(q & 15) - 8, (q >> 4) - 8], axis=1).astype(np.float32)  # low nibbles first
+    want = (_f16(raw, 0)[:, None] * codes).reshape(-1)
+    assert np.array_equal(oracle.dequant(ol.Q4_0, raw.reshape(-1), want.size), want)
+
+
+def _q4k_scales(sc):
+    s = np.zeros((sc.shape[0], 8), np.int64)
+    m = np.zeros_like(s)
+    for j in range(8):
+        if j < 4:
+            s[:, j], m[:, j] = sc[:, j] & 63, sc[:, j + 4] & 63
+        else:
+            s[:, j] = (sc[:, j + 4] & 0xF) | ((sc[:, j - 4] >> 6) << 4)
+            m[:, j] = (sc[:, j + 4] >> 4) | ((sc[:, j] >> 6) << 4)
+    return s, m
+
+
+def test_q4_k_closed_form_single_rounding(oracle):
+    """y = d*sc*q - dmin*m rounded once. d*sc (11+6 bits) and d*sc*q (+4 bits)
+    are exact in fp32, so whether the reference build contracts the
+    expression into an FMA cannot change a single bit; the closed form is
+    computed exactly in float64 and rounded once."""
+    rng = np.random.default_rng(2)
+    raw = rand_blocks(ol.Q4_K, 256 * 32, rng).reshape(-1, 144)
+    d, dmin = _f16(raw, 0), _f16(raw, 2)
+    s, m = _q4k_scales(raw[:, 4:16].astype(np.int64))
+    d1 = (d[:, None] * s.astype(np.float32)).astype(np.float32)
+    m1 = (dmin[:, None] * m.astype(np.float32)).astype(np.float32)
+    qs = raw[:, 16:].reshape(-1, 4, 32).astype(np.int64)
+    q = np.zeros((raw.shape[0], 8, 32), np.int64)
+    q[:, 0::2, :] = qs & 15
+    q[:, 1::2, :] = qs >> 4
+    exact = d1.astype(np.float64)[:, :, None] * q - m1.astype(np.float64)[:, :, None]  # exact in float64
+    want = exact.astype(np.float32).reshape(-1)
+    got = oracle.dequant(ol.Q4_K, raw.reshape(-1), want.size)
+    assert np.array_equal(got, want)
+    # a wrong sub-block pairing (high nibbles with the even scale) must not pass
+    swapped = d1.astype(np.float64)[:, [1, 0, 3, 2, 5, 4, 7, 6], None] * q - m1.astype(np.float64)[:, :, None]
+    assert not np.array_equal(got, swapped.astype(np.float32).reshape(-1))
+
+
+def test_q6_k_closed_form(oracle):
+    """y[e] = (d * sc[e/16]) * (q - 32), two float32 roundings in that order."""
+    rng = np.random.default_rng(3)
+    raw = rand_blocks(ol.Q6_K, 256 * 32, rng).reshape(-1, 210)
+    d = _f16(raw, 208)
+    sc = raw[:, 192:208].view(np.int8).astype(np.float32)
+    ql, qh = raw[:, :128].astype(np.int64), raw[:, 128:192].astype(np.int64)
+    q = np.zeros((raw.shape[0], 256), np.int64)
+    for h in range(2):
+        for l in range(32):
+            a, b, hb = ql[:, 64 * h + l], ql[:, 64 * h + l + 32], qh[:, 32 * h + l]
+            q[:, 128 * h + l] = (a & 15) | ((hb & 3) << 4)
+            q[:, 128 * h + l + 32] = (b & 15) | (((hb >> 2) & 3) << 4)
+            q[:, 128 * h + l + 64] = (a >> 4) | (((hb >> 4) & 3) << 4)
+            q[:, 128 * h + l + 96] = (b >> 4) | (((hb >> 6) & 3) << 4)
+    dsc = (d[:, None] * sc).astype(np.float32)
+    want = (np.repeat(dsc, 16, axis=1) * (q - 32).astype(np.float32)).astype(np.float32).reshape(-1)
+    assert np.array_equal(oracle.dequant(ol.Q6_K, raw.reshape(-1), want.size), want)
+
+
+# ── GEMV / GEMM ──────────────────────────────────────────────────────────────
+def test_gemv_matches_reference_every_tensor(oracle, models_dir):
+    import gguf_read
+
+    n = 0
+    for key in [k for k in FIX.files if k.startswith("gemv/")]:
+        _, m, t = key.split("/", 2)
+        tt, shape, off = gguf_read.tensors(str(models_dir / f"{m}.gguf"))[t]
+        n_in, n_out = shape
+        raw = np.fromfile(models_dir / f"{m}.gguf", np.uint8, count=ol.row_bytes(tt, n_in) * n_out, offset=off)
+        x = np.random.default_rng(1234).uniform(-1, 1, n_in).astype(np.float32)
+        got = oracle.gemv(tt, raw, n_out, n_in, x)
+        ref = FIX[key]
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), key
+        W = oracle.dequant(tt, raw, n_in * n_out).reshape(n_out, n_in).astype(np.float64)
+        exact = W @ x.astype(np.float64)
+        assert np.all(np.abs(got - exact) <= 1e-5 * (np.abs(W) @ np.abs(x)) + 1e-12), key
+        n += 1
+    assert n >= 40
+
+
+def test_gemm_matches_reference(oracle, models_dir):
+    import gguf_read
+
+    for key in [k for k in FIX.files if k.startswith("gemm/")]:
+        _, m, t = key.split("/", 2)
+        tt, shape, off = gguf_read.tensors(str(models_dir / f"{m}.gguf"))[t]
+        n_in, n_out = shape
+        raw = np.fromfile(models_dir / f"{m}.gguf", np.uint8, count=ol.row_bytes(tt, n_in) * n_out, offset=off)
+        X = np.random.default_rng(99).uniform(-1, 1, (5, n_in)).astype(np.float32)
+        got = oracle.gemm(tt, raw, 5, n_out, n_in, X).reshape(-1)
+        ref = FIX[key]
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), key
+
+
+# ── ops ──────────────────────────────────────────────────────────────────────
+def test_ops_match_reference(oracle):
+    x, g = FIX["op/x"], FIX["op/g"]
+    assert np.allclose(oracle.rmsnorm(x, g), FIX["op/rmsnorm"], rtol=1e-6, atol=0)
+    assert np.allclose(oracle.softmax(x), FIX["op/softmax"], rtol=3e-6, atol=1e-12)
+    assert np.allclose(oracle.silu(x), FIX["op/silu"], rtol=3e-6, atol=1e-9)
+    q, k = oracle.rope(FIX["op/rope_q_in"], FIX["op/rope_k_in"], 24, 8, 128, 301, 500000.0)
+    assert np.allclose(q, FIX["op/rope_q"], rtol=1e-5, atol=1e-6)
+    assert np.allclose(k, FIX["op/rope_k"], rtol=1e-5, atol=1e-6)
+
+
+def test_ops_closed_forms(oracle):
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, 1000).astype(np.float32)
+    w = rng.uniform(0.5, 2, 1000).astype(np.float32)
+    x64 = x.astype(np.float64)
+    assert np.allclose(oracle.rmsnorm(x, w, 1e-5), x64 / np.sqrt(np.mean(x64 ** 2) + 1e-5) * w, rtol=2e-6)
+    e = np.exp(x64 - x64.max())
+    assert np.allclose(oracle.softmax(x), e / e.sum(), rtol=2e-6)
+    assert np.allclose(oracle.silu(x), x64 / (1 + np.exp(-x64)), rtol=2e-6, atol=1e-9)
+    # RoPE is a rotation: norms of every (i, i+hd/2) pair are preserved and pos 0 is the identity
+    q0 = rng.normal(0, 1, 2 * 64).astype(np.float32)
+    k0 = rng.normal(0, 1, 64).astype(np.float32)
+    q, k = oracle.rope(q0, k0, 2, 1, 64, 0, 10000.0)
+    assert np.array_equal(q, q0) and np.array_equal(k, k0)
+    q, _ = oracle.rope(q0, k0, 2, 1, 64, 37, 10000.0)
+    a, b = q0.reshape(2, 2, 32), q.reshape(2, 2, 32)
+    assert np.allclose(np.hypot(a[:, 0], a[:, 1]), np.hypot(b[:, 0], b[:, 1]), rtol=1e-5)
+    theta = 37 / 10000.0 ** (2 * 3 / 64)
+    assert np.isclose(b[0, 0, 3], a[0, 0, 3] * np.cos(theta) - a[0, 1, 3] * np.sin(theta), rtol=1e-5)
+
+
+def test_argmax_first_index(oracle):
+    x = np.array([1, 5, 3, 5, 5], np.float32)
+    assert oracle.argmax(x) == 1
+    assert oracle.argmax(np.zeros(7, np.float32)) == 0
+
+
+def test_attention_brute_force(oracle):
+    rng = np.random.default_rng(8)
+    H, KVH, hd, pos = 6, 2, 64, 9
+    q = rng.normal(0, 1, H * hd).astype(np.float32)
+    kc = rng.normal(0, 1, (pos + 1, KVH * hd)).astype(np.float32)
+    vc = rng.normal(0, 1, (pos + 1, KVH * hd)).astype(np.float32)
+    got = oracle.attention(q, kc, vc, H, KVH, hd, pos)
+    for h in range(H):
+        g = h // (H // KVH)  # kv head of query head h
+        s = kc[:, g * hd:(g + 1) * hd].astype(np.float64) @ q[h * hd:(h + 1) * hd] / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        assert np.allclose(got[h * hd:(h + 1) * hd], p @ vc[:, g * hd:(g + 1) * hd], rtol=1e-5, atol=1e-6)
+
+
+# ── model loops ──────────────────────────────────────────────────────────────
+MODELS = ["t-q8", "t-q40", "t-q4k", "t-q6k", "t-qwen"]
+
+
+@pytest.mark.parametrize("m", MODELS)
+def test_model_greedy_matches_reference(oracle, models_dir, m):
+    mod = ol.OracleModel(oracle, str(models_dir / f"{m}.gguf"))
+    prompt = FIX[f"greedy/{m}/prompt"]
+    assert np.array_equal(mod.greedy(prompt, 40), FIX[f"greedy/{m}/tokens"])
+    mod.reset()
+    mod.forward_batch(prompt[:-1], 0, logits=False)
+    cur, pos = int(prompt[-1]), len(prompt) - 1
+    for s in range(4):
+        lg = mod.forward(cur, pos)
+        ref = FIX[f"greedy/{m}/logits"][s]
+        assert np.abs(lg - ref).max() <= 1e-4 * np.abs(ref).max(), (m, s)
+        cur, pos = int(np.argmax(lg)), pos + 1
+
+
+@pytest.mark.parametrize("m", MODELS)
+def test_model_batch_matches_reference(oracle, models_dir, m):
+    mod = ol.OracleModel(oracle, str(models_dir / f"{m}.gguf"))
+    seq = FIX[f"batch/{m}/tokens"]
+    mod.reset()
+    mod.forward_batch(seq[:16], 0, logits=False)
+    lg = mod.forward_batch(seq[16:], 16)
+    ref = FIX[f"batch/{m}/logits"]
+    assert np.abs(lg - ref).max() <= 1e-4 * np.abs(ref).max(), m
+
+
+@pytest.mark.parametrize("k", [2, 4])
+def test_spec_greedy_matches_reference(oracle, models_dir, k):
+    tgt = ol.OracleModel(oracle, str(models_dir / "t-q4k.gguf"))
+    dft = ol.OracleModel(oracle, str(models_dir / "t-q4k-d.gguf"))
+    toks, st = tgt.spec_greedy(dft, FIX["greedy/t-q4k/prompt"], 40, k)
+    assert np.array_equal(toks, FIX[f"spec/k{k}/tokens"])
+    assert [st["accepted"], st["proposed"], st["passes"]] == list(FIX[f"spec/k{k}/stats"])
+
+
+# ── sampler ──────────────────────────────────────────────────────────────────
+def test_mt19937_known_answer(oracle):
+    """std::mt19937 default seed 5489: the 10000th output is 4123659995 (C++ [rand.predef])."""
+    s = oracle.L.orco_sampler_new(0.0, 1.0, 0, 1.0, 64, 5489)
+    for _ in range(9999):
+        oracle.L.orco_mt_next(s)
+    assert oracle.L.orco_mt_next(s) == 4123659995
+    oracle.L.orco_sampler_free(s)
+
+
+def test_sampler_matches_reference(oracle):
+    lg, hist = FIX["sample/logits"], FIX["sample/history"]
+    for i in range(5):
+        T, P, K, pen, last = FIX[f"sample/{i}/params"]
+        seed = int(FIX[f"sample/{i}/seed"][0])
+        s = oracle.L.orco_sampler_new(T, P, int(K), pen, int(last), seed)
+        for h in hist:
+            oracle.L.orco_sampler_record(s, int(h))
+        draws = []
+        for _ in range(64):
+            x = lg.copy()
+            draws.append(oracle.L.orco_sampler_sample(s, ol.fptr(x), x.size))
+        oracle.L.orco_sampler_free(s)
+        assert draws == list(FIX[f"sample/{i}/draws"]), i
+
+
+def test_engine_stochastic_spec_matches_reference(oracle, models_dir):
+    tgt = ol.OracleModel(oracle, str(models_dir / "t-qwen.gguf"))
+    dft = ol.OracleModel(oracle, str(models_dir / "t-qwen-d.gguf"))
+    s = oracle.L.orco_sampler_new(0.8, 0.95, 40, 1.1, 64, 4242)
+    prompt = np.ascontiguousarray(FIX["greedy/t-qwen/prompt"], np.int32)
+    out = np.zeros(64, np.int32)
+    st = np.zeros(3, np.int64)
+    n = oracle.L.orco_spec_engine(tgt.h, dft.h, ol.iptr(prompt), prompt.size, 40, 3, s, ol.iptr(out),
+                                  st.ctypes.data_as(ol._lp))
+    oracle.L.orco_sampler_free(s)
+    assert np.array_equal(out[:n], FIX["espec/tokens"])
+    assert list(st) == list(FIX["espec/stats"])
+
+
+def _probs(oracle, logits, T, P, K, pen=1.0, hist=()):
+    p = np.zeros(logits.size, np.float32)
+    h = np.ascontiguousarray(hist, np.int32)
+    oracle.L.orco_transform_probs(ol.fptr(np.ascontiguousarray(logits, np.float32)), logits.size, ol.iptr(h), h.size,
+                                  T, P, K, pen, ol.fptr(p))
+    return p
+
+
+def test_acceptance_resampling_is_exact_in_distribution(oracle):
+    """min(1,p/q) acceptance + residual resampling emits tokens distributed as p
+    (chi-square over exhaustive uniform grids), and p == q always accepts."""
+    rng = np.random.default_rng(12)
+    n = 12
+    p = _probs(oracle, rng.normal(0, 1, n).astype(np.float32), 0.9, 0.97, 0)
+    q = _probs(oracle, rng.normal(0, 1, n).astype(np.float32), 1.2, 1.0, 0)
+    import ctypes
+
+    acc = ctypes.c_int()
+    G = 20000
+    us = (np.arange(G) + 0.5) / G
+    # the residual draw depends on u_res only; the accept test on u_acc only
+    resid = np.zeros(n)
+    x_rej = int(np.argmax(q - p))  # q > p there, so u_acc = 1 always rejects
+    for ur in us:
+        tok = oracle.L.orco_accept_resample(ol.fptr(p), ol.fptr(q), n, x_rej, 1.0, float(ur), ctypes.byref(acc))
+        assert not acc.value
+        resid[tok] += 1.0 / G
+    emitted = np.zeros(n)
+    for x in range(n):  # proposals x ~ q
+        a = 0.0
+        for ua in us[::10]:
+            oracle.L.orco_accept_resample(ol.fptr(p), ol.fptr(q), n, x, float(ua), 0.5, ctypes.byref(acc))
+            a += acc.value / (G // 10)
+        emitted[x] += q[x] * a
+        emitted += q[x] * (1 - a) * resid
+    assert np.allclose(emitted, p, atol=2e-3), (emitted, p)
+    for x in np.nonzero(p)[0]:  # a proposal always has q[x] > 0
+        tok = oracle.L.orco_accept_resample(ol.fptr(p), ol.fptr(p), n, int(x), 0.999, 0.5, ctypes.byref(acc))
+        assert tok == x and acc.value == 1
+
+
+def test_transform_greedy_limit(oracle):
+    lg = np.random.default_rng(3).normal(0, 1, 50).astype(np.float32)
+    p = _probs(oracle, lg, 0.0, 0.9, 40)
+    assert p[np.argmax(lg)] == 1.0 and p.sum() == 1.0
+    p = _probs(oracle, lg, 0.8, 1.0, 1)
+    assert p[np.argmax(lg)] == 1.0
