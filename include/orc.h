@@ -126,6 +126,15 @@ typedef struct {
 int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_tok, int n_in, const float* d_x, int ldx, int ldy,
                    const float* d_norm_w, float eps, int epilogue, orc_stream_t stream);
 
+/* Live kernel timing (no reference counterpart; the reference times whole
+ * loops with std::chrono, bench_engine.cpp:225-244). While enabled, every
+ * GEMM launch outside graph capture is bracketed by HIP events recorded on
+ * the launch stream, and its algorithmic HBM bytes (weight blocks + x + y)
+ * are recorded. orc_prof_read sums the launches of one kernel family
+ * (type < 0: all types; n_tok 0: all token counts) and waits for them. */
+int orc_prof_enable(int on);
+int orc_prof_read(int type, int n_tok, int64_t* launches, double* total_ms, double* total_bytes);
+
 /* ── elementwise / attention ─────────────────────────────────────────────── */
 /* out[t] = rmsnorm(x[t]) for n_rows rows of n (ops::rmsnorm, ops.cpp:149-195). */
 int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_rows, float eps, orc_stream_t stream);

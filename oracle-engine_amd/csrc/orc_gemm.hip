@@ -27,6 +27,7 @@
 #include "orc_internal.hpp"
 
 #include <algorithm>
+#include <vector>
 
 namespace orc {
 
@@ -551,6 +552,38 @@ static int launch_type(const GemmParams& p, GemmShape sh, hipStream_t s) {
     }
 }
 
+// ── live kernel timing (orc_prof_*) ─────────────────────────────────────────
+struct ProfRec {
+    hipEvent_t a, b;
+    int type, nt;
+    double bytes;
+};
+static bool g_prof_on = false;
+static std::vector<ProfRec> g_prof;     // records of the current region
+static std::vector<hipEvent_t> g_evpool;
+static size_t g_evnext = 0;
+
+static hipEvent_t prof_event() {
+    if (g_evnext == g_evpool.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        g_evpool.push_back(e);
+    }
+    return g_evpool[g_evnext++];
+}
+
+// Algorithmic HBM bytes of one launch: weight blocks + activations read +
+// outputs written (read too when accumulating) + norm weights and biases.
+static double gemm_bytes(const GemmParams& p, int nt) {
+    const int n_out = p.epi == ORC_EPI_SWIGLU ? 2 * p.rows[0] : p.tile_rows_total;
+    const int n_y = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.tile_rows_total;
+    double b = (double)p.row_bytes * n_out + 4.0 * nt * p.n_in + 4.0 * nt * n_y * (p.epi == ORC_EPI_ACCUM ? 2 : 1);
+    if (p.norm_w) b += 4.0 * p.n_in;
+    for (int i = 0; i < p.n_seg; ++i)
+        if (p.bias[i]) b += 4.0 * p.rows[i];
+    return b;
+}
+
 static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
     static bool lds_init = false;
     if (!lds_init) {
@@ -573,6 +606,18 @@ static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
         q.x = p.x + (size_t)t0 * p.ldx;
         for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
         int rc;
+        ProfRec rec{};
+        bool prof = false;
+        if (g_prof_on) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            (void)hipStreamIsCapturing(s, &cs);
+            if (cs == hipStreamCaptureStatusNone && (rec.a = prof_event()) && (rec.b = prof_event())) {
+                prof = hipEventRecord(rec.a, s) == hipSuccess;
+                rec.type = type;
+                rec.nt = q.n_tok;
+                rec.bytes = gemm_bytes(q, q.n_tok);
+            }
+        }
         switch (type) {
             case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, sh, s); break;
             case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, sh, s); break;
@@ -580,6 +625,7 @@ static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
             case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, sh, s); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
         }
+        if (prof && hipEventRecord(rec.b, s) == hipSuccess) g_prof.push_back(rec);
         if (rc) return rc;
     }
     return ORC_OK;
@@ -588,6 +634,33 @@ static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
 }  // namespace orc
 
 using namespace orc;
+
+extern "C" int orc_prof_enable(int on) {
+    g_prof_on = on != 0;
+    if (on) {
+        g_prof.clear();
+        g_evnext = 0;
+    }
+    return ORC_OK;
+}
+
+extern "C" int orc_prof_read(int type, int n_tok, int64_t* launches, double* total_ms, double* total_bytes) {
+    int64_t n = 0;
+    double ms = 0, by = 0;
+    for (const ProfRec& r : g_prof) {
+        if ((type >= 0 && r.type != type) || (n_tok > 0 && r.nt != n_tok)) continue;
+        ORC_HIP_CHECK(hipEventSynchronize(r.b));
+        float e = 0.f;
+        ORC_HIP_CHECK(hipEventElapsedTime(&e, r.a, r.b));
+        ++n;
+        ms += e;
+        by += r.bytes;
+    }
+    if (launches) *launches = n;
+    if (total_ms) *total_ms = ms;
+    if (total_bytes) *total_bytes = by;
+    return ORC_OK;
+}
 
 extern "C" int64_t orc_row_bytes(int type, int64_t n) {
     switch (type) {

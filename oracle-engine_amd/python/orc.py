@@ -71,6 +71,9 @@ ABI = [
     ("orc_argmax_workspace", C.c_size_t, [C.c_int, C.c_int]),
     ("orc_argmax", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
     ("orc_spec_accept_greedy", C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
+    ("orc_prof_enable", C.c_int, [C.c_int]),
+    ("orc_prof_read", C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double),
+                                C.POINTER(C.c_double)]),
 ]
 
 
