@@ -1,29 +1,33 @@
-// Quantized GEMV / GEMM on raw GGML blocks (gfx950), plus the bit-exact
-// dequant codecs and the embedding gather.
+// Quantized GEMV / GEMM on raw GGML blocks (gfx950).
 //
-// Replaces gemv_q / gemv_q_range / gemm_q / dequantize_row
-// (core/gguf_parser.cpp:443-482, 496-997) and the fp16 + block codecs
-// (:1002-1154).
+// Replaces gemv_q / gemv_q_range / gemm_q (core/gguf_parser.cpp:496-997) and
+// the projection sequences of Model::forward / forward_prefill that surround
+// them (RMSNorm, QKV bias, residual add, SwiGLU; core/model.cpp:366-473,
+// 565-643).
 //
-// GEMM design (one kernel family; n_tok = 1 is the decode GEMV):
-//  * A 256-thread workgroup owns a tile of weight rows. Lanes are split into
-//    groups of LPR lanes; each group owns ROWS rows and walks their row bytes
-//    in "units" (a type-specific slice of a block: 16 B of Q4_K nibbles, a
-//    64-value quarter of a Q6_K superblock, one Q8_0/Q4_0 block). Consecutive
-//    lanes take consecutive units, so a wavefront's loads cover contiguous
-//    row bytes; blocks are read straight from the as-uploaded GGUF bytes with
-//    (possibly unaligned) 128-bit loads.
+// Design (one kernel family; n_tok = 1 is the decode GEMV):
+//  * A 256-thread workgroup owns a tile of weight rows. A "row group" of
+//    KS*LPR lanes (LPR lanes in each of KS waves) owns ROWS rows and walks
+//    their row bytes in units: 16 B of Q4_K nibbles (32 values), a 64-value
+//    quarter of a Q6_K superblock, one Q8_0 / Q4_0 block. Blocks are read
+//    straight from the as-uploaded GGUF bytes with (unaligned) 128-bit loads.
+//  * Latency: each lane issues the loads of its first unit before the
+//    activations are staged, and the loads of unit i+1 before computing unit
+//    i, so HBM latency overlaps the L2 staging and the arithmetic.
 //  * The activations of all n_tok tokens for one K tile are staged in LDS
-//    (fp32, with 4 floats of padding every 32/64 values so that the lanes of
-//    a group hit distinct banks), together with per-16-value sums of x used
-//    for the Q4_K minimum term and the Q6_K/Q4_0 code offsets.
-//  * Each weight code is decoded once per row and applied to every token held
-//    in LDS; accumulation is fp32. A lane's partial sum depends only on the
-//    units it owns, and the group reduction is a fixed xor-butterfly, so the
-//    result for a (token, row) pair is bit-identical for every n_tok: the
+//    (fp32, 4 floats of padding every 32/64 values so the lanes of a group hit
+//    distinct banks) with every load in flight at once; per-16-value sums of x
+//    (for the Q4_K minimum and the Q6_K / Q4_0 code offsets) come from a
+//    4-lane shuffle in the same pass. One barrier per K tile.
+//  * RMSNorm prologue: x is staged multiplied by the norm weight and the
+//    per-token 1/rms (reduced while staging) scales the finished dot product:
+//    sum_i w_i (x_i s g_i) = s * sum_i w_i (x_i g_i).
+//  * Each weight code is decoded once per row and applied to every token in
+//    LDS; accumulation is fp32. A lane's partial sum depends only on the units
+//    it owns, the group reduction is a fixed xor butterfly plus a fixed-order
+//    sum over waves, and the RMS reduction uses a fixed thread mapping per
+//    token, so a (token, row) result is bit-identical for every n_tok: the
 //    (k+1)-token verify pass equals k+1 separate decode GEMVs.
-//  * Optional RMSNorm prologue on X and store / accumulate / SwiGLU epilogues
-//    fuse the surrounding transformer ops into the projection launches.
 #include "orc_internal.hpp"
 
 #include <algorithm>
@@ -31,29 +35,13 @@
 
 namespace orc {
 
-// ── per-type geometry ────────────────────────────────────────────────────────
 template <int QT> struct QTr;
-template <> struct QTr<ORC_Q8_0> { static constexpr int BLK_EL = 32, BLK_B = 34, UPB = 1, PP = 32; };
-template <> struct QTr<ORC_Q4_0> { static constexpr int BLK_EL = 32, BLK_B = 18, UPB = 1, PP = 32; };
-template <> struct QTr<ORC_Q4_K> { static constexpr int BLK_EL = 256, BLK_B = 144, UPB = 8, PP = 64; };
-template <> struct QTr<ORC_Q6_K> { static constexpr int BLK_EL = 256, BLK_B = 210, UPB = 4, PP = 64; };
+template <> struct QTr<ORC_Q8_0> { static constexpr int BLK_EL = 32, UPB = 1, PP = 32; };
+template <> struct QTr<ORC_Q4_0> { static constexpr int BLK_EL = 32, UPB = 1, PP = 32; };
+template <> struct QTr<ORC_Q4_K> { static constexpr int BLK_EL = 256, UPB = 8, PP = 64; };
+template <> struct QTr<ORC_Q6_K> { static constexpr int BLK_EL = 256, UPB = 4, PP = 64; };
 
 template <int PP> __device__ __forceinline__ int padx(int k) { return k + 4 * (k / PP); }
-
-// Q4_K 6-bit (scale, min) of sub-block `is` from the 12 scale bytes held in
-// three dwords (core/gguf_parser.cpp:1085-1093).
-__device__ __forceinline__ void q4k_scale_min(int is, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
-                                              uint32_t& mn) {
-    if (is < 4) {
-        sc = (s0 >> (8 * is)) & 63u;
-        mn = (s1 >> (8 * is)) & 63u;
-    } else {
-        const int k = 8 * (is - 4);
-        const uint32_t b8 = (s2 >> k) & 0xFFu;
-        sc = (b8 & 0xFu) | (((s0 >> k) & 0xFFu) >> 6 << 4);
-        mn = (b8 >> 4) | (((s1 >> k) & 0xFFu) >> 6 << 4);
-    }
-}
 
 // Σ_{i<16} w[i] * x[i] with x read from LDS as 4 float4 (sequential FMA chain).
 __device__ __forceinline__ float dot16(const float* w, const float* xl) {
@@ -61,7 +49,7 @@ __device__ __forceinline__ float dot16(const float* w, const float* xl) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float4 v = x4[i];
+        const float4 v = x4[i];
         s = __builtin_fmaf(w[4 * i + 0], v.x, s);
         s = __builtin_fmaf(w[4 * i + 1], v.y, s);
         s = __builtin_fmaf(w[4 * i + 2], v.z, s);
@@ -70,8 +58,9 @@ __device__ __forceinline__ float dot16(const float* w, const float* xl) {
     return s;
 }
 
-// Unpack 4 dwords of codes into 16 floats, byte k of dword i -> w[4i+k].
-__device__ __forceinline__ void bytes_to_f(const uint32_t (&q)[4], float* w) {
+// Bytes of 4 dwords as 16 floats, byte k of dword i -> w[4i+k].
+__device__ __forceinline__ void bytes_to_f(uint32_t a, uint32_t b, uint32_t c, uint32_t d, float* w) {
+    const uint32_t q[4] = {a, b, c, d};
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -79,35 +68,38 @@ __device__ __forceinline__ void bytes_to_f(const uint32_t (&q)[4], float* w) {
 }
 
 struct UnitCtx {
-    const float* xs;  // LDS x, token 0, at tile element 0 (padded layout)
+    const float* xs;  // LDS x (times the norm weight when fused), token 0, tile element 0, padded
     int xs_stride;    // floats between tokens
-    const float* sx;  // LDS per-16 sums of x, token 0
+    const float* sx;  // LDS per-16 sums of the staged x, token 0
     int sx_stride;
     int k0;           // first element of the tile
 };
 
-// ── per-type unit dot products over ROWS rows and NT tokens ──────────────────
-template <int QT, int NT, int ROWS> struct UnitDot;
+// ── per-type units: load() issues the loads, compute() does the arithmetic ───
+template <int QT, int ROWS> struct Unit;
 
-template <int NT, int ROWS> struct UnitDot<ORC_Q4_K, NT, ROWS> {
-    // unit u: superblock u/8, 16-byte nibble chunk c = u%8 of that superblock.
-    // Chunk c holds values 64j+16h+[0,16) (low nibbles, sub-block 2j) and
+template <int ROWS> struct Unit<ORC_Q4_K, ROWS> {
+    // unit u: superblock u/8, 16-byte nibble chunk c = u%8 of it. Chunk c
+    // holds values 64j+16h+[0,16) (low nibbles, sub-block 2j) and
     // 64j+32+16h+[0,16) (high nibbles, sub-block 2j+1), j = c/2, h = c%2.
-    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
-                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
-        const int b = u >> 3, ch = u & 7, j = ch >> 1, h = ch & 1;
-        u32x4 hdr[ROWS], qv[ROWS];
+    u32x4 hdr[ROWS], q[ROWS];
+    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
+        const int b = u >> 3, ch = u & 7;
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
             if (ok[r]) {
                 const uint8_t* blk = rows[r] + (size_t)b * 144;
                 hdr[r] = ld16(blk);
-                qv[r] = ld16(blk + 16 + 16 * ch);
+                q[r] = ld16(blk + 16 + 16 * ch);
             }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
+                                            float (&acc)[ROWS][NT]) const {
+        const int b = u >> 3, ch = u & 7, j = ch >> 1, h = ch & 1;
         const int eA = b * 256 + 64 * j + 16 * h - c.k0, eB = eA + 32;
         const int pA = padx<64>(eA), pB = padx<64>(eB);
-        float dA[ROWS], mA[ROWS], dB[ROWS], mB[ROWS];
-        float wa[ROWS][16], wb[ROWS][16];
+        float dA[ROWS], mA[ROWS], dB[ROWS], mB[ROWS], wa[ROWS][16], wb[ROWS][16];
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
             if (!ok[r]) continue;
@@ -115,13 +107,13 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q4_K, NT, ROWS> {
             uint32_t s0, m0, s1, m1;
             q4k_scale_min(2 * j, hdr[r].y, hdr[r].z, hdr[r].w, s0, m0);
             q4k_scale_min(2 * j + 1, hdr[r].y, hdr[r].z, hdr[r].w, s1, m1);
-            dA[r] = d * (float)s0; mA[r] = dmin * (float)m0;
-            dB[r] = d * (float)s1; mB[r] = dmin * (float)m1;
-            uint32_t lo[4] = {qv[r].x & 0x0F0F0F0Fu, qv[r].y & 0x0F0F0F0Fu, qv[r].z & 0x0F0F0F0Fu, qv[r].w & 0x0F0F0F0Fu};
-            uint32_t hi[4] = {(qv[r].x >> 4) & 0x0F0F0F0Fu, (qv[r].y >> 4) & 0x0F0F0F0Fu, (qv[r].z >> 4) & 0x0F0F0F0Fu,
-                              (qv[r].w >> 4) & 0x0F0F0F0Fu};
-            bytes_to_f(lo, wa[r]);
-            bytes_to_f(hi, wb[r]);
+            dA[r] = d * (float)s0;
+            mA[r] = dmin * (float)m0;
+            dB[r] = d * (float)s1;
+            mB[r] = dmin * (float)m1;
+            bytes_to_f(q[r].x & 0x0F0F0F0Fu, q[r].y & 0x0F0F0F0Fu, q[r].z & 0x0F0F0F0Fu, q[r].w & 0x0F0F0F0Fu, wa[r]);
+            bytes_to_f((q[r].x >> 4) & 0x0F0F0F0Fu, (q[r].y >> 4) & 0x0F0F0F0Fu, (q[r].z >> 4) & 0x0F0F0F0Fu,
+                       (q[r].w >> 4) & 0x0F0F0F0Fu, wb[r]);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -137,15 +129,14 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q4_K, NT, ROWS> {
     }
 };
 
-template <int NT, int ROWS> struct UnitDot<ORC_Q6_K, NT, ROWS> {
+template <int ROWS> struct Unit<ORC_Q6_K, ROWS> {
     // unit u: superblock u/4, quarter v = u%4: half hh = v/2, l0 = 16*(v%2).
     // Group g (0..3) holds values 128hh+32g+l0+[0,16) with scale sc[8hh+2g+v%2].
-    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
-                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
-        const int b = u >> 2, v = u & 3, hh = v >> 1, odd = v & 1, l0 = 16 * odd;
-        u32x4 qa[ROWS], qb[ROWS], qh[ROWS];
-        u32x2 sc[ROWS];
-        uint32_t dh[ROWS];
+    u32x4 qa[ROWS], qb[ROWS], qh[ROWS];
+    u32x2 sc[ROWS];
+    uint32_t dh[ROWS];
+    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
+        const int b = u >> 2, v = u & 3, hh = v >> 1, l0 = 16 * (v & 1);
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
             if (ok[r]) {
@@ -156,6 +147,11 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q6_K, NT, ROWS> {
                 sc[r] = ld8(blk + 192 + 8 * hh);
                 dh[r] = ld2(blk + 208);
             }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
+                                            float (&acc)[ROWS][NT]) const {
+        const int b = u >> 2, v = u & 3, hh = v >> 1, odd = v & 1, l0 = 16 * odd;
         const int e0 = b * 256 + 128 * hh + l0 - c.k0;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -163,14 +159,13 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q6_K, NT, ROWS> {
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 if (!ok[r]) continue;
-                const int si = 2 * g + odd;  // byte index inside the 8 scale bytes
+                const int si = 2 * g + odd;  // byte index inside the 8 scale bytes of this half
                 const uint32_t sw = si < 4 ? sc[r].x : sc[r].y;
-                const int8_t s8 = (int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
-                sg[r] = h2f(dh[r]) * (float)s8;
-                uint32_t qq[4];
+                sg[r] = h2f(dh[r]) * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
                 const uint32_t a4[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w};
                 const uint32_t b4[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
                 const uint32_t h4[4] = {qh[r].x, qh[r].y, qh[r].z, qh[r].w};
+                uint32_t qq[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     uint32_t nib, hb;
@@ -180,7 +175,7 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q6_K, NT, ROWS> {
                     else { nib = (b4[i] >> 4) & 0x0F0F0F0Fu; hb = (h4[i] >> 2) & 0x30303030u; }
                     qq[i] = nib | hb;
                 }
-                bytes_to_f(qq, w[r]);
+                bytes_to_f(qq[0], qq[1], qq[2], qq[3], w[r]);
             }
             const int eg = e0 + 32 * g;
             const int pg = padx<64>(eg);
@@ -192,20 +187,18 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q6_K, NT, ROWS> {
                 for (int r = 0; r < ROWS; ++r) {
                     if (!ok[r]) continue;
                     // codes are stored +32: Σ (q-32) x = Σ q x - 32 Σ x
-                    const float s = dot16(w[r], xt + pg);
-                    acc[r][t] += sg[r] * (s - 32.f * sxg);
+                    acc[r][t] += sg[r] * (dot16(w[r], xt + pg) - 32.f * sxg);
                 }
             }
         }
     }
 };
 
-template <int NT, int ROWS> struct UnitDot<ORC_Q8_0, NT, ROWS> {
-    // unit u: block u (fp16 d + 32 int8 codes), acc += d * Σ q x.
-    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
-                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
-        u32x4 q0[ROWS], q1[ROWS];
-        uint32_t dh[ROWS];
+template <int ROWS> struct Unit<ORC_Q8_0, ROWS> {
+    // unit u: block u (fp16 d + 32 int8 codes): acc += d * Σ q x.
+    u32x4 q0[ROWS], q1[ROWS];
+    uint32_t dh[ROWS];
+    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
             if (ok[r]) {
@@ -214,6 +207,10 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q8_0, NT, ROWS> {
                 q0[r] = ld16(blk + 2);
                 q1[r] = ld16(blk + 18);
             }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
+                                            float (&acc)[ROWS][NT]) const {
         const int e0 = u * 32 - c.k0;
         const int p0 = padx<32>(e0);
         float w[ROWS][32], d[ROWS];
@@ -233,28 +230,28 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q8_0, NT, ROWS> {
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 if (!ok[r]) continue;
-                const float s = dot16(w[r], xt) + 0.f;
-                const float s2 = dot16(w[r] + 16, xt + 16);
-                acc[r][t] += d[r] * (s + s2);
+                acc[r][t] += d[r] * (dot16(w[r], xt) + dot16(w[r] + 16, xt + 16));
             }
         }
     }
 };
 
-template <int NT, int ROWS> struct UnitDot<ORC_Q4_0, NT, ROWS> {
-    // unit u: block u (fp16 d + 16 bytes: low nibble -> value l, high -> l+16),
-    // codes stored +8.
-    __device__ __forceinline__ static void run(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u,
-                                               const UnitCtx& c, float (&acc)[ROWS][NT]) {
-        u32x4 qv[ROWS];
-        uint32_t dh[ROWS];
+template <int ROWS> struct Unit<ORC_Q4_0, ROWS> {
+    // unit u: block u (fp16 d + 16 bytes: low nibble -> value l, high -> l+16), codes stored +8.
+    u32x4 q[ROWS];
+    uint32_t dh[ROWS];
+    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
             if (ok[r]) {
                 const uint8_t* blk = rows[r] + (size_t)u * 18;
                 dh[r] = ld2(blk);
-                qv[r] = ld16(blk + 2);
+                q[r] = ld16(blk + 2);
             }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
+                                            float (&acc)[ROWS][NT]) const {
         const int e0 = u * 32 - c.k0;
         const int p0 = padx<32>(e0);
         float wl[ROWS][16], wh[ROWS][16], d[ROWS];
@@ -262,11 +259,9 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q4_0, NT, ROWS> {
         for (int r = 0; r < ROWS; ++r) {
             if (!ok[r]) continue;
             d[r] = h2f(dh[r]);
-            uint32_t lo[4] = {qv[r].x & 0x0F0F0F0Fu, qv[r].y & 0x0F0F0F0Fu, qv[r].z & 0x0F0F0F0Fu, qv[r].w & 0x0F0F0F0Fu};
-            uint32_t hi[4] = {(qv[r].x >> 4) & 0x0F0F0F0Fu, (qv[r].y >> 4) & 0x0F0F0F0Fu, (qv[r].z >> 4) & 0x0F0F0F0Fu,
-                              (qv[r].w >> 4) & 0x0F0F0F0Fu};
-            bytes_to_f(lo, wl[r]);
-            bytes_to_f(hi, wh[r]);
+            bytes_to_f(q[r].x & 0x0F0F0F0Fu, q[r].y & 0x0F0F0F0Fu, q[r].z & 0x0F0F0F0Fu, q[r].w & 0x0F0F0F0Fu, wl[r]);
+            bytes_to_f((q[r].x >> 4) & 0x0F0F0F0Fu, (q[r].y >> 4) & 0x0F0F0F0Fu, (q[r].z >> 4) & 0x0F0F0F0Fu,
+                       (q[r].w >> 4) & 0x0F0F0F0Fu, wh[r]);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -275,8 +270,7 @@ template <int NT, int ROWS> struct UnitDot<ORC_Q4_0, NT, ROWS> {
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 if (!ok[r]) continue;
-                const float s = dot16(wl[r], xt) + dot16(wh[r], xt + 16);
-                acc[r][t] += d[r] * (s - 8.f * sxs);
+                acc[r][t] += d[r] * ((dot16(wl[r], xt) + dot16(wh[r], xt + 16)) - 8.f * sxs);
             }
         }
     }
@@ -298,17 +292,13 @@ struct GemmParams {
     const float* norm_w;
     float eps;
     int epi;
-    int kt_el;     // K tile in elements (multiple of the block size)
+    int kt_el;     // K tile in elements (a multiple of 1024 when n_in is split)
     int n_ktiles;
 };
 
 constexpr int kWG = 256;
 constexpr int kMaxNT = 5;  // tokens per launch; larger batches are chunked (results unchanged)
 
-// KS waves share one row group (split-K across waves): a group is LPR lanes in
-// each of KS waves, KS*LPR lanes in all, lane li owning units li, li+KS*LPR, ...
-// The butterfly over LPR lanes and the fixed-order sum over the KS waves make
-// the reduction order a function of (LPR, KS) only.
 template <int QT, int NT, int LPR, int KS, int ROWS>
 __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
     using T = QTr<QT>;
@@ -323,9 +313,8 @@ __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
     const int sx_stride = p.kt_el / 16;
     float* xs = smem;
     float* sx = smem + NT * xs_stride;
-    float* red = sx + NT * sx_stride;  // 8 floats of reduction scratch, 8 inverse RMS, then KS partials
-    float* inv = red + 8;
-    float* part = red + 16;
+    float* red = sx + NT * sx_stride;  // 4*NT wave partials of sum x^2, then KS partial sums
+    float* part = red + 4 * NT;
 
     // rows owned by this lane group
     const uint8_t* rows[ROWS];
@@ -350,66 +339,81 @@ __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
         bias[r] = p.bias[seg] ? p.bias[seg] + j : nullptr;
     }
 
-    // optional RMSNorm prologue: inverse RMS per token, same reduction for any n_tok
-    if (p.norm_w) {
-        for (int t = 0; t < NT; ++t) {
-            const float4* xr = (const float4*)(p.x + (size_t)t * p.ldx);
-            float ss = 0.f;
-            for (int i = tid; i < p.n_in / 4; i += kWG) {
-                float4 v = xr[i];
-                ss = __builtin_fmaf(v.x, v.x, ss);
-                ss = __builtin_fmaf(v.y, v.y, ss);
-                ss = __builtin_fmaf(v.z, v.z, ss);
-                ss = __builtin_fmaf(v.w, v.w, ss);
-            }
+    float acc[ROWS][NT], ss[NT];
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-            if (lane == 0) red[wave] = ss;
-            __syncthreads();
-            if (tid == 0) inv[t] = 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)p.n_in + p.eps);
-            __syncthreads();
-        }
+    for (int t = 0; t < NT; ++t) {
+        ss[t] = 0.f;
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r][t] = 0.f;
     }
-
-    float acc[ROWS][NT];
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[r][t] = 0.f;
-
+    const bool norm = p.norm_w != nullptr;
     const int units_per_tile = p.kt_el / T::BLK_EL * T::UPB;
+    Unit<QT, ROWS> cur, nxt;
     for (int kt = 0; kt < p.n_ktiles; ++kt) {
         const int k0 = kt * p.kt_el;
         const int kn = min(p.kt_el, p.n_in - k0);
-        if (kt) __syncthreads();
-        // stage x (normalized when requested) into padded LDS
+        const int u1 = min(p.units_per_row, kt * units_per_tile + units_per_tile);
+        int u = kt * units_per_tile + li;
+        if (u < u1) cur.load(rows, ok, u);  // in flight while x is staged
+        if (kt) __syncthreads();            // previous tile fully consumed
+        // stage the tile: all loads first, then LDS stores and per-16 sums (4-lane shuffle)
         const int q4 = kn / 4;
-        for (int i = tid; i < NT * q4; i += kWG) {
-            const int t = i / q4, k = 4 * (i - t * q4);
-            float4 v = *(const float4*)(p.x + (size_t)t * p.ldx + k0 + k);
-            if (p.norm_w) {
-                const float s = inv[t];
-                const float4 w = *(const float4*)(p.norm_w + k0 + k);
-                v.x = (v.x * s) * w.x; v.y = (v.y * s) * w.y; v.z = (v.z * s) * w.z; v.w = (v.w * s) * w.w;
-            }
-            *(float4*)(xs + t * xs_stride + padx<T::PP>(k)) = v;
-        }
-        __syncthreads();
-        const int n16 = kn / 16;
-        for (int i = tid; i < NT * n16; i += kWG) {
-            const int t = i / n16, g = i - t * n16;
-            const float* src = xs + t * xs_stride + padx<T::PP>(16 * g);
-            float s = 0.f;
+        for (int t = 0; t < NT; ++t) {
+            const float* src = p.x + (size_t)t * p.ldx + k0;
+            for (int b0 = 0; b0 < q4; b0 += 4 * kWG) {
+                float4 v[4];
 #pragma unroll
-            for (int k = 0; k < 16; ++k) s += src[k];
-            sx[t * sx_stride + g] = s;
+                for (int s = 0; s < 4; ++s) {
+                    const int i = b0 + s * kWG + tid;
+                    v[s] = i < q4 ? *(const float4*)(src + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int i = b0 + s * kWG + tid;
+                    float4 a = v[s];
+                    if (norm && i < q4) {
+                        ss[t] = __builtin_fmaf(a.x, a.x, ss[t]);
+                        ss[t] = __builtin_fmaf(a.y, a.y, ss[t]);
+                        ss[t] = __builtin_fmaf(a.z, a.z, ss[t]);
+                        ss[t] = __builtin_fmaf(a.w, a.w, ss[t]);
+                        const float4 g = *(const float4*)(p.norm_w + k0 + 4 * i);
+                        a.x *= g.x; a.y *= g.y; a.z *= g.z; a.w *= g.w;
+                    }
+                    float s16 = (a.x + a.y) + (a.z + a.w);
+                    s16 += __shfl_xor(s16, 1, 64);
+                    s16 += __shfl_xor(s16, 2, 64);
+                    if (i < q4) {
+                        *(float4*)(xs + t * xs_stride + padx<T::PP>(4 * i)) = a;
+                        if ((tid & 3) == 0) sx[t * sx_stride + i / 4] = s16;
+                    }
+                }
+            }
         }
         __syncthreads();
-        UnitCtx c{xs, xs_stride, sx, sx_stride, k0};
-        const int u0 = kt * units_per_tile;
-        const int u1 = min(p.units_per_row, u0 + units_per_tile);
-#pragma unroll 2
-        for (int u = u0 + li; u < u1; u += LT) UnitDot<QT, NT, ROWS>::run(rows, ok, u, c, acc);
+        const UnitCtx c{xs, xs_stride, sx, sx_stride, k0};
+        for (; u < u1; u += LT) {
+            const int un = u + LT;
+            if (un < u1) nxt.load(rows, ok, un);
+            cur.template compute<NT>(u, c, ok, acc);
+            cur = nxt;
+        }
+    }
+
+    // 1/rms per token: a fixed reduction order for every n_tok (as orc_rmsnorm)
+    float inv[NT];
+    if (norm) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float v = ss[t];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (lane == 0) red[4 * t + wave] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            inv[t] = 1.f / sqrtf(((red[4 * t] + red[4 * t + 1]) + (red[4 * t + 2] + red[4 * t + 3])) / (float)p.n_in +
+                                 p.eps);
     }
 
     // reduction: xor butterfly over the LPR lanes of a wave, then the KS waves in fixed order
@@ -423,24 +427,29 @@ __global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
             acc[r][t] = v;
         }
     if (KS > 1) {
-        const int slot = (gl * ROWS) * NT;
+        const int slot = (gl * ROWS) * NT, st = GR * G * ROWS * NT;
         if (lane % LPR == 0)
 #pragma unroll
             for (int r = 0; r < ROWS; ++r)
 #pragma unroll
-                for (int t = 0; t < NT; ++t) part[(wsub * GR * G * ROWS) * NT + slot + r * NT + t] = acc[r][t];
+                for (int t = 0; t < NT; ++t) part[wsub * st + slot + r * NT + t] = acc[r][t];
         __syncthreads();
         if (wsub != 0) return;
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const int o = slot + r * NT + t, st = GR * G * ROWS * NT;
+                const int o = slot + r * NT + t;
                 if (KS == 2) acc[r][t] = part[o] + part[st + o];
                 else acc[r][t] = (part[o] + part[st + o]) + (part[2 * st + o] + part[3 * st + o]);
             }
     }
     if (lane % LPR != 0) return;
+    if (norm)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[r][t] *= inv[t];
     if (p.epi == ORC_EPI_SWIGLU) {
         if (!ok[0]) return;
 #pragma unroll
@@ -476,12 +485,12 @@ static int units_per_block(int type) {
 static int block_elems(int type) { return type == ORC_Q4_K || type == ORC_Q6_K ? 256 : 32; }
 
 constexpr int kRows = 2;
-size_t g_lds_budget = 64 * 1024;  // set from the device limit at first use
+static size_t g_lds_budget = 64 * 1024;  // set from the device limit at first use
 
 static size_t lds_bytes(int type, int nt, int kt, int ks, int lpr) {
     const int PP = (type == ORC_Q4_K || type == ORC_Q6_K) ? 64 : 32;
     const size_t part = (size_t)ks * (4 / ks) * (64 / lpr) * kRows * nt;
-    return (size_t)nt * ((kt + 4 * (kt / PP) + 4) + kt / 16) * 4 + (16 + part) * 4;
+    return (size_t)nt * ((kt + 4 * (kt / PP) + 4) + kt / 16) * 4 + (4 * nt + part) * 4;
 }
 
 struct GemmShape { int lpr, ks; };
@@ -489,11 +498,11 @@ struct GemmShape { int lpr, ks; };
 // Lanes per row group (LPR) and waves per group (KS) depend on (type, n_in,
 // n_out) only, never on n_tok, so every token sees the same reduction order.
 // Narrow matrices get more lanes per row (more workgroups in flight); the
-// smallest K tile (KS*LPR units for kMaxNT tokens) must fit the LDS budget.
+// smallest K tile must fit the LDS budget for kMaxNT tokens.
 static GemmShape choose_shape(int type, int units, int n_out) {
     const int el_per_unit = block_elems(type) / units_per_block(type);
     int cap = 64;
-    while (cap > 8 && lds_bytes(type, kMaxNT, cap * el_per_unit, 1, 64) > g_lds_budget) cap /= 2;
+    while (cap > 8 && lds_bytes(type, kMaxNT, std::max(1024, cap * el_per_unit), 1, 64) > g_lds_budget) cap /= 2;
     int lt;
     if (n_out >= 12288) lt = units >= 96 ? 32 : units >= 32 ? 16 : 8;  // many rows: 1 wave per group
     else {
@@ -515,25 +524,25 @@ static int launch_nt(const GemmParams& p0, GemmShape sh, hipStream_t s) {
     const int tile = (4 / ks) * (64 / lpr) * kRows;
     const int n_items = p.epi == ORC_EPI_SWIGLU ? p.rows[0] * kRows : p.tile_rows_total;
     const int grid = (n_items + tile - 1) / tile;
-    // K tile: as many whole blocks as fit, units per tile a multiple of KS*LPR
+    // K tile: the whole row when it fits; otherwise a multiple of lcm(1024, KS*LPR units)
+    // so that every lane owns the same units and every thread the same x elements.
     const int be = QTr<QT>::BLK_EL, upb = QTr<QT>::UPB;
     const int type = QT;
-    int kt = (p.n_in + be - 1) / be * be;
+    int kt = p.n_in;
     if (lds_bytes(type, NT, kt, ks, lpr) > g_lds_budget) {
-        const int blk_step = std::max(1, ks * lpr / upb);
-        kt = blk_step * be;
-        while (kt + blk_step * be < p.n_in && lds_bytes(type, NT, kt + blk_step * be, ks, lpr) <= g_lds_budget)
-            kt += blk_step * be;
+        const int step = std::max(1024, ks * lpr / upb * be);
+        kt = step;
+        while (kt + step < p.n_in && lds_bytes(type, NT, kt + step, ks, lpr) <= g_lds_budget) kt += step;
     }
     p.kt_el = kt;
     p.n_ktiles = (p.n_in + kt - 1) / kt;
     const size_t lds = lds_bytes(type, NT, kt, ks, lpr);
     if (lds > g_lds_budget) return set_error(ORC_E_UNSUPPORTED, "gemm: K tile does not fit LDS");
-#define L(LPR_, KS_)                                                                                  \
-    if (lpr == LPR_ && ks == KS_) {                                                                   \
-        hipLaunchKernelGGL((k_gemm<QT, NT, LPR_, KS_, kRows>), dim3(grid), dim3(kWG), lds, s, p);     \
-        ORC_LAUNCH_CHECK();                                                                           \
-        return ORC_OK;                                                                                \
+#define L(LPR_, KS_)                                                                              \
+    if (lpr == LPR_ && ks == KS_) {                                                               \
+        hipLaunchKernelGGL((k_gemm<QT, NT, LPR_, KS_, kRows>), dim3(grid), dim3(kWG), lds, s, p); \
+        ORC_LAUNCH_CHECK();                                                                       \
+        return ORC_OK;                                                                            \
     }
     L(8, 1) L(16, 1) L(32, 1) L(8, 2) L(8, 4) L(16, 4)
 #undef L
@@ -559,7 +568,7 @@ struct ProfRec {
     double bytes;
 };
 static bool g_prof_on = false;
-static std::vector<ProfRec> g_prof;     // records of the current region
+static std::vector<ProfRec> g_prof;
 static std::vector<hipEvent_t> g_evpool;
 static size_t g_evnext = 0;
 
@@ -575,9 +584,9 @@ static hipEvent_t prof_event() {
 // Algorithmic HBM bytes of one launch: weight blocks + activations read +
 // outputs written (read too when accumulating) + norm weights and biases.
 static double gemm_bytes(const GemmParams& p, int nt) {
-    const int n_out = p.epi == ORC_EPI_SWIGLU ? 2 * p.rows[0] : p.tile_rows_total;
+    const int n_w = p.epi == ORC_EPI_SWIGLU ? 2 * p.rows[0] : p.tile_rows_total;
     const int n_y = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.tile_rows_total;
-    double b = (double)p.row_bytes * n_out + 4.0 * nt * p.n_in + 4.0 * nt * n_y * (p.epi == ORC_EPI_ACCUM ? 2 : 1);
+    double b = (double)p.row_bytes * n_w + 4.0 * nt * p.n_in + 4.0 * nt * n_y * (p.epi == ORC_EPI_ACCUM ? 2 : 1);
     if (p.norm_w) b += 4.0 * p.n_in;
     for (int i = 0; i < p.n_seg; ++i)
         if (p.bias[i]) b += 4.0 * p.rows[i];
@@ -593,19 +602,16 @@ static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
             g_lds_budget = std::min<size_t>((size_t)v, 160 * 1024);
         lds_init = true;
     }
-    const int upb = units_per_block(type);
-    p.units_per_row = p.n_in / block_elems(type) * upb;
+    p.units_per_row = p.n_in / block_elems(type) * units_per_block(type);
     const int n_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.tile_rows_total;
     const GemmShape sh = choose_shape(type, p.units_per_row, n_out);
     // tokens are processed in chunks of at most kMaxNT; chunking never changes a
     // (token,row) result because the reduction order is independent of n_tok
-    const int total = p.n_tok;
-    for (int t0 = 0; t0 < total; t0 += kMaxNT) {
+    for (int t0 = 0; t0 < p.n_tok; t0 += kMaxNT) {
         GemmParams q = p;
-        q.n_tok = std::min(kMaxNT, total - t0);
+        q.n_tok = std::min(kMaxNT, p.n_tok - t0);
         q.x = p.x + (size_t)t0 * p.ldx;
         for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
-        int rc;
         ProfRec rec{};
         bool prof = false;
         if (g_prof_on) {
@@ -618,6 +624,7 @@ static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
                 rec.bytes = gemm_bytes(q, q.n_tok);
             }
         }
+        int rc;
         switch (type) {
             case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, sh, s); break;
             case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, sh, s); break;
@@ -738,123 +745,3 @@ extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_t
     return gemm_dispatch(p, type, resolve_stream(stream));
 }
 
-// ── bit-exact dequant (core/gguf_parser.cpp:1029-1154) ───────────────────────
-namespace orc {
-// One thread per 32 consecutive output values; rounding exactly as the
-// reference build: Q4_0/Q8_0/F16 one product or exact conversion, Q4_K
-// fma(d*sc, q, -(dmin*m)) (the reference's d1*q - m1f contracts to one FMA),
-// Q6_K (d*sc)*q with two roundings.
-__device__ __forceinline__ void dequant32(int type, const uint8_t* w, int64_t g, float* out) {
-    switch (type) {
-        case ORC_F32:
-            for (int i = 0; i < 32; ++i) out[i] = ((const float*)w)[g * 32 + i];
-            break;
-        case ORC_F16:
-            for (int i = 0; i < 32; ++i) out[i] = h2f(ld2(w + (g * 32 + i) * 2));
-            break;
-        case ORC_Q8_0: {
-            const uint8_t* b = w + g * 34;
-            const float d = h2f(ld2(b));
-            for (int i = 0; i < 32; ++i) out[i] = d * (float)(int8_t)b[2 + i];
-            break;
-        }
-        case ORC_Q4_0: {
-            const uint8_t* b = w + g * 18;
-            const float d = h2f(ld2(b));
-            for (int l = 0; l < 16; ++l) {
-                out[l] = d * (float)((int)(b[2 + l] & 0xF) - 8);
-                out[l + 16] = d * (float)((int)(b[2 + l] >> 4) - 8);
-            }
-            break;
-        }
-        case ORC_Q4_K: {  // 32 values = one sub-block
-            const int64_t sb = g >> 3;
-            const int s = (int)(g & 7), j = s >> 1, hi = s & 1;
-            const uint8_t* b = w + sb * 144;
-            const float d = h2f(ld2(b)), dmin = h2f(ld2(b + 2));
-            uint32_t sc, mn;
-            q4k_scale_min(s, ld4(b + 4), ld4(b + 8), ld4(b + 12), sc, mn);
-            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
-            const uint8_t* qs = b + 16 + 32 * j;
-            for (int l = 0; l < 32; ++l) {
-                const uint32_t q = hi ? (qs[l] >> 4) : (qs[l] & 0xF);
-                out[l] = __builtin_fmaf(d1, (float)q, -m1);
-            }
-            break;
-        }
-        case ORC_Q6_K: {  // 32 values = values 128hh+32gg+[0,32) of superblock sb
-            const int64_t sb = g >> 3;
-            const int s = (int)(g & 7), hh = s >> 2, gg = s & 3;
-            const uint8_t* b = w + sb * 210;
-            const uint8_t* ql = b + 64 * hh;
-            const uint8_t* qh = b + 128 + 32 * hh;
-            const int8_t* sc = (const int8_t*)(b + 192 + 8 * hh);
-            const float d = h2f(ld2(b + 208));
-            for (int l = 0; l < 32; ++l) {
-                const int is = l / 16;
-                int q;
-                if (gg == 0) q = (ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4);
-                else if (gg == 1) q = (ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4);
-                else if (gg == 2) q = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4);
-                else q = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4);
-                out[l] = (d * (float)sc[is + 2 * gg]) * (float)(q - 32);
-            }
-            break;
-        }
-    }
-}
-
-__global__ void k_dequant(int type, const uint8_t* w, int64_t n_groups, float* y) {
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n_groups) return;
-    float v[32];
-    dequant32(type, w, g, v);
-    float4* o = (float4*)(y + g * 32);
-    for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-}
-
-__global__ void k_embed(int type, const uint8_t* table, int n_in, int n_rows, uint64_t row_bytes, const int32_t* ids,
-                        float* y, int ldy) {
-    const int t = blockIdx.y;
-    const int g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g * 32 >= n_in) return;
-    int id = ids[t];
-    if (id < 0 || id >= n_rows) id = 0;
-    float v[32];
-    dequant32(type, table + (uint64_t)id * row_bytes, g, v);
-    float4* o = (float4*)(y + (size_t)t * ldy + g * 32);
-    for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-}
-}  // namespace orc
-
-static bool dq_type_ok(int t) {
-    return t == ORC_F32 || t == ORC_F16 || t == ORC_Q4_0 || t == ORC_Q8_0 || t == ORC_Q4_K || t == ORC_Q6_K;
-}
-
-extern "C" int orc_dequant(int type, const void* d_w, int64_t n_el, float* d_y, orc_stream_t stream) {
-    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (!dq_type_ok(type)) return set_error(ORC_E_UNSUPPORTED, "dequant: unsupported type " + std::to_string(type));
-    const int be = (type == ORC_Q4_K || type == ORC_Q6_K) ? 256 : 32;
-    if (n_el <= 0 || n_el % be || !d_w || !d_y) return set_error(ORC_E_INVALID, "dequant: bad size or pointer");
-    if ((uintptr_t)d_y & 15) return set_error(ORC_E_INVALID, "dequant: output must be 16-byte aligned");
-    const int64_t groups = n_el / 32;
-    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, resolve_stream(stream), type,
-                       (const uint8_t*)d_w, groups, d_y);
-    ORC_LAUNCH_CHECK();
-    return ORC_OK;
-}
-
-extern "C" int orc_embed(int type, const void* d_table, int n_in, int n_rows, const int32_t* d_ids, int n_tok,
-                         float* d_y, int ldy, orc_stream_t stream) {
-    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (!dq_type_ok(type)) return set_error(ORC_E_UNSUPPORTED, "embed: unsupported type " + std::to_string(type));
-    const int be = (type == ORC_Q4_K || type == ORC_Q6_K) ? 256 : 32;
-    if (n_in <= 0 || n_in % be || n_rows <= 0 || n_tok < 0 || ldy < n_in || ldy % 4 || !d_table || !d_ids || !d_y)
-        return set_error(ORC_E_INVALID, "embed: bad arguments");
-    if (n_tok == 0) return ORC_OK;
-    const int groups = n_in / 32;
-    hipLaunchKernelGGL(k_embed, dim3((groups + 63) / 64, n_tok), dim3(64), 0, resolve_stream(stream), type,
-                       (const uint8_t*)d_table, n_in, n_rows, (uint64_t)orc_row_bytes(type, n_in), d_ids, d_y, ldy);
-    ORC_LAUNCH_CHECK();
-    return ORC_OK;
-}

@@ -47,4 +47,19 @@ __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const u16_u
 // Byte k of w as float; the compiler emits one v_cvt_f32_ubyte{k}.
 __device__ __forceinline__ float ubyte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
 
+// Q4_K 6-bit (scale, min) of sub-block `is` from the 12 scale bytes held in
+// three dwords (core/gguf_parser.cpp:1085-1093).
+__device__ __forceinline__ void q4k_scale_min(int is, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
+                                              uint32_t& mn) {
+    if (is < 4) {
+        sc = (s0 >> (8 * is)) & 63u;
+        mn = (s1 >> (8 * is)) & 63u;
+    } else {
+        const int k = 8 * (is - 4);
+        const uint32_t b8 = (s2 >> k) & 0xFFu;
+        sc = (b8 & 0xFu) | (((s0 >> k) & 0xFFu) >> 6 << 4);
+        mn = (b8 >> 4) | (((s1 >> k) & 0xFFu) >> 6 << 4);
+    }
+}
+
 }  // namespace orc
