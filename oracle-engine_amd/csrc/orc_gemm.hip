@@ -6,28 +6,28 @@
 // 565-643).
 //
 // Design (one kernel family; n_tok = 1 is the decode GEMV):
-//  * A 256-thread workgroup owns a tile of weight rows. A "row group" of
-//    KS*LPR lanes (LPR lanes in each of KS waves) owns ROWS rows and walks
-//    their row bytes in units: 16 B of Q4_K nibbles (32 values), a 64-value
-//    quarter of a Q6_K superblock, one Q8_0 / Q4_0 block. Blocks are read
-//    straight from the as-uploaded GGUF bytes with (unaligned) 128-bit loads.
-//  * Latency: each lane issues the loads of its first unit before the
-//    activations are staged, and the loads of unit i+1 before computing unit
-//    i, so HBM latency overlaps the L2 staging and the arithmetic.
-//  * The activations of all n_tok tokens for one K tile are staged in LDS
-//    (fp32, 4 floats of padding every 32/64 values so the lanes of a group hit
-//    distinct banks) with every load in flight at once; per-16-value sums of x
-//    (for the Q4_K minimum and the Q6_K / Q4_0 code offsets) come from a
-//    4-lane shuffle in the same pass. One barrier per K tile.
+//  * Persistent 512-thread workgroups (one or two per CU). A workgroup stages
+//    the activations of all n_tok tokens in LDS once (fp32, 4 floats of
+//    padding every 32/64 values so the lanes of a slot hit distinct banks,
+//    plus per-16-value sums for the Q4_K minimum and the code offsets), then
+//    its waves walk row groups spread over every CU.
+//  * A wave holds G = 64/LPR slots of ROWS rows. A slot's LPR lanes split the
+//    row into units (a 16-byte Q4_K nibble chunk = 32 values, a 64-value
+//    quarter of a Q6_K superblock, one Q8_0 / Q4_0 block); lane li owns units
+//    li, li+LPR, ... and walks them in batches of UPL whose loads are all in
+//    flight at once, straight from the as-uploaded GGUF bytes with 128-bit
+//    loads. The first batch of a wave's first row group is issued before the
+//    activations are staged.
+//  * Each weight code is converted once and applied to every token, 8 codes
+//    at a time against 8 activations read from LDS; fp32 FMA chains.
 //  * RMSNorm prologue: x is staged multiplied by the norm weight and the
 //    per-token 1/rms (reduced while staging) scales the finished dot product:
 //    sum_i w_i (x_i s g_i) = s * sum_i w_i (x_i g_i).
-//  * Each weight code is decoded once per row and applied to every token in
-//    LDS; accumulation is fp32. A lane's partial sum depends only on the units
-//    it owns, the group reduction is a fixed xor butterfly plus a fixed-order
-//    sum over waves, and the RMS reduction uses a fixed thread mapping per
-//    token, so a (token, row) result is bit-identical for every n_tok: the
-//    (k+1)-token verify pass equals k+1 separate decode GEMVs.
+//  * Batch invariance: LPR depends on the type only; a lane's partial sum
+//    runs over its units in a fixed order, the slot reduction is a fixed xor
+//    butterfly and the RMS sum uses a fixed thread mapping, so a (token, row)
+//    result is bit-identical for every n_tok and every launch shape: the
+//    (k+1)-token verify pass equals k+1 decode GEMVs.
 #include "orc_internal.hpp"
 
 #include <algorithm>
@@ -35,45 +35,62 @@
 
 namespace orc {
 
+// LPR: lanes per row slot; EPU: values per unit; PP: LDS padding period.
 template <int QT> struct QTr;
-template <> struct QTr<ORC_Q8_0> { static constexpr int BLK_EL = 32, UPB = 1, PP = 32; };
-template <> struct QTr<ORC_Q4_0> { static constexpr int BLK_EL = 32, UPB = 1, PP = 32; };
-template <> struct QTr<ORC_Q4_K> { static constexpr int BLK_EL = 256, UPB = 8, PP = 64; };
-template <> struct QTr<ORC_Q6_K> { static constexpr int BLK_EL = 256, UPB = 4, PP = 64; };
+template <> struct QTr<ORC_Q8_0> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
+template <> struct QTr<ORC_Q4_0> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
+template <> struct QTr<ORC_Q4_K> { static constexpr int EPU = 32, PP = 64, LPR = 32; };
+template <> struct QTr<ORC_Q6_K> { static constexpr int EPU = 64, PP = 64, LPR = 16; };
 
 template <int PP> __device__ __forceinline__ int padx(int k) { return k + 4 * (k / PP); }
 
-// Σ_{i<16} w[i] * x[i] with x read from LDS as 4 float4 (sequential FMA chain).
-__device__ __forceinline__ float dot16(const float* w, const float* xl) {
-    const float4* x4 = (const float4*)xl;
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 v = x4[i];
-        s = __builtin_fmaf(w[4 * i + 0], v.x, s);
-        s = __builtin_fmaf(w[4 * i + 1], v.y, s);
-        s = __builtin_fmaf(w[4 * i + 2], v.z, s);
-        s = __builtin_fmaf(w[4 * i + 3], v.w, s);
-    }
-    return s;
-}
-
-// Bytes of 4 dwords as 16 floats, byte k of dword i -> w[4i+k].
-__device__ __forceinline__ void bytes_to_f(uint32_t a, uint32_t b, uint32_t c, uint32_t d, float* w) {
-    const uint32_t q[4] = {a, b, c, d};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) w[4 * i + k] = ubyte_f(q[i], k);
-}
-
-struct UnitCtx {
-    const float* xs;  // LDS x (times the norm weight when fused), token 0, tile element 0, padded
+struct XCtx {
+    const float* xs;  // staged x (times the norm weight), token 0, element 0, padded
     int xs_stride;    // floats between tokens
-    const float* sx;  // LDS per-16 sums of the staged x, token 0
+    const float* sx;  // per-16 sums of the staged x, token 0
     int sx_stride;
-    int k0;           // first element of the tile
+    int k0;           // first element staged
 };
+
+// Bytes of two dwords as 8 floats: byte k of a -> w[k], of b -> w[4+k].
+__device__ __forceinline__ void to_f8(uint32_t a, uint32_t b, float* w) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        w[k] = ubyte_f(a, k);
+        w[4 + k] = ubyte_f(b, k);
+    }
+}
+
+// S[r][t] += sum_{i<8} w[r][i] * x_t[e+i] (sequential FMA chain), x from LDS
+// at padded offset pe. The 8 activations of a token are read once for all rows.
+template <int ROWS, int NT>
+__device__ __forceinline__ void dot8(const float (&w)[ROWS][8], const XCtx& c, int pe, float (&S)[ROWS][NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float4 a = *(const float4*)(c.xs + t * c.xs_stride + pe);
+        const float4 b = *(const float4*)(c.xs + t * c.xs_stride + pe + 4);
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            float s = S[r][t];
+            s = __builtin_fmaf(w[r][0], a.x, s);
+            s = __builtin_fmaf(w[r][1], a.y, s);
+            s = __builtin_fmaf(w[r][2], a.z, s);
+            s = __builtin_fmaf(w[r][3], a.w, s);
+            s = __builtin_fmaf(w[r][4], b.x, s);
+            s = __builtin_fmaf(w[r][5], b.y, s);
+            s = __builtin_fmaf(w[r][6], b.z, s);
+            s = __builtin_fmaf(w[r][7], b.w, s);
+            S[r][t] = s;
+        }
+    }
+}
+
+template <int ROWS, int NT> __device__ __forceinline__ void zero(float (&S)[ROWS][NT]) {
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) S[r][t] = 0.f;
+}
 
 // ── per-type units: load() issues the loads, compute() does the arithmetic ───
 template <int QT, int ROWS> struct Unit;
@@ -82,27 +99,47 @@ template <int ROWS> struct Unit<ORC_Q4_K, ROWS> {
     // unit u: superblock u/8, 16-byte nibble chunk c = u%8 of it. Chunk c
     // holds values 64j+16h+[0,16) (low nibbles, sub-block 2j) and
     // 64j+32+16h+[0,16) (high nibbles, sub-block 2j+1), j = c/2, h = c%2.
+    // Per sub-block: d*sc * sum(q x) - dmin*m * sum(x)  (core/gguf_parser.cpp:1096-1121).
     u32x4 hdr[ROWS], q[ROWS];
-    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
+    __device__ __forceinline__ void load(const uint8_t* const (&rp)[ROWS], int u) {
         const int b = u >> 3, ch = u & 7;
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            if (ok[r]) {
-                const uint8_t* blk = rows[r] + (size_t)b * 144;
-                hdr[r] = ld16(blk);
-                q[r] = ld16(blk + 16 + 16 * ch);
-            }
+        for (int r = 0; r < ROWS; ++r) {
+            const uint8_t* blk = rp[r] + (size_t)b * 144;
+            hdr[r] = ld16(blk);
+            q[r] = ld16(blk + 16 + 16 * ch);
+        }
     }
     template <int NT>
-    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
-                                            float (&acc)[ROWS][NT]) const {
+    __device__ __forceinline__ void half(const uint32_t (&m)[ROWS][4], int e, const float (&dd)[ROWS],
+                                         const float (&mm)[ROWS], const XCtx& c, float (&acc)[ROWS][NT]) const {
+        float S[ROWS][NT];
+        zero(S);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            float w[ROWS][8];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) to_f8(m[r][2 * k], m[r][2 * k + 1], w[r]);
+            dot8(w, c, padx<64>(e + 8 * k), S);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float sxv = c.sx[t * c.sx_stride + e / 16];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                acc[r][t] = __builtin_fmaf(dd[r], S[r][t], acc[r][t]);
+                acc[r][t] = __builtin_fmaf(-mm[r], sxv, acc[r][t]);
+            }
+        }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const XCtx& c, float (&acc)[ROWS][NT]) const {
         const int b = u >> 3, ch = u & 7, j = ch >> 1, h = ch & 1;
-        const int eA = b * 256 + 64 * j + 16 * h - c.k0, eB = eA + 32;
-        const int pA = padx<64>(eA), pB = padx<64>(eB);
-        float dA[ROWS], mA[ROWS], dB[ROWS], mB[ROWS], wa[ROWS][16], wb[ROWS][16];
+        const int eA = b * 256 + 64 * j + 16 * h - c.k0;
+        float dA[ROWS], mA[ROWS], dB[ROWS], mB[ROWS];
+        uint32_t lo[ROWS][4], hi[ROWS][4];
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
-            if (!ok[r]) continue;
             const float d = h2f(hdr[r].x & 0xFFFFu), dmin = h2f(hdr[r].x >> 16);
             uint32_t s0, m0, s1, m1;
             q4k_scale_min(2 * j, hdr[r].y, hdr[r].z, hdr[r].w, s0, m0);
@@ -111,61 +148,56 @@ template <int ROWS> struct Unit<ORC_Q4_K, ROWS> {
             mA[r] = dmin * (float)m0;
             dB[r] = d * (float)s1;
             mB[r] = dmin * (float)m1;
-            bytes_to_f(q[r].x & 0x0F0F0F0Fu, q[r].y & 0x0F0F0F0Fu, q[r].z & 0x0F0F0F0Fu, q[r].w & 0x0F0F0F0Fu, wa[r]);
-            bytes_to_f((q[r].x >> 4) & 0x0F0F0F0Fu, (q[r].y >> 4) & 0x0F0F0F0Fu, (q[r].z >> 4) & 0x0F0F0F0Fu,
-                       (q[r].w >> 4) & 0x0F0F0F0Fu, wb[r]);
-        }
+            const uint32_t qq[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float* xt = c.xs + t * c.xs_stride;
-            const float sxA = c.sx[t * c.sx_stride + eA / 16], sxB = c.sx[t * c.sx_stride + eB / 16];
-#pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                if (!ok[r]) continue;
-                const float sA = dot16(wa[r], xt + pA), sB = dot16(wb[r], xt + pB);
-                acc[r][t] += dA[r] * sA - mA[r] * sxA + dB[r] * sB - mB[r] * sxB;
+            for (int i = 0; i < 4; ++i) {
+                lo[r][i] = qq[i] & 0x0F0F0F0Fu;
+                hi[r][i] = (qq[i] >> 4) & 0x0F0F0F0Fu;
             }
         }
+        half<NT>(lo, eA, dA, mA, c, acc);
+        half<NT>(hi, eA + 32, dB, mB, c, acc);
     }
 };
 
 template <int ROWS> struct Unit<ORC_Q6_K, ROWS> {
     // unit u: superblock u/4, quarter v = u%4: half hh = v/2, l0 = 16*(v%2).
-    // Group g (0..3) holds values 128hh+32g+l0+[0,16) with scale sc[8hh+2g+v%2].
+    // Group g (0..3) holds values 128hh+32g+l0+[0,16) with scale sc[8hh+2g+v%2];
+    // codes are stored +32 (core/gguf_parser.cpp:1124-1154).
     u32x4 qa[ROWS], qb[ROWS], qh[ROWS];
     u32x2 sc[ROWS];
     uint32_t dh[ROWS];
-    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
+    __device__ __forceinline__ void load(const uint8_t* const (&rp)[ROWS], int u) {
         const int b = u >> 2, v = u & 3, hh = v >> 1, l0 = 16 * (v & 1);
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            if (ok[r]) {
-                const uint8_t* blk = rows[r] + (size_t)b * 210;
-                qa[r] = ld16(blk + 64 * hh + l0);
-                qb[r] = ld16(blk + 64 * hh + 32 + l0);
-                qh[r] = ld16(blk + 128 + 32 * hh + l0);
-                sc[r] = ld8(blk + 192 + 8 * hh);
-                dh[r] = ld2(blk + 208);
-            }
+        for (int r = 0; r < ROWS; ++r) {
+            const uint8_t* blk = rp[r] + (size_t)b * 210;
+            qa[r] = ld16(blk + 64 * hh + l0);
+            qb[r] = ld16(blk + 64 * hh + 32 + l0);
+            qh[r] = ld16(blk + 128 + 32 * hh + l0);
+            sc[r] = ld8(blk + 192 + 8 * hh);
+            dh[r] = ld2(blk + 208);
+        }
     }
     template <int NT>
-    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
-                                            float (&acc)[ROWS][NT]) const {
+    __device__ __forceinline__ void compute(int u, const XCtx& c, float (&acc)[ROWS][NT]) const {
         const int b = u >> 2, v = u & 3, hh = v >> 1, odd = v & 1, l0 = 16 * odd;
         const int e0 = b * 256 + 128 * hh + l0 - c.k0;
+        float d[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) d[r] = h2f(dh[r]);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            float w[ROWS][16], sg[ROWS];
+            float sg[ROWS];
+            uint32_t qq[ROWS][4];
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
-                if (!ok[r]) continue;
                 const int si = 2 * g + odd;  // byte index inside the 8 scale bytes of this half
                 const uint32_t sw = si < 4 ? sc[r].x : sc[r].y;
-                sg[r] = h2f(dh[r]) * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
+                sg[r] = d[r] * (float)(int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
                 const uint32_t a4[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w};
                 const uint32_t b4[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
                 const uint32_t h4[4] = {qh[r].x, qh[r].y, qh[r].z, qh[r].w};
-                uint32_t qq[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     uint32_t nib, hb;
@@ -173,390 +205,401 @@ template <int ROWS> struct Unit<ORC_Q6_K, ROWS> {
                     else if (g == 1) { nib = b4[i] & 0x0F0F0F0Fu; hb = (h4[i] << 2) & 0x30303030u; }
                     else if (g == 2) { nib = (a4[i] >> 4) & 0x0F0F0F0Fu; hb = h4[i] & 0x30303030u; }
                     else { nib = (b4[i] >> 4) & 0x0F0F0F0Fu; hb = (h4[i] >> 2) & 0x30303030u; }
-                    qq[i] = nib | hb;
+                    qq[r][i] = nib | hb;
                 }
-                bytes_to_f(qq[0], qq[1], qq[2], qq[3], w[r]);
             }
             const int eg = e0 + 32 * g;
-            const int pg = padx<64>(eg);
+            float S[ROWS][NT];
+            zero(S);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                float w[ROWS][8];
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) to_f8(qq[r][2 * k], qq[r][2 * k + 1], w[r]);
+                dot8(w, c, padx<64>(eg + 8 * k), S);
+            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const float* xt = c.xs + t * c.xs_stride;
                 const float sxg = c.sx[t * c.sx_stride + eg / 16];
 #pragma unroll
-                for (int r = 0; r < ROWS; ++r) {
-                    if (!ok[r]) continue;
-                    // codes are stored +32: Σ (q-32) x = Σ q x - 32 Σ x
-                    acc[r][t] += sg[r] * (dot16(w[r], xt + pg) - 32.f * sxg);
-                }
+                for (int r = 0; r < ROWS; ++r)  // sum (q-32) x = sum q x - 32 sum x
+                    acc[r][t] = __builtin_fmaf(sg[r], __builtin_fmaf(-32.f, sxg, S[r][t]), acc[r][t]);
             }
         }
     }
 };
 
 template <int ROWS> struct Unit<ORC_Q8_0, ROWS> {
-    // unit u: block u (fp16 d + 32 int8 codes): acc += d * Σ q x.
+    // unit u: block u (fp16 d + 32 int8 codes), acc += d * sum(q x)
+    // (core/gguf_parser.cpp:1073-1082). Codes are converted as unsigned q+128
+    // (one xor per 4 codes) and the offset removed with the block sum of x.
     u32x4 q0[ROWS], q1[ROWS];
     uint32_t dh[ROWS];
-    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            if (ok[r]) {
-                const uint8_t* blk = rows[r] + (size_t)u * 34;
-                dh[r] = ld2(blk);
-                q0[r] = ld16(blk + 2);
-                q1[r] = ld16(blk + 18);
-            }
-    }
-    template <int NT>
-    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
-                                            float (&acc)[ROWS][NT]) const {
-        const int e0 = u * 32 - c.k0;
-        const int p0 = padx<32>(e0);
-        float w[ROWS][32], d[ROWS];
+    __device__ __forceinline__ void load(const uint8_t* const (&rp)[ROWS], int u) {
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
-            if (!ok[r]) continue;
-            d[r] = h2f(dh[r]);
-            const uint32_t qq[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+            const uint8_t* blk = rp[r] + (size_t)u * 34;
+            dh[r] = ld2(blk);
+            q0[r] = ld16(blk + 2);
+            q1[r] = ld16(blk + 18);
+        }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const XCtx& c, float (&acc)[ROWS][NT]) const {
+        const int e0 = u * 32 - c.k0;
+        const int p0 = padx<32>(e0);
+        float S[ROWS][NT];
+        zero(S);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+        for (int k = 0; k < 4; ++k) {
+            float w[ROWS][8];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) w[r][4 * i + k] = (float)(int8_t)((qq[i] >> (8 * k)) & 0xFFu);
+            for (int r = 0; r < ROWS; ++r) {
+                const uint32_t qq[8] = {q0[r].x, q0[r].y, q0[r].z, q0[r].w, q1[r].x, q1[r].y, q1[r].z, q1[r].w};
+                to_f8(qq[2 * k] ^ 0x80808080u, qq[2 * k + 1] ^ 0x80808080u, w[r]);
+            }
+            dot8(w, c, p0 + 8 * k, S);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const float* xt = c.xs + t * c.xs_stride + p0;
+            const float sx32 = c.sx[t * c.sx_stride + e0 / 16] + c.sx[t * c.sx_stride + e0 / 16 + 1];
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                if (!ok[r]) continue;
-                acc[r][t] += d[r] * (dot16(w[r], xt) + dot16(w[r] + 16, xt + 16));
-            }
+            for (int r = 0; r < ROWS; ++r)
+                acc[r][t] = __builtin_fmaf(h2f(dh[r]), __builtin_fmaf(-128.f, sx32, S[r][t]), acc[r][t]);
         }
     }
 };
 
 template <int ROWS> struct Unit<ORC_Q4_0, ROWS> {
-    // unit u: block u (fp16 d + 16 bytes: low nibble -> value l, high -> l+16), codes stored +8.
+    // unit u: block u (fp16 d + 16 bytes: low nibble -> value l, high -> l+16),
+    // codes stored +8 (core/gguf_parser.cpp:1058-1070).
     u32x4 q[ROWS];
     uint32_t dh[ROWS];
-    __device__ __forceinline__ void load(const uint8_t* const (&rows)[ROWS], const bool (&ok)[ROWS], int u) {
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            if (ok[r]) {
-                const uint8_t* blk = rows[r] + (size_t)u * 18;
-                dh[r] = ld2(blk);
-                q[r] = ld16(blk + 2);
-            }
-    }
-    template <int NT>
-    __device__ __forceinline__ void compute(int u, const UnitCtx& c, const bool (&ok)[ROWS],
-                                            float (&acc)[ROWS][NT]) const {
-        const int e0 = u * 32 - c.k0;
-        const int p0 = padx<32>(e0);
-        float wl[ROWS][16], wh[ROWS][16], d[ROWS];
+    __device__ __forceinline__ void load(const uint8_t* const (&rp)[ROWS], int u) {
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
-            if (!ok[r]) continue;
-            d[r] = h2f(dh[r]);
-            bytes_to_f(q[r].x & 0x0F0F0F0Fu, q[r].y & 0x0F0F0F0Fu, q[r].z & 0x0F0F0F0Fu, q[r].w & 0x0F0F0F0Fu, wl[r]);
-            bytes_to_f((q[r].x >> 4) & 0x0F0F0F0Fu, (q[r].y >> 4) & 0x0F0F0F0Fu, (q[r].z >> 4) & 0x0F0F0F0Fu,
-                       (q[r].w >> 4) & 0x0F0F0F0Fu, wh[r]);
+            const uint8_t* blk = rp[r] + (size_t)u * 18;
+            dh[r] = ld2(blk);
+            q[r] = ld16(blk + 2);
+        }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const XCtx& c, float (&acc)[ROWS][NT]) const {
+        const int e0 = u * 32 - c.k0;
+        const int p0 = padx<32>(e0);
+        float S[ROWS][NT];
+        zero(S);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float w[ROWS][8];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const uint32_t qq[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+                const uint32_t a = qq[2 * (k & 1)], b = qq[2 * (k & 1) + 1];
+                if (k < 2) to_f8(a & 0x0F0F0F0Fu, b & 0x0F0F0F0Fu, w[r]);
+                else to_f8((a >> 4) & 0x0F0F0F0Fu, (b >> 4) & 0x0F0F0F0Fu, w[r]);
+            }
+            dot8(w, c, p0 + 8 * k, S);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const float* xt = c.xs + t * c.xs_stride + p0;
-            const float sxs = c.sx[t * c.sx_stride + e0 / 16] + c.sx[t * c.sx_stride + e0 / 16 + 1];
+            const float sx32 = c.sx[t * c.sx_stride + e0 / 16] + c.sx[t * c.sx_stride + e0 / 16 + 1];
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                if (!ok[r]) continue;
-                acc[r][t] += d[r] * ((dot16(wl[r], xt) + dot16(wh[r], xt + 16)) - 8.f * sxs);
-            }
+            for (int r = 0; r < ROWS; ++r)
+                acc[r][t] = __builtin_fmaf(h2f(dh[r]), __builtin_fmaf(-8.f, sx32, S[r][t]), acc[r][t]);
         }
     }
 };
 
-// ── the GEMM kernel ──────────────────────────────────────────────────────────
-struct GemmParams {
+// ── the kernel ───────────────────────────────────────────────────────────────
+struct QmvParams {
     const uint8_t* w[3];
     float* y[3];
     const float* bias[3];
     int rows[3];
     int n_seg;
-    int tile_rows_total;  // rows (or gate/up pairs) covered by the grid
-    int n_in;
-    int units_per_row;
+    int n_rows;  // logical rows: sum of the segment rows, or 2 x (gate, up) pairs
+    int units;   // units per row
     uint64_t row_bytes;
     const float* x;
-    int ldx, ldy, n_tok;
+    int ldx, ldy, n_tok, n_in;
     const float* norm_w;
     float eps;
     int epi;
-    int kt_el;     // K tile in elements (a multiple of 1024 when n_in is split)
-    int n_ktiles;
+    int n_groups;
 };
 
-constexpr int kWG = 256;
+constexpr int kQWG = 512, kQWaves = kQWG / 64;
 constexpr int kMaxNT = 5;  // tokens per launch; larger batches are chunked (results unchanged)
 
-template <int QT, int NT, int LPR, int KS, int ROWS>
-__global__ __launch_bounds__(kWG) void k_gemm(GemmParams p) {
-    using T = QTr<QT>;
-    extern __shared__ float smem[];
-    constexpr int G = 64 / LPR;     // groups per wave
-    constexpr int GR = 4 / KS;      // wave rows
-    constexpr int LT = KS * LPR;    // lanes per group
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wsub = wave % KS, wrow = wave / KS;
-    const int li = wsub * LPR + lane % LPR, gl = wrow * G + lane / LPR;
-    const int xs_stride = padx<T::PP>(p.kt_el) + 4;
-    const int sx_stride = p.kt_el / 16;
-    float* xs = smem;
-    float* sx = smem + NT * xs_stride;
-    float* red = sx + NT * sx_stride;  // 4*NT wave partials of sum x^2, then KS partial sums
-    float* part = red + 4 * NT;
-
-    // rows owned by this lane group
-    const uint8_t* rows[ROWS];
-    bool ok[ROWS];
-    float* yout[ROWS];
+template <int ROWS> struct RowSet {
+    const uint8_t* rp[ROWS];
+    float* y[ROWS];
     const float* bias[ROWS];
-    const int base = (blockIdx.x * GR * G + gl) * ROWS;
+    bool ok[ROWS];
+    int jl0;  // first logical row of the slot
+};
+
+// Logical rows of a slot. SwiGLU: the first ROWS/2 are gate rows, the rest the
+// up rows of the same indices. Rows past the end are clamped to row 0 so every
+// load stays in bounds; their results are dropped.
+template <int ROWS, int RG>
+__device__ __forceinline__ void map_rows(const QmvParams& p, int g, int slot, RowSet<ROWS>& R) {
+    const int jl0 = g * RG + slot * ROWS;
+    R.jl0 = jl0;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         int seg = 0, j;
-        if (p.epi == ORC_EPI_SWIGLU) {  // slot 0 = gate row, slot 1 = up row of the same index
-            j = base / ROWS;
-            seg = r;
-            ok[r] = j < p.rows[0];
+        constexpr int H = ROWS >= 2 ? ROWS / 2 : 1;  // SwiGLU launches use an even ROWS
+        if (p.epi == ORC_EPI_SWIGLU) {
+            j = jl0 / 2 + r % H;
+            seg = r / H;
+            R.ok[r] = j < p.rows[0];
         } else {
-            j = base + r;
-            ok[r] = j < p.tile_rows_total;
-            while (seg + 1 < p.n_seg && j >= p.rows[seg]) { j -= p.rows[seg]; ++seg; }
+            j = jl0 + r;
+            R.ok[r] = j < p.n_rows;
+            while (seg + 1 < p.n_seg && j >= p.rows[seg]) {
+                j -= p.rows[seg];
+                ++seg;
+            }
         }
-        rows[r] = p.w[seg] + (size_t)(ok[r] ? j : 0) * p.row_bytes;
-        yout[r] = p.y[seg] + j;
-        bias[r] = p.bias[seg] ? p.bias[seg] + j : nullptr;
+        if (!R.ok[r]) {
+            seg = 0;
+            j = 0;
+        }
+        R.rp[r] = p.w[seg] + (size_t)j * p.row_bytes;
+        R.y[r] = p.y[seg] + j;
+        R.bias[r] = p.bias[seg] ? p.bias[seg] + j : nullptr;
+    }
+}
+
+template <int QT, int NT, int ROWS, int UPL, int WPE>
+__global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) void k_qmv(QmvParams p) {
+    using T = QTr<QT>;
+    constexpr int LPR = T::LPR, G = 64 / LPR, RG = G * ROWS;
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = lane / LPR, li = lane % LPR;
+    const int kn = p.n_in;
+    const int xs_stride = padx<T::PP>(kn) + 4;
+    const int sx_stride = kn / 16;
+    float* xs = smem;
+    float* sx = xs + NT * xs_stride;
+    float* red = sx + NT * sx_stride;  // kQWaves x NT wave sums of x^2
+
+    // A lane owns units li, li + LPR, li + 2 LPR, ... of each of its rows and
+    // walks them in batches of UPL (all loads of a batch in flight at once).
+    // Units past the end are clamped to unit 0 so loads stay in bounds.
+    const int n_batches = (p.units + LPR * UPL - 1) / (LPR * UPL);
+    const int gstride = gridDim.x * kQWaves;
+    int g = blockIdx.x + gridDim.x * wave;
+    Unit<QT, ROWS> U[UPL];
+    RowSet<ROWS> R;
+    if (g < p.n_groups) {  // first batch of the first row group: in flight while x is staged
+        map_rows<ROWS, RG>(p, g, slot, R);
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = li + LPR * i;
+            U[i].load(R.rp, u < p.units ? u : 0);
+        }
     }
 
-    float acc[ROWS][NT], ss[NT];
+    // stage x: all loads first, then LDS stores and per-16 sums (4-lane shuffle)
+    const bool norm = p.norm_w != nullptr;
+    float ss[NT];
+    const int q4 = kn / 4;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         ss[t] = 0.f;
+        const float* src = p.x + (size_t)t * p.ldx;
+        for (int b0 = 0; b0 < q4; b0 += 4 * kQWG) {
+            float4 v[4];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) acc[r][t] = 0.f;
-    }
-    const bool norm = p.norm_w != nullptr;
-    const int units_per_tile = p.kt_el / T::BLK_EL * T::UPB;
-    Unit<QT, ROWS> cur, nxt;
-    for (int kt = 0; kt < p.n_ktiles; ++kt) {
-        const int k0 = kt * p.kt_el;
-        const int kn = min(p.kt_el, p.n_in - k0);
-        const int u1 = min(p.units_per_row, kt * units_per_tile + units_per_tile);
-        int u = kt * units_per_tile + li;
-        if (u < u1) cur.load(rows, ok, u);  // in flight while x is staged
-        if (kt) __syncthreads();            // previous tile fully consumed
-        // stage the tile: all loads first, then LDS stores and per-16 sums (4-lane shuffle)
-        const int q4 = kn / 4;
-        for (int t = 0; t < NT; ++t) {
-            const float* src = p.x + (size_t)t * p.ldx + k0;
-            for (int b0 = 0; b0 < q4; b0 += 4 * kWG) {
-                float4 v[4];
+            for (int m = 0; m < 4; ++m) {
+                const int i = b0 + m * kQWG + tid;
+                v[m] = i < q4 ? *(const float4*)(src + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const int i = b0 + s * kWG + tid;
-                    v[s] = i < q4 ? *(const float4*)(src + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int m = 0; m < 4; ++m) {
+                const int i = b0 + m * kQWG + tid;
+                float4 a = v[m];
+                if (norm && i < q4) {
+                    ss[t] = __builtin_fmaf(a.x, a.x, ss[t]);
+                    ss[t] = __builtin_fmaf(a.y, a.y, ss[t]);
+                    ss[t] = __builtin_fmaf(a.z, a.z, ss[t]);
+                    ss[t] = __builtin_fmaf(a.w, a.w, ss[t]);
+                    const float4 gw = *(const float4*)(p.norm_w + 4 * i);
+                    a.x *= gw.x;
+                    a.y *= gw.y;
+                    a.z *= gw.z;
+                    a.w *= gw.w;
                 }
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const int i = b0 + s * kWG + tid;
-                    float4 a = v[s];
-                    if (norm && i < q4) {
-                        ss[t] = __builtin_fmaf(a.x, a.x, ss[t]);
-                        ss[t] = __builtin_fmaf(a.y, a.y, ss[t]);
-                        ss[t] = __builtin_fmaf(a.z, a.z, ss[t]);
-                        ss[t] = __builtin_fmaf(a.w, a.w, ss[t]);
-                        const float4 g = *(const float4*)(p.norm_w + k0 + 4 * i);
-                        a.x *= g.x; a.y *= g.y; a.z *= g.z; a.w *= g.w;
-                    }
-                    float s16 = (a.x + a.y) + (a.z + a.w);
-                    s16 += __shfl_xor(s16, 1, 64);
-                    s16 += __shfl_xor(s16, 2, 64);
-                    if (i < q4) {
-                        *(float4*)(xs + t * xs_stride + padx<T::PP>(4 * i)) = a;
-                        if ((tid & 3) == 0) sx[t * sx_stride + i / 4] = s16;
-                    }
+                float s16 = (a.x + a.y) + (a.z + a.w);
+                s16 += __shfl_xor(s16, 1, 64);
+                s16 += __shfl_xor(s16, 2, 64);
+                if (i < q4) {
+                    *(float4*)(xs + t * xs_stride + padx<T::PP>(4 * i)) = a;
+                    if ((tid & 3) == 0) sx[t * sx_stride + i / 4] = s16;
                 }
             }
         }
-        __syncthreads();
-        const UnitCtx c{xs, xs_stride, sx, sx_stride, k0};
-        for (; u < u1; u += LT) {
-            const int un = u + LT;
-            if (un < u1) nxt.load(rows, ok, un);
-            cur.template compute<NT>(u, c, ok, acc);
-            cur = nxt;
-        }
     }
-
-    // 1/rms per token: a fixed reduction order for every n_tok (as orc_rmsnorm)
-    float inv[NT];
     if (norm) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             float v = ss[t];
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-            if (lane == 0) red[4 * t + wave] = v;
+            if (lane == 0) red[t * kQWaves + wave] = v;
         }
-        __syncthreads();
+    }
+    __syncthreads();
+    float inv[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-            inv[t] = 1.f / sqrtf(((red[4 * t] + red[4 * t + 1]) + (red[4 * t + 2] + red[4 * t + 3])) / (float)p.n_in +
-                                 p.eps);
+    for (int t = 0; t < NT; ++t) {
+        inv[t] = 1.f;
+        if (norm) {
+            const float* rw = red + t * kQWaves;
+            const float tot = ((rw[0] + rw[1]) + (rw[2] + rw[3])) + ((rw[4] + rw[5]) + (rw[6] + rw[7]));
+            inv[t] = 1.f / sqrtf(tot / (float)p.n_in + p.eps);
+        }
     }
 
-    // reduction: xor butterfly over the LPR lanes of a wave, then the KS waves in fixed order
+    const XCtx c{xs, xs_stride, sx, sx_stride, 0};
+    while (g < p.n_groups) {
+        float acc[ROWS][NT];
+        zero(acc);
+        for (int bt = 0; bt < n_batches; ++bt) {
+            if (bt > 0) {
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
+                for (int i = 0; i < UPL; ++i) {
+                    const int u = li + LPR * (bt * UPL + i);
+                    U[i].load(R.rp, u < p.units ? u : 0);
+                }
+            }
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float v = acc[r][t];
-#pragma unroll
-            for (int o = LPR / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-            acc[r][t] = v;
+            for (int i = 0; i < UPL; ++i) {
+                const int u = li + LPR * (bt * UPL + i);
+                if (u < p.units) U[i].template compute<NT>(u, c, acc);
+            }
         }
-    if (KS > 1) {
-        const int slot = (gl * ROWS) * NT, st = GR * G * ROWS * NT;
-        if (lane % LPR == 0)
-#pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-                for (int t = 0; t < NT; ++t) part[wsub * st + slot + r * NT + t] = acc[r][t];
-        __syncthreads();
-        if (wsub != 0) return;
+        // slot reduction: fixed xor butterfly over the LPR lanes
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const int o = slot + r * NT + t;
-                if (KS == 2) acc[r][t] = part[o] + part[st + o];
-                else acc[r][t] = (part[o] + part[st + o]) + (part[2 * st + o] + part[3 * st + o]);
+                float v = acc[r][t];
+#pragma unroll
+                for (int o = LPR / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+                acc[r][t] = v;
             }
-    }
-    if (lane % LPR != 0) return;
-    if (norm)
+
+        if (p.epi == ORC_EPI_SWIGLU) {
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
+            for (int r = 0; r < ROWS / 2; ++r)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[r][t] *= inv[t];
-    if (p.epi == ORC_EPI_SWIGLU) {
-        if (!ok[0]) return;
+                for (int t = 0; t < NT; ++t)
+                    if (li == (r * NT + t) % LPR && R.ok[r]) {
+                        const float gv = acc[r][t] * inv[t], uv = acc[r + ROWS / 2][t] * inv[t];
+                        R.y[r][(size_t)t * p.ldy] = (gv / (1.f + expf(-gv))) * uv;
+                    }
+        } else {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float g = acc[0][t], u = acc[1][t];
-            yout[0][(size_t)t * p.ldy] = (g / (1.f + expf(-g))) * u;
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    if (li == (r * NT + t) % LPR && R.ok[r]) {
+                        float v = acc[r][t] * inv[t];
+                        if (R.bias[r]) v += *R.bias[r];
+                        float* dst = R.y[r] + (size_t)t * p.ldy;
+                        if (p.epi == ORC_EPI_ACCUM) *dst += v;
+                        else *dst = v;
+                    }
         }
-        return;
-    }
+
+        g += gstride;
+        if (g < p.n_groups) {
+            map_rows<ROWS, RG>(p, g, slot, R);
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        if (!ok[r]) continue;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float v = acc[r][t];
-            if (bias[r]) v += *bias[r];
-            float* dst = yout[r] + (size_t)t * p.ldy;
-            if (p.epi == ORC_EPI_ACCUM) *dst += v;
-            else *dst = v;
+            for (int i = 0; i < UPL; ++i) {
+                const int u = li + LPR * i;
+                U[i].load(R.rp, u < p.units ? u : 0);
+            }
         }
     }
 }
 
-// ── host-side launch ────────────────────────────────────────────────────────
-static int units_per_block(int type) {
-    switch (type) {
-        case ORC_Q8_0: case ORC_Q4_0: return 1;
-        case ORC_Q4_K: return 8;
-        case ORC_Q6_K: return 4;
-        default: return 0;
-    }
+// ── host side ────────────────────────────────────────────────────────────────
+static int g_n_cu = 256;
+static size_t g_lds_max = 64 * 1024;
+
+int gemm_device_init(int device) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && v > 0) g_n_cu = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > 0)
+        g_lds_max = std::min<size_t>((size_t)v, 160 * 1024);
+    return ORC_OK;
 }
+
+void gemm_device_release() {}
+
+static int elems_per_unit(int type) { return type == ORC_Q6_K ? 64 : 32; }
 static int block_elems(int type) { return type == ORC_Q4_K || type == ORC_Q6_K ? 256 : 32; }
+static int pad_period(int type) { return type == ORC_Q4_K || type == ORC_Q6_K ? 64 : 32; }
 
-constexpr int kRows = 2;
-static size_t g_lds_budget = 64 * 1024;  // set from the device limit at first use
-
-static size_t lds_bytes(int type, int nt, int kt, int ks, int lpr) {
-    const int PP = (type == ORC_Q4_K || type == ORC_Q6_K) ? 64 : 32;
-    const size_t part = (size_t)ks * (4 / ks) * (64 / lpr) * kRows * nt;
-    return (size_t)nt * ((kt + 4 * (kt / PP) + 4) + kt / 16) * 4 + (4 * nt + part) * 4;
+static size_t qmv_lds(int type, int nt, int kn) {
+    const int pp = pad_period(type);
+    return ((size_t)nt * ((kn + 4 * (kn / pp) + 4) + kn / 16) + (size_t)kQWaves * nt) * sizeof(float);
 }
 
-struct GemmShape { int lpr, ks; };
-
-// Lanes per row group (LPR) and waves per group (KS) depend on (type, n_in,
-// n_out) only, never on n_tok, so every token sees the same reduction order.
-// Narrow matrices get more lanes per row (more workgroups in flight); the
-// smallest K tile must fit the LDS budget for kMaxNT tokens.
-static GemmShape choose_shape(int type, int units, int n_out) {
-    const int el_per_unit = block_elems(type) / units_per_block(type);
-    int cap = 64;
-    while (cap > 8 && lds_bytes(type, kMaxNT, std::max(1024, cap * el_per_unit), 1, 64) > g_lds_budget) cap /= 2;
-    int lt;
-    if (n_out >= 12288) lt = units >= 96 ? 32 : units >= 32 ? 16 : 8;  // many rows: 1 wave per group
-    else {
-        lt = 8;
-        while (lt * 2 <= units && lt * 2 <= 64) lt *= 2;  // up to one unit per lane
-    }
-    lt = std::min(lt, cap);
-    GemmShape g;
-    if (n_out >= 12288 || lt < 16) { g.ks = 1; g.lpr = std::min(lt, 32); }
-    else if (lt == 16) { g.ks = 2; g.lpr = 8; }
-    else { g.ks = 4; g.lpr = lt / 4; }
-    return g;
+// Tokens per launch: as many as fit the LDS of one workgroup (multi-token
+// launches run one workgroup per CU), at most kMaxNT. Chunking never changes a
+// (token, row) result.
+static int max_tokens(int type, int n_in) {
+    int nt = kMaxNT;
+    while (nt > 1 && qmv_lds(type, nt, n_in) > g_lds_max) --nt;
+    return qmv_lds(type, nt, n_in) <= g_lds_max ? nt : 0;
 }
 
+template <int QT, int NT, int ROWS, int UPL, int WPE>
+static int launch_shape(const QmvParams& p0, hipStream_t s) {
+    QmvParams p = p0;
+    const int rg = (64 / QTr<QT>::LPR) * ROWS;
+    p.n_groups = (p.n_rows + rg - 1) / rg;
+    // persistent grid: WPE/2 workgroups per CU, at most one per row group
+    const int grid = std::max(1, std::min(p.n_groups, (WPE / 2) * g_n_cu));
+    const size_t lds = qmv_lds(QT, NT, p.n_in);
+    if (lds > g_lds_max) return set_error(ORC_E_UNSUPPORTED, "gemm: activations do not fit LDS");
+    hipLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE>), dim3(grid), dim3(kQWG), lds, s, p);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+// Rows per slot, units per lane per batch and waves per SIMD (WPE) per type,
+// token count and matrix height, from a sweep of the C1-C3 matrix shapes on
+// MI355X (none of them changes a (token, row) result). SwiGLU pairs gate and
+// up rows inside a slot and needs an even ROWS.
 template <int QT, int NT>
-static int launch_nt(const GemmParams& p0, GemmShape sh, hipStream_t s) {
-    GemmParams p = p0;
-    const int lpr = sh.lpr, ks = sh.ks;
-    const int tile = (4 / ks) * (64 / lpr) * kRows;
-    const int n_items = p.epi == ORC_EPI_SWIGLU ? p.rows[0] * kRows : p.tile_rows_total;
-    const int grid = (n_items + tile - 1) / tile;
-    // K tile: the whole row when it fits; otherwise a multiple of lcm(1024, KS*LPR units)
-    // so that every lane owns the same units and every thread the same x elements.
-    const int be = QTr<QT>::BLK_EL, upb = QTr<QT>::UPB;
-    const int type = QT;
-    int kt = p.n_in;
-    if (lds_bytes(type, NT, kt, ks, lpr) > g_lds_budget) {
-        const int step = std::max(1024, ks * lpr / upb * be);
-        kt = step;
-        while (kt + step < p.n_in && lds_bytes(type, NT, kt + step, ks, lpr) <= g_lds_budget) kt += step;
+static int launch_nt(const QmvParams& p, hipStream_t s) {
+    const bool pair = p.epi == ORC_EPI_SWIGLU;
+    const bool tall = p.n_rows >= 32768;  // LM heads
+    if constexpr (NT == 1) {
+        if ((QT == ORC_Q6_K && tall) || pair) return launch_shape<QT, NT, 2, 1, 4>(p, s);
+        return launch_shape<QT, NT, 1, 3, 4>(p, s);
+    } else {
+        if (pair || tall) return launch_shape<QT, NT, 2, 1, 2>(p, s);
+        return launch_shape<QT, NT, 1, 1, 2>(p, s);
     }
-    p.kt_el = kt;
-    p.n_ktiles = (p.n_in + kt - 1) / kt;
-    const size_t lds = lds_bytes(type, NT, kt, ks, lpr);
-    if (lds > g_lds_budget) return set_error(ORC_E_UNSUPPORTED, "gemm: K tile does not fit LDS");
-#define L(LPR_, KS_)                                                                              \
-    if (lpr == LPR_ && ks == KS_) {                                                               \
-        hipLaunchKernelGGL((k_gemm<QT, NT, LPR_, KS_, kRows>), dim3(grid), dim3(kWG), lds, s, p); \
-        ORC_LAUNCH_CHECK();                                                                       \
-        return ORC_OK;                                                                            \
-    }
-    L(8, 1) L(16, 1) L(32, 1) L(8, 2) L(8, 4) L(16, 4)
-#undef L
-    return set_error(ORC_E_INVALID, "gemm: no kernel for this shape");
 }
 
 template <int QT>
-static int launch_type(const GemmParams& p, GemmShape sh, hipStream_t s) {
+static int launch_type(const QmvParams& p, hipStream_t s) {
     switch (p.n_tok) {
-        case 1: return launch_nt<QT, 1>(p, sh, s);
-        case 2: return launch_nt<QT, 2>(p, sh, s);
-        case 3: return launch_nt<QT, 3>(p, sh, s);
-        case 4: return launch_nt<QT, 4>(p, sh, s);
-        case 5: return launch_nt<QT, 5>(p, sh, s);
+        case 1: return launch_nt<QT, 1>(p, s);
+        case 2: return launch_nt<QT, 2>(p, s);
+        case 3: return launch_nt<QT, 3>(p, s);
+        case 4: return launch_nt<QT, 4>(p, s);
+        case 5: return launch_nt<QT, 5>(p, s);
         default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..5");
     }
 }
@@ -583,9 +626,9 @@ static hipEvent_t prof_event() {
 
 // Algorithmic HBM bytes of one launch: weight blocks + activations read +
 // outputs written (read too when accumulating) + norm weights and biases.
-static double gemm_bytes(const GemmParams& p, int nt) {
-    const int n_w = p.epi == ORC_EPI_SWIGLU ? 2 * p.rows[0] : p.tile_rows_total;
-    const int n_y = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.tile_rows_total;
+static double gemm_bytes(const QmvParams& p, int nt) {
+    const int n_w = p.epi == ORC_EPI_SWIGLU ? 2 * p.rows[0] : p.n_rows;
+    const int n_y = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.n_rows;
     double b = (double)p.row_bytes * n_w + 4.0 * nt * p.n_in + 4.0 * nt * n_y * (p.epi == ORC_EPI_ACCUM ? 2 : 1);
     if (p.norm_w) b += 4.0 * p.n_in;
     for (int i = 0; i < p.n_seg; ++i)
@@ -593,23 +636,15 @@ static double gemm_bytes(const GemmParams& p, int nt) {
     return b;
 }
 
-static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
-    static bool lds_init = false;
-    if (!lds_init) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && v > 0)
-            g_lds_budget = std::min<size_t>((size_t)v, 160 * 1024);
-        lds_init = true;
-    }
-    p.units_per_row = p.n_in / block_elems(type) * units_per_block(type);
-    const int n_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.tile_rows_total;
-    const GemmShape sh = choose_shape(type, p.units_per_row, n_out);
-    // tokens are processed in chunks of at most kMaxNT; chunking never changes a
+static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
+    p.units = p.n_in / elems_per_unit(type);
+    const int ntmax = max_tokens(type, p.n_in);
+    if (ntmax < 1) return set_error(ORC_E_UNSUPPORTED, "gemm: n_in too large for the activations to fit LDS");
+    // tokens are processed in chunks of at most ntmax; chunking never changes a
     // (token,row) result because the reduction order is independent of n_tok
-    for (int t0 = 0; t0 < p.n_tok; t0 += kMaxNT) {
-        GemmParams q = p;
-        q.n_tok = std::min(kMaxNT, p.n_tok - t0);
+    for (int t0 = 0; t0 < p.n_tok; t0 += ntmax) {
+        QmvParams q = p;
+        q.n_tok = std::min(ntmax, p.n_tok - t0);
         q.x = p.x + (size_t)t0 * p.ldx;
         for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
         ProfRec rec{};
@@ -626,10 +661,10 @@ static int gemm_dispatch(GemmParams p, int type, hipStream_t s) {
         }
         int rc;
         switch (type) {
-            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, sh, s); break;
-            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, sh, s); break;
-            case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, sh, s); break;
-            case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, sh, s); break;
+            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, s); break;
+            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, s); break;
+            case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s); break;
+            case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, s); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
         }
         if (prof && hipEventRecord(rec.b, s) == hipSuccess) g_prof.push_back(rec);
@@ -697,12 +732,12 @@ extern "C" int orc_gemm(int type, const void* d_w, int n_tok, int n_out, int n_i
                         float* d_y, int ldy, orc_stream_t stream) {
     if (int rc = check_gemm_shape(type, n_tok, n_in, d_x, ldx, ldy, d_w)) return rc;
     if (n_out <= 0 || !d_y || (n_tok > 1 && ldy < n_out)) return set_error(ORC_E_INVALID, "gemm: bad output");
-    GemmParams p{};
+    QmvParams p{};
     p.w[0] = (const uint8_t*)d_w;
     p.y[0] = d_y;
     p.rows[0] = n_out;
     p.n_seg = 1;
-    p.tile_rows_total = n_out;
+    p.n_rows = n_out;
     p.n_in = n_in;
     p.row_bytes = (uint64_t)orc_row_bytes(type, n_in);
     p.x = d_x;
@@ -721,7 +756,7 @@ extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_t
         return set_error(ORC_E_INVALID, "gemm_fused: SwiGLU needs gate and up segments of equal rows");
     if (epilogue < ORC_EPI_STORE || epilogue > ORC_EPI_SWIGLU) return set_error(ORC_E_INVALID, "bad epilogue");
     if (d_norm_w && ((uintptr_t)d_norm_w & 15)) return set_error(ORC_E_INVALID, "norm weights must be 16-byte aligned");
-    GemmParams p{};
+    QmvParams p{};
     int total = 0;
     for (int i = 0; i < n_segs; ++i) {
         if (!segs[i].d_w || !segs[i].d_y || segs[i].n_out <= 0) return set_error(ORC_E_INVALID, "gemm_fused: bad segment");
@@ -732,7 +767,7 @@ extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_t
         total += segs[i].n_out;
     }
     p.n_seg = n_segs;
-    p.tile_rows_total = total;
+    p.n_rows = epilogue == ORC_EPI_SWIGLU ? 2 * segs[0].n_out : total;
     p.n_in = n_in;
     p.row_bytes = (uint64_t)orc_row_bytes(type, n_in);
     p.x = d_x;
@@ -744,4 +779,3 @@ extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_t
     p.epi = epilogue;
     return gemm_dispatch(p, type, resolve_stream(stream));
 }
-

@@ -12,6 +12,9 @@ namespace orc {
 int set_error(int code, const std::string& msg);
 hipStream_t resolve_stream(orc_stream_t s);
 bool initialized();
+// Per-device GEMM state (CU count, LDS limit, split-K workspace), set up by orc_init.
+int gemm_device_init(int device);
+void gemm_device_release();
 
 #define ORC_HIP_CHECK(expr)                                                                       \
     do {                                                                                          \

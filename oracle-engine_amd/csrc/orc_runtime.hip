@@ -49,6 +49,7 @@ extern "C" int orc_init(int device) {
     ORC_HIP_CHECK(hipSetDevice(device));
     if (g_stream) (void)hipStreamDestroy(g_stream);
     ORC_HIP_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    if (int rc = gemm_device_init(device)) return rc;
     g_device = device;
     return ORC_OK;
 }
@@ -60,6 +61,7 @@ extern "C" int orc_shutdown(void) {
         (void)hipStreamDestroy(g_stream);
     }
     g_stream = nullptr;
+    gemm_device_release();
     g_device = -1;
     return ORC_OK;
 }
