@@ -39,6 +39,12 @@ int orch_greedy(orch_model* m, const int32_t* prompt, int n_prompt, int n_gen, i
  * rounds. Returns tokens written. */
 int orch_spec_greedy(orch_model* tgt, orch_model* dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                      int32_t* out, int64_t* stats, int prefill);
+/* Decode loops replay captured HIP graphs (on, the default) or launch every
+ * kernel from the host (off); the token streams are identical. Drops the
+ * graphs captured so far (the next loop captures them again, e.g. with
+ * kernel timing events once orc_prof_enable is on). Returns the previous
+ * setting. No reference counterpart. */
+int orch_set_graphs(int on);
 /* Quantized weight bytes one decode step streams (layers + LM head if logits). */
 double orch_weight_bytes(const orch_model* m, int logits);
 /* Block the host until all device work of the library has finished. */

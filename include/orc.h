@@ -128,11 +128,16 @@ int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_tok, int n_i
 
 /* Live kernel timing (no reference counterpart; the reference times whole
  * loops with std::chrono, bench_engine.cpp:225-244). While enabled, every
- * GEMM launch outside graph capture is bracketed by HIP events recorded on
- * the launch stream, and its algorithmic HBM bytes (weight blocks + x + y)
- * are recorded. orc_prof_read sums the launches of one kernel family
- * (type < 0: all types; n_tok 0: all token counts) and waits for them. */
+ * GEMM launch made outside stream capture carries a start and a stop HIP
+ * event (hipExtLaunchKernelGGL: both take the timestamps of the kernel's own
+ * dispatch on its stream) and its algorithmic HBM bytes (weight blocks + x +
+ * y) are noted. Once the work has run, orc_prof_accumulate adds every launch's
+ * elapsed time to its record; orc_prof_read sums the records of one kernel
+ * family (type < 0: all types; n_tok 0: all token counts). orc_prof_enable:
+ * 1 = on and clear all records, 2 = on keeping them, 0 = off (accumulate is
+ * then a no-op); returns the previous state. */
 int orc_prof_enable(int on);
+int orc_prof_accumulate(void);
 int orc_prof_read(int type, int n_tok, int64_t* launches, double* total_ms, double* total_bytes);
 
 /* ── elementwise / attention ─────────────────────────────────────────────── */
@@ -147,6 +152,15 @@ int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_r
  * bit-identical. KV cache layout: [n_kv][ctx][hd] fp32 per layer. */
 int orc_rope_kv_store(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim, int start_pos,
                       const float* d_rope, float* d_kcache, float* d_vcache, int ctx, orc_stream_t stream);
+/* As orc_rope_kv_store with the first position read on the device:
+ * start_pos = *d_pos + pos_off (d_pos null: start_pos = pos_off). A graph
+ * captured with a device position replays at whatever position the device
+ * holds; tokens whose position falls outside [0, ctx) are skipped. No
+ * reference counterpart (the reference passes pos by value,
+ * core/model.cpp:340); used for captured decode / verify rounds. */
+int orc_rope_kv_store_at(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
+                         const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kcache, float* d_vcache,
+                         int ctx, orc_stream_t stream);
 /* Causal GQA attention for n_tok query tokens at positions start_pos..,
  * each attending to KV positions [0, start_pos + t] (model.cpp:410-435,
  * 604-626). q rows have stride ldq, output rows stride ldo. Scale
@@ -156,6 +170,25 @@ size_t orc_attn_workspace(int n_tok, int n_heads, int head_dim, int max_pos);
 int orc_attn_gqa(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv, int head_dim, int start_pos,
                  const float* d_kcache, const float* d_vcache, int ctx, float* d_out, int ldo, void* d_work,
                  orc_stream_t stream);
+/* As orc_attn_gqa with start_pos = *d_pos + pos_off read on the device (d_pos
+ * null: start_pos = pos_off). With a device position the grid covers the whole
+ * context, so the launch is valid for any position a replayed graph reaches;
+ * d_work must hold orc_attn_workspace(n_tok, n_heads, head_dim, ctx) bytes. */
+int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv, int head_dim, const int32_t* d_pos,
+                    int pos_off, const float* d_kcache, const float* d_vcache, int ctx, float* d_out, int ldo,
+                    void* d_work, orc_stream_t stream);
+
+/* RoPE + KV store + causal GQA attention in one launch (the attention block
+ * of Model::forward / forward_prefill, core/model.cpp:401-435, 595-626):
+ * for n_tok QKV rows (layout as orc_rope_kv_store, left unmodified) at
+ * positions start_pos.. (start_pos = *d_pos + pos_off, or pos_off when d_pos
+ * is null), rotates q and k, stores k and v of every token in the cache and
+ * writes each token's attention output (rows of ldo floats). Results equal
+ * orc_rope_kv_store followed by orc_attn_gqa up to fp32 rounding. At most 8
+ * query heads per kv head; head_dim 64 or 128; 16-byte aligned rows. */
+int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
+                      const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kcache, float* d_vcache,
+                      int ctx, float* d_out, int ldo, orc_stream_t stream);
 
 /* ── argmax, sampling, acceptance ────────────────────────────────────────── */
 /* out[r] = first index of the maximum of row r (ops::argmax ops.cpp:490-497,
@@ -169,6 +202,17 @@ int orc_argmax(const float* d_x, int n_rows, int n, int ld, int32_t* d_out, void
  * next token (first mismatch, or the bonus tgt[n_draft] when all match). */
 int orc_spec_accept_greedy(const int32_t* d_tgt_ids, const int32_t* d_draft_ids, int n_draft, int32_t* d_out,
                            orc_stream_t stream);
+/* Device-resident round state for captured spec rounds: as
+ * orc_spec_accept_greedy, and also out[2 .. 2+a] = the emitted ids
+ * tgt[0..a], *d_pos += a + 1 and *d_next = the next input token (d_out holds
+ * n_draft + 3 ints). The position advance is bench_engine.cpp:352-355. */
+int orc_spec_accept_greedy_at(const int32_t* d_tgt_ids, const int32_t* d_draft_ids, int n_draft, int32_t* d_out,
+                              int32_t* d_pos, int32_t* d_next, orc_stream_t stream);
+/* Tail of a captured greedy decode step (bench_engine.cpp:233-240 keeps the
+ * chain on the host): d_tok[1] (the step's argmax) is appended at
+ * d_hist[*d_count] and copied to d_tok[0] (the next input); *d_pos and
+ * *d_count advance by one. The caller sizes d_hist for every step it replays. */
+int orc_decode_advance(int32_t* d_tok, int32_t* d_hist, int32_t* d_pos, int32_t* d_count, orc_stream_t stream);
 
 #ifdef __cplusplus
 }

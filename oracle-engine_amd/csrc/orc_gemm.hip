@@ -30,6 +30,8 @@
 //    (k+1)-token verify pass equals k+1 decode GEMVs.
 #include "orc_internal.hpp"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <vector>
 
@@ -561,8 +563,13 @@ static int max_tokens(int type, int n_in) {
     return qmv_lds(type, nt, n_in) <= g_lds_max ? nt : 0;
 }
 
+// Kernel timing of one launch: start / stop events taken from its dispatch.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
 template <int QT, int NT, int ROWS, int UPL, int WPE>
-static int launch_shape(const QmvParams& p0, hipStream_t s) {
+static int launch_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& ev) {
     QmvParams p = p0;
     const int rg = (64 / QTr<QT>::LPR) * ROWS;
     p.n_groups = (p.n_rows + rg - 1) / rg;
@@ -570,7 +577,10 @@ static int launch_shape(const QmvParams& p0, hipStream_t s) {
     const int grid = std::max(1, std::min(p.n_groups, (WPE / 2) * g_n_cu));
     const size_t lds = qmv_lds(QT, NT, p.n_in);
     if (lds > g_lds_max) return set_error(ORC_E_UNSUPPORTED, "gemm: activations do not fit LDS");
-    hipLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE>), dim3(grid), dim3(kQWG), lds, s, p);
+    if (ev.start)
+        hipExtLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE>), dim3(grid), dim3(kQWG), lds, s, ev.start, ev.stop, 0, p);
+    else
+        hipLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE>), dim3(grid), dim3(kQWG), lds, s, p);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }
@@ -580,26 +590,26 @@ static int launch_shape(const QmvParams& p0, hipStream_t s) {
 // MI355X (none of them changes a (token, row) result). SwiGLU pairs gate and
 // up rows inside a slot and needs an even ROWS.
 template <int QT, int NT>
-static int launch_nt(const QmvParams& p, hipStream_t s) {
+static int launch_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     const bool pair = p.epi == ORC_EPI_SWIGLU;
     const bool tall = p.n_rows >= 32768;  // LM heads
     if constexpr (NT == 1) {
-        if ((QT == ORC_Q6_K && tall) || pair) return launch_shape<QT, NT, 2, 1, 4>(p, s);
-        return launch_shape<QT, NT, 1, 3, 4>(p, s);
+        if ((QT == ORC_Q6_K && tall) || pair) return launch_shape<QT, NT, 2, 1, 4>(p, s, ev);
+        return launch_shape<QT, NT, 1, 3, 4>(p, s, ev);
     } else {
-        if (pair || tall) return launch_shape<QT, NT, 2, 1, 2>(p, s);
-        return launch_shape<QT, NT, 1, 1, 2>(p, s);
+        if (pair || tall) return launch_shape<QT, NT, 2, 1, 2>(p, s, ev);
+        return launch_shape<QT, NT, 1, 1, 2>(p, s, ev);
     }
 }
 
 template <int QT>
-static int launch_type(const QmvParams& p, hipStream_t s) {
+static int launch_type(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     switch (p.n_tok) {
-        case 1: return launch_nt<QT, 1>(p, s);
-        case 2: return launch_nt<QT, 2>(p, s);
-        case 3: return launch_nt<QT, 3>(p, s);
-        case 4: return launch_nt<QT, 4>(p, s);
-        case 5: return launch_nt<QT, 5>(p, s);
+        case 1: return launch_nt<QT, 1>(p, s, ev);
+        case 2: return launch_nt<QT, 2>(p, s, ev);
+        case 3: return launch_nt<QT, 3>(p, s, ev);
+        case 4: return launch_nt<QT, 4>(p, s, ev);
+        case 5: return launch_nt<QT, 5>(p, s, ev);
         default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..5");
     }
 }
@@ -609,6 +619,8 @@ struct ProfRec {
     hipEvent_t a, b;
     int type, nt;
     double bytes;
+    double sum_ms = 0;  // accumulated over orc_prof_accumulate calls
+    int64_t n = 0;
 };
 static bool g_prof_on = false;
 static std::vector<ProfRec> g_prof;
@@ -648,12 +660,13 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
         q.x = p.x + (size_t)t0 * p.ldx;
         for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
         ProfRec rec{};
-        bool prof = false;
-        if (g_prof_on) {
+        LaunchEvents ev;
+        if (g_prof_on) {  // host launches only: a captured launch carries no events
             hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
             (void)hipStreamIsCapturing(s, &cs);
             if (cs == hipStreamCaptureStatusNone && (rec.a = prof_event()) && (rec.b = prof_event())) {
-                prof = hipEventRecord(rec.a, s) == hipSuccess;
+                ev.start = rec.a;
+                ev.stop = rec.b;
                 rec.type = type;
                 rec.nt = q.n_tok;
                 rec.bytes = gemm_bytes(q, q.n_tok);
@@ -661,14 +674,14 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
         }
         int rc;
         switch (type) {
-            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, s); break;
-            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, s); break;
-            case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s); break;
-            case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, s); break;
+            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, s, ev); break;
+            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, s, ev); break;
+            case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s, ev); break;
+            case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, s, ev); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
         }
-        if (prof && hipEventRecord(rec.b, s) == hipSuccess) g_prof.push_back(rec);
         if (rc) return rc;
+        if (ev.start) g_prof.push_back(rec);
     }
     return ORC_OK;
 }
@@ -678,10 +691,23 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
 using namespace orc;
 
 extern "C" int orc_prof_enable(int on) {
+    const int prev = g_prof_on ? 1 : 0;
     g_prof_on = on != 0;
-    if (on) {
+    if (on == 1) {
         g_prof.clear();
         g_evnext = 0;
+    }
+    return prev;
+}
+
+extern "C" int orc_prof_accumulate(void) {
+    if (!g_prof_on) return ORC_OK;
+    for (ProfRec& r : g_prof) {
+        ORC_HIP_CHECK(hipEventSynchronize(r.b));
+        float e = 0.f;
+        ORC_HIP_CHECK(hipEventElapsedTime(&e, r.a, r.b));
+        r.sum_ms += e;
+        ++r.n;
     }
     return ORC_OK;
 }
@@ -691,12 +717,9 @@ extern "C" int orc_prof_read(int type, int n_tok, int64_t* launches, double* tot
     double ms = 0, by = 0;
     for (const ProfRec& r : g_prof) {
         if ((type >= 0 && r.type != type) || (n_tok > 0 && r.nt != n_tok)) continue;
-        ORC_HIP_CHECK(hipEventSynchronize(r.b));
-        float e = 0.f;
-        ORC_HIP_CHECK(hipEventElapsedTime(&e, r.a, r.b));
-        ++n;
-        ms += e;
-        by += r.bytes;
+        n += r.n;
+        ms += r.sum_ms;
+        by += r.bytes * (double)r.n;
     }
     if (launches) *launches = n;
     if (total_ms) *total_ms = ms;

@@ -40,9 +40,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* x, con
 
 // ── RoPE on q,k + KV store. One workgroup per token. ─────────────────────────
 // rope table: [pos][half] of (cos, sin); KV cache per layer: [n_kv][ctx][hd].
-__global__ __launch_bounds__(256) void k_rope_kv(float* qkv, int ldqkv, int n_heads, int n_kv, int hd, int start_pos,
-                                                 const float2* rope, float* kc, float* vc, int ctx) {
-    const int t = blockIdx.x, pos = start_pos + t, half = hd / 2;
+// The first position is *d_pos + pos_off (d_pos may be null): with a device
+// position a captured graph stays valid while decoding advances.
+__device__ __forceinline__ int start_position(const int* d_pos, int pos_off) { return (d_pos ? *d_pos : 0) + pos_off; }
+
+__global__ __launch_bounds__(256) void k_rope_kv(float* qkv, int ldqkv, int n_heads, int n_kv, int hd,
+                                                 const int* d_pos, int pos_off, const float2* rope, float* kc,
+                                                 float* vc, int ctx) {
+    const int t = blockIdx.x, pos = start_position(d_pos, pos_off) + t, half = hd / 2;
+    if (pos < 0 || pos >= ctx) return;  // outside the cache: nothing to rotate or store
     float* row = qkv + (size_t)t * ldqkv;
     const float2* cs = rope + (size_t)pos * half;
     const int nrot = (n_heads + n_kv) * half;
@@ -74,8 +80,8 @@ constexpr int kCH = 32, kRB = 16;
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_partial(const float* q, int ldq, int n_tok, int n_heads, int n_kv,
-                                                      int start_pos, const float* kc, const float* vc, int ctx,
-                                                      float* work) {
+                                                      const int* d_pos, int pos_off, const float* kc, const float* vc,
+                                                      int ctx, float* work) {
     __shared__ float Ks[kCH][HD + 4];
     __shared__ float Vs[kCH][HD];
     __shared__ float Qs[kRB][HD];
@@ -83,7 +89,9 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* q, int ldq, i
     const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int gqa = n_heads / n_kv;
     const int p0 = c * kCH;
-    const int pmax = start_pos + n_tok - 1;
+    const int start_pos = start_position(d_pos, pos_off);
+    const int pmax = min(start_pos + n_tok, ctx) - 1;
+    if (p0 > pmax) return;  // chunk past the last position (grids sized for the whole context)
     const int np = min(kCH, pmax + 1 - p0);
     const float scale = 1.f / sqrtf((float)HD);
     const float* kg = kc + ((size_t)g * ctx + p0) * HD;
@@ -164,10 +172,11 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* q, int ldq, i
 }
 
 template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, int start_pos, const float* work,
-                                                     float* out, int ldo) {
+__global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, const int* d_pos, int pos_off, int ctx,
+                                                     const float* work, float* out, int ldo) {
     const int h = blockIdx.x, t = blockIdx.y, k = threadIdx.x;
-    const int nch = (start_pos + t) / kCH + 1;  // chunks that hold positions <= start_pos + t
+    const int last = min(start_position(d_pos, pos_off) + t, ctx - 1);
+    const int nch = last / kCH + 1;  // chunks that hold positions <= start_pos + t
     float M = -INFINITY;
     for (int c = 0; c < nch; ++c) {
         const float* w = work + (((size_t)c * n_heads + h) * n_tok + t) * (HD + 2);
@@ -183,6 +192,224 @@ __global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, int
         O = __builtin_fmaf(w[k], f, O);
     }
     out[(size_t)t * ldo + h * HD + k] = O / L;
+}
+
+// ── fused RoPE + KV store + causal GQA attention (one launch per layer) ──────
+// Grid (kv head g, token t): a workgroup serves the gqa query heads of kv head
+// g for token t at position pt = start + t. It rotates its q rows and its own
+// K row (ops::rope rotate-half pairs, core/ops.cpp:440-485), stores K/V of
+// position pt in the cache (each new position is written by exactly one
+// workgroup), and attends to positions 0..pt (core/model.cpp:410-435,
+// 604-626): positions before `start` come from the cache, the new ones
+// (start..pt) straight from the QKV rows, rotated on the fly, so no
+// workgroup reads a cache row another one is writing. Positions are walked in
+// blocks of kPB with an online softmax: scores in LDS (16 lanes per position,
+// coalesced 128-bit row reads), block max / sum per row, then P.V with
+// 16-byte columns per lane and position subsets reduced at the end.
+constexpr int kAT = 512, kPB = 512, kRMax = 8;
+
+template <int HD>
+__device__ __forceinline__ void rope_pair(const float* v, const float2* cs, int d, float& out) {
+    // rotated value of element d of a head vector v with (cos, sin) table cs
+    constexpr int half = HD / 2;
+    if (d < half) {
+        const float2 c = cs[d];
+        out = v[d] * c.x - v[d + half] * c.y;
+    } else {
+        const float2 c = cs[d - half];
+        out = v[d - half] * c.y + v[d] * c.x;
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv, int n_heads, int n_kv,
+                                                    const int* d_pos, int pos_off, const float2* rope, float* kc,
+                                                    float* vc, int ctx, float* out, int ldo) {
+    constexpr int DPT = HD / 16;            // dims per lane in the score phase (16 lanes per position)
+    constexpr int NC = HD / 4;              // float4 columns in the P.V phase
+    constexpr int NPS = kAT / NC;           // position subsets in the P.V phase
+    constexpr int half = HD / 2;
+    __shared__ float Qs[kRMax][HD];
+    __shared__ float S[kRMax][kPB];
+    __shared__ float st_m[kRMax], st_l[kRMax], st_a[kRMax];
+    __shared__ float red[NPS][HD];
+    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int R = n_heads / n_kv;
+    const int start = start_position(d_pos, pos_off);
+    const int pt = start + t;
+    if (pt < 0 || pt >= ctx) return;  // outside the cache (graph replays past the end): nothing to do
+    const int P = pt + 1;
+    const float scale = 1.f / sqrtf((float)HD);
+    const float* qrow = qkv + (size_t)t * ldqkv;
+    const float2* cs_t = rope + (size_t)pt * half;
+
+    // rotated q rows of the group, K/V of position pt into the cache
+    for (int i = tid; i < R * HD; i += kAT) {
+        const int r = i / HD, d = i - r * HD;
+        float v;
+        rope_pair<HD>(qrow + (g * R + r) * HD, cs_t, d, v);
+        Qs[r][d] = v;
+    }
+    if (tid < HD) {
+        const float* kr = qrow + (n_heads + g) * HD;
+        float v;
+        rope_pair<HD>(kr, cs_t, tid, v);
+        const size_t o = ((size_t)g * ctx + pt) * HD + tid;
+        kc[o] = v;
+        vc[o] = qrow[(n_heads + n_kv + g) * HD + tid];
+    }
+    if (tid < kRMax) {
+        st_m[tid] = -INFINITY;
+        st_l[tid] = 0.f;
+    }
+    float4 acc[kRMax];
+#pragma unroll
+    for (int r = 0; r < kRMax; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int lane16 = tid & 15, pgrp = tid >> 4;  // score phase: 32 positions per pass
+    const int col = tid % NC, ps = tid / NC;       // P.V phase
+    const float* kg = kc + (size_t)g * ctx * HD;
+    const float* vg = vc + (size_t)g * ctx * HD;
+    __syncthreads();
+
+    for (int b0 = 0; b0 < P; b0 += kPB) {
+        const int nb = min(kPB, P - b0);
+        // scores S[r][p] = (q_r . k_p) * scale; a lane loads its slice of SB
+        // rows before any arithmetic, so SB row loads are in flight at once
+        constexpr int SB = 4;
+        const int d0 = lane16 * DPT;
+        for (int pp0 = pgrp; pp0 < nb; pp0 += SB * (kAT / 16)) {
+            float kv[SB][DPT];
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                const int pp = pp0 + j * (kAT / 16), p = b0 + pp;
+                if (pp >= nb) {
+#pragma unroll
+                    for (int i = 0; i < DPT; ++i) kv[j][i] = 0.f;
+                } else if (p < start) {
+                    const float4* src = (const float4*)(kg + (size_t)p * HD + d0);
+#pragma unroll
+                    for (int i = 0; i < DPT / 4; ++i) {
+                        const float4 v = src[i];
+                        kv[j][4 * i] = v.x;
+                        kv[j][4 * i + 1] = v.y;
+                        kv[j][4 * i + 2] = v.z;
+                        kv[j][4 * i + 3] = v.w;
+                    }
+                } else {  // a new position: K from the QKV row of its token, rotated here
+                    const float* kr = qkv + (size_t)(p - start) * ldqkv + (n_heads + g) * HD;
+                    const float2* cs = rope + (size_t)p * half;
+#pragma unroll
+                    for (int i = 0; i < DPT; ++i) rope_pair<HD>(kr, cs, d0 + i, kv[j][i]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                const int pp = pp0 + j * (kAT / 16);
+                float dr[kRMax];
+#pragma unroll
+                for (int r = 0; r < kRMax; ++r) {
+                    float sum = 0.f;
+                    if (r < R) {
+#pragma unroll
+                        for (int i = 0; i < DPT; ++i) sum = __builtin_fmaf(Qs[r][d0 + i], kv[j][i], sum);
+                    }
+                    dr[r] = sum;
+                }
+#pragma unroll
+                for (int r = 0; r < kRMax; ++r) {
+#pragma unroll
+                    for (int o = 8; o >= 1; o >>= 1) dr[r] += __shfl_xor(dr[r], o, 16);
+                }
+                if (pp < nb && lane16 < R) {
+                    float sum = dr[0];
+#pragma unroll
+                    for (int r = 1; r < kRMax; ++r)
+                        if (lane16 == r) sum = dr[r];
+                    S[lane16][pp] = sum * scale;
+                }
+            }
+        }
+        __syncthreads();
+        // online softmax: wave r owns row r (max, exp, sum over the block)
+        {
+            const int w = tid >> 6, ln = tid & 63;
+            for (int r = w; r < R; r += kAT / 64) {
+                float m = -INFINITY;
+                for (int p = ln; p < nb; p += 64) m = fmaxf(m, S[r][p]);
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+                const float m_old = st_m[r];
+                const float m_new = fmaxf(m_old, m);
+                float l = 0.f;
+                for (int p = ln; p < nb; p += 64) {
+                    const float e = expf(S[r][p] - m_new);
+                    S[r][p] = e;
+                    l += e;
+                }
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+                if (ln == 0) {
+                    const float a = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
+                    st_a[r] = a;
+                    st_l[r] = st_l[r] * a + l;
+                    st_m[r] = m_new;
+                }
+            }
+        }
+        __syncthreads();
+        // O_r = a_r O_r + sum_p P[r][p] V[p]
+#pragma unroll
+        for (int r = 0; r < kRMax; ++r) {
+            if (r < R) {
+                const float a = st_a[r];
+                acc[r].x *= a;
+                acc[r].y *= a;
+                acc[r].z *= a;
+                acc[r].w *= a;
+            }
+        }
+        constexpr int VB = 8;  // V rows in flight per lane
+        for (int pp0 = ps; pp0 < nb; pp0 += VB * NPS) {
+            float4 v[VB];
+#pragma unroll
+            for (int j = 0; j < VB; ++j) {
+                const int pp = pp0 + j * NPS, p = b0 + pp;
+                if (pp >= nb) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                else if (p < start) v[j] = *(const float4*)(vg + (size_t)p * HD + 4 * col);
+                else
+                    v[j] = *(const float4*)(qkv + (size_t)(p - start) * ldqkv + (n_heads + n_kv + g) * HD + 4 * col);
+            }
+#pragma unroll
+            for (int j = 0; j < VB; ++j) {
+                const int pp = pp0 + j * NPS;
+                if (pp >= nb) break;
+#pragma unroll
+                for (int r = 0; r < kRMax; ++r) {
+                    if (r < R) {
+                        const float w = S[r][pp];
+                        acc[r].x = __builtin_fmaf(w, v[j].x, acc[r].x);
+                        acc[r].y = __builtin_fmaf(w, v[j].y, acc[r].y);
+                        acc[r].z = __builtin_fmaf(w, v[j].z, acc[r].z);
+                        acc[r].w = __builtin_fmaf(w, v[j].w, acc[r].w);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    // reduce the position subsets in a fixed order, normalise, store
+#pragma unroll
+    for (int r = 0; r < kRMax; ++r) {
+        if (r >= R) break;
+        *(float4*)&red[ps][4 * col] = acc[r];
+        __syncthreads();
+        if (tid < HD) {
+            float o = 0.f;
+            for (int k = 0; k < NPS; ++k) o += red[k][tid];
+            out[(size_t)t * ldo + (g * R + r) * HD + tid] = o / st_l[r];
+        }
+        __syncthreads();
+    }
 }
 
 // ── argmax (first index of the maximum) ──────────────────────────────────────
@@ -226,12 +453,30 @@ __global__ __launch_bounds__(64) void k_argmax2(const VI* part, int n_slices, in
     if (threadIdx.x == 0) out[row] = best.i == 0x7FFFFFFF ? 0 : best.i;
 }
 
-__global__ void k_accept_greedy(const int32_t* tgt, const int32_t* dft, int n_draft, int32_t* out) {
+__global__ void k_accept_greedy(const int32_t* tgt, const int32_t* dft, int n_draft, int32_t* out, int32_t* pos,
+                                int32_t* next) {
     if (threadIdx.x != 0) return;
     int a = 0;
     while (a < n_draft && tgt[a] == dft[a]) ++a;
     out[0] = a;
     out[1] = tgt[a];
+    if (pos) {  // device-resident round state: emitted ids, next position, next input
+        for (int i = 0; i <= a; ++i) out[2 + i] = tgt[i];
+        *pos += a + 1;
+        *next = tgt[a];
+    }
+}
+
+// One captured greedy step ends here: the argmax of the step (tok[1]) is
+// appended to the history and becomes the next input; position and count
+// advance on the device.
+__global__ void k_decode_advance(int32_t* tok, int32_t* hist, int32_t* pos, int32_t* count) {
+    if (threadIdx.x != 0) return;
+    const int32_t t = tok[1];
+    hist[*count] = t;
+    *count += 1;
+    *pos += 1;
+    tok[0] = t;
 }
 
 }  // namespace orc
@@ -250,18 +495,26 @@ extern "C" int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int
     return ORC_OK;
 }
 
-extern "C" int orc_rope_kv_store(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
-                                 int start_pos, const float* d_rope, float* d_kc, float* d_vc, int ctx,
-                                 orc_stream_t s) {
+extern "C" int orc_rope_kv_store_at(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
+                                    const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kc, float* d_vc,
+                                    int ctx, orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (n_tok < 0 || n_heads <= 0 || n_kv <= 0 || head_dim <= 0 || head_dim % 2 || start_pos < 0 ||
-        start_pos + n_tok > ctx || ldqkv < (n_heads + 2 * n_kv) * head_dim || !d_qkv || !d_rope || !d_kc || !d_vc)
+    if (n_tok < 0 || n_heads <= 0 || n_kv <= 0 || head_dim <= 0 || head_dim % 2 ||
+        (!d_pos && (pos_off < 0 || pos_off + n_tok > ctx)) || ldqkv < (n_heads + 2 * n_kv) * head_dim || !d_qkv ||
+        !d_rope || !d_kc || !d_vc)
         return set_error(ORC_E_INVALID, "rope_kv_store: bad args (positions must fit the context)");
     if (!n_tok) return ORC_OK;
     hipLaunchKernelGGL(k_rope_kv, dim3(n_tok), dim3(256), 0, resolve_stream(s), d_qkv, ldqkv, n_heads, n_kv, head_dim,
-                       start_pos, (const float2*)d_rope, d_kc, d_vc, ctx);
+                       d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
+}
+
+extern "C" int orc_rope_kv_store(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
+                                 int start_pos, const float* d_rope, float* d_kc, float* d_vc, int ctx,
+                                 orc_stream_t s) {
+    return orc_rope_kv_store_at(d_qkv, ldqkv, n_tok, n_heads, n_kv, head_dim, nullptr, start_pos, d_rope, d_kc, d_vc,
+                                ctx, s);
 }
 
 extern "C" size_t orc_attn_workspace(int n_tok, int n_heads, int head_dim, int max_pos) {
@@ -269,31 +522,40 @@ extern "C" size_t orc_attn_workspace(int n_tok, int n_heads, int head_dim, int m
     return nch * (size_t)n_heads * (size_t)n_tok * (size_t)(head_dim + 2) * sizeof(float);
 }
 
-extern "C" int orc_attn_gqa(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv, int head_dim, int start_pos,
-                            const float* d_kc, const float* d_vc, int ctx, float* d_out, int ldo, void* d_work,
-                            orc_stream_t s) {
+extern "C" int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv, int head_dim,
+                               const int32_t* d_pos, int pos_off, const float* d_kc, const float* d_vc, int ctx,
+                               float* d_out, int ldo, void* d_work, orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || start_pos < 0 || start_pos + n_tok > ctx ||
+    if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || (!d_pos && (pos_off < 0 || pos_off + n_tok > ctx)) ||
         !d_q || !d_kc || !d_vc || !d_out || !d_work || ldq % 4 || ((uintptr_t)d_q & 15))
         return set_error(ORC_E_INVALID, "attn_gqa: bad args");
     if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_gqa: head_dim must be 64 or 128");
-    const int nch = (start_pos + n_tok + kCH - 1) / kCH;
+    // a device position sizes the grid for the whole context (chunks past the
+    // last position exit at once); a host position sizes it exactly
+    const int nch = d_pos ? (ctx + kCH - 1) / kCH : (pos_off + n_tok + kCH - 1) / kCH;
     hipStream_t st = resolve_stream(s);
     if (head_dim == 64) {
         hipLaunchKernelGGL(k_attn_partial<64>, dim3(nch, n_kv), dim3(256), 0, st, d_q, ldq, n_tok, n_heads, n_kv,
-                           start_pos, d_kc, d_vc, ctx, (float*)d_work);
+                           d_pos, pos_off, d_kc, d_vc, ctx, (float*)d_work);
         ORC_LAUNCH_CHECK();
-        hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_heads, n_tok), dim3(64), 0, st, n_tok, n_heads, start_pos,
-                           (const float*)d_work, d_out, ldo);
+        hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_heads, n_tok), dim3(64), 0, st, n_tok, n_heads, d_pos, pos_off,
+                           ctx, (const float*)d_work, d_out, ldo);
     } else {
         hipLaunchKernelGGL(k_attn_partial<128>, dim3(nch, n_kv), dim3(256), 0, st, d_q, ldq, n_tok, n_heads, n_kv,
-                           start_pos, d_kc, d_vc, ctx, (float*)d_work);
+                           d_pos, pos_off, d_kc, d_vc, ctx, (float*)d_work);
         ORC_LAUNCH_CHECK();
-        hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_heads, n_tok), dim3(128), 0, st, n_tok, n_heads, start_pos,
-                           (const float*)d_work, d_out, ldo);
+        hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_heads, n_tok), dim3(128), 0, st, n_tok, n_heads, d_pos, pos_off,
+                           ctx, (const float*)d_work, d_out, ldo);
     }
     ORC_LAUNCH_CHECK();
     return ORC_OK;
+}
+
+extern "C" int orc_attn_gqa(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv, int head_dim, int start_pos,
+                            const float* d_kc, const float* d_vc, int ctx, float* d_out, int ldo, void* d_work,
+                            orc_stream_t s) {
+    return orc_attn_gqa_at(d_q, ldq, n_tok, n_heads, n_kv, head_dim, nullptr, start_pos, d_kc, d_vc, ctx, d_out, ldo,
+                           d_work, s);
 }
 
 static int argmax_slices(int n) { return std::max(1, std::min(256, (n + kArgBlock - 1) / kArgBlock)); }
@@ -316,7 +578,49 @@ extern "C" int orc_spec_accept_greedy(const int32_t* d_tgt, const int32_t* d_dft
                                       orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
     if (n_draft < 0 || !d_tgt || !d_out || (n_draft && !d_dft)) return set_error(ORC_E_INVALID, "accept: bad args");
-    hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64), 0, resolve_stream(s), d_tgt, d_dft, n_draft, d_out);
+    hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64), 0, resolve_stream(s), d_tgt, d_dft, n_draft, d_out,
+                       (int32_t*)nullptr, (int32_t*)nullptr);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_spec_accept_greedy_at(const int32_t* d_tgt, const int32_t* d_dft, int n_draft, int32_t* d_out,
+                                         int32_t* d_pos, int32_t* d_next, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n_draft < 0 || !d_tgt || !d_out || (n_draft && !d_dft) || !d_pos || !d_next)
+        return set_error(ORC_E_INVALID, "accept: bad args");
+    hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64), 0, resolve_stream(s), d_tgt, d_dft, n_draft, d_out, d_pos,
+                       d_next);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_decode_advance(int32_t* d_tok, int32_t* d_hist, int32_t* d_pos, int32_t* d_count, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_tok || !d_hist || !d_pos || !d_count) return set_error(ORC_E_INVALID, "decode_advance: null pointer");
+    hipLaunchKernelGGL(k_decode_advance, dim3(1), dim3(64), 0, resolve_stream(s), d_tok, d_hist, d_pos, d_count);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+
+extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
+                                 const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kc, float* d_vc,
+                                 int ctx, float* d_out, int ldo, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || (!d_pos && (pos_off < 0 || pos_off + n_tok > ctx)) ||
+        ldqkv < (n_heads + 2 * n_kv) * head_dim || ldqkv % 4 || ldo % 4 || !d_qkv || !d_rope || !d_kc || !d_vc ||
+        !d_out || ((uintptr_t)d_qkv & 15) || ((uintptr_t)d_kc & 15) || ((uintptr_t)d_vc & 15))
+        return set_error(ORC_E_INVALID, "attn_fused: bad args");
+    if (n_heads / n_kv > kRMax) return set_error(ORC_E_UNSUPPORTED, "attn_fused: more than 8 query heads per kv head");
+    if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_fused: head_dim must be 64 or 128");
+    hipStream_t st = resolve_stream(s);
+    if (head_dim == 64)
+        hipLaunchKernelGGL(k_attn_fused<64>, dim3(n_kv, n_tok), dim3(kAT), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos,
+                           pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+    else
+        hipLaunchKernelGGL(k_attn_fused<128>, dim3(n_kv, n_tok), dim3(kAT), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos,
+                           pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

@@ -103,3 +103,10 @@ extern "C" int orch_spec_greedy(orch_model* t, orch_model* d, const int32_t* pro
 extern "C" double orch_weight_bytes(const orch_model* h, int logits) { return h->m.weight_bytes(logits != 0); }
 
 extern "C" int orch_sync(void) { return orc_device_sync(); }
+
+extern "C" int orch_set_graphs(int on) {
+    const int prev = session().graphs() ? 1 : 0;
+    session().set_graphs(on != 0);
+    return prev;
+}
+

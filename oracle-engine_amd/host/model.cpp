@@ -137,6 +137,10 @@ bool Model::load(const std::string& path, int ctx_len) {
     logits_.assign((size_t)V, 0.f);
     loaded_ = true;
     reset();
+    fused_attn_ = cfg.n_heads % cfg.n_kv_heads == 0 && cfg.n_heads / cfg.n_kv_heads <= 8 &&
+                  (cfg.head_dim == 64 || cfg.head_dim == 128);
+    static uint64_t next_uid = 0;
+    uid_ = ++next_uid;
     return true;
 }
 
@@ -179,7 +183,8 @@ int Model::gemm_segs(const std::vector<std::pair<const Mat*, std::pair<float*, c
     return 0;
 }
 
-int Model::chunk_dev(const int32_t* d_ids, int n, int sp, bool logits, int32_t* d_argmax, orc_stream_t s) {
+int Model::chunk_dev(const int32_t* d_ids, int n, const int32_t* d_pos, int sp, bool logits, int32_t* d_argmax,
+                     orc_stream_t s) {
     const int D = cfg.embed_dim, NQ = cfg.n_q_total(), NKV = cfg.n_kv_total(), FF = cfg.ffn_hidden;
     const int QKV = NQ + 2 * NKV, C = cfg.ctx_len, V = cfg.n_vocab;
     int rc;
@@ -193,9 +198,15 @@ int Model::chunk_dev(const int32_t* d_ids, int n, int sp, bool logits, int32_t* 
         CK(gemm_segs({{&L.q, {d_qkv_, L.bq}}, {&L.k, {d_qkv_ + NQ, L.bk}}, {&L.v, {d_qkv_ + NQ + NKV, L.bv}}}, n,
                      d_x_, D, QKV, L.attn_norm, ORC_EPI_STORE, s));
         // RoPE + KV store (model.cpp:401-408), attention (model.cpp:410-435)
-        CK(orc_rope_kv_store(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, sp, d_rope_, kc, vc, C, s));
-        CK(orc_attn_gqa(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, sp, kc, vc, C, d_attn_, NQ,
-                        d_attn_ws_, s));
+        if (fused_attn_) {  // one launch: rotate, store K/V, attend
+            CK(orc_attn_fused_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc, vc,
+                                 C, d_attn_, NQ, s));
+        } else {
+            CK(orc_rope_kv_store_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc,
+                                    vc, C, s));
+            CK(orc_attn_gqa_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, kc, vc, C,
+                               d_attn_, NQ, d_attn_ws_, s));
+        }
         // x += O attn   (model.cpp:438-444)
         CK(gemm_segs({{&L.o, {d_x_, nullptr}}}, n, d_attn_, NQ, D, nullptr, ORC_EPI_ACCUM, s));
         // h = silu(gate xn) * up xn   (model.cpp:449-464)
@@ -225,10 +236,25 @@ int Model::forward_dev(const int32_t* d_ids, int n, int sp, bool logits, int32_t
     }
     for (int t0 = 0; t0 < n; t0 += kMaxBatch) {
         const int m = std::min(kMaxBatch, n - t0);
-        if (int rc = chunk_dev(d_ids + t0, m, sp + t0, logits, d_argmax ? d_argmax + t0 : nullptr, s)) {
+        if (int rc = chunk_dev(d_ids + t0, m, nullptr, sp + t0, logits, d_argmax ? d_argmax + t0 : nullptr, s)) {
             err_ = orc_last_error();
             return rc;
         }
+    }
+    return 0;
+}
+
+int Model::forward_dev_at(const int32_t* d_ids, int n, const int32_t* d_pos, int pos_off, bool logits,
+                          int32_t* d_argmax, orc_stream_t s) {
+    if (!loaded_) return ORC_E_INVALID;
+    if (n <= 0) return 0;
+    if (n > kMaxBatch) {
+        err_ = "forward_dev_at: more than kMaxBatch tokens";
+        return ORC_E_INVALID;
+    }
+    if (int rc = chunk_dev(d_ids, n, d_pos, pos_off, logits, d_argmax, s)) {
+        err_ = orc_last_error();
+        return rc;
     }
     return 0;
 }
@@ -261,7 +287,7 @@ void Model::forward_prefill(const int32_t* tokens, int n, int sp, float* out_log
     for (int t0 = 0; t0 < n; t0 += kMaxBatch) {
         const int m = std::min(kMaxBatch, n - t0);
         if (orc_memcpy_h2d(d_ids_, ids.data() + t0, (size_t)m * 4, nullptr)) return;
-        if (chunk_dev(d_ids_, m, sp + t0, out_logits != nullptr, nullptr, nullptr)) {
+        if (chunk_dev(d_ids_, m, nullptr, sp + t0, out_logits != nullptr, nullptr, nullptr)) {
             err_ = orc_last_error();
             std::fprintf(stderr, "[Model] forward_prefill failed: %s\n", err_.c_str());
             return;

@@ -49,6 +49,9 @@ public:
     // (core/model.cpp:64); a larger value sizes the device KV cache for it.
     bool load(const std::string& gguf_path, int ctx_len = 0);
     bool is_loaded() const { return loaded_; }
+    // Distinct for every successful load of any Model in the process (keys
+    // captured graphs, which bake in this model's device buffers).
+    uint64_t uid() const { return uid_; }
 
     // Reference-compatible host API.
     const float* forward(int32_t token_id, int pos, bool compute_logits = true);
@@ -66,6 +69,11 @@ public:
     // Returns 0 or an ORC_E_* code. Nothing crosses to the host.
     int forward_dev(const int32_t* d_ids, int n, int start_pos, bool compute_logits, int32_t* d_argmax,
                     orc_stream_t s = nullptr);
+    // As forward_dev with the first position read on the device (*d_pos +
+    // pos_off), so a captured graph of the call replays at any position; the
+    // caller keeps positions inside the context. n <= kMaxBatch.
+    int forward_dev_at(const int32_t* d_ids, int n, const int32_t* d_pos, int pos_off, bool compute_logits,
+                       int32_t* d_argmax, orc_stream_t s = nullptr);
     float* d_logits() const { return d_logits_; }
     const char* last_error() const { return err_.c_str(); }
 
@@ -86,6 +94,8 @@ private:
     };
     GGUFParser gguf_;
     bool loaded_ = false;
+    uint64_t uid_ = 0;
+    bool fused_attn_ = false;  // one-launch RoPE + KV store + attention supports this shape
     std::vector<Layer> layers_;
     Mat embd_, head_;
     const float* out_norm_ = nullptr;
@@ -97,7 +107,8 @@ private:
     std::string err_;
 
     bool fail(const std::string& m);
-    int chunk_dev(const int32_t* d_ids, int n, int start_pos, bool logits, int32_t* d_argmax, orc_stream_t s);
+    int chunk_dev(const int32_t* d_ids, int n, const int32_t* d_pos, int start_pos, bool logits, int32_t* d_argmax,
+                  orc_stream_t s);
     int gemm_segs(const std::vector<std::pair<const Mat*, std::pair<float*, const float*>>>& segs, int n,
                   const float* x, int ldx, int ldy, const float* norm, int epi, orc_stream_t s);
     void free_dev();

@@ -4,17 +4,107 @@
 #include <cstdio>
 
 DecodeSession::DecodeSession(int max_tokens, int max_k) : max_tokens_(max_tokens), max_k_(max_k) {
+    orc_init(0);  // idempotent; the session may be created before any model is loaded
     orc_malloc((void**)&d_hist_, (size_t)(max_tokens + 2) * 4);
     orc_malloc((void**)&d_vin_, (size_t)(max_k + 2) * 4);
     orc_malloc((void**)&d_tgt_, (size_t)(max_k + 2) * 4);
-    orc_malloc((void**)&d_acc_, 4 * 4);
+    orc_malloc((void**)&d_acc_, (size_t)(max_k + 4) * 4);
+    orc_malloc((void**)&d_pos_, 4 * 4);
+    orc_malloc((void**)&d_tok_, 4 * 4);
 }
 
 DecodeSession::~DecodeSession() {
+    drop(greedy_g_);
+    drop(spec_g_);
     orc_free(d_hist_);
     orc_free(d_vin_);
     orc_free(d_tgt_);
     orc_free(d_acc_);
+    orc_free(d_pos_);
+    orc_free(d_tok_);
+}
+
+void DecodeSession::drop(Captured& c) {
+    orc_graph_destroy(c.g);
+    orc_graph_destroy(c.fill);
+    c = Captured();
+}
+
+// Ends a capture that failed part-way so the stream leaves capture mode.
+static int abort_capture(int rc) {
+    orc_graph_t g = nullptr;
+    if (orc_graph_end(nullptr, &g) == 0) orc_graph_destroy(g);
+    return rc;
+}
+
+// One captured greedy step: forward at *d_pos with input d_tok[0], argmax
+// into d_tok[1], then append / advance on the device.
+int DecodeSession::greedy_graphed(Model& m, int pos, int32_t first, int n_gen, int32_t* out) {
+    if (greedy_g_.a != m.uid() || !greedy_g_.g) {
+        drop(greedy_g_);
+        if (int rc = orc_graph_begin(nullptr)) return rc;
+        if (int rc = m.forward_dev_at(d_tok_, 1, d_pos_, 0, true, d_tok_ + 1)) return abort_capture(rc);
+        if (int rc = orc_decode_advance(d_tok_, d_hist_, d_pos_, d_pos_ + 1, nullptr)) return abort_capture(rc);
+        if (int rc = orc_graph_end(nullptr, &greedy_g_.g)) return rc;
+        greedy_g_.a = m.uid();
+    }
+    const int32_t state[2] = {pos, 0};
+    if (int rc = orc_memcpy_h2d(d_pos_, state, 8, nullptr)) return rc;
+    if (int rc = orc_memcpy_h2d(d_tok_, &first, 4, nullptr)) return rc;
+    for (int s = 0; s < n_gen; ++s)
+        if (int rc = orc_graph_launch(greedy_g_.g, nullptr)) return rc;
+    if (int rc = orc_memcpy_d2h(out, d_hist_, (size_t)n_gen * 4, nullptr)) return rc;
+    return n_gen;
+}
+
+// One captured round: k draft steps at *d_pos + i, the (k+1)-token verify at
+// *d_pos, acceptance (which advances *d_pos and writes the next input into
+// d_vin[0]). A second graph refills the draft KV at *d_pos - 1 when every
+// proposal was accepted.
+int DecodeSession::spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx,
+                                int32_t* out, SpecStats& S) {
+    if (spec_g_.a != tgt.uid() || spec_g_.b != dft.uid() || spec_g_.k != k || !spec_g_.g) {
+        drop(spec_g_);
+        if (int rc = orc_graph_begin(nullptr)) return rc;
+        for (int i = 0; i < k; ++i)
+            if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1)) return abort_capture(rc);
+        if (int rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, d_tgt_)) return abort_capture(rc);
+        if (int rc = orc_spec_accept_greedy_at(d_tgt_, d_vin_ + 1, k, d_acc_, d_pos_, d_vin_, nullptr))
+            return abort_capture(rc);
+        if (int rc = orc_graph_end(nullptr, &spec_g_.g)) return rc;
+        if (int rc = orc_graph_begin(nullptr)) return rc;
+        if (int rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr)) return abort_capture(rc);
+        if (int rc = orc_graph_end(nullptr, &spec_g_.fill)) return rc;
+        spec_g_.a = tgt.uid();
+        spec_g_.b = dft.uid();
+        spec_g_.k = k;
+    }
+    if (int rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr)) return rc;
+    if (int rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr)) return rc;
+    std::vector<int32_t> h(k + 3);
+    int ng = 0;
+    while (ng < n_gen && pos + k + 1 <= ctx) {
+        if (int rc = orc_graph_launch(spec_g_.g, nullptr)) return rc;
+        if (int rc = orc_memcpy_d2h(h.data(), d_acc_, (size_t)(k + 3) * 4, nullptr)) return rc;
+        const int a = h[0];
+        S.proposed += k;
+        S.passes++;
+        S.rounds++;
+        bool capped = false;
+        for (int i = 0; i <= a; ++i) {
+            out[ng++] = h[2 + i];
+            if (i < a) S.accepted++;
+            if (ng >= n_gen) {
+                capped = true;
+                break;
+            }
+        }
+        if (a == k && !capped)
+            if (int rc = orc_graph_launch(spec_g_.fill, nullptr)) return rc;
+        pos += a + 1;
+    }
+    orc_stream_sync(nullptr);
+    return ng;
 }
 
 int DecodeSession::prefill(Model& m, const int32_t* prompt, int n_prompt) {
@@ -31,6 +121,7 @@ int DecodeSession::greedy(Model& m, const int32_t* prompt, int n_prompt, int n_g
     if (pos + n_gen > (int)m.cfg.ctx_len) return ORC_E_INVALID;
     int32_t first = prompt[n_prompt - 1];
     if (first < 0 || first >= (int32_t)m.cfg.n_vocab) first = 0;
+    if (graphs_) return greedy_graphed(m, pos, first, n_gen, out);
     if (int rc = orc_memcpy_h2d(d_hist_, &first, 4, nullptr)) return rc;
     for (int s = 0; s < n_gen; ++s)
         if (int rc = m.forward_dev(d_hist_ + s, 1, pos + s, true, d_hist_ + s + 1)) return rc;
@@ -48,6 +139,7 @@ int DecodeSession::spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, in
     int32_t next = prompt[n_prompt - 1];
     if (next < 0 || next >= (int32_t)tgt.cfg.n_vocab) next = 0;
     const int ctx = (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len);
+    if (graphs_) return spec_graphed(tgt, dft, pos, next, n_gen, k, ctx, out, S);
     std::vector<int32_t> ids(k + 2);
     while (ng < n_gen && pos + k + 1 <= ctx) {
         if (int rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr)) return rc;

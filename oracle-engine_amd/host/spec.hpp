@@ -15,12 +15,25 @@ struct SpecStats {
 };
 
 // Device scratch reused across calls (no allocation in the decode loops).
+// With graphs on (the default), one greedy step and one speculative round
+// are each captured once per (models, k) and replayed: positions and the
+// next input token live on the device, so a captured graph is valid for every
+// position, and the host only launches graphs and reads the round's ids.
 class DecodeSession {
 public:
     explicit DecodeSession(int max_tokens = 4096, int max_k = 16);
     ~DecodeSession();
     DecodeSession(const DecodeSession&) = delete;
     DecodeSession& operator=(const DecodeSession&) = delete;
+
+    // Also drops captured graphs: the next loop captures them again (e.g.
+    // after kernel timing was switched on, to include its event nodes).
+    void set_graphs(bool on) {
+        graphs_ = on;
+        drop(greedy_g_);
+        drop(spec_g_);
+    }
+    bool graphs() const { return graphs_; }
 
     // Batched prefill of prompt[0 .. n_prompt-2] into the model's KV cache.
     int prefill(Model& m, const int32_t* prompt, int n_prompt);
@@ -32,8 +45,21 @@ public:
 
 private:
     int max_tokens_, max_k_;
+    bool graphs_ = true;
     int32_t* d_hist_ = nullptr;  // greedy token chain
     int32_t* d_vin_ = nullptr;   // [next, d0 .. d_{k-1}]
     int32_t* d_tgt_ = nullptr;   // verify argmax ids
-    int32_t* d_acc_ = nullptr;   // accepted count, next token
+    int32_t* d_acc_ = nullptr;   // accepted count, next token, emitted ids
+    int32_t* d_pos_ = nullptr;   // device position (+ step count for greedy)
+    int32_t* d_tok_ = nullptr;   // greedy step input / output
+    struct Captured {
+        uint64_t a = 0, b = 0;  // model uids
+        int k = -1;
+        orc_graph_t g = nullptr, fill = nullptr;
+    };
+    Captured greedy_g_, spec_g_;
+    void drop(Captured& c);
+    int greedy_graphed(Model& m, int pos, int32_t first, int n_gen, int32_t* out);
+    int spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx, int32_t* out,
+                     SpecStats& S);
 };

@@ -65,13 +65,22 @@ ABI = [
     ("orc_rmsnorm", C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_float, _vp]),
     ("orc_rope_kv_store", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp,
                                     C.c_int, _vp]),
+    ("orc_rope_kv_store_at", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp,
+                                       _vp, C.c_int, _vp]),
     ("orc_attn_workspace", C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int]),
     ("orc_attn_gqa", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp,
                                C.c_int, _vp, _vp]),
+    ("orc_attn_gqa_at", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp,
+                                  C.c_int, _vp, C.c_int, _vp, _vp]),
+    ("orc_attn_fused_at", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp,
+                                    C.c_int, _vp, C.c_int, _vp]),
     ("orc_argmax_workspace", C.c_size_t, [C.c_int, C.c_int]),
     ("orc_argmax", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
     ("orc_spec_accept_greedy", C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
+    ("orc_spec_accept_greedy_at", C.c_int, [_vp, _vp, C.c_int, _vp, _vp, _vp, _vp]),
+    ("orc_decode_advance", C.c_int, [_vp, _vp, _vp, _vp, _vp]),
     ("orc_prof_enable", C.c_int, [C.c_int]),
+    ("orc_prof_accumulate", C.c_int, []),
     ("orc_prof_read", C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double),
                                 C.POINTER(C.c_double)]),
 ]
@@ -165,6 +174,7 @@ HOST_ABI = [
     ("orch_forward_batch", C.c_int, [_vp, _ip, C.c_int, C.c_int, _fp]),
     ("orch_greedy", C.c_int, [_vp, _ip, C.c_int, C.c_int, _ip, C.c_int]),
     ("orch_spec_greedy", C.c_int, [_vp, _vp, _ip, C.c_int, C.c_int, C.c_int, _ip, C.POINTER(C.c_int64), C.c_int]),
+    ("orch_set_graphs", C.c_int, [C.c_int]),
     ("orch_weight_bytes", C.c_double, [_vp, C.c_int]),
     ("orch_sync", C.c_int, []),
 ]

@@ -210,6 +210,53 @@ def test_attention(dev, oracle, H, KVH, hd, sp, nt):
         assert np.allclose(got[t], want, rtol=1e-5, atol=2e-6), np.abs(got[t] - want).max()
 
 
+@pytest.mark.parametrize("H,KVH,hd,sp,nt,devpos", [(24, 8, 128, 0, 1, False), (24, 8, 128, 200, 1, True),
+                                                   (24, 8, 128, 127, 5, True), (28, 4, 128, 700, 7, False),
+                                                   (14, 2, 64, 31, 9, True), (32, 8, 64, 1000, 1, False),
+                                                   (24, 8, 128, 1300, 5, True)])
+def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos):
+    """Fused RoPE + KV store + attention equals the oracle's rope then
+    attention over the prefilled cache plus the new rows; the new K/V rows
+    land in the cache; the QKV rows are left as they were."""
+    print(f"[gpu] attn_fused H={H} KVH={KVH} hd={hd} sp={sp} nt={nt} devpos={devpos}", flush=True)
+    rng = np.random.default_rng(sp * 7 + nt)
+    base = 500000.0
+    ctx = sp + nt + 5
+    ld = (H + 2 * KVH) * hd
+    qkv = rng.normal(0, 1, (nt, ld)).astype(np.float32)
+    K = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    V = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    tab = rope_table(ctx, hd, base)
+    dq, dt, dK, dV = dev.upload(qkv), dev.upload(tab), dev.upload(K), dev.upload(V)
+    dO = dev.alloc(nt * H * hd * 4)
+    if devpos:
+        dp = dev.upload(np.array([sp - 3], np.int32))
+        dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, dp.ptr, 3, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
+                                          H * hd, None))
+    else:
+        dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
+                                          H * hd, None))
+    got = dO.read(np.float32).reshape(nt, H * hd)
+    Kc = dK.read(np.float32).reshape(KVH, ctx, hd)
+    Vc = dV.read(np.float32).reshape(KVH, ctx, hd)
+    assert np.array_equal(dq.read(np.float32).reshape(nt, ld), qkv)
+    kref, vref = K.copy(), V.copy()
+    qs = []
+    for t in range(nt):
+        q, k = oracle.rope(qkv[t, :H * hd], qkv[t, H * hd:(H + KVH) * hd], H, KVH, hd, sp + t, base)
+        qs.append(q)
+        kref[:, sp + t, :] = k.reshape(KVH, hd)
+        vref[:, sp + t, :] = qkv[t, (H + KVH) * hd:].reshape(KVH, hd)
+    assert np.allclose(Kc[:, :sp + nt], kref[:, :sp + nt], rtol=1e-5, atol=2e-6)
+    assert np.array_equal(Vc[:, :sp + nt], vref[:, :sp + nt])
+    assert np.array_equal(Kc[:, sp + nt:], K[:, sp + nt:]) and np.array_equal(Vc[:, sp + nt:], V[:, sp + nt:])
+    kc = kref.transpose(1, 0, 2).reshape(ctx, KVH * hd)
+    vc = vref.transpose(1, 0, 2).reshape(ctx, KVH * hd)
+    for t in range(nt):
+        want = oracle.attention(qs[t], kc, vc, H, KVH, hd, sp + t)
+        assert np.allclose(got[t], want, rtol=2e-5, atol=4e-6), (t, np.abs(got[t] - want).max())
+
+
 def test_argmax_first_index(dev, oracle):
     rng = np.random.default_rng(9)
     rows, n = 6, 128256

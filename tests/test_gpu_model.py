@@ -148,3 +148,46 @@ def test_load_rejects_bad_files(tmp_path, models_dir):
     trunc.write_bytes(data[: len(data) // 2])
     with pytest.raises(orc.OrcError):
         orc.Model(trunc)
+
+
+def _set_graphs(on):
+    import orc
+
+    return orc.load_host_lib().orch_set_graphs(int(on))
+
+
+@pytest.mark.parametrize("k", [2, 4])
+def test_graph_replay_matches_host_launches(omodels, k):
+    """Captured decode graphs (device-resident positions) give the same
+    greedy and speculative streams and stats as host-launched kernels."""
+    print(f"[gpu] graphs vs launches k={k}", flush=True)
+    tgt, dft = omodels("t-q4k"), omodels("t-q4k-d")
+    prompt = FIX["greedy/t-q4k/prompt"]
+    prev = _set_graphs(False)
+    try:
+        g0 = tgt.greedy(prompt, 40)
+        s0, st0 = tgt.spec_greedy(dft, prompt, 40, k)
+    finally:
+        _set_graphs(prev)
+    _set_graphs(True)
+    g1 = tgt.greedy(prompt, 40)
+    s1, st1 = tgt.spec_greedy(dft, prompt, 40, k)
+    assert np.array_equal(g0, g1)
+    assert np.array_equal(s0, s1) and st0 == st1
+
+
+def test_graph_replay_all_accepted_refill(omodels):
+    """Self-draft: every round takes the all-accepted branch, which replays
+    the draft KV refill graph; stream equals the host-launched one."""
+    tgt = omodels("t-q4k")
+    same = omodels("t-q4k", 512 + 1)
+    prompt = FIX["greedy/t-q4k/prompt"]
+    prev = _set_graphs(False)
+    try:
+        s0, st0 = tgt.spec_greedy(same, prompt, 40, 3)
+    finally:
+        _set_graphs(prev)
+    _set_graphs(True)
+    s1, st1 = tgt.spec_greedy(same, prompt, 40, 3)
+    assert np.array_equal(s0, s1) and st0 == st1
+    assert st1["accepted"] >= st1["proposed"] - 3
