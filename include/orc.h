@@ -185,7 +185,8 @@ int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv,
  * is null), rotates q and k, stores k and v of every token in the cache and
  * writes each token's attention output (rows of ldo floats). Results equal
  * orc_rope_kv_store followed by orc_attn_gqa up to fp32 rounding. At most 8
- * query heads per kv head; head_dim 64 or 128; 16-byte aligned rows. */
+ * query heads per kv head and 16 tokens per call; head_dim 64 or 128;
+ * 16-byte aligned rows. */
 int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
                       const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kcache, float* d_vcache,
                       int ctx, float* d_out, int ldo, orc_stream_t stream);

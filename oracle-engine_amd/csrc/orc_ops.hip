@@ -203,10 +203,11 @@ __global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, con
 // 604-626): positions before `start` come from the cache, the new ones
 // (start..pt) straight from the QKV rows, rotated on the fly, so no
 // workgroup reads a cache row another one is writing. Positions are walked in
-// blocks of kPB with an online softmax: scores in LDS (16 lanes per position,
-// coalesced 128-bit row reads), block max / sum per row, then P.V with
-// 16-byte columns per lane and position subsets reduced at the end.
-constexpr int kAT = 512, kPB = 512, kRMax = 8;
+// blocks of kPB with an online softmax: one lane per position forms its dot
+// products over the whole row (q rows broadcast from LDS, no cross-lane
+// reductions), scores in LDS, block max / sum per row, then P.V with 16-byte
+// columns per lane and position subsets reduced in a fixed order at the end.
+constexpr int kAT = 512, kPB = 512, kRMax = 8, kMaxTokAttn = 16;
 
 template <int HD>
 __device__ __forceinline__ void rope_pair(const float* v, const float2* cs, int d, float& out) {
@@ -225,11 +226,13 @@ template <int HD>
 __global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv, int n_heads, int n_kv,
                                                     const int* d_pos, int pos_off, const float2* rope, float* kc,
                                                     float* vc, int ctx, float* out, int ldo) {
-    constexpr int DPT = HD / 16;            // dims per lane in the score phase (16 lanes per position)
-    constexpr int NC = HD / 4;              // float4 columns in the P.V phase
-    constexpr int NPS = kAT / NC;           // position subsets in the P.V phase
+    constexpr int NC = HD / 4;     // float4 columns in the P.V phase
+    constexpr int NPS = kAT / NC;  // position subsets in the P.V phase
+    constexpr int VB = 16;         // V rows in flight per lane
     constexpr int half = HD / 2;
+    static_assert(kPB == kAT, "one score position per lane per block");
     __shared__ float Qs[kRMax][HD];
+    __shared__ __align__(16) float Kn[kMaxTokAttn][HD];  // rotated K rows of the batch's own positions
     __shared__ float S[kRMax][kPB];
     __shared__ float st_m[kRMax], st_l[kRMax], st_a[kRMax];
     __shared__ float red[NPS][HD];
@@ -242,8 +245,27 @@ __global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv,
     const float scale = 1.f / sqrtf((float)HD);
     const float* qrow = qkv + (size_t)t * ldqkv;
     const float2* cs_t = rope + (size_t)pt * half;
+    const int col = tid % NC, ps = tid / NC;
+    // rotated K of this kv head for tokens 0..t (positions start..pt)
+    for (int i = tid; i < (t + 1) * HD; i += kAT) {
+        const int j = i / HD, d = i - j * HD;
+        float k;
+        rope_pair<HD>(qkv + (size_t)j * ldqkv + (n_heads + g) * HD, rope + (size_t)(start + j) * half, d, k);
+        Kn[j][d] = k;
+    }
+    const float* kg = kc + (size_t)g * ctx * HD;
+    const float* vg = vc + (size_t)g * ctx * HD;
 
-    // rotated q rows of the group, K/V of position pt into the cache
+    auto load_v = [&](float4 (&v)[VB], int b0, int nb, int pp0) {
+#pragma unroll
+        for (int j = 0; j < VB; ++j) {
+            const int pp = pp0 + j * NPS, p = b0 + pp;
+            if (pp >= nb) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            else if (p < start) v[j] = *(const float4*)(vg + (size_t)p * HD + 4 * col);
+            else v[j] = *(const float4*)(qkv + (size_t)(p - start) * ldqkv + (n_heads + n_kv + g) * HD + 4 * col);
+        }
+    };
+
     for (int i = tid; i < R * HD; i += kAT) {
         const int r = i / HD, d = i - r * HD;
         float v;
@@ -265,70 +287,48 @@ __global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv,
     float4 acc[kRMax];
 #pragma unroll
     for (int r = 0; r < kRMax; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int lane16 = tid & 15, pgrp = tid >> 4;  // score phase: 32 positions per pass
-    const int col = tid % NC, ps = tid / NC;       // P.V phase
-    const float* kg = kc + (size_t)g * ctx * HD;
-    const float* vg = vc + (size_t)g * ctx * HD;
     __syncthreads();
 
     for (int b0 = 0; b0 < P; b0 += kPB) {
         const int nb = min(kPB, P - b0);
-        // scores S[r][p] = (q_r . k_p) * scale; a lane loads its slice of SB
-        // rows before any arithmetic, so SB row loads are in flight at once
-        constexpr int SB = 4;
-        const int d0 = lane16 * DPT;
-        for (int pp0 = pgrp; pp0 < nb; pp0 += SB * (kAT / 16)) {
-            float kv[SB][DPT];
+        // scores: lane tid owns position b0 + tid and forms its R dot products
+        // over the whole row (q rows broadcast from LDS), KC dims at a time
+        if (tid < nb) {
+            const int p = b0 + tid;
+            // the whole row in flight at once: the cache, or the staged rotated row
+            float4 kv[HD / 4];
+            if (p < start) {
+                const float4* src = (const float4*)(kg + (size_t)p * HD);
 #pragma unroll
-            for (int j = 0; j < SB; ++j) {
-                const int pp = pp0 + j * (kAT / 16), p = b0 + pp;
-                if (pp >= nb) {
+                for (int i = 0; i < HD / 4; ++i) kv[i] = src[i];
+            } else {
+                const float4* src = (const float4*)&Kn[p - start][0];
 #pragma unroll
-                    for (int i = 0; i < DPT; ++i) kv[j][i] = 0.f;
-                } else if (p < start) {
-                    const float4* src = (const float4*)(kg + (size_t)p * HD + d0);
+                for (int i = 0; i < HD / 4; ++i) kv[i] = src[i];
+            }
+            float dr[kRMax];
 #pragma unroll
-                    for (int i = 0; i < DPT / 4; ++i) {
-                        const float4 v = src[i];
-                        kv[j][4 * i] = v.x;
-                        kv[j][4 * i + 1] = v.y;
-                        kv[j][4 * i + 2] = v.z;
-                        kv[j][4 * i + 3] = v.w;
+            for (int r = 0; r < kRMax; ++r) {
+                float sum = 0.f;
+                if (r < R) {
+#pragma unroll
+                    for (int i = 0; i < HD / 4; ++i) {
+                        const float4 q = *(const float4*)&Qs[r][4 * i];
+                        sum = __builtin_fmaf(q.x, kv[i].x, sum);
+                        sum = __builtin_fmaf(q.y, kv[i].y, sum);
+                        sum = __builtin_fmaf(q.z, kv[i].z, sum);
+                        sum = __builtin_fmaf(q.w, kv[i].w, sum);
                     }
-                } else {  // a new position: K from the QKV row of its token, rotated here
-                    const float* kr = qkv + (size_t)(p - start) * ldqkv + (n_heads + g) * HD;
-                    const float2* cs = rope + (size_t)p * half;
-#pragma unroll
-                    for (int i = 0; i < DPT; ++i) rope_pair<HD>(kr, cs, d0 + i, kv[j][i]);
                 }
+                dr[r] = sum;
             }
 #pragma unroll
-            for (int j = 0; j < SB; ++j) {
-                const int pp = pp0 + j * (kAT / 16);
-                float dr[kRMax];
-#pragma unroll
-                for (int r = 0; r < kRMax; ++r) {
-                    float sum = 0.f;
-                    if (r < R) {
-#pragma unroll
-                        for (int i = 0; i < DPT; ++i) sum = __builtin_fmaf(Qs[r][d0 + i], kv[j][i], sum);
-                    }
-                    dr[r] = sum;
-                }
-#pragma unroll
-                for (int r = 0; r < kRMax; ++r) {
-#pragma unroll
-                    for (int o = 8; o >= 1; o >>= 1) dr[r] += __shfl_xor(dr[r], o, 16);
-                }
-                if (pp < nb && lane16 < R) {
-                    float sum = dr[0];
-#pragma unroll
-                    for (int r = 1; r < kRMax; ++r)
-                        if (lane16 == r) sum = dr[r];
-                    S[lane16][pp] = sum * scale;
-                }
-            }
+            for (int r = 0; r < kRMax; ++r)
+                if (r < R) S[r][tid] = dr[r] * scale;
         }
+        // first V batch in flight during the softmax
+        float4 v[VB];
+        load_v(v, b0, nb, ps);
         __syncthreads();
         // online softmax: wave r owns row r (max, exp, sum over the block)
         {
@@ -368,17 +368,8 @@ __global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv,
                 acc[r].w *= a;
             }
         }
-        constexpr int VB = 8;  // V rows in flight per lane
         for (int pp0 = ps; pp0 < nb; pp0 += VB * NPS) {
-            float4 v[VB];
-#pragma unroll
-            for (int j = 0; j < VB; ++j) {
-                const int pp = pp0 + j * NPS, p = b0 + pp;
-                if (pp >= nb) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                else if (p < start) v[j] = *(const float4*)(vg + (size_t)p * HD + 4 * col);
-                else
-                    v[j] = *(const float4*)(qkv + (size_t)(p - start) * ldqkv + (n_heads + n_kv + g) * HD + 4 * col);
-            }
+            if (pp0 > ps) load_v(v, b0, nb, pp0);
 #pragma unroll
             for (int j = 0; j < VB; ++j) {
                 const int pp = pp0 + j * NPS;
@@ -613,6 +604,7 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
         !d_out || ((uintptr_t)d_qkv & 15) || ((uintptr_t)d_kc & 15) || ((uintptr_t)d_vc & 15))
         return set_error(ORC_E_INVALID, "attn_fused: bad args");
     if (n_heads / n_kv > kRMax) return set_error(ORC_E_UNSUPPORTED, "attn_fused: more than 8 query heads per kv head");
+    if (n_tok > kMaxTokAttn) return set_error(ORC_E_UNSUPPORTED, "attn_fused: at most 16 tokens per launch");
     if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_fused: head_dim must be 64 or 128");
     hipStream_t st = resolve_stream(s);
     if (head_dim == 64)
