@@ -39,6 +39,16 @@ int orch_greedy(orch_model* m, const int32_t* prompt, int n_prompt, int n_gen, i
  * rounds. Returns tokens written. */
 int orch_spec_greedy(orch_model* tgt, orch_model* dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                      int32_t* out, int64_t* stats, int prefill);
+/* The Engine's stochastic speculative loop (core/engine.cpp:100-240) with
+ * the device sampler: resets both models, prefills n_prompt-1 tokens (also
+ * recorded in the sampler history), greedy draft of k, target sampling at
+ * every verify position (sample + the Engine's second record), accept while
+ * equal, refill the draft when all k match. sampler = temperature, top_p,
+ * repeat_penalty; isampler = top_k, repeat_last; seed as std::mt19937 takes
+ * it. stats[0..2] = accepted, proposed, target forwards. Returns tokens
+ * written. */
+int orch_spec_engine(orch_model* tgt, orch_model* dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
+                     const float* sampler, const int32_t* isampler, uint64_t seed, int32_t* out, int64_t* stats);
 /* Decode loops replay captured HIP graphs (on, the default) or launch every
  * kernel from the host (off); the token streams are identical. Drops the
  * graphs captured so far (the next loop captures them again, e.g. with

@@ -209,6 +209,38 @@ int orc_spec_accept_greedy(const int32_t* d_tgt_ids, const int32_t* d_draft_ids,
  * n_draft + 3 ints). The position advance is bench_engine.cpp:352-355. */
 int orc_spec_accept_greedy_at(const int32_t* d_tgt_ids, const int32_t* d_draft_ids, int n_draft, int32_t* d_out,
                               int32_t* d_pos, int32_t* d_next, orc_stream_t stream);
+/* ── device sampler (core/sampler.cpp:7-105) ─────────────────────────────── */
+/* Sampler state in device memory: mt19937 seeded with (uint32_t)seed as
+ * std::mt19937 is (the reference passes a 64-bit seed that the engine
+ * truncates, sampler.cpp:7-8), the parameters of SamplerParams
+ * (sampler.hpp:16-22) and the history, initialised with n_hist recorded ids.
+ * top_k 0 = all tokens (exact up to 16384 tokens, the 16384 most probable
+ * beyond); repeat_last < 2048. */
+size_t orc_sampler_state_bytes(void);
+int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty, int repeat_last,
+                     uint64_t seed, const int32_t* d_hist, int n_hist, orc_stream_t stream);
+/* Sampler::sample (sampler.cpp:91-97) on one row of n_vocab logits: penalty,
+ * temperature, softmax, top-k, top-p, draw, record. Like the reference it
+ * rewrites the row in place (it ends up holding the probabilities). */
+int orc_sample(void* d_state, float* d_logits, int n_vocab, int32_t* d_out, orc_stream_t stream);
+/* Sampler::record (sampler.cpp:99-105) of n device ids, in order. */
+int orc_sampler_record(void* d_state, const int32_t* d_tok, int n, orc_stream_t stream);
+/* The last min(cap, size) history entries into d_out, their count into *d_n. */
+int orc_sampler_history(const void* d_state, int32_t* d_out, int cap, int32_t* d_n, orc_stream_t stream);
+/* Engine-style stochastic verify (core/engine.cpp:183-232) over the k+1 rows
+ * of one batched verify pass (row i = target logits at the i-th verify
+ * position, rows ld floats apart; rows are rewritten by sampling): for each
+ * draft id, sample (recording it) and record it again as the Engine does,
+ * stop at the first mismatch; if all k match, sample the bonus row the same
+ * way. At most max_emit ids are emitted (or *d_budget, which is then
+ * decremented). d_out: [0] emitted, [1] accepted, [2] rows sampled (the
+ * reference's target forwards), [3] 1 if all drafts matched (the caller then
+ * refills the draft's KV), [4..] the emitted ids (k+5 ints). With d_pos and
+ * d_next the round state advances: *d_pos += emitted, *d_next = last id. */
+int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, int n_vocab, const int32_t* d_draft, int n_draft,
+                           int max_emit, int32_t* d_budget, int32_t* d_out, int32_t* d_pos, int32_t* d_next,
+                           orc_stream_t stream);
+
 /* Tail of a captured greedy decode step (bench_engine.cpp:233-240 keeps the
  * chain on the host): d_tok[1] (the step's argmax) is appended at
  * d_hist[*d_count] and copied to d_tok[0] (the next input); *d_pos and

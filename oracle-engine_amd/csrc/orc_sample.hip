@@ -1,0 +1,457 @@
+// Device sampler and Engine-style stochastic acceptance (gfx950).
+//
+// Replaces Sampler::sample / record (core/sampler.cpp:15-105) and the
+// stochastic verify loop of Engine::generate (core/engine.cpp:150-240) with
+// kernels, so only the emitted ids cross to the host.
+//
+// One 1024-thread workgroup samples one row of logits, in place as the
+// reference does (the row ends up holding the probabilities):
+//  * repeat penalty over the device-resident history, one entry at a time
+//    (repeated ids compound), then temperature (skipped for T <= 0 or 1);
+//  * T <= 0: first index of the maximum;
+//  * otherwise softmax: block max, block sum of expf(l - max), p = e * (1/sum);
+//  * top-k by an exact 4-pass radix select on the bits of p (p >= 0, so the
+//    bit patterns order like the values), then the candidates (p >= the k-th
+//    value) are sorted by (p desc, index asc) with a bitonic sort in LDS;
+//    at most 16384 candidates (top_k = 0, "all tokens" in the reference, is
+//    exact for vocabularies up to that size and keeps the 16384 most probable
+//    tokens beyond it);
+//  * top-p cut at cumulative >= top_p, r = u * total with
+//    u = generate_canonical<float, 24>(mt19937) as libstdc++ forms it, then
+//    r -= p_i until r <= 0 (fallback: the first candidate);
+//  * the token is recorded; the history keeps the reference's trim rule
+//    (more than 2 * repeat_last entries: drop the oldest repeat_last).
+// mt19937 runs in one lane from a state kept in device memory.
+#include "orc_internal.hpp"
+
+#include <cstring>
+
+namespace orc {
+
+constexpr int kST = 1024;          // threads of a sampling workgroup
+constexpr int kSampHist = 4096;    // history capacity (repeat_last <= 2047)
+constexpr int kCandMax = 16384;    // candidates sorted in LDS (largest top_k; top_k = 0 means this many)
+
+struct DevSampler {
+    uint32_t mt[624];
+    int mti;
+    float temp, top_p, pen;
+    int top_k, last;
+    int nh;
+    int32_t hist[kSampHist];
+};
+
+__device__ uint32_t mt_next(DevSampler* s) {
+    if (s->mti >= 624) {
+        for (int i = 0; i < 624; i++) {
+            const uint32_t y = (s->mt[i] & 0x80000000u) | (s->mt[(i + 1) % 624] & 0x7FFFFFFFu);
+            s->mt[i] = s->mt[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908B0DFu : 0u);
+        }
+        s->mti = 0;
+    }
+    uint32_t y = s->mt[s->mti++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9D2C5680u;
+    y ^= (y << 15) & 0xEFC60000u;
+    y ^= y >> 18;
+    return y;
+}
+
+// generate_canonical<float, 24>(mt19937): one 32-bit draw / 2^32, kept below 1
+__device__ float mt_canonical(DevSampler* s) {
+    float r = (float)mt_next(s) / 4294967296.0f;
+    if (r >= 1.0f) r = __builtin_bit_cast(float, 0x3F7FFFFFu);  // largest float below 1
+    return r;
+}
+
+__device__ void record_tok(DevSampler* s, int32_t tok) {
+    if (s->nh >= kSampHist) {  // only reachable with repeat_last == 0, where history is never read
+        for (int i = 0; i < kSampHist / 2; ++i) s->hist[i] = s->hist[i + kSampHist / 2];
+        s->nh = kSampHist / 2;
+    }
+    s->hist[s->nh++] = tok;
+    if (s->nh > s->last * 2) {
+        for (int i = 0; i + s->last < s->nh; ++i) s->hist[i] = s->hist[i + s->last];
+        s->nh -= s->last;
+    }
+}
+
+struct SampScratch {
+    float red[kST / 64];
+    int ired[kST / 64];
+    unsigned int hist[256];
+    int bcast[4];
+    unsigned long long cand[kCandMax];
+};
+
+__device__ float block_max(float v, SampScratch& sh) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = sh.red[0];
+    for (int w = 1; w < kST / 64; ++w) m = fmaxf(m, sh.red[w]);
+    __syncthreads();
+    return m;
+}
+
+__device__ float block_sum(float v, SampScratch& sh) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = sh.red[0];
+    for (int w = 1; w < kST / 64; ++w) m += sh.red[w];  // fixed order
+    __syncthreads();
+    return m;
+}
+
+// first index of the maximum over the block
+__device__ int block_argmax(const float* x, int n, SampScratch& sh) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += kST) {
+        const float v = x[i];
+        if (v > bv || (v == bv && i < bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sh.red[threadIdx.x >> 6] = bv;
+        sh.ired[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    float v = sh.red[0];
+    int idx = sh.ired[0];
+    for (int w = 1; w < kST / 64; ++w)
+        if (sh.red[w] > v || (sh.red[w] == v && sh.ired[w] < idx)) {
+            v = sh.red[w];
+            idx = sh.ired[w];
+        }
+    __syncthreads();
+    return idx == 0x7FFFFFFF ? 0 : idx;
+}
+
+// ascending bitonic sort of sh.cand[0 .. m), m a power of two <= kCandMax
+__device__ void bitonic_sort(SampScratch& sh, int m) {
+    for (int size = 2; size <= m; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < m; i += kST) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool up = (i & size) == 0;
+                    const unsigned long long a = sh.cand[i], b = sh.cand[j];
+                    if ((a > b) == up) {
+                        sh.cand[i] = b;
+                        sh.cand[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Sampler::sample on one row (core/sampler.cpp:91-97). Whole workgroup.
+__device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) {
+    const int tid = threadIdx.x;
+    // repeat penalty (sampler.cpp:15-27), sequential so repeated ids compound
+    if (tid == 0 && s->pen > 1.f && s->nh > 0) {
+        const int start = s->nh - s->last > 0 ? s->nh - s->last : 0;
+        for (int i = start; i < s->nh; ++i) {
+            const int32_t id = s->hist[i];
+            if (id < 0 || id >= n) continue;
+            const float l = lg[id];
+            lg[id] = l > 0.f ? l / s->pen : l * s->pen;
+        }
+    }
+    __syncthreads();
+    const float T = s->temp;
+    if (T <= 0.f) {  // sampler.cpp:50: argmax of the penalised logits
+        const int32_t tok = block_argmax(lg, n, sh);
+        return tok;
+    }
+    // temperature (sampler.cpp:35-39) and the maximum in one pass
+    const bool scale = T != 1.f;
+    const float inv_t = 1.f / T;
+    float mx = -INFINITY;
+    for (int i = tid; i < n; i += kST) {
+        float l = lg[i];
+        if (scale) {
+            l *= inv_t;
+            lg[i] = l;
+        }
+        mx = fmaxf(mx, l);
+    }
+    mx = block_max(mx, sh);
+    // softmax (ops::softmax: e = exp(l - max), p = e * (1/sum))
+    float sum = 0.f;
+    for (int i = tid; i < n; i += kST) {
+        const float e = expf(lg[i] - mx);
+        lg[i] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, sh);
+    const float inv_s = 1.f / sum;
+    for (int i = tid; i < n; i += kST) lg[i] = lg[i] * inv_s;
+    __syncthreads();
+    // top-k threshold: exact radix select of the k-th largest p
+    const int k = min(s->top_k > 0 ? s->top_k : n, min(n, kCandMax));
+    unsigned int prefix = 0, mask = 0;
+    int krem = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = tid; b < 256; b += kST) sh.hist[b] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += kST) {
+            const unsigned int key = __builtin_bit_cast(unsigned int, lg[i]);
+            if ((key & mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int cum = 0, sel = 0;
+            for (int b = 255; b >= 0; --b) {
+                const int c = (int)sh.hist[b];
+                if (cum + c >= krem) {
+                    sel = b;
+                    break;
+                }
+                cum += c;
+            }
+            sh.bcast[0] = sel;
+            sh.bcast[1] = krem - cum;
+        }
+        __syncthreads();
+        prefix |= (unsigned int)sh.bcast[0] << shift;
+        mask |= 255u << shift;
+        krem = sh.bcast[1];
+        __syncthreads();
+    }
+    const unsigned int thr = prefix;  // bits of the k-th largest p; krem of its ties are kept
+    // candidates: every p >= thr (key = ~bits(p) : index sorts p desc, index asc)
+    if (tid == 0) sh.bcast[2] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += kST) {
+        const unsigned int key = __builtin_bit_cast(unsigned int, lg[i]);
+        if (key >= thr) {
+            const int slot = atomicAdd(&sh.bcast[2], 1);
+            if (slot < kCandMax) sh.cand[slot] = ((unsigned long long)(~key) << 32) | (unsigned int)i;
+        }
+    }
+    __syncthreads();
+    int nc = sh.bcast[2];
+    if (nc > kCandMax) {
+        // more ties at the threshold than LDS holds: take every p > thr and
+        // then the lowest-index ties, in index order
+        __syncthreads();
+        if (tid == 0) sh.bcast[2] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += kST) {
+            const unsigned int key = __builtin_bit_cast(unsigned int, lg[i]);
+            if (key > thr) {
+                const int slot = atomicAdd(&sh.bcast[2], 1);
+                sh.cand[slot] = ((unsigned long long)(~key) << 32) | (unsigned int)i;
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int c = sh.bcast[2];
+            for (int i = 0, got = 0; i < n && got < krem; ++i)
+                if (__builtin_bit_cast(unsigned int, lg[i]) == thr) {
+                    sh.cand[c++] = ((unsigned long long)(~thr) << 32) | (unsigned int)i;
+                    ++got;
+                }
+            sh.bcast[2] = c;
+        }
+        __syncthreads();
+        nc = sh.bcast[2];
+    }
+    int m = 1;
+    while (m < nc) m <<= 1;
+    for (int i = nc + tid; i < m; i += kST) sh.cand[i] = ~0ull;  // padding sorts last
+    __syncthreads();
+    bitonic_sort(sh, m);
+    // top-p cut and the draw (sampler.cpp:66-85), one lane
+    int32_t tok = 0;
+    if (tid == 0) {
+        float cum = 0.f;
+        int cut = k;
+        for (int i = 0; i < k; ++i) {
+            cum += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
+            if (cum >= s->top_p) {
+                cut = i + 1;
+                break;
+            }
+        }
+        float total = 0.f;
+        for (int i = 0; i < cut; ++i) total += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
+        float r = mt_canonical(s) * total;
+        tok = (int32_t)(sh.cand[0] & 0xFFFFFFFFu);
+        for (int i = 0; i < cut; ++i) {
+            const int32_t id = (int32_t)(sh.cand[i] & 0xFFFFFFFFu);
+            r -= lg[id];
+            if (r <= 0.f) {
+                tok = id;
+                break;
+            }
+        }
+        sh.bcast[3] = tok;
+    }
+    __syncthreads();
+    tok = sh.bcast[3];
+    __syncthreads();
+    return tok;
+}
+
+__global__ void k_sampler_init(DevSampler* s, uint32_t seed, float temp, float top_p, float pen, int top_k,
+                               int last, const int32_t* hist, int n_hist) {
+    if (threadIdx.x != 0) return;
+    s->mt[0] = seed;
+    for (int i = 1; i < 624; i++) s->mt[i] = 1812433253u * (s->mt[i - 1] ^ (s->mt[i - 1] >> 30)) + (uint32_t)i;
+    s->mti = 624;
+    s->temp = temp;
+    s->top_p = top_p;
+    s->pen = pen;
+    s->top_k = top_k;
+    s->last = last;
+    s->nh = 0;
+    for (int i = 0; i < n_hist; ++i) record_tok(s, hist[i]);
+}
+
+__global__ __launch_bounds__(kST) void k_sample(DevSampler* s, float* lg, int n, int32_t* out) {
+    __shared__ SampScratch sh;
+    const int32_t tok = sample_row(s, lg, n, sh);
+    if (threadIdx.x == 0) {
+        record_tok(s, tok);  // sampler.cpp:95
+        *out = tok;
+    }
+}
+
+__global__ void k_sampler_record(DevSampler* s, const int32_t* tok, int n) {
+    if (threadIdx.x != 0) return;
+    for (int i = 0; i < n; ++i) record_tok(s, tok[i]);
+}
+
+// Engine-style stochastic verify (core/engine.cpp:183-232) over the rows of
+// one batched verify pass: row i is the target's logits at the i-th verify
+// position. For each draft token: sample (records), record again (the
+// Engine's second record, engine.cpp:194-195), stop at the first mismatch;
+// when every draft token matched, sample the bonus row the same way. At most
+// max_emit tokens are emitted (the caller's remaining budget; read from and
+// decremented in *d_budget when given).
+// out: [0] emitted, [1] accepted, [2] rows sampled (target forwards of the
+// reference loop), [3] 1 if all drafts were accepted and the bonus emitted,
+// [4 ..] the emitted ids. With d_pos / d_next the device round state advances.
+__global__ __launch_bounds__(kST) void k_accept_engine(DevSampler* s, float* logits, int ld, int n_vocab,
+                                                        const int32_t* draft, int n_draft, int max_emit,
+                                                        int32_t* d_budget, int32_t* out, int32_t* d_pos,
+                                                        int32_t* d_next) {
+    __shared__ SampScratch sh;
+    if (d_budget) max_emit = *d_budget;
+    int emitted = 0, accepted = 0, rows = 0, all = 0;
+    int32_t last_tok = 0;
+    for (int i = 0; i <= n_draft && emitted < max_emit; ++i) {
+        const int32_t tok = sample_row(s, logits + (size_t)i * ld, n_vocab, sh);
+        ++rows;
+        if (threadIdx.x == 0) {
+            record_tok(s, tok);  // Sampler::sample's own record
+            record_tok(s, tok);  // the Engine's second record
+            out[4 + emitted] = tok;
+        }
+        __syncthreads();
+        ++emitted;
+        last_tok = tok;
+        if (i == n_draft) {  // bonus row after a fully accepted round
+            all = 1;
+            break;
+        }
+        if (tok != draft[i]) break;
+        ++accepted;
+    }
+    if (threadIdx.x == 0) {
+        out[0] = emitted;
+        out[1] = accepted;
+        out[2] = rows;
+        out[3] = all;
+        if (d_pos) {
+            *d_pos += emitted;
+            *d_next = last_tok;
+        }
+        if (d_budget) *d_budget -= emitted;
+    }
+}
+
+__global__ void k_sampler_history(const DevSampler* s, int32_t* out, int cap, int32_t* n_out) {
+    if (threadIdx.x != 0) return;
+    const int n = s->nh < cap ? s->nh : cap;
+    for (int i = 0; i < n; ++i) out[i] = s->hist[s->nh - n + i];
+    *n_out = n;
+}
+
+}  // namespace orc
+
+using namespace orc;
+
+extern "C" size_t orc_sampler_state_bytes(void) { return sizeof(DevSampler); }
+
+extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty,
+                                int repeat_last, uint64_t seed, const int32_t* d_hist, int n_hist,
+                                orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || repeat_last < 0 || repeat_last >= kSampHist / 2 || n_hist < 0 || (n_hist && !d_hist) ||
+        top_k < 0 || top_k > kCandMax)
+        return set_error(ORC_E_INVALID, "sampler_init: bad args (0 <= top_k <= 16384, repeat_last < 2048)");
+    hipLaunchKernelGGL(k_sampler_init, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state,
+                       (uint32_t)seed, temperature, top_p, repeat_penalty, top_k, repeat_last, d_hist, n_hist);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_sample(void* d_state, float* d_logits, int n_vocab, int32_t* d_out, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || !d_logits || !d_out || n_vocab <= 0) return set_error(ORC_E_INVALID, "sample: bad args");
+    hipLaunchKernelGGL(k_sample, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_logits, n_vocab,
+                       d_out);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_sampler_record(void* d_state, const int32_t* d_tok, int n, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || n < 0 || (n && !d_tok)) return set_error(ORC_E_INVALID, "sampler_record: bad args");
+    if (!n) return ORC_OK;
+    hipLaunchKernelGGL(k_sampler_record, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state, d_tok, n);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_sampler_history(const void* d_state, int32_t* d_out, int cap, int32_t* d_n, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || !d_out || !d_n || cap <= 0) return set_error(ORC_E_INVALID, "sampler_history: bad args");
+    hipLaunchKernelGGL(k_sampler_history, dim3(1), dim3(64), 0, resolve_stream(s), (const DevSampler*)d_state,
+                       d_out, cap, d_n);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, int n_vocab, const int32_t* d_draft,
+                                      int n_draft, int max_emit, int32_t* d_budget, int32_t* d_out, int32_t* d_pos,
+                                      int32_t* d_next, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || !d_logits || !d_out || n_vocab <= 0 || ld < n_vocab || n_draft < 0 || (n_draft && !d_draft) ||
+        (max_emit < 1 && !d_budget) || (!d_pos) != (!d_next))
+        return set_error(ORC_E_INVALID, "accept_engine: bad args");
+    hipLaunchKernelGGL(k_accept_engine, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_logits,
+                       ld, n_vocab, d_draft, n_draft, max_emit, d_budget, d_out, d_pos, d_next);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}

@@ -11,11 +11,18 @@ DecodeSession::DecodeSession(int max_tokens, int max_k) : max_tokens_(max_tokens
     orc_malloc((void**)&d_acc_, (size_t)(max_k + 4) * 4);
     orc_malloc((void**)&d_pos_, 4 * 4);
     orc_malloc((void**)&d_tok_, 4 * 4);
+    orc_malloc(&d_samp_, orc_sampler_state_bytes());
+    orc_malloc((void**)&d_eout_, (size_t)(max_k + 8) * 4);
+    orc_malloc((void**)&d_budget_, 4);
 }
 
 DecodeSession::~DecodeSession() {
     drop(greedy_g_);
     drop(spec_g_);
+    drop(eng_g_);
+    orc_free(d_samp_);
+    orc_free(d_eout_);
+    orc_free(d_budget_);
     orc_free(d_hist_);
     orc_free(d_vin_);
     orc_free(d_tgt_);
@@ -171,6 +178,91 @@ int DecodeSession::spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, in
             if (int rc = dft.forward_dev(d_vin_ + k, 1, pos + k, false, nullptr)) return rc;
         }
         pos += a + 1;
+    }
+    orc_stream_sync(nullptr);
+    return ng;
+}
+
+int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
+                               const SamplerConfig& sc, int32_t* out, SpecStats* st) {
+    if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return ORC_E_INVALID;
+    if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return ORC_E_INVALID;
+    SpecStats local;
+    SpecStats& S = st ? *st : local;
+    const int V = (int)tgt.cfg.n_vocab;
+    const int ctx = (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len);
+    std::vector<int32_t> ids(prompt, prompt + n_prompt);
+    for (auto& t : ids)
+        if (t < 0 || t >= V) t = 0;
+    // engine.cpp:115-125: reset, prefill n-1 prompt tokens on both models, record them
+    tgt.reset();
+    dft.reset();
+    int pos = 0;
+    if (n_prompt > 1) {
+        tgt.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
+        dft.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
+        pos = n_prompt - 1;
+    }
+    int32_t* d_ph = nullptr;
+    if (n_prompt > 1) {
+        if (int rc = orc_malloc((void**)&d_ph, (size_t)(n_prompt - 1) * 4)) return rc;
+        if (int rc = orc_memcpy_h2d(d_ph, ids.data(), (size_t)(n_prompt - 1) * 4, nullptr)) return rc;
+    }
+    int rc = orc_sampler_init(d_samp_, sc.temperature, sc.top_p, sc.top_k, sc.repeat_penalty, sc.repeat_last, sc.seed,
+                              d_ph, n_prompt - 1, nullptr);
+    orc_stream_sync(nullptr);
+    orc_free(d_ph);
+    if (rc) return rc;
+
+    if (graphs_ && (eng_g_.a != tgt.uid() || eng_g_.b != dft.uid() || eng_g_.k != k || !eng_g_.g)) {
+        drop(eng_g_);
+        if ((rc = orc_graph_begin(nullptr))) return rc;
+        for (int i = 0; i < k; ++i)
+            if ((rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))) return abort_capture(rc);
+        if ((rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, nullptr))) return abort_capture(rc);
+        if ((rc = orc_spec_accept_engine(d_samp_, tgt.d_logits(), V, V, d_vin_ + 1, k, 0, d_budget_, d_eout_, d_pos_,
+                                         d_vin_, nullptr)))
+            return abort_capture(rc);
+        if ((rc = orc_graph_end(nullptr, &eng_g_.g))) return rc;
+        if ((rc = orc_graph_begin(nullptr))) return rc;
+        if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) return abort_capture(rc);
+        if ((rc = orc_graph_end(nullptr, &eng_g_.fill))) return rc;
+        eng_g_.a = tgt.uid();
+        eng_g_.b = dft.uid();
+        eng_g_.k = k;
+    }
+    const int32_t next = ids[n_prompt - 1];
+    if ((rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr))) return rc;
+    if ((rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr))) return rc;
+    if ((rc = orc_memcpy_h2d(d_budget_, &n_gen, 4, nullptr))) return rc;
+    std::vector<int32_t> h(k + 5);
+    int ng = 0;
+    while (ng < n_gen && pos + k + 1 <= ctx) {
+        if (graphs_) {
+            if ((rc = orc_graph_launch(eng_g_.g, nullptr))) return rc;
+        } else {
+            for (int i = 0; i < k; ++i)
+                if ((rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))) return rc;
+            if ((rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, nullptr))) return rc;
+            if ((rc = orc_spec_accept_engine(d_samp_, tgt.d_logits(), V, V, d_vin_ + 1, k, 0, d_budget_, d_eout_,
+                                             d_pos_, d_vin_, nullptr)))
+                return rc;
+        }
+        if ((rc = orc_memcpy_d2h(h.data(), d_eout_, (size_t)(k + 5) * 4, nullptr))) return rc;
+        const int emitted = h[0];
+        S.accepted += h[1];
+        S.proposed += k;
+        S.passes += h[2];
+        S.rounds++;
+        for (int i = 0; i < emitted && ng < n_gen; ++i) out[ng++] = h[4 + i];
+        if (h[3] && ng < n_gen) {  // every proposal accepted: the draft lacks d_{k-1} (engine.cpp:230)
+            if (graphs_) {
+                if ((rc = orc_graph_launch(eng_g_.fill, nullptr))) return rc;
+            } else if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) {
+                return rc;
+            }
+        }
+        pos += emitted;
     }
     orc_stream_sync(nullptr);
     return ng;

@@ -14,6 +14,13 @@ struct SpecStats {
     long accepted = 0, proposed = 0, passes = 0, rounds = 0;
 };
 
+// SamplerParams (core/sampler.hpp:16-22) plus the seed.
+struct SamplerConfig {
+    float temperature = 0.8f, top_p = 0.95f, repeat_penalty = 1.1f;
+    int top_k = 40, repeat_last = 64;
+    uint64_t seed = 42;
+};
+
 // Device scratch reused across calls (no allocation in the decode loops).
 // With graphs on (the default), one greedy step and one speculative round
 // are each captured once per (models, k) and replayed: positions and the
@@ -32,6 +39,7 @@ public:
         graphs_ = on;
         drop(greedy_g_);
         drop(spec_g_);
+        drop(eng_g_);
     }
     bool graphs() const { return graphs_; }
 
@@ -42,6 +50,13 @@ public:
     // Speculative greedy with draft length k after both models are prefilled.
     int spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k, int32_t* out,
                     SpecStats* st);
+    // The Engine's stochastic speculative loop (core/engine.cpp:100-240):
+    // resets and prefills both models with prompt[0 .. n_prompt-2] (recorded
+    // in the sampler history), greedy draft proposals, target samples with the
+    // device sampler at every verify position, accept while equal.
+    // stats: accepted, proposed, target forwards of the reference loop.
+    int spec_engine(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
+                    const SamplerConfig& sc, int32_t* out, SpecStats* st);
 
 private:
     int max_tokens_, max_k_;
@@ -57,7 +72,10 @@ private:
         int k = -1;
         orc_graph_t g = nullptr, fill = nullptr;
     };
-    Captured greedy_g_, spec_g_;
+    Captured greedy_g_, spec_g_, eng_g_;
+    void* d_samp_ = nullptr;      // device sampler state
+    int32_t* d_eout_ = nullptr;   // Engine-style acceptance output (k+5 ints)
+    int32_t* d_budget_ = nullptr; // tokens still to emit
     void drop(Captured& c);
     int greedy_graphed(Model& m, int pos, int32_t first, int n_gen, int32_t* out);
     int spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx, int32_t* out,

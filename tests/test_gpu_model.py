@@ -191,3 +191,40 @@ def test_graph_replay_all_accepted_refill(omodels):
     s1, st1 = tgt.spec_greedy(same, prompt, 40, 3)
     assert np.array_equal(s0, s1) and st0 == st1
     assert st1["accepted"] >= st1["proposed"] - 3
+
+
+def test_device_sampler_matches_reference(dev):
+    """orc_sample reproduces the reference Sampler's draws (penalty, temperature,
+    softmax, top-k, top-p, mt19937 draw, history trim): 64 draws per case."""
+    L = dev.L
+    lg, hist = FIX["sample/logits"], FIX["sample/history"].astype(np.int32)
+    state = dev.alloc(L.orc_sampler_state_bytes())
+    dh, dl, do = dev.upload(hist), dev.alloc(lg.nbytes), dev.alloc(4)
+    for i in range(5):
+        T, P, K, pen, last = FIX[f"sample/{i}/params"]
+        seed = int(FIX[f"sample/{i}/seed"][0])
+        print(f"[gpu] sampler case {i} T={T} top_p={P} top_k={K}", flush=True)
+        dev.check(L.orc_sampler_init(state.ptr, float(T), float(P), int(K), float(pen), int(last), seed, dh.ptr,
+                                     hist.size, None))
+        draws = []
+        for _ in range(64):
+            dl.write(lg)
+            dev.check(L.orc_sample(state.ptr, dl.ptr, lg.size, do.ptr, None))
+            draws.append(int(do.read(np.int32)[0]))
+        assert draws == list(FIX[f"sample/{i}/draws"]), i
+
+
+def test_engine_stochastic_spec_matches_reference(omodels):
+    """The Engine's stochastic speculative loop on the device (greedy draft,
+    sampled verify with the double record) gives the reference's stream and
+    stats, with graphs and with host launches."""
+    tgt, dft = omodels("t-qwen"), omodels("t-qwen-d")
+    prompt = FIX["greedy/t-qwen/prompt"]
+    for graphs in (True, False):
+        prev = _set_graphs(graphs)
+        try:
+            toks, st = tgt.spec_engine(dft, prompt, 40, 3, 0.8, 0.95, 40, 1.1, 64, 4242)
+        finally:
+            _set_graphs(prev)
+        assert np.array_equal(toks, FIX["espec/tokens"]), graphs
+        assert [st["accepted"], st["proposed"], st["passes"]] == list(FIX["espec/stats"]), graphs
