@@ -49,6 +49,19 @@ int orch_spec_greedy(orch_model* tgt, orch_model* dft, const int32_t* prompt, in
  * written. */
 int orch_spec_engine(orch_model* tgt, orch_model* dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                      const float* sampler, const int32_t* isampler, uint64_t seed, int32_t* out, int64_t* stats);
+/* Speculative sampling with the exact-distribution rule (no reference
+ * counterpart; the reference's Engine accepts on equal samples, as
+ * orch_spec_engine does). Same reset, prefill, recorded prompt and sampler
+ * arguments as orch_spec_engine. Per round the draft proposes k ids, each
+ * drawn from its logits through the sampler transform (penalty window =
+ * history + the round's earlier proposals); the target scores the round in
+ * one batched pass; proposal i is accepted with min(1, p_i/q_i); the first
+ * rejection emits a draw from norm(max(0, p_i - q_i)); a fully accepted round
+ * emits a bonus draw from p_k. Every emitted id is recorded once. The emitted
+ * stream is distributed as sampling the target alone. stats[0..2] =
+ * accepted, proposed, target passes. Returns tokens written. */
+int orch_spec_sampled(orch_model* tgt, orch_model* dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
+                      const float* sampler, const int32_t* isampler, uint64_t seed, int32_t* out, int64_t* stats);
 /* Decode loops replay captured HIP graphs (on, the default) or launch every
  * kernel from the host (off); the token streams are identical. Drops the
  * graphs captured so far (the next loop captures them again, e.g. with

@@ -241,6 +241,37 @@ int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, int n_vocab, 
                            int max_emit, int32_t* d_budget, int32_t* d_out, int32_t* d_pos, int32_t* d_next,
                            orc_stream_t stream);
 
+/* ── speculative sampling, min(1, p/q) with residual resampling ──────────────
+ * No reference counterpart: the reference's Engine accepts a proposal when
+ * the target's own sample equals it (core/engine.cpp:183-232), which the
+ * functions above reproduce. These give the exact-distribution rule. */
+/* The sampler's transform of `rows` rows of logits written out as
+ * distributions: penalty over the history plus the pending proposals
+ * d_extra[0 .. extra_base + r) for row r, temperature, softmax, top-k, top-p,
+ * kept set renormalised into d_p (zeros elsewhere); T <= 0 puts all mass on
+ * the argmax. The logits rows are rewritten (sampler.cpp:15-85 does the same
+ * steps on one row). Nothing is recorded and no random number is drawn. */
+int orc_transform_probs(const void* d_state, float* d_logits, int ld, int n_vocab, int rows, const int32_t* d_extra,
+                        int extra_base, float* d_p, int ldp, orc_stream_t stream);
+/* One draw from the distribution d_p (one mt19937 uniform u; first index
+ * where the running sum of p reaches u * sum(p)); the id goes to d_out[0] and,
+ * if given, d_out2[0]. Not recorded. */
+int orc_draw(void* d_state, const float* d_p, int n_vocab, int32_t* d_out, int32_t* d_out2, orc_stream_t stream);
+/* The acceptance test of proposal x with explicit uniforms: accept when
+ * q[x] > 0 and u_acc * q[x] < p[x]; otherwise draw from norm(max(0, p - q))
+ * with u_res (argmax of p if that is empty). d_out = [id, accepted]. */
+int orc_accept_resample(const float* d_p, const float* d_q, int n_vocab, int32_t x, float u_acc, float u_res,
+                        int32_t* d_out, orc_stream_t stream);
+/* One round's acceptance chain: proposal i (drawn from row i of d_q) is
+ * accepted with probability min(1, p_i[x_i] / q_i[x_i]); the first rejection
+ * emits a residual draw and ends the round; when all k are accepted a bonus
+ * id is drawn from p_k. Uniforms come from the state's mt19937 (acceptance,
+ * then the residual or bonus draw); each emitted id is recorded once.
+ * d_out layout, budget and round state as orc_spec_accept_engine. */
+int orc_spec_accept_stochastic(void* d_state, const float* d_p, int ldp, const float* d_q, int ldq, int n_vocab,
+                               const int32_t* d_x, int k, int max_emit, int32_t* d_budget, int32_t* d_out,
+                               int32_t* d_pos, int32_t* d_next, orc_stream_t stream);
+
 /* Tail of a captured greedy decode step (bench_engine.cpp:233-240 keeps the
  * chain on the host): d_tok[1] (the step's argmax) is appended at
  * d_hist[*d_count] and copied to d_tok[0] (the next input); *d_pos and

@@ -1,8 +1,11 @@
-// Device sampler and Engine-style stochastic acceptance (gfx950).
+// Device sampler, Engine-style stochastic acceptance and speculative
+// sampling (gfx950).
 //
 // Replaces Sampler::sample / record (core/sampler.cpp:15-105) and the
 // stochastic verify loop of Engine::generate (core/engine.cpp:150-240) with
-// kernels, so only the emitted ids cross to the host.
+// kernels, so only the emitted ids cross to the host. The same transform,
+// written out as distributions, feeds the min(1, p/q) acceptance chain with
+// residual resampling (no reference counterpart).
 //
 // One 1024-thread workgroup samples one row of logits, in place as the
 // reference does (the row ends up holding the probabilities):
@@ -80,7 +83,9 @@ struct SampScratch {
     float red[kST / 64];
     int ired[kST / 64];
     unsigned int hist[256];
-    int bcast[4];
+    int bcast[8];
+    float fb[2];
+    double dscan[kST];
     unsigned long long cand[kCandMax];
 };
 
@@ -162,25 +167,27 @@ __device__ void bitonic_sort(SampScratch& sh, int m) {
     }
 }
 
-// Sampler::sample on one row (core/sampler.cpp:91-97). Whole workgroup.
-__device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) {
+// Repeat penalty (sampler.cpp:15-27) over the last repeat_last entries of
+// history + extra (extra: proposals not yet recorded), one entry at a time so
+// repeated ids compound. One lane; the caller synchronises.
+__device__ void penalize(const DevSampler* s, float* lg, int n, const int32_t* extra, int n_extra) {
+    if (threadIdx.x != 0 || !(s->pen > 1.f)) return;
+    const int L = s->nh + n_extra;
+    const int start = L - s->last > 0 ? L - s->last : 0;
+    for (int i = start; i < L; ++i) {
+        const int32_t id = i < s->nh ? s->hist[i] : extra[i - s->nh];
+        if (id < 0 || id >= n) continue;
+        const float l = lg[id];
+        lg[id] = l > 0.f ? l / s->pen : l * s->pen;
+    }
+}
+
+// Temperature, softmax (p written over lg) and the top-k candidates sorted by
+// (p desc, index asc) into sh.cand[0 .. k) (sampler.cpp:35-64). T > 0 only.
+// Returns k.
+__device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& sh) {
     const int tid = threadIdx.x;
-    // repeat penalty (sampler.cpp:15-27), sequential so repeated ids compound
-    if (tid == 0 && s->pen > 1.f && s->nh > 0) {
-        const int start = s->nh - s->last > 0 ? s->nh - s->last : 0;
-        for (int i = start; i < s->nh; ++i) {
-            const int32_t id = s->hist[i];
-            if (id < 0 || id >= n) continue;
-            const float l = lg[id];
-            lg[id] = l > 0.f ? l / s->pen : l * s->pen;
-        }
-    }
-    __syncthreads();
     const float T = s->temp;
-    if (T <= 0.f) {  // sampler.cpp:50: argmax of the penalised logits
-        const int32_t tok = block_argmax(lg, n, sh);
-        return tok;
-    }
     // temperature (sampler.cpp:35-39) and the maximum in one pass
     const bool scale = T != 1.f;
     const float inv_t = 1.f / T;
@@ -280,22 +287,42 @@ __device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) 
     for (int i = nc + tid; i < m; i += kST) sh.cand[i] = ~0ull;  // padding sorts last
     __syncthreads();
     bitonic_sort(sh, m);
-    // top-p cut and the draw (sampler.cpp:66-85), one lane
-    int32_t tok = 0;
-    if (tid == 0) {
-        float cum = 0.f;
-        int cut = k;
-        for (int i = 0; i < k; ++i) {
-            cum += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
-            if (cum >= s->top_p) {
-                cut = i + 1;
-                break;
-            }
+    return k;
+}
+
+// Top-p cut over the sorted candidates (sampler.cpp:66-77): sh.bcast[4] = cut,
+// sh.fb[0] = total kept mass. One lane; the caller synchronises.
+__device__ void topp_cut(const DevSampler* s, const float* lg, int k, SampScratch& sh) {
+    if (threadIdx.x != 0) return;
+    float cum = 0.f;
+    int cut = k;
+    for (int i = 0; i < k; ++i) {
+        cum += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
+        if (cum >= s->top_p) {
+            cut = i + 1;
+            break;
         }
-        float total = 0.f;
-        for (int i = 0; i < cut; ++i) total += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
-        float r = mt_canonical(s) * total;
-        tok = (int32_t)(sh.cand[0] & 0xFFFFFFFFu);
+    }
+    float total = 0.f;
+    for (int i = 0; i < cut; ++i) total += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
+    sh.bcast[4] = cut;
+    sh.fb[0] = total;
+}
+
+// Sampler::sample on one row (core/sampler.cpp:91-97) without the record.
+// Whole workgroup.
+__device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) {
+    const int tid = threadIdx.x;
+    penalize(s, lg, n, nullptr, 0);
+    __syncthreads();
+    if (s->temp <= 0.f) return block_argmax(lg, n, sh);  // sampler.cpp:50
+    const int k = topk_sorted(s, lg, n, sh);
+    topp_cut(s, lg, k, sh);
+    // the draw (sampler.cpp:78-85), one lane
+    if (tid == 0) {
+        const int cut = sh.bcast[4];
+        float r = mt_canonical(s) * sh.fb[0];
+        int32_t tok = (int32_t)(sh.cand[0] & 0xFFFFFFFFu);
         for (int i = 0; i < cut; ++i) {
             const int32_t id = (int32_t)(sh.cand[i] & 0xFFFFFFFFu);
             r -= lg[id];
@@ -307,9 +334,129 @@ __device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) 
         sh.bcast[3] = tok;
     }
     __syncthreads();
-    tok = sh.bcast[3];
+    const int32_t tok = sh.bcast[3];
     __syncthreads();
     return tok;
+}
+
+// The same transform as sampling, written out as a distribution: p_out holds
+// the kept set renormalised (zeros elsewhere); T <= 0 puts all mass on the
+// argmax. Whole workgroup.
+__device__ void transform_row(const DevSampler* s, float* lg, int n, const int32_t* extra, int n_extra, float* p_out,
+                              SampScratch& sh) {
+    const int tid = threadIdx.x;
+    penalize(s, lg, n, extra, n_extra);
+    __syncthreads();
+    if (s->temp <= 0.f) {
+        const int a = block_argmax(lg, n, sh);
+        for (int i = tid; i < n; i += kST) p_out[i] = i == a ? 1.f : 0.f;
+        __syncthreads();
+        return;
+    }
+    const int k = topk_sorted(s, lg, n, sh);
+    topp_cut(s, lg, k, sh);
+    for (int i = tid; i < n; i += kST) p_out[i] = 0.f;
+    __syncthreads();
+    const int cut = sh.bcast[4];
+    const float total = sh.fb[0];
+    for (int i = tid; i < cut; i += kST) {
+        const int id = (int)(sh.cand[i] & 0xFFFFFFFFu);
+        p_out[id] = lg[id] / total;
+    }
+    __syncthreads();
+}
+
+// First index whose running sum of the positive parts of w(i) reaches
+// target (r = target; r -= w(i) while w(i) > 0; stop at r <= 0), sums in
+// double; falls back to the last positive index (0 if there is none).
+// Whole workgroup.
+template <typename W>
+__device__ int block_pick(int n, W w, double target, SampScratch& sh) {
+    const int tid = threadIdx.x;
+    const int chunk = (n + kST - 1) / kST;
+    const int b = min(n, tid * chunk), e = min(n, b + chunk);
+    double loc = 0.0;
+    int last = -1;
+    for (int i = b; i < e; ++i) {
+        const float d = w(i);
+        if (d > 0.f) {
+            loc += (double)d;
+            last = i;
+        }
+    }
+    sh.dscan[tid] = loc;
+    if (tid == 0) {
+        sh.bcast[5] = 0x7FFFFFFF;
+        sh.bcast[6] = -1;
+    }
+    __syncthreads();
+    if (tid == 0) {  // exclusive prefix in thread order
+        double run = 0.0;
+        for (int t = 0; t < kST; ++t) {
+            const double v = sh.dscan[t];
+            sh.dscan[t] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    const double prefix = sh.dscan[tid];
+    if (last >= 0) {
+        atomicMax(&sh.bcast[6], last);
+        if (prefix < target && target <= prefix + loc) {
+            double r = target - prefix;
+            int got = last;  // rounding left r > 0: the chunk's last positive
+            for (int i = b; i < e; ++i) {
+                const float d = w(i);
+                if (!(d > 0.f)) continue;
+                r -= (double)d;
+                if (r <= 0.0) {
+                    got = i;
+                    break;
+                }
+            }
+            atomicMin(&sh.bcast[5], got);
+        } else if (target <= 0.0 && prefix == 0.0) {
+            for (int i = b; i < e; ++i)
+                if (w(i) > 0.f) {
+                    atomicMin(&sh.bcast[5], i);
+                    break;
+                }
+        }
+    }
+    __syncthreads();
+    const int pick = sh.bcast[5] != 0x7FFFFFFF ? sh.bcast[5] : max(sh.bcast[6], 0);
+    __syncthreads();
+    return pick;
+}
+
+// min(1, p/q) acceptance of proposal x with residual resampling (no reference
+// counterpart): accept when q[x] > 0 and u_acc * q[x] < p[x]; otherwise draw
+// from norm(max(0, p - q)) with u_res (argmax of p when the residual is
+// empty). Returns the emitted id; *accepted set on lane 0. Whole workgroup.
+__device__ int32_t accept_resample(const float* p, const float* q, int n, int32_t x, float u_acc, float u_res,
+                                   int* accepted, SampScratch& sh) {
+    const float qx = q[x], px = p[x];
+    if (qx > 0.f && u_acc * qx < px) {
+        *accepted = 1;
+        return x;
+    }
+    *accepted = 0;
+    auto resid = [&](int i) { return p[i] - q[i]; };
+    // total of the positive residual (double), then the draw
+    double loc = 0.0;
+    for (int i = threadIdx.x; i < n; i += kST) {
+        const float d = p[i] - q[i];
+        if (d > 0.f) loc += (double)d;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) loc += __shfl_xor(loc, o, 64);
+    if ((threadIdx.x & 63) == 0) sh.dscan[threadIdx.x >> 6] = loc;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < kST / 64; ++w) tot += sh.dscan[w];
+    __syncthreads();
+    if (!(tot > 0.0)) return block_argmax(p, n, sh);
+    return block_pick(n, resid, (double)u_res * tot, sh);
 }
 
 __global__ void k_sampler_init(DevSampler* s, uint32_t seed, float temp, float top_p, float pen, int top_k,
@@ -390,6 +537,117 @@ __global__ __launch_bounds__(kST) void k_accept_engine(DevSampler* s, float* log
     }
 }
 
+// Rows of logits -> distributions (kept set renormalised): row r uses the
+// proposals extra[0 .. extra_base + r) as pending history for the penalty.
+__global__ __launch_bounds__(kST) void k_transform(const DevSampler* s, float* lg, int ld, int n,
+                                                    const int32_t* extra, int extra_base, float* p, int ldp) {
+    __shared__ SampScratch sh;
+    const int r = blockIdx.x;
+    transform_row(s, lg + (size_t)r * ld, n, extra, extra_base + r, p + (size_t)r * ldp, sh);
+}
+
+__device__ float lane0_uniform(DevSampler* s, SampScratch& sh) {
+    if (threadIdx.x == 0) sh.fb[1] = mt_canonical(s);
+    __syncthreads();
+    const float u = sh.fb[1];
+    __syncthreads();
+    return u;
+}
+
+__device__ double block_total(const float* p, int n, SampScratch& sh) {
+    double loc = 0.0;
+    for (int i = threadIdx.x; i < n; i += kST)
+        if (p[i] > 0.f) loc += (double)p[i];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) loc += __shfl_xor(loc, o, 64);
+    if ((threadIdx.x & 63) == 0) sh.dscan[threadIdx.x >> 6] = loc;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < kST / 64; ++w) tot += sh.dscan[w];
+    __syncthreads();
+    return tot;
+}
+
+// One draw from a distribution p (u from the state's mt19937).
+__global__ __launch_bounds__(kST) void k_draw(DevSampler* s, const float* p, int n, int32_t* out, int32_t* out2) {
+    __shared__ SampScratch sh;
+    const float u = lane0_uniform(s, sh);
+    const double tot = block_total(p, n, sh);
+    const int tok = block_pick(n, [&](int i) { return p[i]; }, (double)u * tot, sh);
+    if (threadIdx.x == 0) {
+        out[0] = tok;
+        if (out2) out2[0] = tok;
+    }
+}
+
+__global__ __launch_bounds__(kST) void k_accept_resample(const float* p, const float* q, int n, int32_t x,
+                                                          float u_acc, float u_res, int32_t* out) {
+    __shared__ SampScratch sh;
+    int acc = 0;
+    const int32_t tok = accept_resample(p, q, n, x, u_acc, u_res, &acc, sh);
+    if (threadIdx.x == 0) {
+        out[0] = tok;
+        out[1] = acc;
+    }
+}
+
+// Speculative sampling acceptance chain over one round (no reference
+// counterpart; replaces the Engine rule in the north-star mode): for proposal
+// i (drawn from the draft's q_i), accept with min(1, p_i/q_i) or emit a draw
+// from norm(max(0, p_i - q_i)) and stop; when all k are accepted emit a draw
+// from p_k. Uniforms come from the state's mt19937 (acceptance, then the
+// residual or bonus draw); emitted ids are recorded once. Output layout as
+// k_accept_engine.
+__global__ __launch_bounds__(kST) void k_accept_chain(DevSampler* s, const float* p, int ldp, const float* q, int ldq,
+                                                       int n, const int32_t* x, int k, int max_emit, int32_t* d_budget,
+                                                       int32_t* out, int32_t* d_pos, int32_t* d_next) {
+    __shared__ SampScratch sh;
+    if (d_budget) max_emit = *d_budget;
+    int emitted = 0, accepted = 0, all = 0;
+    int32_t last_tok = 0;
+    for (int i = 0; i <= k && emitted < max_emit; ++i) {
+        const float* pi = p + (size_t)i * ldp;
+        int32_t tok;
+        if (i == k) {
+            const float u = lane0_uniform(s, sh);
+            const double tot = block_total(pi, n, sh);
+            tok = block_pick(n, [&](int j) { return pi[j]; }, (double)u * tot, sh);
+            all = 1;
+        } else {
+            const float ua = lane0_uniform(s, sh);
+            const float* qi = q + (size_t)i * ldq;
+            const float qx = qi[x[i]], px = pi[x[i]];
+            if (qx > 0.f && ua * qx < px) {
+                tok = x[i];
+                ++accepted;
+            } else {
+                const float ur = lane0_uniform(s, sh);
+                int acc = 0;
+                tok = accept_resample(pi, qi, n, x[i], 1.f, ur, &acc, sh);  // u_acc = 1: the residual branch
+            }
+        }
+        if (threadIdx.x == 0) {
+            record_tok(s, tok);
+            out[4 + emitted] = tok;
+        }
+        __syncthreads();
+        ++emitted;
+        last_tok = tok;
+        if (i == k || tok != x[i] || i + 1 > accepted) break;
+    }
+    if (threadIdx.x == 0) {
+        out[0] = emitted;
+        out[1] = accepted;
+        out[2] = emitted;
+        out[3] = all;
+        if (d_pos) {
+            *d_pos += emitted;
+            *d_next = last_tok;
+        }
+        if (d_budget) *d_budget -= emitted;
+    }
+}
+
 __global__ void k_sampler_history(const DevSampler* s, int32_t* out, int cap, int32_t* n_out) {
     if (threadIdx.x != 0) return;
     const int n = s->nh < cap ? s->nh : cap;
@@ -452,6 +710,52 @@ extern "C" int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, in
         return set_error(ORC_E_INVALID, "accept_engine: bad args");
     hipLaunchKernelGGL(k_accept_engine, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_logits,
                        ld, n_vocab, d_draft, n_draft, max_emit, d_budget, d_out, d_pos, d_next);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_transform_probs(const void* d_state, float* d_logits, int ld, int n_vocab, int rows,
+                                   const int32_t* d_extra, int extra_base, float* d_p, int ldp, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || !d_logits || !d_p || n_vocab <= 0 || rows < 1 || ld < n_vocab || ldp < n_vocab ||
+        extra_base < 0 || ((extra_base + rows > 1) && !d_extra))
+        return set_error(ORC_E_INVALID, "transform_probs: bad args");
+    hipLaunchKernelGGL(k_transform, dim3(rows), dim3(kST), 0, resolve_stream(s), (const DevSampler*)d_state,
+                       d_logits, ld, n_vocab, d_extra, extra_base, d_p, ldp);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_draw(void* d_state, const float* d_p, int n_vocab, int32_t* d_out, int32_t* d_out2,
+                        orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || !d_p || !d_out || n_vocab <= 0) return set_error(ORC_E_INVALID, "draw: bad args");
+    hipLaunchKernelGGL(k_draw, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_p, n_vocab, d_out,
+                       d_out2);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_accept_resample(const float* d_p, const float* d_q, int n_vocab, int32_t x, float u_acc,
+                                   float u_res, int32_t* d_out, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_p || !d_q || !d_out || n_vocab <= 0 || x < 0 || x >= n_vocab)
+        return set_error(ORC_E_INVALID, "accept_resample: bad args");
+    hipLaunchKernelGGL(k_accept_resample, dim3(1), dim3(kST), 0, resolve_stream(s), d_p, d_q, n_vocab, x, u_acc,
+                       u_res, d_out);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_spec_accept_stochastic(void* d_state, const float* d_p, int ldp, const float* d_q, int ldq,
+                                          int n_vocab, const int32_t* d_x, int k, int max_emit, int32_t* d_budget,
+                                          int32_t* d_out, int32_t* d_pos, int32_t* d_next, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || !d_p || !d_out || n_vocab <= 0 || ldp < n_vocab || k < 0 || (k && (!d_q || !d_x || ldq < n_vocab)) ||
+        (max_emit < 1 && !d_budget) || (!d_pos) != (!d_next))
+        return set_error(ORC_E_INVALID, "accept_stochastic: bad args");
+    hipLaunchKernelGGL(k_accept_chain, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_p, ldp, d_q,
+                       ldq, n_vocab, d_x, k, max_emit, d_budget, d_out, d_pos, d_next);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

@@ -111,10 +111,7 @@ extern "C" int orch_set_graphs(int on) {
 }
 
 
-extern "C" int orch_spec_engine(orch_model* t, orch_model* d, const int32_t* prompt, int np, int n_gen, int k,
-                                const float* sampler, const int32_t* isampler, uint64_t seed, int32_t* out,
-                                int64_t* stats) {
-    if (!t || !d || !prompt || !out || !sampler || !isampler) return -1;
+static SamplerConfig sampler_config(const float* sampler, const int32_t* isampler, uint64_t seed) {
     SamplerConfig sc;
     sc.temperature = sampler[0];
     sc.top_p = sampler[1];
@@ -122,8 +119,32 @@ extern "C" int orch_spec_engine(orch_model* t, orch_model* d, const int32_t* pro
     sc.top_k = isampler[0];
     sc.repeat_last = isampler[1];
     sc.seed = seed;
+    return sc;
+}
+
+extern "C" int orch_spec_engine(orch_model* t, orch_model* d, const int32_t* prompt, int np, int n_gen, int k,
+                                const float* sampler, const int32_t* isampler, uint64_t seed, int32_t* out,
+                                int64_t* stats) {
+    if (!t || !d || !prompt || !out || !sampler || !isampler) return -1;
     SpecStats st;
-    const int rc = session().spec_engine(t->m, d->m, prompt, np, n_gen, k, sc, out, &st);
+    const int rc = session().spec_engine(t->m, d->m, prompt, np, n_gen, k, sampler_config(sampler, isampler, seed),
+                                         out, &st);
+    if (rc < 0) return fail(t, rc);
+    if (stats) {
+        stats[0] = st.accepted;
+        stats[1] = st.proposed;
+        stats[2] = st.passes;
+    }
+    return rc;
+}
+
+extern "C" int orch_spec_sampled(orch_model* t, orch_model* d, const int32_t* prompt, int np, int n_gen, int k,
+                                 const float* sampler, const int32_t* isampler, uint64_t seed, int32_t* out,
+                                 int64_t* stats) {
+    if (!t || !d || !prompt || !out || !sampler || !isampler) return -1;
+    SpecStats st;
+    const int rc = session().spec_sampled(t->m, d->m, prompt, np, n_gen, k, sampler_config(sampler, isampler, seed),
+                                          out, &st);
     if (rc < 0) return fail(t, rc);
     if (stats) {
         stats[0] = st.accepted;

@@ -20,6 +20,9 @@ DecodeSession::~DecodeSession() {
     drop(greedy_g_);
     drop(spec_g_);
     drop(eng_g_);
+    drop(smp_g_);
+    orc_free(d_p_);
+    orc_free(d_q_);
     orc_free(d_samp_);
     orc_free(d_eout_);
     orc_free(d_budget_);
@@ -183,6 +186,36 @@ int DecodeSession::spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, in
     return ng;
 }
 
+// engine.cpp:115-125: reset both models, prefill prompt[0 .. n-2] on each
+// and initialise the device sampler with those ids recorded. ids = the
+// prompt with out-of-range ids clamped to 0 (model.cpp:352-356).
+int DecodeSession::begin_sampled(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, const SamplerConfig& sc,
+                                 std::vector<int32_t>& ids) {
+    const int V = (int)tgt.cfg.n_vocab;
+    ids.assign(prompt, prompt + n_prompt);
+    for (auto& t : ids)
+        if (t < 0 || t >= V) t = 0;
+    tgt.reset();
+    dft.reset();
+    if (n_prompt > 1) {
+        tgt.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
+        dft.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
+    }
+    int32_t* d_ph = nullptr;
+    if (n_prompt > 1) {
+        if (int rc = orc_malloc((void**)&d_ph, (size_t)(n_prompt - 1) * 4)) return rc;
+        if (int rc = orc_memcpy_h2d(d_ph, ids.data(), (size_t)(n_prompt - 1) * 4, nullptr)) {
+            orc_free(d_ph);
+            return rc;
+        }
+    }
+    int rc = orc_sampler_init(d_samp_, sc.temperature, sc.top_p, sc.top_k, sc.repeat_penalty, sc.repeat_last, sc.seed,
+                              d_ph, n_prompt - 1, nullptr);
+    orc_stream_sync(nullptr);
+    orc_free(d_ph);
+    return rc;
+}
+
 int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                                const SamplerConfig& sc, int32_t* out, SpecStats* st) {
     if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return ORC_E_INVALID;
@@ -191,28 +224,10 @@ int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, in
     SpecStats& S = st ? *st : local;
     const int V = (int)tgt.cfg.n_vocab;
     const int ctx = (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len);
-    std::vector<int32_t> ids(prompt, prompt + n_prompt);
-    for (auto& t : ids)
-        if (t < 0 || t >= V) t = 0;
-    // engine.cpp:115-125: reset, prefill n-1 prompt tokens on both models, record them
-    tgt.reset();
-    dft.reset();
-    int pos = 0;
-    if (n_prompt > 1) {
-        tgt.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
-        dft.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
-        pos = n_prompt - 1;
-    }
-    int32_t* d_ph = nullptr;
-    if (n_prompt > 1) {
-        if (int rc = orc_malloc((void**)&d_ph, (size_t)(n_prompt - 1) * 4)) return rc;
-        if (int rc = orc_memcpy_h2d(d_ph, ids.data(), (size_t)(n_prompt - 1) * 4, nullptr)) return rc;
-    }
-    int rc = orc_sampler_init(d_samp_, sc.temperature, sc.top_p, sc.top_k, sc.repeat_penalty, sc.repeat_last, sc.seed,
-                              d_ph, n_prompt - 1, nullptr);
-    orc_stream_sync(nullptr);
-    orc_free(d_ph);
+    std::vector<int32_t> ids;
+    int rc = begin_sampled(tgt, dft, prompt, n_prompt, sc, ids);
     if (rc) return rc;
+    int pos = n_prompt - 1;
 
     if (graphs_ && (eng_g_.a != tgt.uid() || eng_g_.b != dft.uid() || eng_g_.k != k || !eng_g_.g)) {
         drop(eng_g_);
@@ -258,6 +273,92 @@ int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, in
         if (h[3] && ng < n_gen) {  // every proposal accepted: the draft lacks d_{k-1} (engine.cpp:230)
             if (graphs_) {
                 if ((rc = orc_graph_launch(eng_g_.fill, nullptr))) return rc;
+            } else if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) {
+                return rc;
+            }
+        }
+        pos += emitted;
+    }
+    orc_stream_sync(nullptr);
+    return ng;
+}
+
+// One round of speculative sampling: k draft steps, each followed by the
+// sampler transform of its logits (pending proposals d_vin[1 .. i] in the
+// penalty window) into q_i and a draw x_i = d_vin[i+1]; one batched target
+// pass over d_vin[0 .. k]; the transform of its k+1 rows into p; the
+// acceptance chain, which advances *d_pos and writes the next input to d_vin[0].
+int DecodeSession::sampled_round(Model& tgt, Model& dft, int k, int V) {
+    for (int i = 0; i < k; ++i) {
+        float* q = d_q_ + (size_t)i * V;
+        if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, nullptr)) return rc;
+        if (int rc = orc_transform_probs(d_samp_, dft.d_logits(), V, V, 1, d_vin_ + 1, i, q, V, nullptr)) return rc;
+        if (int rc = orc_draw(d_samp_, q, V, d_vin_ + i + 1, nullptr, nullptr)) return rc;
+    }
+    if (int rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, nullptr)) return rc;
+    if (int rc = orc_transform_probs(d_samp_, tgt.d_logits(), V, V, k + 1, d_vin_ + 1, 0, d_p_, V, nullptr)) return rc;
+    return orc_spec_accept_stochastic(d_samp_, d_p_, V, d_q_, V, V, d_vin_ + 1, k, 0, d_budget_, d_eout_, d_pos_,
+                                      d_vin_, nullptr);
+}
+
+int DecodeSession::spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
+                                const SamplerConfig& sc, int32_t* out, SpecStats* st) {
+    if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return ORC_E_INVALID;
+    if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return ORC_E_INVALID;
+    SpecStats local;
+    SpecStats& S = st ? *st : local;
+    const int V = (int)tgt.cfg.n_vocab;
+    const int ctx = (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len);
+    const size_t need = (size_t)(max_k_ + 1) * V;
+    if (need > pq_cap_) {  // p: k+1 rows, q: k rows of the vocabulary
+        orc_free(d_p_);
+        orc_free(d_q_);
+        d_p_ = d_q_ = nullptr;
+        pq_cap_ = 0;
+        drop(smp_g_);
+        if (int rc = orc_malloc((void**)&d_p_, need * 4)) return rc;
+        if (int rc = orc_malloc((void**)&d_q_, need * 4)) return rc;
+        pq_cap_ = need;
+    }
+    std::vector<int32_t> ids;
+    int rc = begin_sampled(tgt, dft, prompt, n_prompt, sc, ids);
+    if (rc) return rc;
+    int pos = n_prompt - 1;
+
+    if (graphs_ && (smp_g_.a != tgt.uid() || smp_g_.b != dft.uid() || smp_g_.k != k || !smp_g_.g)) {
+        drop(smp_g_);
+        if ((rc = orc_graph_begin(nullptr))) return rc;
+        if ((rc = sampled_round(tgt, dft, k, V))) return abort_capture(rc);
+        if ((rc = orc_graph_end(nullptr, &smp_g_.g))) return rc;
+        if ((rc = orc_graph_begin(nullptr))) return rc;
+        if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) return abort_capture(rc);
+        if ((rc = orc_graph_end(nullptr, &smp_g_.fill))) return rc;
+        smp_g_.a = tgt.uid();
+        smp_g_.b = dft.uid();
+        smp_g_.k = k;
+    }
+    const int32_t next = ids[n_prompt - 1];
+    if ((rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr))) return rc;
+    if ((rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr))) return rc;
+    if ((rc = orc_memcpy_h2d(d_budget_, &n_gen, 4, nullptr))) return rc;
+    std::vector<int32_t> h(k + 5);
+    int ng = 0;
+    while (ng < n_gen && pos + k + 1 <= ctx) {
+        if (graphs_)
+            rc = orc_graph_launch(smp_g_.g, nullptr);
+        else
+            rc = sampled_round(tgt, dft, k, V);
+        if (rc) return rc;
+        if ((rc = orc_memcpy_d2h(h.data(), d_eout_, (size_t)(k + 5) * 4, nullptr))) return rc;
+        const int emitted = h[0];
+        S.accepted += h[1];
+        S.proposed += k;
+        S.passes += 1;
+        S.rounds++;
+        for (int i = 0; i < emitted && ng < n_gen; ++i) out[ng++] = h[4 + i];
+        if (h[3] && ng < n_gen) {  // every proposal accepted: the draft lacks x_{k-1}
+            if (graphs_) {
+                if ((rc = orc_graph_launch(smp_g_.fill, nullptr))) return rc;
             } else if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) {
                 return rc;
             }

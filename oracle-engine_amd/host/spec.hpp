@@ -40,6 +40,7 @@ public:
         drop(greedy_g_);
         drop(spec_g_);
         drop(eng_g_);
+        drop(smp_g_);
     }
     bool graphs() const { return graphs_; }
 
@@ -58,6 +59,16 @@ public:
     int spec_engine(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                     const SamplerConfig& sc, int32_t* out, SpecStats* st);
 
+    // Speculative sampling with the exact-distribution rule (no reference
+    // counterpart): same reset / prefill / recorded prompt as spec_engine; the
+    // draft proposes x_i ~ q_i (its logits through the sampler transform, with
+    // pending proposals in the penalty window), the target scores the round in
+    // one batch, proposal i is accepted with min(1, p_i/q_i), a rejection
+    // emits a residual draw, a fully accepted round a bonus draw from p_k.
+    // stats: accepted, proposed, target passes (one per round).
+    int spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
+                     const SamplerConfig& sc, int32_t* out, SpecStats* st);
+
 private:
     int max_tokens_, max_k_;
     bool graphs_ = true;
@@ -72,11 +83,17 @@ private:
         int k = -1;
         orc_graph_t g = nullptr, fill = nullptr;
     };
-    Captured greedy_g_, spec_g_, eng_g_;
+    Captured greedy_g_, spec_g_, eng_g_, smp_g_;
+    float* d_p_ = nullptr;  // target distributions, k+1 rows
+    float* d_q_ = nullptr;  // draft distributions, k rows
+    size_t pq_cap_ = 0;     // floats in each of d_p_ / d_q_
     void* d_samp_ = nullptr;      // device sampler state
     int32_t* d_eout_ = nullptr;   // Engine-style acceptance output (k+5 ints)
     int32_t* d_budget_ = nullptr; // tokens still to emit
     void drop(Captured& c);
+    int begin_sampled(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, const SamplerConfig& sc,
+                      std::vector<int32_t>& ids);
+    int sampled_round(Model& tgt, Model& dft, int k, int V);
     int greedy_graphed(Model& m, int pos, int32_t first, int n_gen, int32_t* out);
     int spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx, int32_t* out,
                      SpecStats& S);

@@ -87,6 +87,11 @@ ABI = [
     ("orc_sampler_history", C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
     ("orc_spec_accept_engine", C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp,
                                          _vp]),
+    ("orc_transform_probs", C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp]),
+    ("orc_draw", C.c_int, [_vp, _vp, C.c_int, _vp, _vp, _vp]),
+    ("orc_accept_resample", C.c_int, [_vp, _vp, C.c_int, C.c_int32, C.c_float, C.c_float, _vp, _vp]),
+    ("orc_spec_accept_stochastic", C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
+                                             _vp, _vp, _vp, _vp]),
     ("orc_prof_enable", C.c_int, [C.c_int]),
     ("orc_prof_accumulate", C.c_int, []),
     ("orc_prof_read", C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double),
@@ -184,6 +189,8 @@ HOST_ABI = [
     ("orch_spec_greedy", C.c_int, [_vp, _vp, _ip, C.c_int, C.c_int, C.c_int, _ip, C.POINTER(C.c_int64), C.c_int]),
     ("orch_spec_engine", C.c_int, [_vp, _vp, _ip, C.c_int, C.c_int, C.c_int, _fp, _ip, C.c_uint64, _ip,
                                    C.POINTER(C.c_int64)]),
+    ("orch_spec_sampled", C.c_int, [_vp, _vp, _ip, C.c_int, C.c_int, C.c_int, _fp, _ip, C.c_uint64, _ip,
+                                    C.POINTER(C.c_int64)]),
     ("orch_set_graphs", C.c_int, [C.c_int]),
     ("orch_weight_bytes", C.c_double, [_vp, C.c_int]),
     ("orch_sync", C.c_int, []),
@@ -284,6 +291,19 @@ class Model:
         n = self._check(self.L.orch_spec_engine(self.h, draft.h, prompt.ctypes.data_as(_ip), prompt.size, n_gen, k,
                                                 fs.ctypes.data_as(_fp), iv.ctypes.data_as(_ip), int(seed),
                                                 out.ctypes.data_as(_ip), st.ctypes.data_as(C.POINTER(C.c_int64))))
+        return out[:n], {"accepted": int(st[0]), "proposed": int(st[1]), "passes": int(st[2])}
+
+    def spec_sampled(self, draft, prompt, n_gen, k, temperature=0.8, top_p=0.95, top_k=40, repeat_penalty=1.1,
+                     repeat_last=64, seed=42):
+        """Speculative sampling (min(1, p/q) acceptance, residual resampling) on the device."""
+        prompt = _i32(prompt)
+        out = np.empty(n_gen + k + 2, np.int32)
+        st = np.zeros(3, np.int64)
+        fs = np.array([temperature, top_p, repeat_penalty], np.float32)
+        iv = np.array([top_k, repeat_last], np.int32)
+        n = self._check(self.L.orch_spec_sampled(self.h, draft.h, prompt.ctypes.data_as(_ip), prompt.size, n_gen, k,
+                                                 fs.ctypes.data_as(_fp), iv.ctypes.data_as(_ip), int(seed),
+                                                 out.ctypes.data_as(_ip), st.ctypes.data_as(C.POINTER(C.c_int64))))
         return out[:n], {"accepted": int(st[0]), "proposed": int(st[1]), "passes": int(st[2])}
 
     def weight_bytes(self, logits=True):

@@ -881,3 +881,99 @@ int32_t orco_accept_resample(const float* p, const float* q, int n, int32_t x, f
     }
     return last;
 }
+
+/* One draw from non-negative weights w with the uniform u: the first index
+ * whose running sum (double) of the positive weights reaches u * total;
+ * the last positive index if rounding leaves the sum short. */
+int32_t orco_pick(const float* w, int n, float u) {
+    double tot = 0.0;
+    for (int i = 0; i < n; i++) if (w[i] > 0.f) tot += w[i];
+    double r = (double)u * tot;
+    int last = -1;
+    for (int i = 0; i < n; i++) {
+        if (!(w[i] > 0.f)) continue;
+        last = i;
+        r -= w[i];
+        if (r <= 0.0) return i;
+    }
+    return last < 0 ? 0 : last;
+}
+
+int orco_accept_chain(orco_sampler* s, const float* p, const float* q, int n, const int32_t* x, int k, int max_emit,
+                      int32_t* out, int* accepted, int* all) {
+    int emitted = 0;
+    *accepted = *all = 0;
+    for (int i = 0; i <= k && emitted < max_emit; i++) {
+        int32_t tok;
+        int acc = 0;
+        const float* pi = p + (size_t)i * n;
+        if (i == k) {
+            tok = orco_pick(pi, n, mt_canonical(s));
+            *all = 1;
+        } else {
+            const float* qi = q + (size_t)i * n;
+            const float ua = mt_canonical(s);
+            if (qi[x[i]] > 0.f && ua * qi[x[i]] < pi[x[i]]) { tok = x[i]; acc = 1; }
+            else tok = orco_accept_resample(pi, qi, n, x[i], 1.f, mt_canonical(s), &acc);
+        }
+        orco_sampler_record(s, tok);
+        out[emitted++] = tok;
+        if (i == k || !acc) break;
+        ++*accepted;
+    }
+    return emitted;
+}
+
+/* penalty window: the last `last` entries of history + pending proposals */
+static int window(const orco_sampler* s, const int32_t* pend, int npend, int32_t* win) {
+    int L = s->nh + npend, st = L - s->last > 0 ? L - s->last : 0, n = 0;
+    for (int i = st; i < L; i++) win[n++] = i < s->nh ? s->hist[i] : pend[i - s->nh];
+    return n;
+}
+
+int orco_spec_sampled(orco_model* tg, orco_model* df, const int32_t* prompt, int np, int n_gen, int k,
+                      orco_sampler* s, int32_t* out, int64_t* st) {
+    orco_model_reset(tg);
+    orco_model_reset(df);
+    const int V = tg->V, CTX = tg->CTX < df->CTX ? tg->CTX : df->CTX;
+    int pos = 0, ng = 0;
+    st[0] = st[1] = st[2] = 0;
+    if (np > 1) { /* prompt[0..np-2] prefilled and recorded, as engine.cpp:115-125 */
+        orco_model_forward_batch(tg, prompt, np - 1, 0, NULL);
+        orco_model_forward_batch(df, prompt, np - 1, 0, NULL);
+        for (int i = 0; i < np - 1; i++) orco_sampler_record(s, prompt[i]);
+        pos = np - 1;
+    }
+    int32_t next = prompt[np - 1];
+    float* lg = (float*)malloc(sizeof(float) * (size_t)(k + 1) * V);
+    float* p = (float*)malloc(sizeof(float) * (size_t)(k + 1) * V);
+    float* q = (float*)malloc(sizeof(float) * (size_t)k * V);
+    int32_t* win = (int32_t*)malloc(sizeof(int32_t) * (size_t)(s->last + 1));
+    int32_t vin[65];
+    while (ng < n_gen && pos + k + 1 <= CTX) {
+        vin[0] = next;
+        for (int i = 0; i < k; i++) { /* proposals x_i ~ q_i */
+            orco_model_forward(df, vin[i], pos + i, lg);
+            int nw = window(s, vin + 1, i, win);
+            orco_transform_probs(lg, V, win, nw, s->temp, s->top_p, s->top_k, s->pen, q + (size_t)i * V);
+            vin[i + 1] = orco_pick(q + (size_t)i * V, V, mt_canonical(s));
+        }
+        orco_model_forward_batch(tg, vin, k + 1, pos, lg);
+        for (int r = 0; r <= k; r++) {
+            int nw = window(s, vin + 1, r, win);
+            orco_transform_probs(lg + (size_t)r * V, V, win, nw, s->temp, s->top_p, s->top_k, s->pen,
+                                 p + (size_t)r * V);
+        }
+        st[1] += k;
+        st[2]++;
+        int acc = 0, all = 0;
+        const int emitted = orco_accept_chain(s, p, q, V, vin + 1, k, n_gen - ng, out + ng, &acc, &all);
+        st[0] += acc;
+        ng += emitted;
+        next = out[ng - 1];
+        pos += emitted;
+        if (all && ng < n_gen) orco_model_forward(df, vin[k], pos - 1, NULL); /* the draft lacks x_{k-1} */
+    }
+    free(lg); free(p); free(q); free(win);
+    return ng;
+}

@@ -87,6 +87,29 @@ int orco_transform_probs(const float* logits, int n, const int32_t* hist, int n_
  * from norm(max(0, p - q)) using u_res. */
 int32_t orco_accept_resample(const float* p, const float* q, int n, int32_t x, float u_acc, float u_res,
                              int* accepted);
+/* One draw from non-negative weights with the uniform u (first index where
+ * the double running sum reaches u * total). */
+int32_t orco_pick(const float* w, int n, float u);
+/* One round's acceptance chain over rows p[0..k] and q[0..k-1] (n floats
+ * each) for the proposals x[0..k-1]: u_acc per proposal from the sampler's
+ * mt19937, accept when q_i[x_i] > 0 and u_acc * q_i[x_i] < p_i[x_i], else one
+ * more uniform for the residual draw and stop; after k acceptances a bonus
+ * draw from p_k. At most max_emit ids; each emitted id is recorded. Returns
+ * the number emitted. */
+int orco_accept_chain(orco_sampler* s, const float* p, const float* q, int n, const int32_t* x, int k, int max_emit,
+                      int32_t* out, int* accepted, int* all);
+/* Speculative sampling loop (no reference counterpart; the round shape is
+ * bench_engine.cpp:300-356): the draft proposes x_i ~ q_i (its logits through
+ * the sampler transform, pending proposals in the penalty window), the target
+ * scores next, x_0..x_{k-1} in one batch, proposal i is accepted with
+ * min(1, p_i/q_i), a rejection emits a residual draw, a fully accepted round
+ * a bonus draw from p_k. Uniforms from the sampler's mt19937 in this order:
+ * the k proposal draws, then per proposal u_acc (and u_res on rejection),
+ * then the bonus. Emitted ids are recorded once; prompt[0..np-2] is
+ * prefilled and recorded first (engine.cpp:115-125). Rounds run while
+ * pos + k + 1 <= the smaller context. stats: accepted, proposed, rounds. */
+int orco_spec_sampled(orco_model* tgt, orco_model* dft, const int32_t* prompt, int np, int n_gen, int k,
+                      orco_sampler* s, int32_t* out, int64_t* stats);
 
 #ifdef __cplusplus
 }

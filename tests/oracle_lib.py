@@ -78,6 +78,11 @@ class Oracle:
         L.orco_transform_probs.argtypes = [_fp, C.c_int, _ip, C.c_int, C.c_float, C.c_float, C.c_int, C.c_float, _fp]
         L.orco_accept_resample.restype = C.c_int32
         L.orco_accept_resample.argtypes = [_fp, _fp, C.c_int, C.c_int32, C.c_float, C.c_float, C.POINTER(C.c_int)]
+        L.orco_accept_chain.argtypes = [C.c_void_p, _fp, _fp, C.c_int, _ip, C.c_int, C.c_int, _ip,
+                                        C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        L.orco_pick.restype = C.c_int32
+        L.orco_pick.argtypes = [_fp, C.c_int, C.c_float]
+        L.orco_spec_sampled.argtypes = [C.c_void_p, C.c_void_p, _ip, C.c_int, C.c_int, C.c_int, C.c_void_p, _ip, _lp]
 
     # codecs / kernels
     def dequant(self, t, raw, n):
@@ -178,4 +183,15 @@ class OracleModel:
         st = np.zeros(3, np.int64)
         n = self.o.L.orco_spec_greedy(self.h, draft.h, iptr(prompt), prompt.size, n_gen, k, iptr(out),
                                       st.ctypes.data_as(_lp))
+        return out[:n], {"accepted": int(st[0]), "proposed": int(st[1]), "passes": int(st[2])}
+
+    def spec_sampled(self, draft, prompt, n_gen, k, temperature=0.8, top_p=0.95, top_k=40, repeat_penalty=1.1,
+                     repeat_last=64, seed=42):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(n_gen + k + 2, np.int32)
+        st = np.zeros(3, np.int64)
+        s = self.o.L.orco_sampler_new(temperature, top_p, top_k, repeat_penalty, repeat_last, seed)
+        n = self.o.L.orco_spec_sampled(self.h, draft.h, iptr(prompt), prompt.size, n_gen, k, s, iptr(out),
+                                       st.ctypes.data_as(_lp))
+        self.o.L.orco_sampler_free(s)
         return out[:n], {"accepted": int(st[0]), "proposed": int(st[1]), "passes": int(st[2])}

@@ -345,3 +345,43 @@ def test_transform_greedy_limit(oracle):
     assert p[np.argmax(lg)] == 1.0 and p.sum() == 1.0
     p = _probs(oracle, lg, 0.8, 1.0, 1)
     assert p[np.argmax(lg)] == 1.0
+
+
+@pytest.mark.parametrize("k", [2, 4])
+def test_sampled_spec_greedy_limit(oracle, models_dir, k):
+    """Speculative sampling at T = 0 without penalty puts all of p and q on the
+    argmax: proposals are the draft's greedy ids, acceptance is equality, the
+    residual is the target's argmax. So the stream and stats are the
+    reference's batched speculative greedy ones."""
+    tgt = ol.OracleModel(oracle, str(models_dir / "t-q4k.gguf"))
+    dft = ol.OracleModel(oracle, str(models_dir / "t-q4k-d.gguf"))
+    toks, st = tgt.spec_sampled(dft, FIX["greedy/t-q4k/prompt"], 40, k, 0.0, 1.0, 0, 1.0, 64, 7)
+    assert np.array_equal(toks, FIX[f"spec/k{k}/tokens"])
+    assert [st["accepted"], st["proposed"], st["passes"]] == list(FIX[f"spec/k{k}/stats"])
+
+
+def test_sampled_spec_first_token_is_target_distributed(oracle, models_dir):
+    """The first emitted id of speculative sampling is distributed as the
+    target's own sampler distribution at that position, whatever the draft
+    proposes (chi-square over seeds; p from the transform of the target's
+    logits, the draft an independent model, so most proposals are rejected
+    and the residual draw is what is tested)."""
+    tgt = ol.OracleModel(oracle, str(models_dir / "t-qwen.gguf"))
+    dft = ol.OracleModel(oracle, str(models_dir / "t-qwen-d.gguf"))
+    prompt = np.ascontiguousarray(FIX["greedy/t-qwen/prompt"][:3], np.int32)
+    T, P, K = 1.5, 1.0, 5
+    tgt.reset()
+    tgt.forward_batch(prompt[:-1], 0, logits=False)
+    lg = tgt.forward(int(prompt[-1]), prompt.size - 1)
+    p = _probs(oracle, lg, T, P, K, 1.1, prompt[:-1])
+    N = 300
+    counts = np.zeros(lg.size)
+    for seed in range(N):
+        toks, _ = tgt.spec_sampled(dft, prompt, 1, 1, T, P, K, 1.1, 64, seed)
+        counts[toks[0]] += 1
+    keep = p > 0
+    assert keep.sum() == K and counts[~keep].sum() == 0
+    exp = N * p[keep]
+    chi2 = ((counts[keep] - exp) ** 2 / exp).sum()
+    # 4 degrees of freedom: P(chi2 > 23.5) = 1e-4
+    assert chi2 < 23.5, (chi2, counts[keep], exp)
