@@ -5,7 +5,12 @@
 // them (RMSNorm, QKV bias, residual add, SwiGLU; core/model.cpp:366-473,
 // 565-643).
 //
-// Design (one kernel family; n_tok = 1 is the decode GEMV):
+// Two kernel families. Q4_K and Q6_K matrices (a Q4_K_M target's) run on the
+// matrix cores (k_mmq, below); Q8_0 and Q4_0 on the vector ALUs (k_qmv).
+// Either way one matrix always uses one family and one reduction order, so
+// n-token results equal n decode results bit for bit.
+//
+// k_qmv design (n_tok = 1 is the decode GEMV):
 //  * Persistent 512-thread workgroups (one or two per CU). A workgroup stages
 //    the activations of all n_tok tokens in LDS once (fp32, 4 floats of
 //    padding every 32/64 values so the lanes of a slot hit distinct banks,
@@ -45,6 +50,15 @@ template <> struct QTr<ORC_Q4_K> { static constexpr int EPU = 32, PP = 64, LPR =
 template <> struct QTr<ORC_Q6_K> { static constexpr int EPU = 64, PP = 64, LPR = 16; };
 
 template <int PP> __device__ __forceinline__ int padx(int k) { return k + 4 * (k / PP); }
+
+// Segment pointers held in scalar registers: readfirstlane keeps the
+// compiler from turning a lane-dependent choice between them back into a
+// vector load from the parameter block (and a wait on it).
+template <class T> __device__ __forceinline__ T* spin(T* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (T*)(((uint64_t)hi << 32) | lo);
+}
 
 struct XCtx {
     const float* xs;  // staged x (times the norm weight), token 0, element 0, padded
@@ -351,27 +365,31 @@ __device__ __forceinline__ void map_rows(const QmvParams& p, int g, int slot, Ro
     R.jl0 = jl0;
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        int seg = 0, j;
+        // segments by comparisons and constant indices (see mrow)
         constexpr int H = ROWS >= 2 ? ROWS / 2 : 1;  // SwiGLU launches use an even ROWS
+        int j;
+        bool s1, s2 = false;
         if (p.epi == ORC_EPI_SWIGLU) {
             j = jl0 / 2 + r % H;
-            seg = r / H;
+            s1 = r / H == 1;  // compile-time per r
             R.ok[r] = j < p.rows[0];
         } else {
             j = jl0 + r;
             R.ok[r] = j < p.n_rows;
-            while (seg + 1 < p.n_seg && j >= p.rows[seg]) {
-                j -= p.rows[seg];
-                ++seg;
-            }
+            s1 = p.n_seg > 1 && j >= p.rows[0];
+            s2 = p.n_seg > 2 && j >= p.rows[0] + p.rows[1];
+            j = s2 ? j - p.rows[0] - p.rows[1] : (s1 ? j - p.rows[0] : j);
         }
         if (!R.ok[r]) {
-            seg = 0;
+            s1 = s2 = false;
             j = 0;
         }
-        R.rp[r] = p.w[seg] + (size_t)j * p.row_bytes;
-        R.y[r] = p.y[seg] + j;
-        R.bias[r] = p.bias[seg] ? p.bias[seg] + j : nullptr;
+        const uint8_t* w = s2 ? spin(p.w[2]) : (s1 ? spin(p.w[1]) : spin(p.w[0]));
+        float* yb = s2 ? spin(p.y[2]) : (s1 ? spin(p.y[1]) : spin(p.y[0]));
+        const float* bb = s2 ? spin(p.bias[2]) : (s1 ? spin(p.bias[1]) : spin(p.bias[0]));
+        R.rp[r] = w + (size_t)j * p.row_bytes;
+        R.y[r] = yb + j;
+        R.bias[r] = bb ? bb + j : nullptr;
     }
 }
 
@@ -531,6 +549,643 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
     }
 }
 
+// ── matrix-core path (Q4_K, Q6_K) ────────────────────────────────────────────
+// Activations are the MFMA's A operand (16 token rows, the batch's tokens and
+// padding), weights the B operand (16 weight rows of a tile), so D[token][row]
+// lands with one weight row per lane: lane l holds D[4 (l/16) + i][l % 16].
+// Each activation x' (x times the norm weight times a per-token power of two
+// that keeps it inside the fp16 range) is split as hi = fp16(x'),
+// lo = fp16(x' - hi); hi + lo carries ~22 bits and every product with a
+// weight code is exact in fp32, so D matches an fp32 dot product to fp32
+// rounding.
+//  * Q4_K: the 6-bit sub-block scale is folded into the code (sc * q <= 945,
+//    exact in fp16), so one v_mfma_f32_16x16x32_f16 chain covers a whole unit
+//    whatever sub-blocks its k values come from; d scales the chain and the
+//    minimum term dmin * m * sum(x) is added per sub-block on the VALU.
+//  * Q6_K: scales are int8 (sc * q does not fit fp16), so every 16-value
+//    sub-block gets its own v_mfma_f32_16x16x16_f16 pair scaled by d * sc.
+//    The four lanes of a weight row load 16-byte runs and exchange 4-byte
+//    words (permlane16/32 swaps) so each sub-block's 16 codes spread over the
+//    four lane groups as the instruction expects.
+// A unit is half a superblock (128 values) of one row. The eight waves of a
+// workgroup split a tile's units into fixed contiguous ranges and their
+// partial sums are added in wave order, so a (token, row) result does not
+// depend on the token count: a (k+1)-token verify equals k+1 decode GEMVs.
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kMWG = 512, kMW = kMWG / 64;
+constexpr int kMmqMaxNT = 8;
+
+// code permutation of one 8-value slice (bytes 0,2 / 1,3 / 4,6 / 5,7 of a
+// nibble or byte run land in consecutive halves); it is its own inverse
+__device__ __forceinline__ int perm8(int j) { return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1); }
+
+template <int QT> struct MTr;
+template <> struct MTr<ORC_Q4_K> { static constexpr int SL = 4, AB = 32; };  // slices per unit, A bytes per (slice, lane)
+template <> struct MTr<ORC_Q6_K> { static constexpr int SL = 8, AB = 16; };
+
+// A-operand slot (byte offset inside a token-major entry table) of element kk
+// (0..255) of superblock b, and the position j of the element in its slot.
+template <int QT> __device__ __forceinline__ void a_slot(int b, int kk, int& u, int& i, int& c, int& j);
+template <> __device__ __forceinline__ void a_slot<ORC_Q4_K>(int b, int kk, int& u, int& i, int& c, int& j) {
+    const int g = kk >> 6, nib = (kk >> 5) & 1, o = kk & 31;
+    u = 2 * b + (g >> 1);
+    c = 2 * (g & 1) + (o >> 4);
+    i = 2 * nib + ((o >> 3) & 1);
+    j = perm8(o & 7);
+}
+template <> __device__ __forceinline__ void a_slot<ORC_Q6_K>(int b, int kk, int& u, int& i, int& c, int& j) {
+    const int hh = kk >> 7, r = kk & 127, g = r >> 5, jh = (r >> 4) & 1, k16 = r & 15;
+    u = 2 * b + hh;
+    i = 2 * g + jh;
+    c = k16 >> 2;
+    j = perm8(k16 & 3);  // perm8 maps 0..3 onto 0,2,1,3
+}
+
+// Loads through the global address space (a generic pointer would make
+// them flat loads, which LDS waits also have to drain).
+typedef const __attribute__((address_space(1))) u32x4_u* g16p;
+typedef const __attribute__((address_space(1))) u32x2_u* g8p;
+typedef const __attribute__((address_space(1))) u16_u* g2p;
+__device__ __forceinline__ u32x4 ldg16(const uint8_t* p) { return *(g16p)p; }
+__device__ __forceinline__ u32x2 ldg8(const uint8_t* p) { return *(g8p)p; }
+__device__ __forceinline__ uint32_t ldg2(const uint8_t* p) { return *(g2p)p; }
+
+// Q4_K (scale, min) of sub-block 4h + k (h = 0, 1 is wave-uniform, k = 0..3
+// may differ per lane), branch-free (core/gguf_parser.cpp:1085-1093).
+__device__ __forceinline__ void q4k_sm(int h, int k, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc, uint32_t& mn) {
+    const uint32_t b0 = (s0 >> (8 * k)) & 0xFFu, b1 = (s1 >> (8 * k)) & 0xFFu, b2 = (s2 >> (8 * k)) & 0xFFu;
+    sc = h ? ((b2 & 0xFu) | ((b0 >> 6) << 4)) : (b0 & 63u);
+    mn = h ? ((b2 >> 4) | ((b1 >> 6) << 4)) : (b1 & 63u);
+}
+
+// Loaded bytes of one unit of one row.
+template <int QT> struct MUnit;
+template <> struct MUnit<ORC_Q4_K> {
+    u32x4 hdr, q;  // d, dmin, 12 scale bytes; 16 code bytes of the lane's run
+    __device__ __forceinline__ void load(const uint8_t* row, int u, int c) {
+        const uint8_t* blk = row + (size_t)(u >> 1) * 144;
+        hdr = ldg16(blk);
+        q = ldg16(blk + 16 + 64 * (u & 1) + 16 * c);
+    }
+};
+template <> struct MUnit<ORC_Q6_K> {
+    u32x4 ql, qh;
+    u32x2 sc;
+    uint32_t dh;
+    __device__ __forceinline__ void load(const uint8_t* row, int u, int c) {
+        const uint8_t* blk = row + (size_t)(u >> 1) * 210;
+        const int hh = u & 1;
+        ql = ldg16(blk + 64 * hh + 16 * c);
+        qh = ldg16(blk + 128 + 32 * hh + 16 * (c & 1));
+        sc = ldg8(blk + 192 + 8 * hh);
+        dh = ldg2(blk + 208);
+    }
+};
+
+// 4x4 transpose of dwords across the four 16-lane groups: afterwards group c
+// holds in v[w] what group w held in v[c].
+__device__ __forceinline__ void xpose4(uint32_t& v0, uint32_t& v1, uint32_t& v2, uint32_t& v3) {
+    auto a = __builtin_amdgcn_permlane32_swap(v0, v2, false, false);
+    auto b = __builtin_amdgcn_permlane32_swap(v1, v3, false, false);
+    auto e = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    auto f = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    v0 = e[0];
+    v1 = e[1];
+    v2 = f[0];
+    v3 = f[1];
+}
+
+__device__ __forceinline__ h2v as_h2(uint32_t v) { return __builtin_bit_cast(h2v, v); }
+
+// Where a unit's activations live in LDS.
+struct MCtx {
+    const uint8_t* abase;  // A entries: [unit][slice][lane group][token] hi | lo
+    int a_stride_u;        // bytes per unit
+    const float* sx;       // Q4_K: sums of x g over each 32-value sub-block, [token][sub-block]
+    int sx_stride;
+    const float* esc;      // 2^-e of each (unit, token), [unit][NTP]
+};
+
+template <int NT> constexpr int ntp() { return (NT + 3) & ~3; }
+
+// Q4_K unit of TR tiles: one scale-folded chain per tile, then
+// acc += d 2^-e D - sum over the unit's sub-blocks of dmin m sum(x g).
+template <int NT, int TR>
+__device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int u, int lane, const MCtx& m,
+                                             f4v (&acc)[TR]) {
+    const int c = lane >> 4, t = lane & 15;
+    const int h = u & 1;
+    f4v D[TR];
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) D[tr] = f4v{0.f, 0.f, 0.f, 0.f};
+    // scale-folded codes: slices 0,1 use sub-block 4h + 2(c/2), slices 2,3 the next one
+    uint32_t bq[TR][4][4];
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) {
+        uint32_t s0, m0, s1, m1;
+        q4k_sm(h, 2 * (c >> 1), M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, s0, m0);
+        q4k_sm(h, 2 * (c >> 1) + 1, M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, s1, m1);
+        const _Float16 f0 = (_Float16)(float)s0, f1 = (_Float16)(float)s1;
+        const h2v sc0{f0, f0}, sc1{f1, f1};
+        const h2v of0{(_Float16)(-1024.f * (float)s0), (_Float16)(-1024.f * (float)s0)};
+        const h2v of1{(_Float16)(-1024.f * (float)s1), (_Float16)(-1024.f * (float)s1)};
+        const uint32_t w[4] = {M[tr].q.x, M[tr].q.y, M[tr].q.z, M[tr].q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t va = w[2 * (i & 1)], vb = w[2 * (i & 1) + 1];
+            const int sh = 4 * (i >> 1);
+            const uint32_t r[4] = {((va >> sh) & 0x000F000Fu) | 0x64006400u, ((va >> (sh + 8)) & 0x000F000Fu) | 0x64006400u,
+                                   ((vb >> sh) & 0x000F000Fu) | 0x64006400u, ((vb >> (sh + 8)) & 0x000F000Fu) | 0x64006400u};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const h2v x = as_h2(r[k]);
+                // (1024 + q) sc - 1024 sc = sc q, exact with one rounding
+                const h2v y = (i >> 1) ? __builtin_elementwise_fma(x, sc1, of1) : __builtin_elementwise_fma(x, sc0, of0);
+                bq[tr][i][k] = __builtin_bit_cast(uint32_t, y);
+            }
+        }
+    }
+    // every LDS read of the unit under one branch, all in flight together
+    u32x4 ah[4], al[4];
+    float4 es = make_float4(0.f, 0.f, 0.f, 0.f), s4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ah[i] = al[i] = u32x4{0u, 0u, 0u, 0u};
+        s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (t < NT) {
+        const uint8_t* ap = m.abase + (size_t)u * m.a_stride_u + (size_t)(c * NT + t) * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ah[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 32);
+            al[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 32 + 16);
+        }
+    }
+    if (4 * c < NT) {
+        es = *(const float4*)(m.esc + u * ntp<NT>() + 4 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s4[i] = *(const float4*)(m.sx + min(4 * c + i, NT - 1) * m.sx_stride + 4 * u);
+    }
+    // hi and lo products in two independent chains, added at the end
+    f4v Dl[TR];
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) Dl[tr] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h8v ahi = __builtin_bit_cast(h8v, ah[i]), alo = __builtin_bit_cast(h8v, al[i]);
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) {
+            const h8v b = __builtin_bit_cast(h8v, u32x4{bq[tr][i][0], bq[tr][i][1], bq[tr][i][2], bq[tr][i][3]});
+            D[tr] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, D[tr], 0, 0, 0);
+            Dl[tr] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, Dl[tr], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) D[tr] = D[tr] + Dl[tr];
+    const float esv[4] = {es.x, es.y, es.z, es.w};
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) {
+        const float d = h2f(M[tr].hdr.x & 0xFFFFu), dmin = h2f(M[tr].hdr.x >> 16);
+        float mm[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint32_t sc, mn;
+            q4k_sm(h, s, M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, sc, mn);
+            mm[s] = dmin * (float)mn;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float a = __builtin_fmaf(d * esv[i], D[tr][i], acc[tr][i]);
+            a = __builtin_fmaf(-mm[0], s4[i].x, a);
+            a = __builtin_fmaf(-mm[1], s4[i].y, a);
+            a = __builtin_fmaf(-mm[2], s4[i].z, a);
+            a = __builtin_fmaf(-mm[3], s4[i].w, a);
+            acc[tr][i] = a;
+        }
+    }
+}
+
+// Q6_K unit of TR tiles: eight 16-value sub-blocks, each its own scaled pair.
+template <int NT, int TR>
+__device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int u, int lane, const MCtx& m,
+                                             f4v (&acc)[TR]) {
+    const int c = lane >> 4, t = lane & 15;
+    uint32_t ql[TR][4], qh[TR][4];
+    float dd[TR];
+    f4v T[TR];
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) {
+        ql[tr][0] = M[tr].ql.x;
+        ql[tr][1] = M[tr].ql.y;
+        ql[tr][2] = M[tr].ql.z;
+        ql[tr][3] = M[tr].ql.w;
+        qh[tr][0] = M[tr].qh.x;
+        qh[tr][1] = M[tr].qh.y;
+        qh[tr][2] = M[tr].qh.z;
+        qh[tr][3] = M[tr].qh.w;
+        xpose4(ql[tr][0], ql[tr][1], ql[tr][2], ql[tr][3]);
+        xpose4(qh[tr][0], qh[tr][1], qh[tr][2], qh[tr][3]);
+        dd[tr] = h2f(M[tr].dh);
+        T[tr] = f4v{0.f, 0.f, 0.f, 0.f};
+    }
+    // every LDS read of the unit under one branch, all in flight together
+    u32x4 av[8];
+    float4 es = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) av[i] = u32x4{0u, 0u, 0u, 0u};
+    if (t < NT) {
+        const uint8_t* ap = m.abase + (size_t)u * m.a_stride_u + (size_t)(c * NT + t) * 16;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) av[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 16);
+    }
+    if (4 * c < NT) es = *(const float4*)(m.esc + u * ntp<NT>() + 4 * c);
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh) {
+            const int i = 2 * g + jh, src = 2 * (g & 1) + jh;
+            const h4v ahi = __builtin_bit_cast(h4v, u32x2{av[i].x, av[i].y}), alo = __builtin_bit_cast(h4v, u32x2{av[i].z, av[i].w});
+#pragma unroll
+            for (int tr = 0; tr < TR; ++tr) {
+                const uint32_t q = ((ql[tr][src] >> (4 * (g >> 1))) & 0x0F0F0F0Fu) |
+                                   (((qh[tr][src] >> (2 * g)) & 0x03030303u) << 4);
+                const h2v lo2 = as_h2((q & 0x00FF00FFu) | 0x64006400u), hi2 = as_h2(((q >> 8) & 0x00FF00FFu) | 0x64006400u);
+                const h2v off{(_Float16)-1056.f, (_Float16)-1056.f};  // 1024 + 32: codes are stored +32
+                const h2v b0 = lo2 + off, b1 = hi2 + off;
+                const h4v b{b0[0], b0[1], b1[0], b1[1]};
+                const f4v Dh = __builtin_amdgcn_mfma_f32_16x16x16f16(ahi, b, f4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const f4v D = Dh + __builtin_amdgcn_mfma_f32_16x16x16f16(alo, b, f4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const uint32_t sw = i < 4 ? M[tr].sc.x : M[tr].sc.y;
+                const float s = dd[tr] * (float)(int8_t)((sw >> (8 * (i & 3))) & 0xFFu);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) T[tr][k] = __builtin_fmaf(s, D[k], T[tr][k]);
+            }
+        }
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) {
+        acc[tr][0] = __builtin_fmaf(es.x, T[tr][0], acc[tr][0]);
+        acc[tr][1] = __builtin_fmaf(es.y, T[tr][1], acc[tr][1]);
+        acc[tr][2] = __builtin_fmaf(es.z, T[tr][2], acc[tr][2]);
+        acc[tr][3] = __builtin_fmaf(es.w, T[tr][3], acc[tr][3]);
+    }
+}
+
+// DPP reductions inside one 16-lane row (fixed order): xor 1, xor 2, then the
+// half-row and row mirrors
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+    return v;
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v = quad_sum(v);
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    return v;
+}
+
+// Row -> segment by comparisons over values passed by value (scalar
+// registers): no array or struct holds them, so a lane-dependent choice
+// stays a register select instead of an indexed load.
+__device__ __forceinline__ int seg_of(int j, int n_seg, int r0, int r1, int& jj) {
+    const bool s1 = n_seg > 1 && j >= r0;
+    const bool s2 = n_seg > 2 && j >= r0 + r1;
+    jj = s2 ? j - r0 - r1 : (s1 ? j - r0 : j);
+    return s2 ? 2 : (s1 ? 1 : 0);
+}
+template <class T> __device__ __forceinline__ T* pick3(int s, T* a, T* b, T* c) { return s == 2 ? c : (s == 1 ? b : a); }
+
+// KS1 = false: the eight waves of a workgroup split one tile's units (small
+// matrices, where tiles are few); true: each wave owns whole tiles and its
+// ring of loads runs on across them without barriers (tall matrices).
+template <int QT, int NT, int TR, int UW, int SW, bool KS1>
+__global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mmq(QmvParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t msm[];
+    // wave index through readfirstlane: unit indices derived from it are
+    // then known to be wave-uniform (scalar branches, no exec masking)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane >> 4, n = lane & 15;
+    const int kn = p.n_in;
+    const int U = kn / 128;                                      // units per row
+    const int a_stride_u = MTr<QT>::SL * 4 * NT * MTr<QT>::AB;  // bytes per unit (all tokens)
+    constexpr int NTP = ntp<NT>();
+    uint8_t* abase = msm;
+    float* sx = (float*)(msm + (size_t)U * a_stride_u);  // Q4_K: [NT][kn/32]
+    const int sx_stride = kn / 32;
+    float* esc = sx + (QT == ORC_Q4_K ? NT * sx_stride : 0);  // [U][NTP]
+    float* red = esc + U * NTP;                                // [NT][kMW * 4] sums of x^2 per 16-lane row
+    float* part = red + NT * kMW * 4;                          // [kMW][TR][NT][16]
+    const MCtx mc{abase, a_stride_u, sx, sx_stride, esc};
+    const uint8_t *const sw0 = spin(p.w[0]), *const sw1 = spin(p.w[1]), *const sw2 = spin(p.w[2]);
+    float *const sy0 = spin(p.y[0]), *const sy1 = spin(p.y[1]), *const sy2 = spin(p.y[2]);
+    const float *const sb0 = spin(p.bias[0]), *const sb1 = spin(p.bias[1]), *const sb2 = spin(p.bias[2]);
+    const int n_seg = p.n_seg, r0 = p.rows[0], r1 = p.rows[1];
+    // weight row of logical row jl (clamped to row 0 past the end: loads stay in bounds)
+    auto wrow = [=](int jl) {
+        int jj;
+        const int sgi = seg_of(jl < p.n_rows ? jl : 0, n_seg, r0, r1, jj);
+        return pick3(sgi, sw0, sw1, sw2) + (size_t)jj * p.row_bytes;
+    };
+    // output (and bias) of logical row jl; false past the end
+    auto orow = [=](int jl, float*& y, const float*& bias) {
+        if (jl >= p.n_rows) return false;
+        int jj;
+        const int sgi = seg_of(jl, n_seg, r0, r1, jj);
+        y = pick3(sgi, sy0, sy1, sy2) + jj;
+        const float* bb = pick3(sgi, sb0, sb1, sb2);
+        bias = bb ? bb + jj : nullptr;
+        return true;
+    };
+
+    const int u0 = wave * U / kMW, u1 = (wave + 1) * U / kMW;
+    const bool swiglu = p.epi == ORC_EPI_SWIGLU;
+    const int rows_out = swiglu ? p.rows[0] : p.n_rows;
+    const int n_tiles = swiglu ? (rows_out + 15) / 16 : (rows_out + 16 * TR - 1) / (16 * TR);
+
+    auto tile_rows = [&](int tile, const uint8_t* (&rp)[TR]) {
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) {
+            const int jl = swiglu ? tr * r0 + (tile * 16 + n < r0 ? tile * 16 + n : r0) : (tile * TR + tr) * 16 + n;
+            rp[tr] = wrow(jl);
+        }
+    };
+    // a ring of UW units of the TR rows in flight: unit u sits in slot
+    // (u - u0) % UW and its slot is refilled with unit u + UW once consumed
+    MUnit<QT> buf[UW][TR];
+
+    // the unit range a wave computes: its own eighth (split tiles) or all
+    const int k0u = KS1 ? 0 : u0, k1u = KS1 ? U : u1;
+    int tile = KS1 ? blockIdx.x * kMW + wave : blockIdx.x;
+    const int tstride = KS1 ? gridDim.x * kMW : gridDim.x;
+    const uint8_t* rp[TR];
+    // the first tile's first units go out right after the first pass of x
+    // loads (so waiting for x does not wait for them) and stay in flight
+    // while x is staged
+    bool ring_started = false;
+    auto start_ring = [&]() {
+        ring_started = true;
+        if (tile < n_tiles) {
+            tile_rows(tile, rp);
+#pragma unroll
+            for (int k = 0; k < UW; ++k)
+                if (k0u + k < k1u) {
+#pragma unroll
+                    for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(rp[tr], k0u + k, c);
+                }
+        }
+    };
+
+    // ── stage this wave's K range as hi/lo fp16 in the A layout ──
+    // Lane q of a pass holds 8 consecutive values (group q); a 16-lane row
+    // holds one unit. Each (unit, token) gets its own power of two 2^e that
+    // brings max |x g| below 2^14 (reduced inside the row with DPP), so the
+    // halves stay in range; the sums of x g for the Q4_K minimum and of x^2
+    // for the norm are taken unscaled.
+    constexpr int GPL = SW / 4;  // groups per lane per pass of SW units
+    const bool norm = p.norm_w != nullptr;
+    float ssl[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) ssl[t] = 0.f;
+    for (int cs = u0; cs < u1; cs += SW) {
+        const int ng = 16 * min(SW, u1 - cs);
+        float v[NT][GPL][8], gw[GPL][8];
+#pragma unroll
+        for (int k = 0; k < GPL; ++k) {
+            const int q = lane + 64 * k;
+            const int qc = q < ng ? q : 0;  // lanes past the range read group 0 and are masked below
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float* src = p.x + (size_t)t * p.ldx + 128 * cs + 8 * qc;
+                *(float4*)v[t][k] = *(const float4*)src;
+                *(float4*)(v[t][k] + 4) = *(const float4*)(src + 4);
+            }
+            // norm weights (x itself stands in when there are none; unused then)
+            const float* gp = (norm ? p.norm_w : p.x) + 128 * cs + 8 * qc;
+            *(float4*)gw[k] = *(const float4*)gp;
+            *(float4*)(gw[k] + 4) = *(const float4*)(gp + 4);
+        }
+        if (!ring_started) start_ring();
+        if (norm) {
+#pragma unroll
+            for (int k = 0; k < GPL; ++k) {
+                const bool in = lane + 64 * k < ng;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        ssl[t] = __builtin_fmaf(in ? v[t][k][e] : 0.f, v[t][k][e], ssl[t]);
+                        v[t][k][e] *= gw[k][e];
+                    }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < GPL; ++k) {
+            const int q = lane + 64 * k;
+            const bool valid = q < ng;
+            const int k0 = 128 * cs + 8 * q, b = k0 >> 8;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float mx = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[t][k][e]));
+                mx = row_max(valid ? mx : 0.f);
+                int e2 = 0;
+                if (mx > 0.f && mx <= 3.0e38f) {
+                    int ex;
+                    (void)frexpf(mx, &ex);  // mx < 2^ex
+                    e2 = 14 - ex;
+                }
+                const float up = ldexpf(1.f, e2);
+                float s8 = ((v[t][k][0] + v[t][k][1]) + (v[t][k][2] + v[t][k][3])) +
+                           ((v[t][k][4] + v[t][k][5]) + (v[t][k][6] + v[t][k][7]));
+                if constexpr (QT == ORC_Q4_K) s8 = quad_sum(s8);
+                if (!valid) continue;
+                if ((lane & 15) == 0) esc[(cs + (q >> 4)) * NTP + t] = ldexpf(1.f, -e2);
+                float w[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w[e] = v[t][k][e] * up;
+                if constexpr (QT == ORC_Q4_K) {
+                    int u, i, cc, j;
+                    a_slot<QT>(b, k0 & 255, u, i, cc, j);
+                    h8v hi, lo;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const _Float16 he = (_Float16)w[e];
+                        hi[perm8(e)] = he;
+                        lo[perm8(e)] = (_Float16)(w[e] - (float)he);
+                    }
+                    uint8_t* ap = abase + (size_t)u * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 32;
+                    *(h8v*)ap = hi;
+                    *(h8v*)(ap + 16) = lo;
+                    if ((lane & 3) == 0) sx[t * sx_stride + (k0 >> 5)] = s8;
+                } else {
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        int u, i, cc, j;
+                        a_slot<QT>(b, (k0 & 255) + 4 * hf, u, i, cc, j);
+                        h4v hi, lo;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const _Float16 he = (_Float16)w[4 * hf + e];
+                            hi[perm8(e)] = he;
+                            lo[perm8(e)] = (_Float16)(w[4 * hf + e] - (float)he);
+                        }
+                        uint8_t* ap = abase + (size_t)u * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 16;
+                        *(h4v*)ap = hi;
+                        *(h4v*)(ap + 8) = lo;
+                    }
+                }
+            }
+        }
+    }
+    if (!ring_started) start_ring();
+    if (norm) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float r = row_sum(ssl[t]);
+            if ((lane & 15) == 0) red[t * kMW * 4 + wave * 4 + c] = r;
+        }
+    }
+    if constexpr (KS1) {
+        __syncthreads();  // every wave reads every unit
+    } else {
+        // the wave reads only what it wrote: order its LDS stores before its loads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    auto inv_rms = [&](int tok) {
+        if (!norm) return 1.f;
+        float ss = 0.f;
+        for (int j = 0; j < kMW * 4; ++j) ss += red[tok * kMW * 4 + j];
+        return 1.f / sqrtf(ss / (float)kn + p.eps);
+    };
+    float inv_l[4] = {1.f, 1.f, 1.f, 1.f};  // whole-tile mode: 1/rms of the lane's tokens 4c + i
+    if constexpr (KS1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) inv_l[i] = inv_rms(min(4 * c + i, NT - 1));
+    }
+
+    while (tile < n_tiles) {
+        // the slot of unit uu is refilled after use with unit uu + UW, or,
+        // past the end of the tile, with unit k of the wave's next tile
+        const int next = tile + tstride;
+        const uint8_t* rpn[TR];
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) rpn[tr] = rp[tr];
+        if (next < n_tiles) tile_rows(next, rpn);
+        f4v acc[TR];
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) acc[tr] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (int ub = k0u; ub < k1u; ub += UW) {
+#pragma unroll
+            for (int k = 0; k < UW; ++k)
+                if (ub + k < k1u) {
+                    if constexpr (QT == ORC_Q4_K)
+                        mmq_unit_q4k<NT, TR>(buf[k], ub + k, lane, mc, acc);
+                    else
+                        mmq_unit_q6k<NT, TR>(buf[k], ub + k, lane, mc, acc);
+                    if (ub + k + UW < k1u) {
+#pragma unroll
+                        for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(rp[tr], ub + k + UW, c);
+                    } else if (next < n_tiles && k0u + k < k1u) {
+#pragma unroll
+                        for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(rpn[tr], k0u + k, c);
+                    }
+                }
+        }
+        const int this_tile = tile;
+        tile = next;
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) rp[tr] = rpn[tr];
+        if constexpr (KS1) {
+            // whole rows in one wave: the lane's outputs (token 4c + i, row n) directly
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tok = 4 * c + i;
+                if (tok >= NT) continue;
+                const float inv = inv_l[i];
+                if (swiglu) {
+                    const int j = this_tile * 16 + n;
+                    if (j < p.rows[0]) {
+                        const float gv = acc[0][i] * inv, uv = acc[TR - 1][i] * inv;
+                        sy0[j + (size_t)tok * p.ldy] = (gv / (1.f + expf(-gv))) * uv;
+                    }
+                } else {
+#pragma unroll
+                    for (int tr = 0; tr < TR; ++tr) {
+                        float* y;
+                        const float* bias;
+                        if (orow((this_tile * TR + tr) * 16 + n, y, bias)) {
+                            float v = acc[tr][i] * inv;
+                            if (bias) v += *bias;
+                            float* dst = y + (size_t)tok * p.ldy;
+                            if (p.epi == ORC_EPI_ACCUM) *dst += v;
+                            else *dst = v;
+                        }
+                    }
+                }
+            }
+            continue;
+        }
+        // partial sums of this wave's units for the lane's tokens 4c + i
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tok = 4 * c + i;
+                if (tok < NT) part[((wave * TR + tr) * NT + tok) * 16 + n] = acc[tr][i];
+            }
+        __syncthreads();
+        // wave-ordered sum and the epilogue: one thread per (tile row, token)
+        if (swiglu) {
+            if (tid < NT * 16) {
+                const int tok = tid >> 4, r = tid & 15, j = this_tile * 16 + r;
+                float gs = 0.f, us = 0.f;
+                for (int w = 0; w < kMW; ++w) {
+                    gs += part[((w * TR + 0) * NT + tok) * 16 + r];
+                    us += part[((w * TR + (TR - 1)) * NT + tok) * 16 + r];
+                }
+                const float inv = inv_rms(tok);
+                if (j < p.rows[0]) {
+                    const float gv = gs * inv, uv = us * inv;
+                    sy0[j + (size_t)tok * p.ldy] = (gv / (1.f + expf(-gv))) * uv;
+                }
+            }
+        } else if (tid < TR * NT * 16) {
+            const int tr = tid / (NT * 16), tok = (tid >> 4) % NT, r = tid & 15;
+            float s = 0.f;
+            for (int w = 0; w < kMW; ++w) s += part[((w * TR + tr) * NT + tok) * 16 + r];
+            const float inv = inv_rms(tok);
+            const int jl = (this_tile * TR + tr) * 16 + r;
+            float* y;
+            const float* bias;
+            if (orow(jl, y, bias)) {
+                float v = s * inv;
+                if (bias) v += *bias;
+                float* dst = y + (size_t)tok * p.ldy;
+                if (p.epi == ORC_EPI_ACCUM) *dst += v;
+                else *dst = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // ── host side ────────────────────────────────────────────────────────────────
 static int g_n_cu = 256;
 static size_t g_lds_max = 64 * 1024;
@@ -614,6 +1269,73 @@ static int launch_type(const QmvParams& p, hipStream_t s, const LaunchEvents& ev
     }
 }
 
+// matrix-core path: LDS bytes, tokens per launch and the launch
+static size_t mmq_lds(int type, int nt, int kn, int tr) {
+    const int ntp = (nt + 3) & ~3;
+    size_t b = (size_t)nt * kn * 4;                              // hi + lo halves of every element
+    if (type == ORC_Q4_K) b += (size_t)nt * (kn / 32) * 4;       // per-sub-block sums
+    b += (size_t)(kn / 128) * ntp * 4;                           // per-(unit, token) scales
+    b += (size_t)(nt * kMW * 4 + kMW * tr * nt * 16) * 4;        // x^2 row sums, partial sums
+    return b;
+}
+
+static bool mmq_type(int type) { return type == ORC_Q4_K || type == ORC_Q6_K; }
+
+static int mmq_max_tokens(int type, int n_in) {
+    int nt = kMmqMaxNT;
+    while (nt > 1 && mmq_lds(type, nt, n_in, 2) > g_lds_max) --nt;
+    return mmq_lds(type, nt, n_in, 2) <= g_lds_max ? nt : 0;
+}
+
+template <int QT, int NT, int TR, int UW, int SW, bool KS1>
+static int mmq_shape(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
+    const bool swiglu = p.epi == ORC_EPI_SWIGLU;
+    const int rows_out = swiglu ? p.rows[0] : p.n_rows;
+    const int n_tiles = swiglu ? (rows_out + 15) / 16 : (rows_out + 16 * TR - 1) / (16 * TR);
+    const int grid = std::max(1, std::min(KS1 ? (n_tiles + kMW - 1) / kMW : n_tiles, g_n_cu));
+    const size_t lds = mmq_lds(QT, NT, p.n_in, TR);
+    if (lds > g_lds_max) return set_error(ORC_E_UNSUPPORTED, "gemm: activations do not fit LDS");
+    if (ev.start)
+        hipExtLaunchKernelGGL((k_mmq<QT, NT, TR, UW, SW, KS1>), dim3(grid), dim3(kMWG), lds, s, ev.start, ev.stop, 0, p);
+    else
+        hipLaunchKernelGGL((k_mmq<QT, NT, TR, UW, SW, KS1>), dim3(grid), dim3(kMWG), lds, s, p);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+// Two tiles per wave (one activation read for both) once there are enough
+// rows to keep every CU busy; SwiGLU always pairs a gate tile with its up tile.
+// UW: units of a wave's range in flight at once (a ring over longer ranges
+// and across tiles); SW: units staged per pass. Tall matrices (at least two
+// tiles per wave of the whole GPU) give each wave whole tiles; the split
+// depends on the shape only, never on the token count.
+template <int QT, int NT>
+static int mmq_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
+    const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
+    const bool two = p.epi == ORC_EPI_SWIGLU || (QT == ORC_Q4_K && p.n_rows >= 32 * g_n_cu);
+    const int rows_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.n_rows;
+    const bool tall = rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU;
+    if (tall) return two ? mmq_shape<QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<QT, NT, 1, 6, 4, true>(p, s, ev);
+    if (per_wave <= 3) return two ? mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev) : mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
+    if (per_wave <= 4) return two ? mmq_shape<QT, NT, 2, 4, 4, false>(p, s, ev) : mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
+    return two ? mmq_shape<QT, NT, 2, 4, 8, false>(p, s, ev) : mmq_shape<QT, NT, 1, 4, 8, false>(p, s, ev);
+}
+
+template <int QT>
+static int mmq_type_launch(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
+    switch (p.n_tok) {
+        case 1: return mmq_nt<QT, 1>(p, s, ev);
+        case 2: return mmq_nt<QT, 2>(p, s, ev);
+        case 3: return mmq_nt<QT, 3>(p, s, ev);
+        case 4: return mmq_nt<QT, 4>(p, s, ev);
+        case 5: return mmq_nt<QT, 5>(p, s, ev);
+        case 6: return mmq_nt<QT, 6>(p, s, ev);
+        case 7: return mmq_nt<QT, 7>(p, s, ev);
+        case 8: return mmq_nt<QT, 8>(p, s, ev);
+        default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..8");
+    }
+}
+
 // ── live kernel timing (orc_prof_*) ─────────────────────────────────────────
 struct ProfRec {
     hipEvent_t a, b;
@@ -650,7 +1372,8 @@ static double gemm_bytes(const QmvParams& p, int nt) {
 
 static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
     p.units = p.n_in / elems_per_unit(type);
-    const int ntmax = max_tokens(type, p.n_in);
+    const bool mm = mmq_type(type);
+    const int ntmax = mm ? mmq_max_tokens(type, p.n_in) : max_tokens(type, p.n_in);
     if (ntmax < 1) return set_error(ORC_E_UNSUPPORTED, "gemm: n_in too large for the activations to fit LDS");
     // tokens are processed in chunks of at most ntmax; chunking never changes a
     // (token,row) result because the reduction order is independent of n_tok
@@ -674,8 +1397,8 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
         }
         int rc;
         switch (type) {
-            case ORC_Q4_K: rc = launch_type<ORC_Q4_K>(q, s, ev); break;
-            case ORC_Q6_K: rc = launch_type<ORC_Q6_K>(q, s, ev); break;
+            case ORC_Q4_K: rc = mmq_type_launch<ORC_Q4_K>(q, s, ev); break;
+            case ORC_Q6_K: rc = mmq_type_launch<ORC_Q6_K>(q, s, ev); break;
             case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s, ev); break;
             case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, s, ev); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
