@@ -184,12 +184,17 @@ int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv,
  * positions start_pos.. (start_pos = *d_pos + pos_off, or pos_off when d_pos
  * is null), rotates q and k, stores k and v of every token in the cache and
  * writes each token's attention output (rows of ldo floats). Results equal
- * orc_rope_kv_store followed by orc_attn_gqa up to fp32 rounding. At most 8
- * query heads per kv head and 16 tokens per call; head_dim 64 or 128;
- * 16-byte aligned rows. */
+ * orc_rope_kv_store followed by orc_attn_gqa up to fp32 rounding; a token's
+ * result does not depend on n_tok. At most 8 query heads per kv head and 16
+ * tokens per call; head_dim 64 or 128; 16-byte aligned rows.
+ * Long contexts are split over up to 32 chunks per (token, kv head) whose
+ * partial results a second launch merges: d_work holds
+ * orc_attn_fused_workspace(n_heads, n_kv, head_dim) bytes, 16-byte aligned;
+ * calls that share a workspace must not overlap. */
+size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim);
 int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
                       const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kcache, float* d_vcache,
-                      int ctx, float* d_out, int ldo, orc_stream_t stream);
+                      int ctx, float* d_out, int ldo, void* d_work, orc_stream_t stream);
 
 /* ── argmax, sampling, acceptance ────────────────────────────────────────── */
 /* out[r] = first index of the maximum of row r (ops::argmax ops.cpp:490-497,

@@ -834,16 +834,8 @@ __device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int
     }
 }
 
-// DPP reductions inside one 16-lane row (fixed order): xor 1, xor 2, then the
+// DPP reductions inside one 16-lane row (fixed order): the quad sum, then the
 // half-row and row mirrors
-template <int CTRL> __device__ __forceinline__ float dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float quad_sum(float v) {
-    v += dpp<0xB1>(v);  // quad_perm [1,0,3,2]
-    v += dpp<0x4E>(v);  // quad_perm [2,3,0,1]
-    return v;
-}
 __device__ __forceinline__ float row_sum(float v) {
     v = quad_sum(v);
     v += dpp<0x141>(v);  // row_half_mirror

@@ -50,6 +50,17 @@ __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *(const u16_u
 // Byte k of w as float; the compiler emits one v_cvt_f32_ubyte{k}.
 __device__ __forceinline__ float ubyte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
 
+// DPP lane exchange inside a row of 16 lanes, and the sum over each group of
+// four consecutive lanes in a fixed order (xor 1, then xor 2)
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+    return v;
+}
+
 // Q4_K 6-bit (scale, min) of sub-block `is` from the 12 scale bytes held in
 // three dwords (core/gguf_parser.cpp:1085-1093).
 __device__ __forceinline__ void q4k_scale_min(int is, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,

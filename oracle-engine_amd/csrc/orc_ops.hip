@@ -8,6 +8,7 @@
 // (benchmark/bench_engine.cpp:337-355).
 #include "orc_internal.hpp"
 
+#include <algorithm>
 #include <cfloat>
 
 namespace orc {
@@ -194,91 +195,127 @@ __global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, con
     out[(size_t)t * ldo + h * HD + k] = O / L;
 }
 
-// ── fused RoPE + KV store + causal GQA attention (one launch per layer) ──────
-// Grid (kv head g, token t): a workgroup serves the gqa query heads of kv head
-// g for token t at position pt = start + t. It rotates its q rows and its own
-// K row (ops::rope rotate-half pairs, core/ops.cpp:440-485), stores K/V of
-// position pt in the cache (each new position is written by exactly one
-// workgroup), and attends to positions 0..pt (core/model.cpp:410-435,
-// 604-626): positions before `start` come from the cache, the new ones
-// (start..pt) straight from the QKV rows, rotated on the fly, so no
-// workgroup reads a cache row another one is writing. Positions are walked in
-// blocks of kPB with an online softmax: one lane per position forms its dot
-// products over the whole row (q rows broadcast from LDS, no cross-lane
-// reductions), scores in LDS, block max / sum per row, then P.V with 16-byte
-// columns per lane and position subsets reduced in a fixed order at the end.
-constexpr int kAT = 512, kPB = 512, kRMax = 8, kMaxTokAttn = 16;
+// ── fused RoPE + KV store + causal GQA attention, split over KV chunks ──────
+// Grid (chunk c, kv head g, token t). Token t sits at position pt = start + t
+// and attends to positions 0..pt (core/model.cpp:410-435, 604-626), cut into
+// chunks of CP positions, CP a function of pt alone (so a token's result does
+// not depend on how many tokens share the launch: a (k+1)-token verify pass
+// equals k+1 decode steps bit for bit). A workgroup:
+//  * rotates the gqa query heads of kv head g (ops::rope rotate-half pairs,
+//    core/ops.cpp:440-485) into LDS;
+//  * walks its chunk in sub-blocks of kSB positions: four lanes per position
+//    form the scores from K rows (the cache, or for the batch's own positions
+//    the QKV rows rotated in the lane, so no workgroup reads a cache row
+//    another one is writing), an online softmax per head, then P.V with the
+//    sub-block's V rows, which were loaded before the scores;
+//  * the workgroup of the last chunk stores K (rotated) and V of position pt;
+//  * writes its chunk's (O, m, l) per head to the workspace; k_attn_merge
+//    (the next launch, so no fence is needed) merges the chunks in chunk
+//    order: O = sum_c O_c e^(m_c - M) / sum_c l_c e^(m_c - M). A token whose
+//    positions fit one chunk gets its output written directly.
+constexpr int kSW = 256, kSB = 64, kNCMax = 32, kRMax = 8, kMaxTokAttn = 16;
 
-template <int HD>
-__device__ __forceinline__ void rope_pair(const float* v, const float2* cs, int d, float& out) {
-    // rotated value of element d of a head vector v with (cos, sin) table cs
-    constexpr int half = HD / 2;
-    if (d < half) {
-        const float2 c = cs[d];
-        out = v[d] * c.x - v[d + half] * c.y;
-    } else {
-        const float2 c = cs[d - half];
-        out = v[d - half] * c.y + v[d] * c.x;
-    }
+__device__ __forceinline__ int chunk_positions(int P) {
+    const int per = (P + kNCMax - 1) / kNCMax;
+    return (per + kSB - 1) / kSB * kSB;
 }
 
+// rotate-half of the pair (a = x[i], b = x[i + hd/2]) by (cos, sin) = cs, with
+// one fixed rounding sequence wherever a row is rotated
+__device__ __forceinline__ float rot_lo(float a, float b, float2 cs) { return __builtin_fmaf(a, cs.x, -(b * cs.y)); }
+__device__ __forceinline__ float rot_hi(float a, float b, float2 cs) { return __builtin_fmaf(b, cs.x, a * cs.y); }
+
+// floats per partial row: O[HD], m, l, padded to whole 128-byte lines
+template <int HD> constexpr int part_stride() { return HD + 32; }
+
 template <int HD>
-__global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv, int n_heads, int n_kv,
+__global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv, int n_heads, int n_kv,
                                                     const int* d_pos, int pos_off, const float2* rope, float* kc,
-                                                    float* vc, int ctx, float* out, int ldo) {
-    constexpr int NC = HD / 4;     // float4 columns in the P.V phase
-    constexpr int NPS = kAT / NC;  // position subsets in the P.V phase
-    constexpr int VB = 16;         // V rows in flight per lane
+                                                    float* vc, int ctx, float* out, int ldo, float* work) {
     constexpr int half = HD / 2;
-    static_assert(kPB == kAT, "one score position per lane per block");
-    __shared__ float Qs[kRMax][HD];
-    __shared__ __align__(16) float Kn[kMaxTokAttn][HD];  // rotated K rows of the batch's own positions
-    __shared__ float S[kRMax][kPB];
+    constexpr int FL = HD / 16;     // float4 of a K row per lane (four lanes per position)
+    constexpr int NC = HD / 4;      // float4 columns in the P.V phase
+    constexpr int NPS = kSW / NC;   // position subsets in the P.V phase
+    constexpr int VPL = kSB / NPS;  // V rows per lane per sub-block
+    constexpr int PS = part_stride<HD>();
+    static_assert(kSB * 4 == kSW, "four lanes per position");
+    __shared__ __align__(16) float Qs[kRMax][HD];
+    __shared__ float S[kRMax][kSB];
     __shared__ float st_m[kRMax], st_l[kRMax], st_a[kRMax];
-    __shared__ float red[NPS][HD];
-    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    __shared__ __align__(16) float red[NPS][HD];
+    const int c = blockIdx.x, g = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int R = n_heads / n_kv;
     const int start = start_position(d_pos, pos_off);
     const int pt = start + t;
     if (pt < 0 || pt >= ctx) return;  // outside the cache (graph replays past the end): nothing to do
-    const int P = pt + 1;
+    const int P = pt + 1, CP = chunk_positions(P), nch = (P + CP - 1) / CP;
+    if (c >= nch) return;  // grids cover the most chunks any position needs
+    const int p0 = c * CP, p1 = min(P, p0 + CP);
     const float scale = 1.f / sqrtf((float)HD);
-    const float* qrow = qkv + (size_t)t * ldqkv;
-    const float2* cs_t = rope + (size_t)pt * half;
-    const int col = tid % NC, ps = tid / NC;
-    // rotated K of this kv head for tokens 0..t (positions start..pt)
-    for (int i = tid; i < (t + 1) * HD; i += kAT) {
-        const int j = i / HD, d = i - j * HD;
-        float k;
-        rope_pair<HD>(qkv + (size_t)j * ldqkv + (n_heads + g) * HD, rope + (size_t)(start + j) * half, d, k);
-        Kn[j][d] = k;
-    }
+    const size_t kvh = (size_t)(n_heads + g) * HD, vvh = (size_t)(n_heads + n_kv + g) * HD;
     const float* kg = kc + (size_t)g * ctx * HD;
     const float* vg = vc + (size_t)g * ctx * HD;
+    const int sp = tid >> 2, sl = tid & 3;    // score phase: position in the sub-block, lane of four
+    const int col = tid % NC, ps = tid / NC;  // P.V phase: float4 column, position subset
 
-    auto load_v = [&](float4 (&v)[VB], int b0, int nb, int pp0) {
+    // K row of position p as float4s sl + 4 j (the pair partner of float4 j <
+    // FL/2 is float4 j + FL/2 of the same lane); zero past the chunk
+    auto load_k = [&](float4 (&k)[FL], int p, bool valid) {
+        if (!valid) {
 #pragma unroll
-        for (int j = 0; j < VB; ++j) {
-            const int pp = pp0 + j * NPS, p = b0 + pp;
-            if (pp >= nb) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-            else if (p < start) v[j] = *(const float4*)(vg + (size_t)p * HD + 4 * col);
-            else v[j] = *(const float4*)(qkv + (size_t)(p - start) * ldqkv + (n_heads + n_kv + g) * HD + 4 * col);
+            for (int j = 0; j < FL; ++j) k[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else if (p < start) {
+            const float* src = kg + (size_t)p * HD;
+#pragma unroll
+            for (int j = 0; j < FL; ++j) k[j] = *(const float4*)(src + 4 * (sl + 4 * j));
+        } else {
+            const float* src = qkv + (size_t)(p - start) * ldqkv + kvh;
+            const float2* cs = rope + (size_t)p * half;
+#pragma unroll
+            for (int j = 0; j < FL; ++j) k[j] = *(const float4*)(src + 4 * (sl + 4 * j));
+#pragma unroll
+            for (int j = 0; j < FL / 2; ++j) {
+                const int f = sl + 4 * j;
+                const float4 c01 = *(const float4*)(cs + 4 * f), c23 = *(const float4*)(cs + 4 * f + 2);
+                const float4 a = k[j], b = k[j + FL / 2];
+                const float2 e0{c01.x, c01.y}, e1{c01.z, c01.w}, e2{c23.x, c23.y}, e3{c23.z, c23.w};
+                k[j] = make_float4(rot_lo(a.x, b.x, e0), rot_lo(a.y, b.y, e1), rot_lo(a.z, b.z, e2), rot_lo(a.w, b.w, e3));
+                k[j + FL / 2] =
+                    make_float4(rot_hi(a.x, b.x, e0), rot_hi(a.y, b.y, e1), rot_hi(a.z, b.z, e2), rot_hi(a.w, b.w, e3));
+            }
         }
     };
 
-    for (int i = tid; i < R * HD; i += kAT) {
-        const int r = i / HD, d = i - r * HD;
-        float v;
-        rope_pair<HD>(qrow + (g * R + r) * HD, cs_t, d, v);
-        Qs[r][d] = v;
-    }
-    if (tid < HD) {
-        const float* kr = qrow + (n_heads + g) * HD;
-        float v;
-        rope_pair<HD>(kr, cs_t, tid, v);
-        const size_t o = ((size_t)g * ctx + pt) * HD + tid;
+    // the first sub-block's V rows and this lane's share of its K row go out
+    // first; the later sub-blocks' are loaded at the end of the one before
+    float4 v[VPL], k[FL];
+    auto load_v = [&](int b0, int nb) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int pp = ps + NPS * j, p = b0 + pp;
+            if (pp >= nb) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            else if (p < start) v[j] = *(const float4*)(vg + (size_t)p * HD + 4 * col);
+            else v[j] = *(const float4*)(qkv + (size_t)(p - start) * ldqkv + vvh + 4 * col);
+        }
+    };
+    load_v(p0, min(kSB, p1 - p0));
+    load_k(k, p0 + sp, sp < min(kSB, p1 - p0));
+
+    // this token's K (rotated) and V at pt go to the cache, from the last chunk
+    if (c == nch - 1 && tid < HD) {
+        const float* kr = qkv + (size_t)t * ldqkv + kvh;
+        const float2* cs = rope + (size_t)pt * half;
+        const int d = tid;
+        const float v = d < half ? rot_lo(kr[d], kr[d + half], cs[d]) : rot_hi(kr[d - half], kr[d], cs[d - half]);
+        const size_t o = ((size_t)g * ctx + pt) * HD + d;
         kc[o] = v;
-        vc[o] = qrow[(n_heads + n_kv + g) * HD + tid];
+        vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
+    }
+    for (int i = tid; i < R * HD; i += kSW) {
+        const int r = i / HD, d = i - r * HD;
+        const float* qr = qkv + (size_t)t * ldqkv + (size_t)(g * R + r) * HD;
+        const float2* cs = rope + (size_t)pt * half;
+        Qs[r][d] = d < half ? rot_lo(qr[d], qr[d + half], cs[d]) : rot_hi(qr[d - half], qr[d], cs[d - half]);
     }
     if (tid < kRMax) {
         st_m[tid] = -INFINITY;
@@ -287,65 +324,50 @@ __global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv,
     float4 acc[kRMax];
 #pragma unroll
     for (int r = 0; r < kRMax; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    __syncthreads();
 
-    for (int b0 = 0; b0 < P; b0 += kPB) {
-        const int nb = min(kPB, P - b0);
-        // scores: lane tid owns position b0 + tid and forms its R dot products
-        // over the whole row (q rows broadcast from LDS), KC dims at a time
-        if (tid < nb) {
-            const int p = b0 + tid;
-            // the whole row in flight at once: the cache, or the staged rotated row
-            float4 kv[HD / 4];
-            if (p < start) {
-                const float4* src = (const float4*)(kg + (size_t)p * HD);
+    for (int b0 = p0; b0 < p1; b0 += kSB) {
+        const int nb = min(kSB, p1 - b0);
+        __syncthreads();  // Qs written (first sub-block); S and st_a consumed (later ones)
+        // scores: each lane's partial dot over its FL float4s, summed over the four lanes
+        float dr[kRMax];
 #pragma unroll
-                for (int i = 0; i < HD / 4; ++i) kv[i] = src[i];
-            } else {
-                const float4* src = (const float4*)&Kn[p - start][0];
+        for (int r = 0; r < kRMax; ++r) {
+            float s = 0.f;
+            if (r < R) {
 #pragma unroll
-                for (int i = 0; i < HD / 4; ++i) kv[i] = src[i];
-            }
-            float dr[kRMax];
-#pragma unroll
-            for (int r = 0; r < kRMax; ++r) {
-                float sum = 0.f;
-                if (r < R) {
-#pragma unroll
-                    for (int i = 0; i < HD / 4; ++i) {
-                        const float4 q = *(const float4*)&Qs[r][4 * i];
-                        sum = __builtin_fmaf(q.x, kv[i].x, sum);
-                        sum = __builtin_fmaf(q.y, kv[i].y, sum);
-                        sum = __builtin_fmaf(q.z, kv[i].z, sum);
-                        sum = __builtin_fmaf(q.w, kv[i].w, sum);
-                    }
+                for (int j = 0; j < FL; ++j) {
+                    const float4 q = *(const float4*)&Qs[r][4 * (sl + 4 * j)];
+                    s = __builtin_fmaf(q.x, k[j].x, s);
+                    s = __builtin_fmaf(q.y, k[j].y, s);
+                    s = __builtin_fmaf(q.z, k[j].z, s);
+                    s = __builtin_fmaf(q.w, k[j].w, s);
                 }
-                dr[r] = sum;
+                s = quad_sum(s);
             }
+            dr[r] = s;
+        }
+        if (sl == 0) {
 #pragma unroll
             for (int r = 0; r < kRMax; ++r)
-                if (r < R) S[r][tid] = dr[r] * scale;
+                if (r < R) S[r][sp] = sp < nb ? dr[r] * scale : -INFINITY;
         }
-        // first V batch in flight during the softmax
-        float4 v[VB];
-        load_v(v, b0, nb, ps);
+        // the next sub-block's K rows, in flight during the softmax and P.V
+        const int b1 = b0 + kSB;
+        if (b1 < p1) load_k(k, b1 + sp, sp < min(kSB, p1 - b1));
         __syncthreads();
-        // online softmax: wave r owns row r (max, exp, sum over the block)
+        // online softmax over the sub-block: wave w owns heads w, w + 4
         {
             const int w = tid >> 6, ln = tid & 63;
-            for (int r = w; r < R; r += kAT / 64) {
-                float m = -INFINITY;
-                for (int p = ln; p < nb; p += 64) m = fmaxf(m, S[r][p]);
+            for (int r = w; r < R; r += kSW / 64) {
+                const float s = S[r][ln];
+                float m = s;
 #pragma unroll
                 for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
                 const float m_old = st_m[r];
                 const float m_new = fmaxf(m_old, m);
-                float l = 0.f;
-                for (int p = ln; p < nb; p += 64) {
-                    const float e = expf(S[r][p] - m_new);
-                    S[r][p] = e;
-                    l += e;
-                }
+                const float e = ln < nb ? expf(s - m_new) : 0.f;
+                S[r][ln] = e;
+                float l = e;
 #pragma unroll
                 for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
                 if (ln == 0) {
@@ -357,7 +379,7 @@ __global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv,
             }
         }
         __syncthreads();
-        // O_r = a_r O_r + sum_p P[r][p] V[p]
+        // O_r = a_r O_r + sum_p e_r[p] V[p]
 #pragma unroll
         for (int r = 0; r < kRMax; ++r) {
             if (r < R) {
@@ -368,38 +390,88 @@ __global__ __launch_bounds__(kAT) void k_attn_fused(const float* qkv, int ldqkv,
                 acc[r].w *= a;
             }
         }
-        for (int pp0 = ps; pp0 < nb; pp0 += VB * NPS) {
-            if (pp0 > ps) load_v(v, b0, nb, pp0);
 #pragma unroll
-            for (int j = 0; j < VB; ++j) {
-                const int pp = pp0 + j * NPS;
-                if (pp >= nb) break;
+        for (int j = 0; j < VPL; ++j) {
+            const int pp = ps + NPS * j;
+            if (pp < nb) {
 #pragma unroll
                 for (int r = 0; r < kRMax; ++r) {
                     if (r < R) {
-                        const float w = S[r][pp];
-                        acc[r].x = __builtin_fmaf(w, v[j].x, acc[r].x);
-                        acc[r].y = __builtin_fmaf(w, v[j].y, acc[r].y);
-                        acc[r].z = __builtin_fmaf(w, v[j].z, acc[r].z);
-                        acc[r].w = __builtin_fmaf(w, v[j].w, acc[r].w);
+                        const float e = S[r][pp];
+                        acc[r].x = __builtin_fmaf(e, v[j].x, acc[r].x);
+                        acc[r].y = __builtin_fmaf(e, v[j].y, acc[r].y);
+                        acc[r].z = __builtin_fmaf(e, v[j].z, acc[r].z);
+                        acc[r].w = __builtin_fmaf(e, v[j].w, acc[r].w);
                     }
                 }
             }
         }
-        __syncthreads();
+        if (b1 < p1) load_v(b1, min(kSB, p1 - b1));
     }
-    // reduce the position subsets in a fixed order, normalise, store
+
+    // sum the position subsets in a fixed order: the output (one chunk) or
+    // this chunk's partial row
+    const bool single = nch == 1;
+    float* part = work + ((size_t)t * n_kv + g) * kNCMax * R * PS;
 #pragma unroll
     for (int r = 0; r < kRMax; ++r) {
         if (r >= R) break;
+        __syncthreads();
         *(float4*)&red[ps][4 * col] = acc[r];
         __syncthreads();
         if (tid < HD) {
             float o = 0.f;
+#pragma unroll
             for (int k = 0; k < NPS; ++k) o += red[k][tid];
-            out[(size_t)t * ldo + (g * R + r) * HD + tid] = o / st_l[r];
+            if (single) {
+                out[(size_t)t * ldo + (g * R + r) * HD + tid] = o / st_l[r];
+            } else {
+                float* pr = part + ((size_t)c * R + r) * PS;
+                pr[tid] = o;
+                if (tid == 0) {
+                    pr[HD] = st_m[r];
+                    pr[HD + 1] = st_l[r];
+                }
+            }
         }
-        __syncthreads();
+    }
+}
+
+// Merge of the chunk partials of k_attn_split: one workgroup per (kv head,
+// token), chunks in chunk order. Tokens with a single chunk were written
+// directly and are skipped.
+template <int HD>
+__global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const int* d_pos, int pos_off, int ctx,
+                                                    const float* work, float* out, int ldo) {
+    constexpr int PS = part_stride<HD>();
+    __shared__ float sf[kRMax][kNCMax];  // e^(m_c - M) per head and chunk
+    __shared__ float sL[kRMax];
+    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int R = n_heads / n_kv;
+    const int pt = start_position(d_pos, pos_off) + t;
+    if (pt < 0 || pt >= ctx) return;
+    const int P = pt + 1, CP = chunk_positions(P), nch = (P + CP - 1) / CP;
+    if (nch == 1) return;
+    const float* part = work + ((size_t)t * n_kv + g) * kNCMax * R * PS;
+    if (tid < R) {
+        const int r = tid;
+        float M = -INFINITY;
+        for (int c = 0; c < nch; ++c) M = fmaxf(M, part[((size_t)c * R + r) * PS + HD]);
+        float L = 0.f;
+        for (int c = 0; c < nch; ++c) {
+            const float* pr = part + ((size_t)c * R + r) * PS;
+            const float f = expf(pr[HD] - M);
+            sf[r][c] = f;
+            L = __builtin_fmaf(pr[HD + 1], f, L);
+        }
+        sL[r] = L;
+    }
+    __syncthreads();
+    for (int i = tid; i < R * HD; i += kSW) {
+        const int r = i / HD, d = i - r * HD;
+        float O = 0.f;
+        for (int c = 0; c < nch; ++c) O = __builtin_fmaf(part[((size_t)c * R + r) * PS + d], sf[r][c], O);
+        out[(size_t)t * ldo + (g * R + r) * HD + d] = O / sL[r];
     }
 }
 
@@ -595,24 +667,51 @@ extern "C" int orc_decode_advance(int32_t* d_tok, int32_t* d_hist, int32_t* d_po
 }
 
 
+extern "C" size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim) {
+    if (n_heads <= 0 || n_kv <= 0 || head_dim <= 0) return 0;
+    return (size_t)kMaxTokAttn * n_heads * kNCMax * (head_dim + 32) * sizeof(float);
+}
+
 extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
                                  const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kc, float* d_vc,
-                                 int ctx, float* d_out, int ldo, orc_stream_t s) {
+                                 int ctx, float* d_out, int ldo, void* d_work, orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
     if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || (!d_pos && (pos_off < 0 || pos_off + n_tok > ctx)) ||
         ldqkv < (n_heads + 2 * n_kv) * head_dim || ldqkv % 4 || ldo % 4 || !d_qkv || !d_rope || !d_kc || !d_vc ||
-        !d_out || ((uintptr_t)d_qkv & 15) || ((uintptr_t)d_kc & 15) || ((uintptr_t)d_vc & 15))
+        !d_out || !d_work || ((uintptr_t)d_qkv & 15) || ((uintptr_t)d_kc & 15) || ((uintptr_t)d_vc & 15) ||
+        ((uintptr_t)d_rope & 15) || ((uintptr_t)d_work & 15))
         return set_error(ORC_E_INVALID, "attn_fused: bad args");
     if (n_heads / n_kv > kRMax) return set_error(ORC_E_UNSUPPORTED, "attn_fused: more than 8 query heads per kv head");
     if (n_tok > kMaxTokAttn) return set_error(ORC_E_UNSUPPORTED, "attn_fused: at most 16 tokens per launch");
     if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_fused: head_dim must be 64 or 128");
     hipStream_t st = resolve_stream(s);
-    if (head_dim == 64)
-        hipLaunchKernelGGL(k_attn_fused<64>, dim3(n_kv, n_tok), dim3(kAT), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos,
-                           pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
-    else
-        hipLaunchKernelGGL(k_attn_fused<128>, dim3(n_kv, n_tok), dim3(kAT), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos,
-                           pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+    // a host position sizes the grid for the chunks the last token needs; a
+    // device position for the most any position needs
+    int nch = kNCMax;
+    if (!d_pos) {
+        nch = 1;
+        for (int t = 0; t < n_tok; ++t) {
+            const int P = pos_off + t + 1, per = (P + kNCMax - 1) / kNCMax, cp = (per + kSB - 1) / kSB * kSB;
+            nch = std::max(nch, (P + cp - 1) / cp);
+        }
+    }
+    const dim3 grid(nch, n_kv, n_tok);
+    float* w = (float*)d_work;
+    if (head_dim == 64) {
+        hipLaunchKernelGGL(k_attn_split<64>, grid, dim3(kSW), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off,
+                           (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
+        ORC_LAUNCH_CHECK();
+        if (nch > 1)
+            hipLaunchKernelGGL(k_attn_merge<64>, dim3(n_kv, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos, pos_off,
+                               ctx, (const float*)w, d_out, ldo);
+    } else {
+        hipLaunchKernelGGL(k_attn_split<128>, grid, dim3(kSW), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off,
+                           (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
+        ORC_LAUNCH_CHECK();
+        if (nch > 1)
+            hipLaunchKernelGGL(k_attn_merge<128>, dim3(n_kv, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos, pos_off,
+                               ctx, (const float*)w, d_out, ldo);
+    }
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

@@ -1,5 +1,6 @@
 #include "model.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -116,7 +117,8 @@ bool Model::load(const std::string& path, int ctx_len) {
         !alloc((void**)&d_logits_, (size_t)B * V * 4) || !alloc((void**)&d_k_, kv) || !alloc((void**)&d_v_, kv) ||
         !alloc((void**)&d_rope_, (size_t)C * cfg.head_dim * 4) || !alloc((void**)&d_ids_, (size_t)B * 4) ||
         !alloc((void**)&d_am_, (size_t)B * 4) ||
-        !alloc(&d_attn_ws_, orc_attn_workspace(B, cfg.n_heads, cfg.head_dim, C)) ||
+        !alloc(&d_attn_ws_, std::max(orc_attn_workspace(B, cfg.n_heads, cfg.head_dim, C),
+                                     orc_attn_fused_workspace(cfg.n_heads, cfg.n_kv_heads, cfg.head_dim))) ||
         !alloc(&d_am_ws_, orc_argmax_workspace(B, V)))
         return fail(std::string("device allocation failed: ") + orc_last_error());
     // RoPE table with the reference's float arithmetic (ops.cpp:461-466):
@@ -200,7 +202,7 @@ int Model::chunk_dev(const int32_t* d_ids, int n, const int32_t* d_pos, int sp, 
         // RoPE + KV store (model.cpp:401-408), attention (model.cpp:410-435)
         if (fused_attn_) {  // one launch: rotate, store K/V, attend
             CK(orc_attn_fused_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc, vc,
-                                 C, d_attn_, NQ, s));
+                                 C, d_attn_, NQ, d_attn_ws_, s));
         } else {
             CK(orc_rope_kv_store_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc,
                                     vc, C, s));

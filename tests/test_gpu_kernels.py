@@ -210,14 +210,21 @@ def test_attention(dev, oracle, H, KVH, hd, sp, nt):
         assert np.allclose(got[t], want, rtol=1e-5, atol=2e-6), np.abs(got[t] - want).max()
 
 
+def _attn_ws(dev, H, KVH, hd):
+    return dev.alloc(dev.L.orc_attn_fused_workspace(H, KVH, hd))
+
+
 @pytest.mark.parametrize("H,KVH,hd,sp,nt,devpos", [(24, 8, 128, 0, 1, False), (24, 8, 128, 200, 1, True),
                                                    (24, 8, 128, 127, 5, True), (28, 4, 128, 700, 7, False),
                                                    (14, 2, 64, 31, 9, True), (32, 8, 64, 1000, 1, False),
-                                                   (24, 8, 128, 1300, 5, True)])
+                                                   (24, 8, 128, 1300, 5, True), (24, 8, 128, 62, 5, False),
+                                                   (28, 4, 128, 2045, 9, True), (14, 2, 64, 4100, 16, False)])
 def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos):
     """Fused RoPE + KV store + attention equals the oracle's rope then
     attention over the prefilled cache plus the new rows; the new K/V rows
-    land in the cache; the QKV rows are left as they were."""
+    land in the cache; the QKV rows are left as they were. Cases cross chunk
+    boundaries (64 positions per chunk up to 2048, then wider chunks) and a
+    second call on the same workspace repeats the first's outputs."""
     print(f"[gpu] attn_fused H={H} KVH={KVH} hd={hd} sp={sp} nt={nt} devpos={devpos}", flush=True)
     rng = np.random.default_rng(sp * 7 + nt)
     base = 500000.0
@@ -229,14 +236,20 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos):
     tab = rope_table(ctx, hd, base)
     dq, dt, dK, dV = dev.upload(qkv), dev.upload(tab), dev.upload(K), dev.upload(V)
     dO = dev.alloc(nt * H * hd * 4)
-    if devpos:
-        dp = dev.upload(np.array([sp - 3], np.int32))
-        dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, dp.ptr, 3, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
-                                          H * hd, None))
-    else:
-        dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
-                                          H * hd, None))
-    got = dO.read(np.float32).reshape(nt, H * hd)
+    ws = _attn_ws(dev, H, KVH, hd)
+    dp = dev.upload(np.array([sp - 3], np.int32))
+
+    def run():
+        if devpos:
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, dp.ptr, 3, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
+                                              H * hd, ws.ptr, None))
+        else:
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx,
+                                              dO.ptr, H * hd, ws.ptr, None))
+        return dO.read(np.float32).reshape(nt, H * hd)
+
+    got = run()
+    assert np.array_equal(run(), got)
     Kc = dK.read(np.float32).reshape(KVH, ctx, hd)
     Vc = dV.read(np.float32).reshape(KVH, ctx, hd)
     assert np.array_equal(dq.read(np.float32).reshape(nt, ld), qkv)
@@ -255,6 +268,35 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos):
     for t in range(nt):
         want = oracle.attention(qs[t], kc, vc, H, KVH, hd, sp + t)
         assert np.allclose(got[t], want, rtol=2e-5, atol=4e-6), (t, np.abs(got[t] - want).max())
+
+
+@pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 250, 5), (14, 2, 64, 2040, 9), (28, 4, 128, 60, 7)])
+def test_attn_fused_batch_invariant(dev, H, KVH, hd, sp, nt):
+    """One n-token call equals n one-token calls at the following positions
+    bit for bit (the verify pass of a speculative round equals decode)."""
+    print(f"[gpu] attn_fused batch invariance H={H} KVH={KVH} hd={hd} sp={sp} nt={nt}", flush=True)
+    rng = np.random.default_rng(sp + 11 * nt)
+    ctx = sp + nt + 2
+    ld = (H + 2 * KVH) * hd
+    qkv = rng.normal(0, 1, (nt, ld)).astype(np.float32)
+    K = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    V = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    dq, dt = dev.upload(qkv), dev.upload(rope_table(ctx, hd, 1e6))
+    ws = _attn_ws(dev, H, KVH, hd)
+    outs = []
+    for n in (nt, 1):
+        dK, dV = dev.upload(K), dev.upload(V)
+        dO = dev.alloc(nt * H * hd * 4)
+        if n == nt:
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
+                                              H * hd, ws.ptr, None))
+        else:
+            for t in range(nt):
+                dev.check(dev.L.orc_attn_fused_at(dq.at(t * ld * 4), ld, 1, H, KVH, hd, None, sp + t, dt.ptr, dK.ptr,
+                                                  dV.ptr, ctx, dO.at(t * H * hd * 4), H * hd, ws.ptr, None))
+        outs.append((dO.read(np.float32), dK.read(np.float32), dV.read(np.float32)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
 
 
 def test_argmax_first_index(dev, oracle):
