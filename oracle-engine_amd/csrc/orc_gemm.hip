@@ -343,6 +343,7 @@ struct QmvParams {
     float eps;
     int epi;
     int n_groups;
+    int hs;  // k_mmq split-tile mode: units of a wave's range staged at a time
 };
 
 constexpr int kQWG = 512, kQWaves = kQWG / 64;
@@ -675,7 +676,7 @@ template <int NT> constexpr int ntp() { return (NT + 3) & ~3; }
 // Q4_K unit of TR tiles: one scale-folded chain per tile, then
 // acc += d 2^-e D - sum over the unit's sub-blocks of dmin m sum(x g).
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int u, int lane, const MCtx& m,
+__device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
     const int c = lane >> 4, t = lane & 15;
     const int h = u & 1;
@@ -718,7 +719,7 @@ __device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int
         s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (t < NT) {
-        const uint8_t* ap = m.abase + (size_t)u * m.a_stride_u + (size_t)(c * NT + t) * 32;
+        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + (size_t)(c * NT + t) * 32;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             ah[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 32);
@@ -771,7 +772,7 @@ __device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int
 
 // Q6_K unit of TR tiles: eight 16-value sub-blocks, each its own scaled pair.
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int u, int lane, const MCtx& m,
+__device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
     const int c = lane >> 4, t = lane & 15;
     uint32_t ql[TR][4], qh[TR][4];
@@ -798,7 +799,7 @@ __device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int
 #pragma unroll
     for (int i = 0; i < 8; ++i) av[i] = u32x4{0u, 0u, 0u, 0u};
     if (t < NT) {
-        const uint8_t* ap = m.abase + (size_t)u * m.a_stride_u + (size_t)(c * NT + t) * 16;
+        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + (size_t)(c * NT + t) * 16;
 #pragma unroll
         for (int i = 0; i < 8; ++i) av[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 16);
     }
@@ -875,8 +876,11 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
     const int U = kn / 128;                                      // units per row
     const int a_stride_u = MTr<QT>::SL * 4 * NT * MTr<QT>::AB;  // bytes per unit (all tokens)
     constexpr int NTP = ntp<NT>();
+    // A entries: every unit (KS1), or per wave a window of HS units of its
+    // range, restaged window by window when the range does not fit the LDS
+    const int HS = KS1 ? U : p.hs;
     uint8_t* abase = msm;
-    float* sx = (float*)(msm + (size_t)U * a_stride_u);  // Q4_K: [NT][kn/32]
+    float* sx = (float*)(msm + (size_t)(KS1 ? U : kMW * HS) * a_stride_u);  // Q4_K: [NT][kn/32]
     const int sx_stride = kn / 32;
     float* esc = sx + (QT == ORC_Q4_K ? NT * sx_stride : 0);  // [U][NTP]
     float* red = esc + U * NTP;                                // [NT][kMW * 4] sums of x^2 per 16-lane row
@@ -904,6 +908,9 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
     };
 
     const int u0 = wave * U / kMW, u1 = (wave + 1) * U / kMW;
+    const bool multi_win = !KS1 && u0 + HS < u1;
+    // LDS slot of unit u of the window that starts at unit wb
+    auto aslot = [=](int u, int wb) { return KS1 ? u : wave * HS + (u - wb); };
     const bool swiglu = p.epi == ORC_EPI_SWIGLU;
     const int rows_out = swiglu ? p.rows[0] : p.n_rows;
     const int n_tiles = swiglu ? (rows_out + 15) / 16 : (rows_out + 16 * TR - 1) / (16 * TR);
@@ -952,8 +959,10 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
     float ssl[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) ssl[t] = 0.f;
-    for (int cs = u0; cs < u1; cs += SW) {
-        const int ng = 16 * min(SW, u1 - cs);
+    // stages units [s0, s1) of the wave's range; sum_sq adds their x^2 to ssl
+    auto stage = [&](int s0, int s1, bool sum_sq) {
+    for (int cs = s0; cs < s1; cs += SW) {
+        const int ng = 16 * min(SW, s1 - cs);
         float v[NT][GPL][8], gw[GPL][8];
 #pragma unroll
         for (int k = 0; k < GPL; ++k) {
@@ -974,7 +983,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
         if (norm) {
 #pragma unroll
             for (int k = 0; k < GPL; ++k) {
-                const bool in = lane + 64 * k < ng;
+                const bool in = sum_sq && lane + 64 * k < ng;
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -1020,7 +1029,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                         hi[perm8(e)] = he;
                         lo[perm8(e)] = (_Float16)(w[e] - (float)he);
                     }
-                    uint8_t* ap = abase + (size_t)u * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 32;
+                    uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 32;
                     *(h8v*)ap = hi;
                     *(h8v*)(ap + 16) = lo;
                     if ((lane & 3) == 0) sx[t * sx_stride + (k0 >> 5)] = s8;
@@ -1036,7 +1045,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                             hi[perm8(e)] = he;
                             lo[perm8(e)] = (_Float16)(w[4 * hf + e] - (float)he);
                         }
-                        uint8_t* ap = abase + (size_t)u * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 16;
+                        uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 16;
                         *(h4v*)ap = hi;
                         *(h4v*)(ap + 8) = lo;
                     }
@@ -1044,21 +1053,30 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
             }
         }
     }
-    if (!ring_started) start_ring();
-    if (norm) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float r = row_sum(ssl[t]);
-            if ((lane & 15) == 0) red[t * kMW * 4 + wave * 4 + c] = r;
-        }
-    }
-    if constexpr (KS1) {
-        __syncthreads();  // every wave reads every unit
-    } else {
-        // the wave reads only what it wrote: order its LDS stores before its loads
+    };
+    // the wave's LDS accesses before this point are ordered before those after
+    auto wave_lds_sync = [] {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto write_red = [&] {
+        if (norm) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float r = row_sum(ssl[t]);
+                if ((lane & 15) == 0) red[t * kMW * 4 + wave * 4 + c] = r;
+            }
+        }
+    };
+    stage(u0, multi_win ? u0 + HS : u1, true);
+    int wb = u0;  // first unit of the window of the wave's range held in the LDS
+    if (!ring_started) start_ring();
+    if (!multi_win) write_red();  // else once the first tile has staged every window
+    if constexpr (KS1) {
+        __syncthreads();  // every wave reads every unit
+    } else {
+        wave_lds_sync();  // the wave reads only what it wrote
     }
     auto inv_rms = [&](int tok) {
         if (!norm) return 1.f;
@@ -1072,6 +1090,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
         for (int i = 0; i < 4; ++i) inv_l[i] = inv_rms(min(4 * c + i, NT - 1));
     }
 
+    bool first_tile = true;
     while (tile < n_tiles) {
         // the slot of unit uu is refilled after use with unit uu + UW, or,
         // past the end of the tile, with unit k of the wave's next tile
@@ -1087,10 +1106,19 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
 #pragma unroll
             for (int k = 0; k < UW; ++k)
                 if (ub + k < k1u) {
+                    if (multi_win) {  // windows are walked in order, from u0 again for every tile
+                        const int nwb = ub + k == u0 ? u0 : (ub + k == wb + HS ? wb + HS : wb);
+                        if (nwb != wb) {
+                            wave_lds_sync();
+                            stage(nwb, min(u1, nwb + HS), first_tile);
+                            wave_lds_sync();
+                            wb = nwb;
+                        }
+                    }
                     if constexpr (QT == ORC_Q4_K)
-                        mmq_unit_q4k<NT, TR>(buf[k], ub + k, lane, mc, acc);
+                        mmq_unit_q4k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc);
                     else
-                        mmq_unit_q6k<NT, TR>(buf[k], ub + k, lane, mc, acc);
+                        mmq_unit_q6k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc);
                     if (ub + k + UW < k1u) {
 #pragma unroll
                         for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(rp[tr], ub + k + UW, c);
@@ -1100,6 +1128,8 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                     }
                 }
         }
+        if (multi_win && first_tile) write_red();
+        first_tile = false;
         const int this_tile = tile;
         tile = next;
 #pragma unroll
@@ -1261,31 +1291,43 @@ static int launch_type(const QmvParams& p, hipStream_t s, const LaunchEvents& ev
     }
 }
 
-// matrix-core path: LDS bytes, tokens per launch and the launch
-static size_t mmq_lds(int type, int nt, int kn, int tr) {
-    const int ntp = (nt + 3) & ~3;
-    size_t b = (size_t)nt * kn * 4;                              // hi + lo halves of every element
+// matrix-core path: LDS bytes, tokens per launch and the launch. hs: units
+// of a wave's range held at once in split-tile mode (0: every unit of the row)
+static size_t mmq_lds(int type, int nt, int kn, int tr, int hs) {
+    const int U = kn / 128, ntp = (nt + 3) & ~3;
+    size_t b = (size_t)(hs ? kMW * hs : U) * 512 * nt;          // hi + lo halves: 128 values x 4 B per unit and token
     if (type == ORC_Q4_K) b += (size_t)nt * (kn / 32) * 4;       // per-sub-block sums
-    b += (size_t)(kn / 128) * ntp * 4;                           // per-(unit, token) scales
+    b += (size_t)U * ntp * 4;                                    // per-(unit, token) scales
     b += (size_t)(nt * kMW * 4 + kMW * tr * nt * 16) * 4;        // x^2 row sums, partial sums
     return b;
 }
 
 static bool mmq_type(int type) { return type == ORC_Q4_K || type == ORC_Q6_K; }
 
+// tokens per launch: up to kMmqMaxNT as long as one unit per wave fits
 static int mmq_max_tokens(int type, int n_in) {
     int nt = kMmqMaxNT;
-    while (nt > 1 && mmq_lds(type, nt, n_in, 2) > g_lds_max) --nt;
-    return mmq_lds(type, nt, n_in, 2) <= g_lds_max ? nt : 0;
+    while (nt > 1 && mmq_lds(type, nt, n_in, 2, 1) > g_lds_max) --nt;
+    return mmq_lds(type, nt, n_in, 2, 1) <= g_lds_max ? nt : 0;
 }
 
 template <int QT, int NT, int TR, int UW, int SW, bool KS1>
-static int mmq_shape(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
+static int mmq_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& ev) {
+    QmvParams p = p0;
     const bool swiglu = p.epi == ORC_EPI_SWIGLU;
     const int rows_out = swiglu ? p.rows[0] : p.n_rows;
     const int n_tiles = swiglu ? (rows_out + 15) / 16 : (rows_out + 16 * TR - 1) / (16 * TR);
     const int grid = std::max(1, std::min(KS1 ? (n_tiles + kMW - 1) / kMW : n_tiles, g_n_cu));
-    const size_t lds = mmq_lds(QT, NT, p.n_in, TR);
+    // split-tile mode: the fewest staging windows per wave range that fit
+    p.hs = 0;
+    if (!KS1) {
+        const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
+        for (int nwin = 1; nwin <= per_wave; ++nwin) {
+            p.hs = (per_wave + nwin - 1) / nwin;
+            if (mmq_lds(QT, NT, p.n_in, TR, p.hs) <= g_lds_max) break;
+        }
+    }
+    const size_t lds = mmq_lds(QT, NT, p.n_in, TR, p.hs);
     if (lds > g_lds_max) return set_error(ORC_E_UNSUPPORTED, "gemm: activations do not fit LDS");
     if (ev.start)
         hipExtLaunchKernelGGL((k_mmq<QT, NT, TR, UW, SW, KS1>), dim3(grid), dim3(kMWG), lds, s, ev.start, ev.stop, 0, p);
@@ -1306,7 +1348,10 @@ static int mmq_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
     const bool two = p.epi == ORC_EPI_SWIGLU || (QT == ORC_Q4_K && p.n_rows >= 32 * g_n_cu);
     const int rows_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.n_rows;
-    const bool tall = rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU;
+    // whole-tile mode only where every unit fits the LDS at the largest token
+    // count, so the mode (and the reduction order) depends on the shape alone
+    const bool tall = rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU &&
+                      mmq_lds(QT, kMmqMaxNT, p.n_in, two ? 2 : 1, 0) <= g_lds_max;
     if (tall) return two ? mmq_shape<QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<QT, NT, 1, 6, 4, true>(p, s, ev);
     if (per_wave <= 3) return two ? mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev) : mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
     if (per_wave <= 4) return two ? mmq_shape<QT, NT, 2, 4, 4, false>(p, s, ev) : mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);

@@ -154,6 +154,59 @@ def test_gemm_fused_epilogues(dev):
         assert np.array_equal(dr.read(np.float32).reshape(nt, nk), res + plain)
 
 
+@pytest.mark.parametrize("qt,epi", [(ol.Q4_K, "norm"), (ol.Q6_K, "swiglu"), (ol.Q4_K, "accum")])
+def test_gemm_staging_windows(dev, oracle, qt, epi):
+    """Rows too long for every token's activations to fit the LDS at once
+    (n_in = 18944) are staged in windows: with the RMSNorm prologue, the
+    SwiGLU pair and the residual epilogue, over more tiles than workgroups (so
+    windows are restaged for later tiles), 8 tokens equal 8 one-token calls bit
+    for bit and match float64 within 2e-6 of sum |w x|."""
+    import orc
+
+    print(f"[gpu] gemm staging windows type={qt} epi={epi}", flush=True)
+    rng = np.random.default_rng(19)
+    n_in, n_out, nt = 18944, 16 * 300, 8
+    raw = rand_blocks(qt, (2 if epi == "swiglu" else 1) * n_out * n_in, rng)
+    wd = dev.upload(raw)
+    X = rng.normal(0, 1, (nt, n_in)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
+    dg = dev.upload(g)
+    res = rng.normal(0, 1, (nt, n_out)).astype(np.float32)
+
+    def run(lo, n):
+        dx = dev.upload(X[lo:lo + n])
+        dy = dev.upload(res[lo:lo + n]) if epi == "accum" else dev.alloc(n * n_out * 4)
+        rb = ol.row_bytes(qt, n_in)
+        if epi == "swiglu":
+            segs = (orc.Seg * 2)(orc.Seg(wd.ptr, n_out, dy.ptr, None), orc.Seg(wd.ptr + n_out * rb, n_out, dy.ptr, None))
+            dev.check(dev.L.orc_gemm_fused(qt, segs, 2, n, n_in, dx.ptr, n_in, n_out, None, C.c_float(0),
+                                           orc.EPI_SWIGLU, None))
+        else:
+            segs = (orc.Seg * 1)(orc.Seg(wd.ptr, n_out, dy.ptr, None))
+            dev.check(dev.L.orc_gemm_fused(qt, segs, 1, n, n_in, dx.ptr, n_in, n_out,
+                                           dg.ptr if epi == "norm" else None, C.c_float(1e-5),
+                                           orc.EPI_ACCUM if epi == "accum" else orc.EPI_STORE, None))
+        return dy.read(np.float32).reshape(n, n_out)
+
+    got = run(0, nt)
+    single = np.concatenate([run(t, 1) for t in range(nt)])
+    assert np.array_equal(got.view(np.uint32), single.view(np.uint32))
+    W = oracle.dequant(qt, raw, raw.size // ol.row_bytes(qt, n_in) * n_in).reshape(-1, n_in).astype(np.float64)
+    Xd = X.astype(np.float64)
+    if epi == "norm":
+        Xd = Xd / np.sqrt((Xd ** 2).mean(axis=1, keepdims=True) + 1e-5) * g
+    dot = Xd @ W.T
+    scale = np.abs(Xd) @ np.abs(W).T
+    if epi == "swiglu":
+        gt, up = dot[:, :n_out], dot[:, n_out:]
+        want = gt / (1 + np.exp(-gt)) * up
+        tol = 3e-6 * (scale[:, :n_out] * np.abs(up) + scale[:, n_out:] * np.abs(gt)) + 1e-30  # |silu'| <= 1.1
+        assert np.all(np.abs(got - want) <= tol + 1e-6 * np.abs(want))
+    else:
+        want = dot + (res if epi == "accum" else 0)
+        assert np.all(np.abs(got - want) <= 2e-6 * scale + 1e-6 * np.abs(want) + 1e-30)
+
+
 def test_rmsnorm(dev, oracle):
     rng = np.random.default_rng(5)
     for n in (896, 2048, 3072, 3584):
