@@ -394,7 +394,10 @@ __device__ __forceinline__ void map_rows(const QmvParams& p, int g, int slot, Ro
     }
 }
 
-template <int QT, int NT, int ROWS, int UPL, int WPE>
+// PIPE (rows of one batch, many row groups per wave): the next row group's
+// loads go out before the current group's arithmetic, two register sets
+// taking turns.
+template <int QT, int NT, int ROWS, int UPL, int WPE, bool PIPE>
 __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) void k_qmv(QmvParams p) {
     using T = QTr<QT>;
     constexpr int LPR = T::LPR, G = 64 / LPR, RG = G * ROWS;
@@ -487,24 +490,8 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
     }
 
     const XCtx c{xs, xs_stride, sx, sx_stride, 0};
-    while (g < p.n_groups) {
-        float acc[ROWS][NT];
-        zero(acc);
-        for (int bt = 0; bt < n_batches; ++bt) {
-            if (bt > 0) {
-#pragma unroll
-                for (int i = 0; i < UPL; ++i) {
-                    const int u = li + LPR * (bt * UPL + i);
-                    U[i].load(R.rp, u < p.units ? u : 0);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < UPL; ++i) {
-                const int u = li + LPR * (bt * UPL + i);
-                if (u < p.units) U[i].template compute<NT>(u, c, acc);
-            }
-        }
-        // slot reduction: fixed xor butterfly over the LPR lanes
+    // slot reduction (fixed xor butterfly over the LPR lanes) and epilogue
+    auto finish = [&](float (&acc)[ROWS][NT], const RowSet<ROWS>& R) {
 #pragma unroll
         for (int r = 0; r < ROWS; ++r)
 #pragma unroll
@@ -514,7 +501,6 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
                 for (int o = LPR / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
                 acc[r][t] = v;
             }
-
         if (p.epi == ORC_EPI_SWIGLU) {
 #pragma unroll
             for (int r = 0; r < ROWS / 2; ++r)
@@ -537,7 +523,58 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
                         else *dst = v;
                     }
         }
-
+    };
+    if constexpr (PIPE) {
+        Unit<QT, ROWS> V[UPL];
+        RowSet<ROWS> R2;
+        // computes group gc from cur (rows Rc) after issuing group gc + gstride into nxt (rows Rn)
+        auto step = [&](Unit<QT, ROWS> (&cur)[UPL], Unit<QT, ROWS> (&nxt)[UPL], const RowSet<ROWS>& Rc,
+                        RowSet<ROWS>& Rn, int gc) {
+            const int gn = gc + gstride;
+            if (gn < p.n_groups) {
+                map_rows<ROWS, RG>(p, gn, slot, Rn);
+#pragma unroll
+                for (int i = 0; i < UPL; ++i) {
+                    const int u = li + LPR * i;
+                    nxt[i].load(Rn.rp, u < p.units ? u : 0);
+                }
+            }
+            float acc[ROWS][NT];
+            zero(acc);
+#pragma unroll
+            for (int i = 0; i < UPL; ++i) {
+                const int u = li + LPR * i;
+                if (u < p.units) cur[i].template compute<NT>(u, c, acc);
+            }
+            finish(acc, Rc);
+        };
+        while (g < p.n_groups) {
+            step(U, V, R, R2, g);
+            g += gstride;
+            if (g >= p.n_groups) break;
+            step(V, U, R2, R, g);
+            g += gstride;
+        }
+        return;
+    }
+    while (g < p.n_groups) {
+        float acc[ROWS][NT];
+        zero(acc);
+        for (int bt = 0; bt < n_batches; ++bt) {
+            if (bt > 0) {
+#pragma unroll
+                for (int i = 0; i < UPL; ++i) {
+                    const int u = li + LPR * (bt * UPL + i);
+                    U[i].load(R.rp, u < p.units ? u : 0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < UPL; ++i) {
+                const int u = li + LPR * (bt * UPL + i);
+                if (u < p.units) U[i].template compute<NT>(u, c, acc);
+            }
+        }
+        finish(acc, R);
         g += gstride;
         if (g < p.n_groups) {
             map_rows<ROWS, RG>(p, g, slot, R);
@@ -1245,7 +1282,7 @@ struct LaunchEvents {
     hipEvent_t start = nullptr, stop = nullptr;
 };
 
-template <int QT, int NT, int ROWS, int UPL, int WPE>
+template <int QT, int NT, int ROWS, int UPL, int WPE, bool PIPE = false>
 static int launch_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& ev) {
     QmvParams p = p0;
     const int rg = (64 / QTr<QT>::LPR) * ROWS;
@@ -1255,9 +1292,9 @@ static int launch_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& 
     const size_t lds = qmv_lds(QT, NT, p.n_in);
     if (lds > g_lds_max) return set_error(ORC_E_UNSUPPORTED, "gemm: activations do not fit LDS");
     if (ev.start)
-        hipExtLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE>), dim3(grid), dim3(kQWG), lds, s, ev.start, ev.stop, 0, p);
+        hipExtLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), dim3(grid), dim3(kQWG), lds, s, ev.start, ev.stop, 0, p);
     else
-        hipLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE>), dim3(grid), dim3(kQWG), lds, s, p);
+        hipLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), dim3(grid), dim3(kQWG), lds, s, p);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }
@@ -1272,6 +1309,8 @@ static int launch_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) 
     const bool tall = p.n_rows >= 32768;  // LM heads
     if constexpr (NT == 1) {
         if ((QT == ORC_Q6_K && tall) || pair) return launch_shape<QT, NT, 2, 1, 4>(p, s, ev);
+        // tall matrices whose rows are one batch: row groups double-buffered
+        if (tall && p.units <= QTr<QT>::LPR * 3) return launch_shape<QT, NT, 1, 3, 4, true>(p, s, ev);
         return launch_shape<QT, NT, 1, 3, 4>(p, s, ev);
     } else {
         if (pair || tall) return launch_shape<QT, NT, 2, 1, 2>(p, s, ev);

@@ -70,7 +70,8 @@ def _gemm(dev, qt, w_dev, n_tok, n_out, n_in, X):
 
 
 SHAPES = [(ol.Q4_K, 515, 3072), (ol.Q4_K, 64, 3584), (ol.Q6_K, 301, 3072), (ol.Q6_K, 130, 8192),
-          (ol.Q8_0, 700, 896), (ol.Q8_0, 129, 2048), (ol.Q4_0, 257, 2048), (ol.Q6_K, 40, 18944)]
+          (ol.Q8_0, 700, 896), (ol.Q8_0, 129, 2048), (ol.Q4_0, 257, 2048), (ol.Q6_K, 40, 18944),
+          (ol.Q8_0, 40000, 896)]  # the last: an LM-head-tall matrix (double-buffered row groups)
 
 
 @pytest.mark.parametrize("qt,n_out,n_in", SHAPES)
@@ -89,7 +90,7 @@ def test_gemv_vs_exact(dev, oracle, qt, n_out, n_in):
 
 
 @pytest.mark.parametrize("qt,n_out,n_in", [(ol.Q4_K, 200, 3072), (ol.Q6_K, 77, 8192), (ol.Q8_0, 90, 896),
-                                           (ol.Q4_0, 33, 2048), (ol.Q6_K, 24, 18944)])
+                                           (ol.Q4_0, 33, 2048), (ol.Q6_K, 24, 18944), (ol.Q8_0, 40000, 896)])
 def test_gemm_batch_invariant(dev, qt, n_out, n_in):
     """verify(n)[t] is bit-identical to the decode GEMV of token t, n = 1..12."""
     print(f"[gpu] gemm invariance type={qt} {n_out}x{n_in}", flush=True)
