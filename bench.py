@@ -21,7 +21,10 @@ launched from the host for --prof-tokens tokens, every GEMM launch carrying
 start / stop HIP events that take the timestamps of its own dispatch on its
 stream (hipExtLaunchKernelGGL). The dominant kernel family is the one with
 the most GEMM time there; achieved = algorithmic bytes (weight blocks +
-activations + outputs) / its average launch duration.
+activations + outputs) / its average launch duration. traffic: that kernel
+family's HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
+runs (scaled by a copy kernel of known size), read from the committed
+summary in profiles/.
 cpu_baseline: the reference implementation (oracle/_ref, built from the
 reference's sources) on the same two models, bounded sample: prompt 8 ids,
 16 generated tokens, k = 4.
@@ -77,6 +80,19 @@ def cpu_baseline(tgt_path, dft_path, prompt, k):
     return {"value": round(d["tok_s"], 4), "unit": "tok/s", "cores": d["threads"], "kind": "reference",
             "sample": f"reference build (oracle/_ref), same C3 target+draft, prompt 8 ids, {d['tokens']} generated "
                       f"tokens, k={k}, accepted {d['accepted']}/{d['proposed']}"}
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/*.md, a 'TRAFFIC <kernel> bytes_per_launch=N' line), scaled there by a copy kernel."""
+    pdir = os.path.join(ROOT, "profiles")
+    for name in sorted(os.listdir(pdir)) if os.path.isdir(pdir) else []:
+        if name.endswith(".md"):
+            for line in open(os.path.join(pdir, name)):
+                m = re.match(r"TRAFFIC (.+) bytes_per_launch=(\d+)\s*$", line)
+                if m and m.group(1) == kernel:
+                    return int(m.group(2)), f"profiles/{name}"
+    return None, None
 
 
 def main():
@@ -191,8 +207,10 @@ def main():
         fams.sort(key=lambda f: -f["ms"])
         if fams:
             f = fams[0]
+            traffic, traffic_src = measured_traffic(f["kernel"])
             roofline = {"bound": "hbm", "achieved": round(f["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(f["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": f["kernel"],
+                        "frac": round(f["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                        "traffic_source": traffic_src, "kernel": f["kernel"],
                         "avg_launch_us": round(1e3 * f["ms"] / f["launches"], 3),
                         "bytes_per_launch": round(f["bytes"] / f["launches"]),
                         "timing": f"start/stop HIP events of each launch's dispatch over {pst['rounds']} "
