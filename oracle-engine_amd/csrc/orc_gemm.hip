@@ -596,51 +596,42 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
 // lo = fp16(x' - hi); hi + lo carries ~22 bits and every product with a
 // weight code is exact in fp32, so D matches an fp32 dot product to fp32
 // rounding.
-//  * Q4_K: the 6-bit sub-block scale is folded into the code (sc * q <= 945,
-//    exact in fp16), so one v_mfma_f32_16x16x32_f16 chain covers a whole unit
-//    whatever sub-blocks its k values come from; d scales the chain and the
+// A unit is half a superblock (128 values) of one row, in four 32-value
+// slices of one v_mfma_f32_16x16x32_f16 each; lane group c (lanes 16c..16c+15)
+// holds values 8c..8c+7 of a slice, the same for both types:
+//  * Q4_K: a slice is one sub-block; its 6-bit scale is folded into the code
+//    (sc * q <= 945, exact in fp16), d scales the unit's chain and the
 //    minimum term dmin * m * sum(x) is added per sub-block on the VALU.
-//  * Q6_K: scales are int8 (sc * q does not fit fp16), so every 16-value
-//    sub-block gets its own v_mfma_f32_16x16x16_f16 pair scaled by d * sc.
-//    The four lanes of a weight row load 16-byte runs and exchange 4-byte
-//    words (permlane16/32 swaps) so each sub-block's 16 codes spread over the
-//    four lane groups as the instruction expects.
-// A unit is half a superblock (128 values) of one row. The eight waves of a
-// workgroup split a tile's units into fixed contiguous ranges and their
-// partial sums are added in wave order, so a (token, row) result does not
-// depend on the token count: a (k+1)-token verify equals k+1 decode GEMVs.
+//  * Q6_K: a slice spans two 16-value sub-blocks whose int8 scales do not
+//    fit the code exactly (sc * (q - 32) up to 4096), so the scaled code is
+//    split into hi = fp16(sc (q - 32)) and lo = sc (q - 32) - hi (exact,
+//    |lo| <= 1): hi x hi + lo x hi + hi x lo per slice (the lo x lo term,
+//    2^-22 of a product, is dropped), d scales the chain.
+// The eight waves of a workgroup split a tile's units into fixed contiguous
+// ranges and their partial sums are added in wave order, so a (token, row)
+// result does not depend on the token count: a (k+1)-token verify equals k+1
+// decode GEMVs.
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kMWG = 512, kMW = kMWG / 64;
 constexpr int kMmqMaxNT = 8;
 
-// code permutation of one 8-value slice (bytes 0,2 / 1,3 / 4,6 / 5,7 of a
-// nibble or byte run land in consecutive halves); it is its own inverse
+// code permutation of one 8-value run (bytes 0,2 / 1,3 / 4,6 / 5,7 land in
+// consecutive halves when two dwords are unpacked into fp16 pairs)
 __device__ __forceinline__ int perm8(int j) { return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1); }
 
-template <int QT> struct MTr;
-template <> struct MTr<ORC_Q4_K> { static constexpr int SL = 4, AB = 32; };  // slices per unit, A bytes per (slice, lane)
-template <> struct MTr<ORC_Q6_K> { static constexpr int SL = 8, AB = 16; };
+// A entries: per unit, per (slice, lane group, token), 8 hi then 8 lo halves
+constexpr int kASlices = 4, kABytes = 32;
 
-// A-operand slot (byte offset inside a token-major entry table) of element kk
-// (0..255) of superblock b, and the position j of the element in its slot.
-template <int QT> __device__ __forceinline__ void a_slot(int b, int kk, int& u, int& i, int& c, int& j);
-template <> __device__ __forceinline__ void a_slot<ORC_Q4_K>(int b, int kk, int& u, int& i, int& c, int& j) {
-    const int g = kk >> 6, nib = (kk >> 5) & 1, o = kk & 31;
-    u = 2 * b + (g >> 1);
-    c = 2 * (g & 1) + (o >> 4);
-    i = 2 * nib + ((o >> 3) & 1);
-    j = perm8(o & 7);
-}
-template <> __device__ __forceinline__ void a_slot<ORC_Q6_K>(int b, int kk, int& u, int& i, int& c, int& j) {
-    const int hh = kk >> 7, r = kk & 127, g = r >> 5, jh = (r >> 4) & 1, k16 = r & 15;
-    u = 2 * b + hh;
-    i = 2 * g + jh;
-    c = k16 >> 2;
-    j = perm8(k16 & 3);  // perm8 maps 0..3 onto 0,2,1,3
+// A entry of element kk (0..255) of superblock b: unit u, slice i, lane
+// group c, position j of the element among the entry's 8 halves.
+__device__ __forceinline__ void a_slot(int b, int kk, int& u, int& i, int& c, int& j) {
+    u = 2 * b + (kk >> 7);
+    i = (kk >> 5) & 3;
+    c = (kk >> 3) & 3;
+    j = perm8(kk & 7);
 }
 
 // Loads through the global address space (a generic pointer would make
@@ -652,56 +643,53 @@ __device__ __forceinline__ u32x4 ldg16(const uint8_t* p) { return *(g16p)p; }
 __device__ __forceinline__ u32x2 ldg8(const uint8_t* p) { return *(g8p)p; }
 __device__ __forceinline__ uint32_t ldg2(const uint8_t* p) { return *(g2p)p; }
 
-// Q4_K (scale, min) of sub-block 4h + k (h = 0, 1 is wave-uniform, k = 0..3
-// may differ per lane), branch-free (core/gguf_parser.cpp:1085-1093).
+// Q4_K (scale, min) of sub-block 4h + k (h = 0, 1 and k = 0..3),
+// branch-free (core/gguf_parser.cpp:1085-1093).
 __device__ __forceinline__ void q4k_sm(int h, int k, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc, uint32_t& mn) {
     const uint32_t b0 = (s0 >> (8 * k)) & 0xFFu, b1 = (s1 >> (8 * k)) & 0xFFu, b2 = (s2 >> (8 * k)) & 0xFFu;
     sc = h ? ((b2 & 0xFu) | ((b0 >> 6) << 4)) : (b0 & 63u);
     mn = h ? ((b2 >> 4) | ((b1 >> 6) << 4)) : (b1 & 63u);
 }
 
-// Loaded bytes of one unit of one row.
+// Loaded bytes of one unit of one row for lane group c.
 template <int QT> struct MUnit;
 template <> struct MUnit<ORC_Q4_K> {
-    u32x4 hdr, q;  // d, dmin, 12 scale bytes; 16 code bytes of the lane's run
+    // d, dmin, 12 scale bytes; code bytes 8c.. of the unit's first 32 (slices
+    // 0, 1: low, high nibbles) and of its next 32 (slices 2, 3)
+    // (core/gguf_parser.cpp:1096-1121)
+    u32x4 hdr;
+    u32x2 qa, qb;
     __device__ __forceinline__ void load(const uint8_t* row, int u, int c) {
         const uint8_t* blk = row + (size_t)(u >> 1) * 144;
         hdr = ldg16(blk);
-        q = ldg16(blk + 16 + 64 * (u & 1) + 16 * c);
+        const uint8_t* qs = blk + 16 + 64 * (u & 1) + 8 * c;
+        qa = ldg8(qs);
+        qb = ldg8(qs + 32);
     }
 };
 template <> struct MUnit<ORC_Q6_K> {
-    u32x4 ql, qh;
-    u32x2 sc;
+    // low 4 bits of slices 0, 2 (ql bytes 8c..) and 1, 3 (ql bytes 32 + 8c..),
+    // high 2 bits (qh bytes 8c.., bits 2i of slice i), the half's 8 int8
+    // scales, d (core/gguf_parser.cpp:1124-1154)
+    u32x2 qla, qlb, qh, sc;
     uint32_t dh;
     __device__ __forceinline__ void load(const uint8_t* row, int u, int c) {
         const uint8_t* blk = row + (size_t)(u >> 1) * 210;
         const int hh = u & 1;
-        ql = ldg16(blk + 64 * hh + 16 * c);
-        qh = ldg16(blk + 128 + 32 * hh + 16 * (c & 1));
+        qla = ldg8(blk + 64 * hh + 8 * c);
+        qlb = ldg8(blk + 64 * hh + 32 + 8 * c);
+        qh = ldg8(blk + 128 + 32 * hh + 8 * c);
         sc = ldg8(blk + 192 + 8 * hh);
         dh = ldg2(blk + 208);
     }
 };
 
-// 4x4 transpose of dwords across the four 16-lane groups: afterwards group c
-// holds in v[w] what group w held in v[c].
-__device__ __forceinline__ void xpose4(uint32_t& v0, uint32_t& v1, uint32_t& v2, uint32_t& v3) {
-    auto a = __builtin_amdgcn_permlane32_swap(v0, v2, false, false);
-    auto b = __builtin_amdgcn_permlane32_swap(v1, v3, false, false);
-    auto e = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-    auto f = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
-    v0 = e[0];
-    v1 = e[1];
-    v2 = f[0];
-    v3 = f[1];
-}
-
 __device__ __forceinline__ h2v as_h2(uint32_t v) { return __builtin_bit_cast(h2v, v); }
+__device__ __forceinline__ uint32_t as_u32(h2v v) { return __builtin_bit_cast(uint32_t, v); }
 
 // Where a unit's activations live in LDS.
 struct MCtx {
-    const uint8_t* abase;  // A entries: [unit][slice][lane group][token] hi | lo
+    const uint8_t* abase;  // A entries: [unit slot][slice][lane group][token] hi | lo
     int a_stride_u;        // bytes per unit
     const float* sx;       // Q4_K: sums of x g over each 32-value sub-block, [token][sub-block]
     int sx_stride;
@@ -710,165 +698,130 @@ struct MCtx {
 
 template <int NT> constexpr int ntp() { return (NT + 3) & ~3; }
 
+// The lane's A entries of a unit (all four slices, token lane % 16) and the
+// 2^-e of its tokens 4c + i; every LDS read under one branch, all in flight.
+template <int NT>
+__device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h8v (&ah)[4], h8v (&al)[4],
+                                       float4& es) {
+    const int c = lane >> 4, t = lane & 15;
+    u32x4 h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = l[i] = u32x4{0u, 0u, 0u, 0u};
+    es = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < NT) {
+        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + (size_t)(c * NT + t) * kABytes;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * kABytes);
+            l[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * kABytes + 16);
+        }
+    }
+    if (4 * c < NT) es = *(const float4*)(m.esc + u * ntp<NT>() + 4 * c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ah[i] = __builtin_bit_cast(h8v, h[i]);
+        al[i] = __builtin_bit_cast(h8v, l[i]);
+    }
+}
+
 // Q4_K unit of TR tiles: one scale-folded chain per tile, then
 // acc += d 2^-e D - sum over the unit's sub-blocks of dmin m sum(x g).
 template <int NT, int TR>
 __device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
-    const int c = lane >> 4, t = lane & 15;
-    const int h = u & 1;
-    f4v D[TR];
+    const int c = lane >> 4, h = u & 1;
+    h8v ah[4], al[4];
+    float4 es, s4[4];
+    a_load<NT>(u, ua, lane, m, ah, al, es);
 #pragma unroll
-    for (int tr = 0; tr < TR; ++tr) D[tr] = f4v{0.f, 0.f, 0.f, 0.f};
-    // scale-folded codes: slices 0,1 use sub-block 4h + 2(c/2), slices 2,3 the next one
-    uint32_t bq[TR][4][4];
-#pragma unroll
-    for (int tr = 0; tr < TR; ++tr) {
-        uint32_t s0, m0, s1, m1;
-        q4k_sm(h, 2 * (c >> 1), M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, s0, m0);
-        q4k_sm(h, 2 * (c >> 1) + 1, M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, s1, m1);
-        const _Float16 f0 = (_Float16)(float)s0, f1 = (_Float16)(float)s1;
-        const h2v sc0{f0, f0}, sc1{f1, f1};
-        const h2v of0{(_Float16)(-1024.f * (float)s0), (_Float16)(-1024.f * (float)s0)};
-        const h2v of1{(_Float16)(-1024.f * (float)s1), (_Float16)(-1024.f * (float)s1)};
-        const uint32_t w[4] = {M[tr].q.x, M[tr].q.y, M[tr].q.z, M[tr].q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t va = w[2 * (i & 1)], vb = w[2 * (i & 1) + 1];
-            const int sh = 4 * (i >> 1);
-            const uint32_t r[4] = {((va >> sh) & 0x000F000Fu) | 0x64006400u, ((va >> (sh + 8)) & 0x000F000Fu) | 0x64006400u,
-                                   ((vb >> sh) & 0x000F000Fu) | 0x64006400u, ((vb >> (sh + 8)) & 0x000F000Fu) | 0x64006400u};
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const h2v x = as_h2(r[k]);
-                // (1024 + q) sc - 1024 sc = sc q, exact with one rounding
-                const h2v y = (i >> 1) ? __builtin_elementwise_fma(x, sc1, of1) : __builtin_elementwise_fma(x, sc0, of0);
-                bq[tr][i][k] = __builtin_bit_cast(uint32_t, y);
-            }
-        }
-    }
-    // every LDS read of the unit under one branch, all in flight together
-    u32x4 ah[4], al[4];
-    float4 es = make_float4(0.f, 0.f, 0.f, 0.f), s4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        ah[i] = al[i] = u32x4{0u, 0u, 0u, 0u};
-        s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    if (t < NT) {
-        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + (size_t)(c * NT + t) * 32;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ah[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 32);
-            al[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 32 + 16);
-        }
-    }
+    for (int i = 0; i < 4; ++i) s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c < NT) {
-        es = *(const float4*)(m.esc + u * ntp<NT>() + 4 * c);
 #pragma unroll
         for (int i = 0; i < 4; ++i) s4[i] = *(const float4*)(m.sx + min(4 * c + i, NT - 1) * m.sx_stride + 4 * u);
     }
-    // hi and lo products in two independent chains, added at the end
-    f4v Dl[TR];
-#pragma unroll
-    for (int tr = 0; tr < TR; ++tr) Dl[tr] = f4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const h8v ahi = __builtin_bit_cast(h8v, ah[i]), alo = __builtin_bit_cast(h8v, al[i]);
-#pragma unroll
-        for (int tr = 0; tr < TR; ++tr) {
-            const h8v b = __builtin_bit_cast(h8v, u32x4{bq[tr][i][0], bq[tr][i][1], bq[tr][i][2], bq[tr][i][3]});
-            D[tr] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, D[tr], 0, 0, 0);
-            Dl[tr] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, Dl[tr], 0, 0, 0);
-        }
-    }
-#pragma unroll
-    for (int tr = 0; tr < TR; ++tr) D[tr] = D[tr] + Dl[tr];
     const float esv[4] = {es.x, es.y, es.z, es.w};
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
-        const float d = h2f(M[tr].hdr.x & 0xFFFFu), dmin = h2f(M[tr].hdr.x >> 16);
+        f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // hi and lo halves in independent chains
         float mm[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            uint32_t sc, mn;
-            q4k_sm(h, s, M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, sc, mn);
-            mm[s] = dmin * (float)mn;
-        }
+        const float dmin = h2f(M[tr].hdr.x >> 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float a = __builtin_fmaf(d * esv[i], D[tr][i], acc[tr][i]);
-            a = __builtin_fmaf(-mm[0], s4[i].x, a);
-            a = __builtin_fmaf(-mm[1], s4[i].y, a);
-            a = __builtin_fmaf(-mm[2], s4[i].z, a);
-            a = __builtin_fmaf(-mm[3], s4[i].w, a);
-            acc[tr][i] = a;
+            uint32_t sc, mn;
+            q4k_sm(h, i, M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, sc, mn);
+            mm[i] = dmin * (float)mn;
+            // codes as fp16 1024 + q, then (1024 + q) sc - 1024 sc = sc q with one rounding (exact)
+            const u32x2 src = (i >> 1) ? M[tr].qb : M[tr].qa;
+            const int sh = 4 * (i & 1);
+            const _Float16 f = (_Float16)(float)sc;
+            const h2v scv{f, f}, off{(_Float16)(-1024.f * (float)sc), (_Float16)(-1024.f * (float)sc)};
+            const uint32_t r[4] = {((src.x >> sh) & 0x000F000Fu) | 0x64006400u, ((src.x >> (sh + 8)) & 0x000F000Fu) | 0x64006400u,
+                                   ((src.y >> sh) & 0x000F000Fu) | 0x64006400u, ((src.y >> (sh + 8)) & 0x000F000Fu) | 0x64006400u};
+            u32x4 bq;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) bq[k] = as_u32(__builtin_elementwise_fma(as_h2(r[k]), scv, off));
+            const h8v b = __builtin_bit_cast(h8v, bq);
+            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b, D, 0, 0, 0);
+            Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, Dl, 0, 0, 0);
+        }
+        D += Dl;
+        const float d = h2f(M[tr].hdr.x & 0xFFFFu);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float a = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
+            a = __builtin_fmaf(-mm[0], s4[e].x, a);
+            a = __builtin_fmaf(-mm[1], s4[e].y, a);
+            a = __builtin_fmaf(-mm[2], s4[e].z, a);
+            a = __builtin_fmaf(-mm[3], s4[e].w, a);
+            acc[tr][e] = a;
         }
     }
 }
 
-// Q6_K unit of TR tiles: eight 16-value sub-blocks, each its own scaled pair.
+// Q6_K unit of TR tiles: scale-folded hi / lo codes, one chain per tile,
+// acc += d 2^-e D.
 template <int NT, int TR>
 __device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
-    const int c = lane >> 4, t = lane & 15;
-    uint32_t ql[TR][4], qh[TR][4];
-    float dd[TR];
-    f4v T[TR];
+    const int c = lane >> 4;
+    h8v ah[4], al[4];
+    float4 es;
+    a_load<NT>(u, ua, lane, m, ah, al, es);
+    const float esv[4] = {es.x, es.y, es.z, es.w};
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
-        ql[tr][0] = M[tr].ql.x;
-        ql[tr][1] = M[tr].ql.y;
-        ql[tr][2] = M[tr].ql.z;
-        ql[tr][3] = M[tr].ql.w;
-        qh[tr][0] = M[tr].qh.x;
-        qh[tr][1] = M[tr].qh.y;
-        qh[tr][2] = M[tr].qh.z;
-        qh[tr][3] = M[tr].qh.w;
-        xpose4(ql[tr][0], ql[tr][1], ql[tr][2], ql[tr][3]);
-        xpose4(qh[tr][0], qh[tr][1], qh[tr][2], qh[tr][3]);
-        dd[tr] = h2f(M[tr].dh);
-        T[tr] = f4v{0.f, 0.f, 0.f, 0.f};
-    }
-    // every LDS read of the unit under one branch, all in flight together
-    u32x4 av[8];
-    float4 es = make_float4(0.f, 0.f, 0.f, 0.f);
+        f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // hi and lo activation halves in independent chains
 #pragma unroll
-    for (int i = 0; i < 8; ++i) av[i] = u32x4{0u, 0u, 0u, 0u};
-    if (t < NT) {
-        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + (size_t)(c * NT + t) * 16;
+        for (int i = 0; i < 4; ++i) {
+            // 6-bit codes of the lane's 8 values of slice i (stored + 32)
+            const u32x2 src = (i & 1) ? M[tr].qlb : M[tr].qla;
+            const int sh = 4 * (i >> 1);
+            const uint32_t q0 = ((src.x >> sh) & 0x0F0F0F0Fu) | (((M[tr].qh.x >> (2 * i)) & 0x03030303u) << 4);
+            const uint32_t q1 = ((src.y >> sh) & 0x0F0F0F0Fu) | (((M[tr].qh.y >> (2 * i)) & 0x03030303u) << 4);
+            // scale of the lane's 16-value sub-block 2i + c/2
+            const int si = 2 * i + (c >> 1);
+            const uint32_t sw = si < 4 ? M[tr].sc.x : M[tr].sc.y;
+            const _Float16 sf = (_Float16)(float)(int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
+            const h2v sc2{sf, sf}, off{(_Float16)-1056.f, (_Float16)-1056.f};  // 1024 + 32
+            const uint32_t r[4] = {(q0 & 0x00FF00FFu) | 0x64006400u, ((q0 >> 8) & 0x00FF00FFu) | 0x64006400u,
+                                   (q1 & 0x00FF00FFu) | 0x64006400u, ((q1 >> 8) & 0x00FF00FFu) | 0x64006400u};
+            u32x4 bh, bl;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) av[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * 16);
-    }
-    if (4 * c < NT) es = *(const float4*)(m.esc + u * ntp<NT>() + 4 * c);
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int jh = 0; jh < 2; ++jh) {
-            const int i = 2 * g + jh, src = 2 * (g & 1) + jh;
-            const h4v ahi = __builtin_bit_cast(h4v, u32x2{av[i].x, av[i].y}), alo = __builtin_bit_cast(h4v, u32x2{av[i].z, av[i].w});
-#pragma unroll
-            for (int tr = 0; tr < TR; ++tr) {
-                const uint32_t q = ((ql[tr][src] >> (4 * (g >> 1))) & 0x0F0F0F0Fu) |
-                                   (((qh[tr][src] >> (2 * g)) & 0x03030303u) << 4);
-                const h2v lo2 = as_h2((q & 0x00FF00FFu) | 0x64006400u), hi2 = as_h2(((q >> 8) & 0x00FF00FFu) | 0x64006400u);
-                const h2v off{(_Float16)-1056.f, (_Float16)-1056.f};  // 1024 + 32: codes are stored +32
-                const h2v b0 = lo2 + off, b1 = hi2 + off;
-                const h4v b{b0[0], b0[1], b1[0], b1[1]};
-                const f4v Dh = __builtin_amdgcn_mfma_f32_16x16x16f16(ahi, b, f4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                const f4v D = Dh + __builtin_amdgcn_mfma_f32_16x16x16f16(alo, b, f4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                const uint32_t sw = i < 4 ? M[tr].sc.x : M[tr].sc.y;
-                const float s = dd[tr] * (float)(int8_t)((sw >> (8 * (i & 3))) & 0xFFu);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) T[tr][k] = __builtin_fmaf(s, D[k], T[tr][k]);
+            for (int k = 0; k < 4; ++k) {
+                const h2v v = as_h2(r[k]) + off;  // q - 32, exact
+                const h2v hi = v * sc2;
+                bh[k] = as_u32(hi);
+                bl[k] = as_u32(__builtin_elementwise_fma(v, sc2, -hi));  // exact remainder
             }
+            const h8v bhi = __builtin_bit_cast(h8v, bh), blo = __builtin_bit_cast(h8v, bl);
+            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bhi, D, 0, 0, 0);
+            Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bhi, Dl, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], blo, D, 0, 0, 0);
         }
+        D += Dl;
+        const float d = h2f(M[tr].dh);
 #pragma unroll
-    for (int tr = 0; tr < TR; ++tr) {
-        acc[tr][0] = __builtin_fmaf(es.x, T[tr][0], acc[tr][0]);
-        acc[tr][1] = __builtin_fmaf(es.y, T[tr][1], acc[tr][1]);
-        acc[tr][2] = __builtin_fmaf(es.z, T[tr][2], acc[tr][2]);
-        acc[tr][3] = __builtin_fmaf(es.w, T[tr][3], acc[tr][3]);
+        for (int e = 0; e < 4; ++e) acc[tr][e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
     }
 }
 
@@ -911,7 +864,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
     const int c = lane >> 4, n = lane & 15;
     const int kn = p.n_in;
     const int U = kn / 128;                                      // units per row
-    const int a_stride_u = MTr<QT>::SL * 4 * NT * MTr<QT>::AB;  // bytes per unit (all tokens)
+    const int a_stride_u = kASlices * 4 * NT * kABytes;  // bytes per unit (all tokens)
     constexpr int NTP = ntp<NT>();
     // A entries: every unit (KS1), or per wave a window of HS units of its
     // range, restaged window by window when the range does not fit the LDS
@@ -1056,37 +1009,19 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                 float w[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) w[e] = v[t][k][e] * up;
-                if constexpr (QT == ORC_Q4_K) {
-                    int u, i, cc, j;
-                    a_slot<QT>(b, k0 & 255, u, i, cc, j);
-                    h8v hi, lo;
+                int u, i, cc, j;
+                a_slot(b, k0 & 255, u, i, cc, j);
+                h8v hi, lo;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const _Float16 he = (_Float16)w[e];
-                        hi[perm8(e)] = he;
-                        lo[perm8(e)] = (_Float16)(w[e] - (float)he);
-                    }
-                    uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 32;
-                    *(h8v*)ap = hi;
-                    *(h8v*)(ap + 16) = lo;
-                    if ((lane & 3) == 0) sx[t * sx_stride + (k0 >> 5)] = s8;
-                } else {
-#pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) {
-                        int u, i, cc, j;
-                        a_slot<QT>(b, (k0 & 255) + 4 * hf, u, i, cc, j);
-                        h4v hi, lo;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const _Float16 he = (_Float16)w[4 * hf + e];
-                            hi[perm8(e)] = he;
-                            lo[perm8(e)] = (_Float16)(w[4 * hf + e] - (float)he);
-                        }
-                        uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * 16;
-                        *(h4v*)ap = hi;
-                        *(h4v*)(ap + 8) = lo;
-                    }
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 he = (_Float16)w[e];
+                    hi[perm8(e)] = he;
+                    lo[perm8(e)] = (_Float16)(w[e] - (float)he);
                 }
+                uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * kABytes;
+                *(h8v*)ap = hi;
+                *(h8v*)(ap + 16) = lo;
+                if (QT == ORC_Q4_K && (lane & 3) == 0) sx[t * sx_stride + (k0 >> 5)] = s8;
             }
         }
     }
@@ -1391,10 +1326,16 @@ static int mmq_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     // count, so the mode (and the reduction order) depends on the shape alone
     const bool tall = rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU &&
                       mmq_lds(QT, kMmqMaxNT, p.n_in, two ? 2 : 1, 0) <= g_lds_max;
+    // (ring depth and staging width change no result; two-tile and wide-batch
+    // shapes keep them small enough that nothing spills)
     if (tall) return two ? mmq_shape<QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<QT, NT, 1, 6, 4, true>(p, s, ev);
-    if (per_wave <= 3) return two ? mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev) : mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
-    if (per_wave <= 4) return two ? mmq_shape<QT, NT, 2, 4, 4, false>(p, s, ev) : mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
-    return two ? mmq_shape<QT, NT, 2, 4, 8, false>(p, s, ev) : mmq_shape<QT, NT, 1, 4, 8, false>(p, s, ev);
+    if (two) return mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev);
+    if (per_wave <= 3) return mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
+    if constexpr (NT > 4) return mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
+    else {
+        if (per_wave <= 4) return mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
+        return mmq_shape<QT, NT, 1, 4, 8, false>(p, s, ev);
+    }
 }
 
 template <int QT>

@@ -215,10 +215,11 @@ __global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, con
 //    positions fit one chunk gets its output written directly.
 constexpr int kSW = 256, kSB = 64, kNCMax = 32, kRMax = 8, kMaxTokAttn = 16;
 
-__device__ __forceinline__ int chunk_positions(int P) {
+__host__ __device__ inline int chunk_positions(int P) {
     const int per = (P + kNCMax - 1) / kNCMax;
     return (per + kSB - 1) / kSB * kSB;
 }
+__host__ __device__ inline int n_chunks(int P) { return (P + chunk_positions(P) - 1) / chunk_positions(P); }
 
 // rotate-half of the pair (a = x[i], b = x[i + hd/2]) by (cos, sin) = cs, with
 // one fixed rounding sequence wherever a row is rotated
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
     const int start = start_position(d_pos, pos_off);
     const int pt = start + t;
     if (pt < 0 || pt >= ctx) return;  // outside the cache (graph replays past the end): nothing to do
-    const int P = pt + 1, CP = chunk_positions(P), nch = (P + CP - 1) / CP;
+    const int P = pt + 1, CP = chunk_positions(P), nch = n_chunks(P);
     if (c >= nch) return;  // grids cover the most chunks any position needs
     const int p0 = c * CP, p1 = min(P, p0 + CP);
     const float scale = 1.f / sqrtf((float)HD);
@@ -450,7 +451,7 @@ __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const
     const int R = n_heads / n_kv;
     const int pt = start_position(d_pos, pos_off) + t;
     if (pt < 0 || pt >= ctx) return;
-    const int P = pt + 1, CP = chunk_positions(P), nch = (P + CP - 1) / CP;
+    const int P = pt + 1, nch = n_chunks(P);
     if (nch == 1) return;
     const float* part = work + ((size_t)t * n_kv + g) * kNCMax * R * PS;
     if (tid < R) {
@@ -674,7 +675,7 @@ extern "C" size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim) 
 
 extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
                                  const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kc, float* d_vc,
-                                 int ctx, float* d_out, int ldo, void* d_work, orc_stream_t s) {
+                                 int ctx, int pos_limit, float* d_out, int ldo, void* d_work, orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
     if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || (!d_pos && (pos_off < 0 || pos_off + n_tok > ctx)) ||
         ldqkv < (n_heads + 2 * n_kv) * head_dim || ldqkv % 4 || ldo % 4 || !d_qkv || !d_rope || !d_kc || !d_vc ||
@@ -684,16 +685,16 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
     if (n_heads / n_kv > kRMax) return set_error(ORC_E_UNSUPPORTED, "attn_fused: more than 8 query heads per kv head");
     if (n_tok > kMaxTokAttn) return set_error(ORC_E_UNSUPPORTED, "attn_fused: at most 16 tokens per launch");
     if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_fused: head_dim must be 64 or 128");
+    if (pos_limit < 1 || pos_limit > ctx) return set_error(ORC_E_INVALID, "attn_fused: pos_limit must be in [1, ctx]");
     hipStream_t st = resolve_stream(s);
-    // a host position sizes the grid for the chunks the last token needs; a
-    // device position for the most any position needs
-    int nch = kNCMax;
+    // the grid covers the most chunks a token needs: the tokens' own
+    // positions (host position) or any position below pos_limit (device
+    // position); one chunk per token needs no merge launch
+    int nch = 1;
     if (!d_pos) {
-        nch = 1;
-        for (int t = 0; t < n_tok; ++t) {
-            const int P = pos_off + t + 1, per = (P + kNCMax - 1) / kNCMax, cp = (per + kSB - 1) / kSB * kSB;
-            nch = std::max(nch, (P + cp - 1) / cp);
-        }
+        for (int t = 0; t < n_tok; ++t) nch = std::max(nch, n_chunks(pos_off + t + 1));
+    } else {
+        for (int P = 1; P <= pos_limit && nch < kNCMax; ++P) nch = std::max(nch, n_chunks(P));
     }
     const dim3 grid(nch, n_kv, n_tok);
     float* w = (float*)d_work;

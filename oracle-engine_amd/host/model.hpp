@@ -74,6 +74,10 @@ public:
     // caller keeps positions inside the context. n <= kMaxBatch.
     int forward_dev_at(const int32_t* d_ids, int n, const int32_t* d_pos, int pos_off, bool compute_logits,
                        int32_t* d_argmax, orc_stream_t s = nullptr);
+    // Bound (1..ctx_len, 0 = ctx_len) on every position a device-position
+    // pass reaches, for the passes recorded while it is set: it sizes their
+    // attention grids. Results do not depend on it.
+    void set_pos_limit(int limit) { pos_limit_ = limit; }
     float* d_logits() const { return d_logits_; }
     const char* last_error() const { return err_.c_str(); }
 
@@ -96,6 +100,7 @@ private:
     bool loaded_ = false;
     uint64_t uid_ = 0;
     bool fused_attn_ = false;  // one-launch RoPE + KV store + attention supports this shape
+    int pos_limit_ = 0;
     std::vector<Layer> layers_;
     Mat embd_, head_;
     const float* out_norm_ = nullptr;

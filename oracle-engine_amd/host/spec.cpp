@@ -40,6 +40,29 @@ void DecodeSession::drop(Captured& c) {
     c = Captured();
 }
 
+// Position bound recorded into a run's graphs: the run's last position + 1
+// rounded up to a power of two (at least 512), capped at the context. It
+// sizes the attention grids of short runs.
+static int graph_limit(int need, int ctx) {
+    int lim = 512;
+    while (lim < need && lim < ctx) lim *= 2;
+    return std::min(lim, ctx);
+}
+
+// Sets the position bound of the models for the passes being captured and
+// clears it again when the capture is done.
+struct LimitScope {
+    Model *a, *b;
+    LimitScope(Model& x, Model* y, int lim) : a(&x), b(y) {
+        a->set_pos_limit(lim);
+        if (b) b->set_pos_limit(lim);
+    }
+    ~LimitScope() {
+        a->set_pos_limit(0);
+        if (b) b->set_pos_limit(0);
+    }
+};
+
 // Ends a capture that failed part-way so the stream leaves capture mode.
 static int abort_capture(int rc) {
     orc_graph_t g = nullptr;
@@ -50,8 +73,11 @@ static int abort_capture(int rc) {
 // One captured greedy step: forward at *d_pos with input d_tok[0], argmax
 // into d_tok[1], then append / advance on the device.
 int DecodeSession::greedy_graphed(Model& m, int pos, int32_t first, int n_gen, int32_t* out) {
-    if (greedy_g_.a != m.uid() || !greedy_g_.g) {
+    const int lim = graph_limit(pos + n_gen + 1, (int)m.cfg.ctx_len);
+    if (greedy_g_.a != m.uid() || greedy_g_.lim != lim || !greedy_g_.g) {
         drop(greedy_g_);
+        LimitScope ls(m, nullptr, lim);
+        greedy_g_.lim = lim;
         if (int rc = orc_graph_begin(nullptr)) return rc;
         if (int rc = m.forward_dev_at(d_tok_, 1, d_pos_, 0, true, d_tok_ + 1)) return abort_capture(rc);
         if (int rc = orc_decode_advance(d_tok_, d_hist_, d_pos_, d_pos_ + 1, nullptr)) return abort_capture(rc);
@@ -73,8 +99,11 @@ int DecodeSession::greedy_graphed(Model& m, int pos, int32_t first, int n_gen, i
 // proposal was accepted.
 int DecodeSession::spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx,
                                 int32_t* out, SpecStats& S) {
-    if (spec_g_.a != tgt.uid() || spec_g_.b != dft.uid() || spec_g_.k != k || !spec_g_.g) {
+    const int lim = graph_limit(pos + n_gen + k + 2, ctx);
+    if (spec_g_.a != tgt.uid() || spec_g_.b != dft.uid() || spec_g_.k != k || spec_g_.lim != lim || !spec_g_.g) {
         drop(spec_g_);
+        LimitScope ls(tgt, &dft, lim);
+        spec_g_.lim = lim;
         if (int rc = orc_graph_begin(nullptr)) return rc;
         for (int i = 0; i < k; ++i)
             if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1)) return abort_capture(rc);
@@ -229,8 +258,11 @@ int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, in
     if (rc) return rc;
     int pos = n_prompt - 1;
 
-    if (graphs_ && (eng_g_.a != tgt.uid() || eng_g_.b != dft.uid() || eng_g_.k != k || !eng_g_.g)) {
+    const int lim = graph_limit(pos + n_gen + k + 2, ctx);
+    if (graphs_ && (eng_g_.a != tgt.uid() || eng_g_.b != dft.uid() || eng_g_.k != k || eng_g_.lim != lim || !eng_g_.g)) {
         drop(eng_g_);
+        LimitScope ls(tgt, &dft, lim);
+        eng_g_.lim = lim;
         if ((rc = orc_graph_begin(nullptr))) return rc;
         for (int i = 0; i < k; ++i)
             if ((rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))) return abort_capture(rc);
@@ -325,8 +357,11 @@ int DecodeSession::spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, i
     if (rc) return rc;
     int pos = n_prompt - 1;
 
-    if (graphs_ && (smp_g_.a != tgt.uid() || smp_g_.b != dft.uid() || smp_g_.k != k || !smp_g_.g)) {
+    const int lim = graph_limit(pos + n_gen + k + 2, ctx);
+    if (graphs_ && (smp_g_.a != tgt.uid() || smp_g_.b != dft.uid() || smp_g_.k != k || smp_g_.lim != lim || !smp_g_.g)) {
         drop(smp_g_);
+        LimitScope ls(tgt, &dft, lim);
+        smp_g_.lim = lim;
         if ((rc = orc_graph_begin(nullptr))) return rc;
         if ((rc = sampled_round(tgt, dft, k, V))) return abort_capture(rc);
         if ((rc = orc_graph_end(nullptr, &smp_g_.g))) return rc;

@@ -81,6 +81,7 @@ private:
     struct Captured {
         uint64_t a = 0, b = 0;  // model uids
         int k = -1;
+        int lim = 0;            // bound on the positions the graph's passes reach
         orc_graph_t g = nullptr, fill = nullptr;
     };
     Captured greedy_g_, spec_g_, eng_g_, smp_g_;

@@ -268,21 +268,25 @@ def _attn_ws(dev, H, KVH, hd):
     return dev.alloc(dev.L.orc_attn_fused_workspace(H, KVH, hd))
 
 
-@pytest.mark.parametrize("H,KVH,hd,sp,nt,devpos", [(24, 8, 128, 0, 1, False), (24, 8, 128, 200, 1, True),
-                                                   (24, 8, 128, 127, 5, True), (28, 4, 128, 700, 7, False),
-                                                   (14, 2, 64, 31, 9, True), (32, 8, 64, 1000, 1, False),
-                                                   (24, 8, 128, 1300, 5, True), (24, 8, 128, 62, 5, False),
-                                                   (28, 4, 128, 2045, 9, True), (14, 2, 64, 4100, 16, False)])
-def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos):
+@pytest.mark.parametrize("H,KVH,hd,sp,nt,devpos,lim",
+                         [(24, 8, 128, 0, 1, False, 0), (24, 8, 128, 200, 1, True, 0), (24, 8, 128, 127, 5, True, 140),
+                          (28, 4, 128, 700, 7, False, 0), (14, 2, 64, 31, 9, True, 512), (32, 8, 64, 1000, 1, False, 0),
+                          (24, 8, 128, 1300, 5, True, 1400), (24, 8, 128, 62, 5, False, 0),
+                          (28, 4, 128, 2045, 9, True, 0), (14, 2, 64, 4100, 16, False, 0),
+                          (24, 8, 128, 505, 9, True, 520), (24, 8, 128, 380, 5, True, 512)])
+def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim):
     """Fused RoPE + KV store + attention equals the oracle's rope then
     attention over the prefilled cache plus the new rows; the new K/V rows
     land in the cache; the QKV rows are left as they were. Cases cross chunk
     boundaries (64 positions per chunk up to 2048, then wider chunks) and a
-    second call on the same workspace repeats the first's outputs."""
-    print(f"[gpu] attn_fused H={H} KVH={KVH} hd={hd} sp={sp} nt={nt} devpos={devpos}", flush=True)
+    second call on the same workspace repeats the first's outputs. lim: the
+    bound on the positions of a device-position call (0: the context), which
+    sizes its grid."""
+    print(f"[gpu] attn_fused H={H} KVH={KVH} hd={hd} sp={sp} nt={nt} devpos={devpos} lim={lim}", flush=True)
     rng = np.random.default_rng(sp * 7 + nt)
     base = 500000.0
-    ctx = sp + nt + 5
+    ctx = max(sp + nt + 5, lim)
+    lim = lim or ctx
     ld = (H + 2 * KVH) * hd
     qkv = rng.normal(0, 1, (nt, ld)).astype(np.float32)
     K = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
@@ -295,10 +299,10 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos):
 
     def run():
         if devpos:
-            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, dp.ptr, 3, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
-                                              H * hd, ws.ptr, None))
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, dp.ptr, 3, dt.ptr, dK.ptr, dV.ptr, ctx, lim,
+                                              dO.ptr, H * hd, ws.ptr, None))
         else:
-            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx,
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, ctx,
                                               dO.ptr, H * hd, ws.ptr, None))
         return dO.read(np.float32).reshape(nt, H * hd)
 
@@ -324,7 +328,8 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos):
         assert np.allclose(got[t], want, rtol=2e-5, atol=4e-6), (t, np.abs(got[t] - want).max())
 
 
-@pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 250, 5), (14, 2, 64, 2040, 9), (28, 4, 128, 60, 7)])
+@pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 250, 5), (14, 2, 64, 2040, 9), (28, 4, 128, 60, 7),
+                                            (24, 8, 128, 508, 9)])
 def test_attn_fused_batch_invariant(dev, H, KVH, hd, sp, nt):
     """One n-token call equals n one-token calls at the following positions
     bit for bit (the verify pass of a speculative round equals decode)."""
@@ -342,12 +347,12 @@ def test_attn_fused_batch_invariant(dev, H, KVH, hd, sp, nt):
         dK, dV = dev.upload(K), dev.upload(V)
         dO = dev.alloc(nt * H * hd * 4)
         if n == nt:
-            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
-                                              H * hd, ws.ptr, None))
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, ctx,
+                                              dO.ptr, H * hd, ws.ptr, None))
         else:
             for t in range(nt):
                 dev.check(dev.L.orc_attn_fused_at(dq.at(t * ld * 4), ld, 1, H, KVH, hd, None, sp + t, dt.ptr, dK.ptr,
-                                                  dV.ptr, ctx, dO.at(t * H * hd * 4), H * hd, ws.ptr, None))
+                                                  dV.ptr, ctx, ctx, dO.at(t * H * hd * 4), H * hd, ws.ptr, None))
         outs.append((dO.read(np.float32), dK.read(np.float32), dV.read(np.float32)))
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
