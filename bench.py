@@ -46,7 +46,7 @@ sys.path.insert(0, os.path.join(PKG, "python"))
 SYNTH = os.path.join(PKG, "bin", "synth_gguf")
 REF_DRIVER = os.path.join(ROOT, "oracle", "_ref", "ref_driver")
 HBM_PEAK_GBS = 8000.0
-TYPE_NAMES = {2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}
+TYPE_NAMES = {2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K", 256: "Q4_K|Q6_K"}
 
 
 def log(msg):
@@ -197,7 +197,7 @@ def main():
         prof_dt = time.perf_counter() - tp
         L.orc_prof_enable(0)
         H.orch_set_graphs(0 if a.no_graphs else 1)
-        for ty in ((2, 8, 12, 14) if pst else ()):
+        for ty in ((2, 8, 12, 14, 256) if pst else ()):
             for nt in range(1, 6):
                 n, ms, by = C.c_int64(), C.c_double(), C.c_double()
                 L.orc_prof_read(ty, nt, C.byref(n), C.byref(ms), C.byref(by))

@@ -126,6 +126,16 @@ typedef struct {
 int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_tok, int n_in, const float* d_x, int ldx, int ldy,
                    const float* d_norm_w, float eps, int epilogue, orc_stream_t stream);
 
+/* orc_gemm_fused over Q4_K and Q6_K segments of different types in one
+ * launch on the matrix cores (the Q|K|V projections of a Q4_K_M layer, whose
+ * attn_v is Q6_K: core/model.cpp:366-388). types[i] is segment i's type;
+ * every segment has a positive multiple of 16 rows, fewer than 65536; store
+ * or accumulate epilogue. Each segment's rows equal orc_gemm_fused on that
+ * segment alone, bit for bit. No reference counterpart (the reference runs
+ * one gemv_q per tensor). */
+int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n_segs, int n_tok, int n_in, const float* d_x,
+                         int ldx, int ldy, const float* d_norm_w, float eps, int epilogue, orc_stream_t stream);
+
 /* Live kernel timing (no reference counterpart; the reference times whole
  * loops with std::chrono, bench_engine.cpp:225-244). While enabled, every
  * GEMM launch made outside stream capture carries a start and a stop HIP

@@ -344,6 +344,8 @@ struct QmvParams {
     int epi;
     int n_groups;
     int hs;  // k_mmq split-tile mode: units of a wave's range staged at a time
+    int seg_type[3];      // k_mmq mixed launches: weight type of each segment
+    uint64_t seg_rb[3];   // and its row bytes
 };
 
 constexpr int kQWG = 512, kQWaves = kQWG / 64;
@@ -617,6 +619,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kMWG = 512, kMW = kMWG / 64;
 constexpr int kMmqMaxNT = 8;
+constexpr int kMixK = 256;  // k_mmq type parameter: Q4_K and Q6_K segments in one launch
 
 // code permutation of one 8-value run (bytes 0,2 / 1,3 / 4,6 / 5,7 land in
 // consecutive halves when two dwords are unpacked into fp16 pairs)
@@ -651,36 +654,34 @@ __device__ __forceinline__ void q4k_sm(int h, int k, uint32_t s0, uint32_t s1, u
     mn = h ? ((b2 >> 4) | ((b1 >> 6) << 4)) : (b1 & 63u);
 }
 
-// Loaded bytes of one unit of one row for lane group c.
-template <int QT> struct MUnit;
-template <> struct MUnit<ORC_Q4_K> {
-    // d, dmin, 12 scale bytes; code bytes 8c.. of the unit's first 32 (slices
-    // 0, 1: low, high nibbles) and of its next 32 (slices 2, 3)
-    // (core/gguf_parser.cpp:1096-1121)
-    u32x4 hdr;
-    u32x2 qa, qb;
-    __device__ __forceinline__ void load(const uint8_t* row, int u, int c) {
-        const uint8_t* blk = row + (size_t)(u >> 1) * 144;
-        hdr = ldg16(blk);
-        const uint8_t* qs = blk + 16 + 64 * (u & 1) + 8 * c;
-        qa = ldg8(qs);
-        qb = ldg8(qs + 32);
-    }
-};
-template <> struct MUnit<ORC_Q6_K> {
-    // low 4 bits of slices 0, 2 (ql bytes 8c..) and 1, 3 (ql bytes 32 + 8c..),
-    // high 2 bits (qh bytes 8c.., bits 2i of slice i), the half's 8 int8
-    // scales, d (core/gguf_parser.cpp:1124-1154)
-    u32x2 qla, qlb, qh, sc;
-    uint32_t dh;
-    __device__ __forceinline__ void load(const uint8_t* row, int u, int c) {
-        const uint8_t* blk = row + (size_t)(u >> 1) * 210;
-        const int hh = u & 1;
-        qla = ldg8(blk + 64 * hh + 8 * c);
-        qlb = ldg8(blk + 64 * hh + 32 + 8 * c);
-        qh = ldg8(blk + 128 + 32 * hh + 8 * c);
-        sc = ldg8(blk + 192 + 8 * hh);
-        dh = ldg2(blk + 208);
+// Loaded bytes of one unit of one row for lane group c (either type).
+//  Q4_K (core/gguf_parser.cpp:1096-1121): a, b = d, dmin and the 12 scale
+//    bytes; c, d = code bytes 8c.. of the unit's first 32 (slices 0, 1: low,
+//    high nibbles) and of its next 32 (slices 2, 3).
+//  Q6_K (core/gguf_parser.cpp:1124-1154): a, b = low 4 bits of slices 0, 2
+//    (ql bytes 8c..) and 1, 3 (ql bytes 32 + 8c..); c = high 2 bits (qh
+//    bytes 8c.., bits 2i of slice i); d = the half's 8 int8 scales; e = d.
+struct MUnit {
+    u32x2 a, b, c, d;
+    uint32_t e;
+    __device__ __forceinline__ void load(int type, const uint8_t* row, int u, int cg) {
+        if (type == ORC_Q4_K) {
+            const uint8_t* blk = row + (size_t)(u >> 1) * 144;
+            const u32x4 hdr = ldg16(blk);
+            a = u32x2{hdr.x, hdr.y};
+            b = u32x2{hdr.z, hdr.w};
+            const uint8_t* qs = blk + 16 + 64 * (u & 1) + 8 * cg;
+            c = ldg8(qs);
+            d = ldg8(qs + 32);
+        } else {
+            const uint8_t* blk = row + (size_t)(u >> 1) * 210;
+            const int hh = u & 1;
+            a = ldg8(blk + 64 * hh + 8 * cg);
+            b = ldg8(blk + 64 * hh + 32 + 8 * cg);
+            c = ldg8(blk + 128 + 32 * hh + 8 * cg);
+            d = ldg8(blk + 192 + 8 * hh);
+            e = ldg2(blk + 208);
+        }
     }
 };
 
@@ -727,7 +728,7 @@ __device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h
 // Q4_K unit of TR tiles: one scale-folded chain per tile, then
 // acc += d 2^-e D - sum over the unit's sub-blocks of dmin m sum(x g).
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int u, int ua, int lane, const MCtx& m,
+__device__ __forceinline__ void mmq_unit_q4k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
     const int c = lane >> 4, h = u & 1;
     h8v ah[4], al[4];
@@ -744,14 +745,14 @@ __device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int
     for (int tr = 0; tr < TR; ++tr) {
         f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // hi and lo halves in independent chains
         float mm[4];
-        const float dmin = h2f(M[tr].hdr.x >> 16);
+        const float dmin = h2f(M[tr].a.x >> 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint32_t sc, mn;
-            q4k_sm(h, i, M[tr].hdr.y, M[tr].hdr.z, M[tr].hdr.w, sc, mn);
+            q4k_sm(h, i, M[tr].a.y, M[tr].b.x, M[tr].b.y, sc, mn);
             mm[i] = dmin * (float)mn;
             // codes as fp16 1024 + q, then (1024 + q) sc - 1024 sc = sc q with one rounding (exact)
-            const u32x2 src = (i >> 1) ? M[tr].qb : M[tr].qa;
+            const u32x2 src = (i >> 1) ? M[tr].d : M[tr].c;
             const int sh = 4 * (i & 1);
             const _Float16 f = (_Float16)(float)sc;
             const h2v scv{f, f}, off{(_Float16)(-1024.f * (float)sc), (_Float16)(-1024.f * (float)sc)};
@@ -765,7 +766,7 @@ __device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int
             Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, Dl, 0, 0, 0);
         }
         D += Dl;
-        const float d = h2f(M[tr].hdr.x & 0xFFFFu);
+        const float d = h2f(M[tr].a.x & 0xFFFFu);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float a = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
@@ -781,7 +782,7 @@ __device__ __forceinline__ void mmq_unit_q4k(const MUnit<ORC_Q4_K> (&M)[TR], int
 // Q6_K unit of TR tiles: scale-folded hi / lo codes, one chain per tile,
 // acc += d 2^-e D.
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int u, int ua, int lane, const MCtx& m,
+__device__ __forceinline__ void mmq_unit_q6k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
     const int c = lane >> 4;
     h8v ah[4], al[4];
@@ -794,13 +795,13 @@ __device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // 6-bit codes of the lane's 8 values of slice i (stored + 32)
-            const u32x2 src = (i & 1) ? M[tr].qlb : M[tr].qla;
+            const u32x2 src = (i & 1) ? M[tr].b : M[tr].a;
             const int sh = 4 * (i >> 1);
-            const uint32_t q0 = ((src.x >> sh) & 0x0F0F0F0Fu) | (((M[tr].qh.x >> (2 * i)) & 0x03030303u) << 4);
-            const uint32_t q1 = ((src.y >> sh) & 0x0F0F0F0Fu) | (((M[tr].qh.y >> (2 * i)) & 0x03030303u) << 4);
+            const uint32_t q0 = ((src.x >> sh) & 0x0F0F0F0Fu) | (((M[tr].c.x >> (2 * i)) & 0x03030303u) << 4);
+            const uint32_t q1 = ((src.y >> sh) & 0x0F0F0F0Fu) | (((M[tr].c.y >> (2 * i)) & 0x03030303u) << 4);
             // scale of the lane's 16-value sub-block 2i + c/2
             const int si = 2 * i + (c >> 1);
-            const uint32_t sw = si < 4 ? M[tr].sc.x : M[tr].sc.y;
+            const uint32_t sw = si < 4 ? M[tr].d.x : M[tr].d.y;
             const _Float16 sf = (_Float16)(float)(int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
             const h2v sc2{sf, sf}, off{(_Float16)-1056.f, (_Float16)-1056.f};  // 1024 + 32
             const uint32_t r[4] = {(q0 & 0x00FF00FFu) | 0x64006400u, ((q0 >> 8) & 0x00FF00FFu) | 0x64006400u,
@@ -819,7 +820,7 @@ __device__ __forceinline__ void mmq_unit_q6k(const MUnit<ORC_Q6_K> (&M)[TR], int
             D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], blo, D, 0, 0, 0);
         }
         D += Dl;
-        const float d = h2f(M[tr].dh);
+        const float d = h2f(M[tr].e);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[tr][e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
     }
@@ -857,6 +858,8 @@ template <class T> __device__ __forceinline__ T* pick3(int s, T* a, T* b, T* c) 
 // ring of loads runs on across them without barriers (tall matrices).
 template <int QT, int NT, int TR, int UW, int SW, bool KS1>
 __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mmq(QmvParams p) {
+    constexpr bool MIX = QT == kMixK;  // each 16-row tile takes its segment's type
+    constexpr bool SX = QT == ORC_Q4_K || MIX;
     extern __shared__ __attribute__((aligned(16))) uint8_t msm[];
     // wave index through readfirstlane: unit indices derived from it are
     // then known to be wave-uniform (scalar branches, no exec masking)
@@ -872,7 +875,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
     uint8_t* abase = msm;
     float* sx = (float*)(msm + (size_t)(KS1 ? U : kMW * HS) * a_stride_u);  // Q4_K: [NT][kn/32]
     const int sx_stride = kn / 32;
-    float* esc = sx + (QT == ORC_Q4_K ? NT * sx_stride : 0);  // [U][NTP]
+    float* esc = sx + (SX ? NT * sx_stride : 0);  // [U][NTP]
     float* red = esc + U * NTP;                                // [NT][kMW * 4] sums of x^2 per 16-lane row
     float* part = red + NT * kMW * 4;                          // [kMW][TR][NT][16]
     const MCtx mc{abase, a_stride_u, sx, sx_stride, esc};
@@ -880,11 +883,24 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
     float *const sy0 = spin(p.y[0]), *const sy1 = spin(p.y[1]), *const sy2 = spin(p.y[2]);
     const float *const sb0 = spin(p.bias[0]), *const sb1 = spin(p.bias[1]), *const sb2 = spin(p.bias[2]);
     const int n_seg = p.n_seg, r0 = p.rows[0], r1 = p.rows[1];
+    // mixed launches: the segment types packed in one word (a choice between
+    // separately loaded values would be folded into an indexed load of the
+    // parameter block, which then lives on the stack); row bytes follow
+    const uint32_t tys = (uint32_t)p.seg_type[0] | ((uint32_t)p.seg_type[1] << 8) | ((uint32_t)p.seg_type[2] << 16);
+    auto seg_type = [=](int sgi) { return MIX ? (int)((tys >> (8 * sgi)) & 0xFFu) : QT; };
+    const uint64_t rb_q4k = (uint64_t)(kn / 256) * 144, rb_q6k = (uint64_t)(kn / 256) * 210;
     // weight row of logical row jl (clamped to row 0 past the end: loads stay in bounds)
     auto wrow = [=](int jl) {
         int jj;
         const int sgi = seg_of(jl < p.n_rows ? jl : 0, n_seg, r0, r1, jj);
-        return pick3(sgi, sw0, sw1, sw2) + (size_t)jj * p.row_bytes;
+        const uint64_t rb = MIX ? (seg_type(sgi) == ORC_Q4_K ? rb_q4k : rb_q6k) : p.row_bytes;
+        return pick3(sgi, sw0, sw1, sw2) + (size_t)jj * rb;
+    };
+    // weight type of a tile (its first row's segment; mixed launches keep
+    // every segment a whole number of tiles)
+    auto tile_type = [=](int tile) {
+        int jj;
+        return seg_type(seg_of(tile * 16 * TR < p.n_rows ? tile * 16 * TR : 0, n_seg, r0, r1, jj));
     };
     // output (and bias) of logical row jl; false past the end
     auto orow = [=](int jl, float*& y, const float*& bias) {
@@ -914,13 +930,14 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
     };
     // a ring of UW units of the TR rows in flight: unit u sits in slot
     // (u - u0) % UW and its slot is refilled with unit u + UW once consumed
-    MUnit<QT> buf[UW][TR];
+    MUnit buf[UW][TR];
 
     // the unit range a wave computes: its own eighth (split tiles) or all
     const int k0u = KS1 ? 0 : u0, k1u = KS1 ? U : u1;
     int tile = KS1 ? blockIdx.x * kMW + wave : blockIdx.x;
     const int tstride = KS1 ? gridDim.x * kMW : gridDim.x;
     const uint8_t* rp[TR];
+    int tt = tile_type(tile < n_tiles ? tile : 0);  // type of the tile being computed
     // the first tile's first units go out right after the first pass of x
     // loads (so waiting for x does not wait for them) and stay in flight
     // while x is staged
@@ -933,7 +950,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
             for (int k = 0; k < UW; ++k)
                 if (k0u + k < k1u) {
 #pragma unroll
-                    for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(rp[tr], k0u + k, c);
+                    for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(tt, rp[tr], k0u + k, c);
                 }
         }
     };
@@ -1003,7 +1020,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                 const float up = ldexpf(1.f, e2);
                 float s8 = ((v[t][k][0] + v[t][k][1]) + (v[t][k][2] + v[t][k][3])) +
                            ((v[t][k][4] + v[t][k][5]) + (v[t][k][6] + v[t][k][7]));
-                if constexpr (QT == ORC_Q4_K) s8 = quad_sum(s8);
+                if constexpr (SX) s8 = quad_sum(s8);
                 if (!valid) continue;
                 if ((lane & 15) == 0) esc[(cs + (q >> 4)) * NTP + t] = ldexpf(1.f, -e2);
                 float w[8];
@@ -1021,7 +1038,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                 uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * kABytes;
                 *(h8v*)ap = hi;
                 *(h8v*)(ap + 16) = lo;
-                if (QT == ORC_Q4_K && (lane & 3) == 0) sx[t * sx_stride + (k0 >> 5)] = s8;
+                if (SX && (lane & 3) == 0) sx[t * sx_stride + (k0 >> 5)] = s8;
             }
         }
     }
@@ -1071,6 +1088,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
 #pragma unroll
         for (int tr = 0; tr < TR; ++tr) rpn[tr] = rp[tr];
         if (next < n_tiles) tile_rows(next, rpn);
+        const int ttn = next < n_tiles ? tile_type(next) : tt;
         f4v acc[TR];
 #pragma unroll
         for (int tr = 0; tr < TR; ++tr) acc[tr] = f4v{0.f, 0.f, 0.f, 0.f};
@@ -1087,16 +1105,16 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                             wb = nwb;
                         }
                     }
-                    if constexpr (QT == ORC_Q4_K)
+                    if (tt == ORC_Q4_K)
                         mmq_unit_q4k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc);
                     else
                         mmq_unit_q6k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc);
                     if (ub + k + UW < k1u) {
 #pragma unroll
-                        for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(rp[tr], ub + k + UW, c);
+                        for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(tt, rp[tr], ub + k + UW, c);
                     } else if (next < n_tiles && k0u + k < k1u) {
 #pragma unroll
-                        for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(rpn[tr], k0u + k, c);
+                        for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(ttn, rpn[tr], k0u + k, c);
                     }
                 }
         }
@@ -1104,6 +1122,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
         first_tile = false;
         const int this_tile = tile;
         tile = next;
+        tt = ttn;
 #pragma unroll
         for (int tr = 0; tr < TR; ++tr) rp[tr] = rpn[tr];
         if constexpr (KS1) {
@@ -1270,13 +1289,13 @@ static int launch_type(const QmvParams& p, hipStream_t s, const LaunchEvents& ev
 static size_t mmq_lds(int type, int nt, int kn, int tr, int hs) {
     const int U = kn / 128, ntp = (nt + 3) & ~3;
     size_t b = (size_t)(hs ? kMW * hs : U) * 512 * nt;          // hi + lo halves: 128 values x 4 B per unit and token
-    if (type == ORC_Q4_K) b += (size_t)nt * (kn / 32) * 4;       // per-sub-block sums
+    if (type == ORC_Q4_K || type == kMixK) b += (size_t)nt * (kn / 32) * 4;  // per-sub-block sums
     b += (size_t)U * ntp * 4;                                    // per-(unit, token) scales
     b += (size_t)(nt * kMW * 4 + kMW * tr * nt * 16) * 4;        // x^2 row sums, partial sums
     return b;
 }
 
-static bool mmq_type(int type) { return type == ORC_Q4_K || type == ORC_Q6_K; }
+static bool mmq_type(int type) { return type == ORC_Q4_K || type == ORC_Q6_K || type == kMixK; }
 
 // tokens per launch: up to kMmqMaxNT as long as one unit per wave fits
 static int mmq_max_tokens(int type, int n_in) {
@@ -1320,16 +1339,19 @@ static int mmq_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& ev)
 template <int QT, int NT>
 static int mmq_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
-    const bool two = p.epi == ORC_EPI_SWIGLU || (QT == ORC_Q4_K && p.n_rows >= 32 * g_n_cu);
+    const bool two = QT != kMixK && (p.epi == ORC_EPI_SWIGLU || (QT == ORC_Q4_K && p.n_rows >= 32 * g_n_cu));
     const int rows_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.n_rows;
     // whole-tile mode only where every unit fits the LDS at the largest token
-    // count, so the mode (and the reduction order) depends on the shape alone
-    const bool tall = rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU &&
+    // count, so the mode (and the reduction order) depends on the shape alone;
+    // never for mixed launches (their segments are split-tile sized)
+    const bool tall = QT != kMixK && rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU &&
                       mmq_lds(QT, kMmqMaxNT, p.n_in, two ? 2 : 1, 0) <= g_lds_max;
     // (ring depth and staging width change no result; two-tile and wide-batch
     // shapes keep them small enough that nothing spills)
-    if (tall) return two ? mmq_shape<QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<QT, NT, 1, 6, 4, true>(p, s, ev);
-    if (two) return mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev);
+    if constexpr (QT != kMixK) {
+        if (tall) return two ? mmq_shape<QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<QT, NT, 1, 6, 4, true>(p, s, ev);
+        if (two) return mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev);
+    }
     if (per_wave <= 3) return mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
     if constexpr (NT > 4) return mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
     else {
@@ -1378,9 +1400,9 @@ static hipEvent_t prof_event() {
 // Algorithmic HBM bytes of one launch: weight blocks + activations read +
 // outputs written (read too when accumulating) + norm weights and biases.
 static double gemm_bytes(const QmvParams& p, int nt) {
-    const int n_w = p.epi == ORC_EPI_SWIGLU ? 2 * p.rows[0] : p.n_rows;
     const int n_y = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.n_rows;
-    double b = (double)p.row_bytes * n_w + 4.0 * nt * p.n_in + 4.0 * nt * n_y * (p.epi == ORC_EPI_ACCUM ? 2 : 1);
+    double b = 4.0 * nt * p.n_in + 4.0 * nt * n_y * (p.epi == ORC_EPI_ACCUM ? 2 : 1);
+    for (int i = 0; i < p.n_seg; ++i) b += (double)p.seg_rb[i] * p.rows[i];
     if (p.norm_w) b += 4.0 * p.n_in;
     for (int i = 0; i < p.n_seg; ++i)
         if (p.bias[i]) b += 4.0 * p.rows[i];
@@ -1416,6 +1438,7 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
         switch (type) {
             case ORC_Q4_K: rc = mmq_type_launch<ORC_Q4_K>(q, s, ev); break;
             case ORC_Q6_K: rc = mmq_type_launch<ORC_Q6_K>(q, s, ev); break;
+            case kMixK: rc = mmq_type_launch<kMixK>(q, s, ev); break;
             case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s, ev); break;
             case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, s, ev); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
@@ -1503,6 +1526,8 @@ extern "C" int orc_gemm(int type, const void* d_w, int n_tok, int n_out, int n_i
     p.n_rows = n_out;
     p.n_in = n_in;
     p.row_bytes = (uint64_t)orc_row_bytes(type, n_in);
+    p.seg_rb[0] = p.row_bytes;
+    p.seg_type[0] = type;
     p.x = d_x;
     p.ldx = ldx;
     p.ldy = ldy;
@@ -1533,6 +1558,10 @@ extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_t
     p.n_rows = epilogue == ORC_EPI_SWIGLU ? 2 * segs[0].n_out : total;
     p.n_in = n_in;
     p.row_bytes = (uint64_t)orc_row_bytes(type, n_in);
+    for (int i = 0; i < n_segs; ++i) {
+        p.seg_rb[i] = p.row_bytes;
+        p.seg_type[i] = type;
+    }
     p.x = d_x;
     p.ldx = ldx;
     p.ldy = ldy;
@@ -1541,4 +1570,43 @@ extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_t
     p.eps = eps;
     p.epi = epilogue;
     return gemm_dispatch(p, type, resolve_stream(stream));
+}
+
+extern "C" int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n_segs, int n_tok, int n_in,
+                                    const float* d_x, int ldx, int ldy, const float* d_norm_w, float eps, int epilogue,
+                                    orc_stream_t stream) {
+    if (!types || !segs || n_segs < 1 || n_segs > 3) return set_error(ORC_E_INVALID, "gemm_fused_mixed: 1..3 segments");
+    if (epilogue != ORC_EPI_STORE && epilogue != ORC_EPI_ACCUM)
+        return set_error(ORC_E_INVALID, "gemm_fused_mixed: store or accumulate epilogue");
+    if (d_norm_w && ((uintptr_t)d_norm_w & 15)) return set_error(ORC_E_INVALID, "norm weights must be 16-byte aligned");
+    QmvParams p{};
+    int total = 0;
+    for (int i = 0; i < n_segs; ++i) {
+        if (types[i] != ORC_Q4_K && types[i] != ORC_Q6_K)
+            return set_error(ORC_E_UNSUPPORTED, "gemm_fused_mixed: segments must be Q4_K or Q6_K");
+        if (int rc = check_gemm_shape(types[i], n_tok, n_in, d_x, ldx, ldy, segs[i].d_w)) return rc;
+        if (!segs[i].d_y || segs[i].n_out <= 0 || segs[i].n_out % 16)
+            return set_error(ORC_E_INVALID, "gemm_fused_mixed: segment rows must be a positive multiple of 16");
+        if (segs[i].n_out >= 65536)
+            return set_error(ORC_E_UNSUPPORTED, "gemm_fused_mixed: a segment of 65536 rows or more runs alone");
+        p.w[i] = (const uint8_t*)segs[i].d_w;
+        p.y[i] = segs[i].d_y;
+        p.bias[i] = segs[i].d_bias;
+        p.rows[i] = segs[i].n_out;
+        p.seg_type[i] = types[i];
+        p.seg_rb[i] = (uint64_t)orc_row_bytes(types[i], n_in);
+        total += segs[i].n_out;
+    }
+    p.n_seg = n_segs;
+    p.n_rows = total;
+    p.n_in = n_in;
+    p.row_bytes = p.seg_rb[0];
+    p.x = d_x;
+    p.ldx = ldx;
+    p.ldy = ldy;
+    p.n_tok = n_tok;
+    p.norm_w = d_norm_w;
+    p.eps = eps;
+    p.epi = epilogue;
+    return gemm_dispatch(p, kMixK, resolve_stream(stream));
 }

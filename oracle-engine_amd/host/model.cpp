@@ -163,6 +163,27 @@ void Model::warmup() {  // core/model.cpp:238-245
 
 int Model::gemm_segs(const std::vector<std::pair<const Mat*, std::pair<float*, const float*>>>& segs, int n,
                      const float* x, int ldx, int ldy, const float* norm, int epi, orc_stream_t s) {
+    // Q4_K and Q6_K matrices of whole 16-row tiles: one mixed launch
+    bool mixed = segs.size() > 1 && segs.size() <= 3 && (epi == ORC_EPI_STORE || epi == ORC_EPI_ACCUM);
+    bool types_differ = false;
+    for (const auto& sg : segs) {
+        const Mat& m = *sg.first;
+        mixed = mixed && (m.type == ORC_Q4_K || m.type == ORC_Q6_K) && m.n_out % 16 == 0 && m.n_out < 65536;
+        types_differ = types_differ || m.type != segs[0].first->type;
+    }
+    if (mixed && types_differ) {
+        orc_seg sg[3];
+        int ty[3];
+        for (size_t k = 0; k < segs.size(); ++k) {
+            sg[k].d_w = segs[k].first->d;
+            sg[k].n_out = segs[k].first->n_out;
+            sg[k].d_y = segs[k].second.first;
+            sg[k].d_bias = segs[k].second.second;
+            ty[k] = segs[k].first->type;
+        }
+        return orc_gemm_fused_mixed(ty, sg, (int)segs.size(), n, segs[0].first->n_in, x, ldx, ldy, norm,
+                                    norm ? 1e-5f : 0.f, epi, s);
+    }
     // one fused launch per run of consecutive same-type matrices
     size_t i = 0;
     while (i < segs.size()) {

@@ -155,6 +155,43 @@ def test_gemm_fused_epilogues(dev):
         assert np.array_equal(dr.read(np.float32).reshape(nt, nk), res + plain)
 
 
+@pytest.mark.parametrize("n_in,rows,types,bias", [(3072, (3072, 1024, 1024), (ol.Q4_K, ol.Q4_K, ol.Q6_K), False),
+                                                  (512, (448, 64, 64), (ol.Q4_K, ol.Q4_K, ol.Q6_K), True),
+                                                  (8192, (160, 96), (ol.Q6_K, ol.Q4_K), False)])
+def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
+    """One launch over Q4_K and Q6_K segments (a Q4_K_M layer's Q|K|V) gives
+    every segment's rows bit for bit as the per-type launches do, for 1..8
+    tokens, with the RMSNorm prologue and QKV bias."""
+    import orc
+
+    print(f"[gpu] gemm mixed n_in={n_in} rows={rows} types={types}", flush=True)
+    rng = np.random.default_rng(n_in + len(rows))
+    ws = [dev.upload(rand_blocks(t, r * n_in, rng)) for t, r in zip(types, rows)]
+    bs = [dev.upload(rng.normal(0, 0.1, r).astype(np.float32)) if bias else None for r in rows]
+    g = dev.upload(rng.uniform(0.5, 1.5, n_in).astype(np.float32))
+    ld = sum(rows)
+    offs = np.cumsum((0,) + rows)[:-1]
+    for nt in (1, 5, 8):
+        dx = dev.upload(rng.normal(0, 1, (nt, n_in)).astype(np.float32))
+        dy, dz = dev.alloc(nt * ld * 4), dev.alloc(nt * ld * 4)
+        segs = (orc.Seg * len(rows))(*[orc.Seg(w.ptr, r, dy.ptr + int(o) * 4, b.ptr if b else None)
+                                       for w, r, o, b in zip(ws, rows, offs, bs)])
+        ty = np.array(types, np.int32)
+        dev.check(dev.L.orc_gemm_fused_mixed(ty.ctypes.data_as(C.POINTER(C.c_int32)), segs, len(rows), nt, n_in,
+                                             dx.ptr, n_in, ld, g.ptr, C.c_float(1e-5), orc.EPI_STORE, None))
+        for i, (t, w, r, o, b) in enumerate(zip(types, ws, rows, offs, bs)):
+            one = (orc.Seg * 1)(orc.Seg(w.ptr, r, dz.ptr + int(o) * 4, b.ptr if b else None))
+            dev.check(dev.L.orc_gemm_fused(t, one, 1, nt, n_in, dx.ptr, n_in, ld, g.ptr, C.c_float(1e-5),
+                                           orc.EPI_STORE, None))
+        got, want = dy.read(np.float32).reshape(nt, ld), dz.read(np.float32).reshape(nt, ld)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), nt
+    # error path: a segment that is not a whole number of 16-row tiles
+    bad = (orc.Seg * 2)(orc.Seg(ws[0].ptr, 40, dy.ptr, None), orc.Seg(ws[1].ptr, 16, dy.ptr, None))
+    ty = np.array(types[:2], np.int32)
+    assert dev.L.orc_gemm_fused_mixed(ty.ctypes.data_as(C.POINTER(C.c_int32)), bad, 2, 1, n_in, dx.ptr, n_in, ld,
+                                      None, C.c_float(0), orc.EPI_STORE, None) != 0
+
+
 @pytest.mark.parametrize("qt,epi", [(ol.Q4_K, "norm"), (ol.Q6_K, "swiglu"), (ol.Q4_K, "accum")])
 def test_gemm_staging_windows(dev, oracle, qt, epi):
     """Rows too long for every token's activations to fit the LDS at once
