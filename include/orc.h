@@ -197,16 +197,23 @@ int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv,
  * orc_rope_kv_store followed by orc_attn_gqa up to fp32 rounding; a token's
  * result does not depend on n_tok. At most 8 query heads per kv head and 16
  * tokens per call; head_dim 64 or 128; 16-byte aligned rows.
- * A token's positions are split over up to 32 chunks (64 positions each up
- * to 2048) whose partial results a second launch merges: d_work holds
- * orc_attn_fused_workspace(n_heads, n_kv, head_dim) bytes, 16-byte aligned;
- * calls that share a workspace must not overlap. pos_limit (1..ctx) bounds
- * every position the call (or a captured graph replaying it at later device
- * positions) reaches; it sizes a device-position call's grid. */
+ * A token attending to at most orc_attn_wg_limit() positions is computed by
+ * one workgroup per kv head; a longer one's positions are split over up to
+ * 32 chunks (64 positions each up to 2048) whose partial results a second
+ * launch merges: d_work holds orc_attn_fused_workspace(n_heads, n_kv,
+ * head_dim) bytes, 16-byte aligned; calls that share a workspace must not
+ * overlap. With device positions, every token position p of the call (or of
+ * a captured graph replaying it at later device positions) must satisfy
+ * pos_floor <= p < pos_limit (0 <= pos_floor < pos_limit <= ctx): the call
+ * launches only the kernels such positions need (a token outside the range
+ * may be left unwritten) and sizes their grids by pos_limit. Host-position
+ * calls take pos_floor = 0, pos_limit = ctx. */
 size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim);
+int orc_attn_wg_limit(void);
 int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
                       const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kcache, float* d_vcache,
-                      int ctx, int pos_limit, float* d_out, int ldo, void* d_work, orc_stream_t stream);
+                      int ctx, int pos_floor, int pos_limit, float* d_out, int ldo, void* d_work,
+                      orc_stream_t stream);
 
 /* ── argmax, sampling, acceptance ────────────────────────────────────────── */
 /* out[r] = first index of the maximum of row r (ops::argmax ops.cpp:490-497,

@@ -725,15 +725,14 @@ __device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h
     }
 }
 
-// Q4_K unit of TR tiles: one scale-folded chain per tile, then
-// acc += d 2^-e D - sum over the unit's sub-blocks of dmin m sum(x g).
+// Q4_K unit of TR tiles with the lane's A entries given: one scale-folded
+// chain per tile, then acc += d 2^-e D - sum over the unit's sub-blocks of
+// dmin m sum(x g).
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_unit_q4k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
-                                             f4v (&acc)[TR]) {
+__device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int lane, const MCtx& m, const h8v (&ah)[4],
+                                             const h8v (&al)[4], float4 es, f4v (&acc)[TR]) {
     const int c = lane >> 4, h = u & 1;
-    h8v ah[4], al[4];
-    float4 es, s4[4];
-    a_load<NT>(u, ua, lane, m, ah, al, es);
+    float4 s4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * c < NT) {
@@ -779,15 +778,22 @@ __device__ __forceinline__ void mmq_unit_q4k(const MUnit (&M)[TR], int u, int ua
     }
 }
 
-// Q6_K unit of TR tiles: scale-folded hi / lo codes, one chain per tile,
-// acc += d 2^-e D.
+// Q4_K unit of TR tiles, A entries from the LDS.
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_unit_q6k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
+__device__ __forceinline__ void mmq_unit_q4k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
-    const int c = lane >> 4;
     h8v ah[4], al[4];
     float4 es;
     a_load<NT>(u, ua, lane, m, ah, al, es);
+    mmq_core_q4k<NT, TR>(M, u, lane, m, ah, al, es, acc);
+}
+
+// Q6_K unit of TR tiles with the lane's A entries given: scale-folded hi /
+// lo codes, one chain per tile, acc += d 2^-e D.
+template <int NT, int TR>
+__device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, const h8v (&ah)[4], const h8v (&al)[4],
+                                             float4 es, f4v (&acc)[TR]) {
+    const int c = lane >> 4;
     const float esv[4] = {es.x, es.y, es.z, es.w};
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
@@ -824,6 +830,16 @@ __device__ __forceinline__ void mmq_unit_q6k(const MUnit (&M)[TR], int u, int ua
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[tr][e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
     }
+}
+
+// Q6_K unit of TR tiles, A entries from the LDS.
+template <int NT, int TR>
+__device__ __forceinline__ void mmq_unit_q6k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
+                                             f4v (&acc)[TR]) {
+    h8v ah[4], al[4];
+    float4 es;
+    a_load<NT>(u, ua, lane, m, ah, al, es);
+    mmq_core_q6k<NT, TR>(M, lane, ah, al, es, acc);
 }
 
 // DPP reductions inside one 16-lane row (fixed order): the quad sum, then the

@@ -9,6 +9,7 @@
 #include "orc_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cfloat>
 
 namespace orc {
@@ -221,6 +222,13 @@ __host__ __device__ inline int chunk_positions(int P) {
 }
 __host__ __device__ inline int n_chunks(int P) { return (P + chunk_positions(P) - 1) / chunk_positions(P); }
 
+// Tokens attending to at most kWGMax positions take k_attn_wg (one launch, at
+// most two passes of its waves); longer ones the split over workgroups plus
+// the merge, which keeps more CUs streaming K and V.
+constexpr int kWGMax = 256;
+// waves of a k_attn_wg workgroup (the register budget of head_dim 128 allows 8)
+template <int HD> constexpr int wg_waves() { return HD == 128 ? 8 : 16; }
+
 // rotate-half of the pair (a = x[i], b = x[i + hd/2]) by (cos, sin) = cs, with
 // one fixed rounding sequence wherever a row is rotated
 __device__ __forceinline__ float rot_lo(float a, float b, float2 cs) { return __builtin_fmaf(a, cs.x, -(b * cs.y)); }
@@ -250,7 +258,7 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
     const int pt = start + t;
     if (pt < 0 || pt >= ctx) return;  // outside the cache (graph replays past the end): nothing to do
     const int P = pt + 1, CP = chunk_positions(P), nch = n_chunks(P);
-    if (c >= nch) return;  // grids cover the most chunks any position needs
+    if (P <= kWGMax || c >= nch) return;  // short contexts: k_attn_wg; grids cover the most chunks any position needs
     const int p0 = c * CP, p1 = min(P, p0 + CP);
     const float scale = 1.f / sqrtf((float)HD);
     const size_t kvh = (size_t)(n_heads + g) * HD, vvh = (size_t)(n_heads + n_kv + g) * HD;
@@ -452,7 +460,7 @@ __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const
     const int pt = start_position(d_pos, pos_off) + t;
     if (pt < 0 || pt >= ctx) return;
     const int P = pt + 1, nch = n_chunks(P);
-    if (nch == 1) return;
+    if (P <= kWGMax || nch == 1) return;
     const float* part = work + ((size_t)t * n_kv + g) * kNCMax * R * PS;
     if (tid < R) {
         const int r = tid;
@@ -473,6 +481,195 @@ __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const
         float O = 0.f;
         for (int c = 0; c < nch; ++c) O = __builtin_fmaf(part[((size_t)c * R + r) * PS + d], sf[r][c], O);
         out[(size_t)t * ldo + (g * R + r) * HD + d] = O / sL[r];
+    }
+}
+
+// ── short contexts: all chunks of a (kv head, token) in one workgroup ───────
+// Tokens attending to at most kWGMax positions: one workgroup of kWW waves per
+// (kv head g, token t). Wave w takes positions [w CPW, (w + 1) CPW) with
+// CPW = ceil(P / waves), a function of the position alone (so an n-token call
+// still equals n one-token calls bit for bit), in passes of 16: four lanes
+// per position form the scores (K rows from the cache, or for the batch's
+// own positions the QKV rows rotated in the lane), the wave keeps its own
+// online softmax (max and sum by lane exchanges over the 16 positions), and
+// each lane accumulates P.V for HD/64 dims from the pass's V rows, which were
+// loaded before the scores. The waves' (O, m, l) are merged through LDS in
+// wave order: one launch, no workspace, no fence.
+template <int HD, int RM>
+__global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qkv, int ldqkv, int n_heads, int n_kv, const int* d_pos,
+                                                 int pos_off, const float2* rope, float* kc, float* vc, int ctx,
+                                                 float* out, int ldo) {
+    constexpr int half = HD / 2, FL = HD / 16, DPL = HD / 64;
+    constexpr int kWW = wg_waves<HD>(), kWT = kWW * 64;
+    __shared__ __align__(16) float Qs[RM][HD];
+    __shared__ __align__(16) float Es[kWW][RM][16];  // a pass's exp(s - m) per wave, head, position
+    __shared__ __align__(16) float Ow[kWW][RM][HD];
+    __shared__ float mw[kWW][RM], lw[kWW][RM];
+    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int R = n_heads / n_kv;
+    const int start = start_position(d_pos, pos_off);
+    const int pt = start + t;
+    if (pt < 0 || pt >= ctx) return;  // outside the cache (graph replays past the end): nothing to do
+    const int P = pt + 1;
+    if (P > kWGMax) return;  // split over workgroups instead
+    const float scale = 1.f / sqrtf((float)HD);
+    const size_t kvh = (size_t)(n_heads + g) * HD, vvh = (size_t)(n_heads + n_kv + g) * HD;
+    const float* kg = kc + (size_t)g * ctx * HD;
+    const float* vg = vc + (size_t)g * ctx * HD;
+    const int sp = lane >> 2, sl = lane & 3;
+
+    // this token's K (rotated) and V at pt go to the cache
+    if (tid < HD) {
+        const float* kr = qkv + (size_t)t * ldqkv + kvh;
+        const float2* cs = rope + (size_t)pt * half;
+        const int d = tid;
+        const float v = d < half ? rot_lo(kr[d], kr[d + half], cs[d]) : rot_hi(kr[d - half], kr[d], cs[d - half]);
+        const size_t o = ((size_t)g * ctx + pt) * HD + d;
+        kc[o] = v;
+        vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
+    }
+    for (int i = tid; i < R * HD; i += kWT) {
+        const int r = i / HD, d = i - r * HD;
+        const float* qr = qkv + (size_t)t * ldqkv + (size_t)(g * R + r) * HD;
+        const float2* cs = rope + (size_t)pt * half;
+        Qs[r][d] = d < half ? rot_lo(qr[d], qr[d + half], cs[d]) : rot_hi(qr[d - half], qr[d], cs[d - half]);
+    }
+    const int CPW = (P + kWW - 1) / kWW;
+    const int p0 = w * CPW, p1 = min(P, p0 + CPW);
+
+    // K row of position p as this lane's FL float4s (float4 sl + 4 j; its
+    // pair partner is float4 j + FL/2 of the same lane); zero when invalid
+    auto load_k = [&](float4 (&k)[FL], int p, bool valid) {
+        if (!valid) {
+#pragma unroll
+            for (int j = 0; j < FL; ++j) k[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else if (p < start) {
+            const float* src = kg + (size_t)p * HD;
+#pragma unroll
+            for (int j = 0; j < FL; ++j) k[j] = *(const float4*)(src + 4 * (sl + 4 * j));
+        } else {
+            const float* src = qkv + (size_t)(p - start) * ldqkv + kvh;
+            const float2* cs = rope + (size_t)p * half;
+#pragma unroll
+            for (int j = 0; j < FL; ++j) k[j] = *(const float4*)(src + 4 * (sl + 4 * j));
+#pragma unroll
+            for (int j = 0; j < FL / 2; ++j) {
+                const int f = sl + 4 * j;
+                const float4 c01 = *(const float4*)(cs + 4 * f), c23 = *(const float4*)(cs + 4 * f + 2);
+                const float4 a = k[j], b = k[j + FL / 2];
+                const float2 e0{c01.x, c01.y}, e1{c01.z, c01.w}, e2{c23.x, c23.y}, e3{c23.z, c23.w};
+                k[j] = make_float4(rot_lo(a.x, b.x, e0), rot_lo(a.y, b.y, e1), rot_lo(a.z, b.z, e2), rot_lo(a.w, b.w, e3));
+                k[j + FL / 2] =
+                    make_float4(rot_hi(a.x, b.x, e0), rot_hi(a.y, b.y, e1), rot_hi(a.z, b.z, e2), rot_hi(a.w, b.w, e3));
+            }
+        }
+    };
+
+    float m[RM], l[RM], O[RM][DPL];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) O[r][k] = 0.f;
+    }
+    __syncthreads();  // Qs written
+    for (int b0 = p0; b0 < p1; b0 += 16) {
+        const int nb = min(16, p1 - b0);
+        // V of the pass's positions, this lane's DPL dims, first
+        float vv[16][DPL];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int p = b0 + j;
+            const float* src = p < start ? vg + (size_t)p * HD : qkv + (size_t)(p - start) * ldqkv + vvh;
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) vv[j][k] = 0.f;
+            if (j < nb) {
+                if constexpr (DPL == 2) {
+                    const float2 v2 = *(const float2*)(src + 2 * lane);
+                    vv[j][0] = v2.x;
+                    vv[j][1] = v2.y;
+                } else {
+                    vv[j][0] = src[lane];
+                }
+            }
+        }
+        float4 k[FL];
+        load_k(k, b0 + sp, sp < nb);
+#pragma unroll
+        for (int r = 0; r < RM; ++r) {
+            if (r >= R) break;
+            float sc = 0.f;
+#pragma unroll
+            for (int j = 0; j < FL; ++j) {
+                const float4 q = *(const float4*)&Qs[r][4 * (sl + 4 * j)];
+                sc = __builtin_fmaf(q.x, k[j].x, sc);
+                sc = __builtin_fmaf(q.y, k[j].y, sc);
+                sc = __builtin_fmaf(q.z, k[j].z, sc);
+                sc = __builtin_fmaf(q.w, k[j].w, sc);
+            }
+            sc = sp < nb ? quad_sum(sc) * scale : -INFINITY;
+            // max and sum over the pass's 16 positions (lanes 4 apart)
+            float mx = sc;
+#pragma unroll
+            for (int o = 4; o <= 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            const float m_new = fmaxf(m[r], mx);
+            const float a = m[r] == -INFINITY ? 0.f : expf(m[r] - m_new);
+            const float e = sp < nb ? expf(sc - m_new) : 0.f;
+            float es = e;
+#pragma unroll
+            for (int o = 4; o <= 32; o <<= 1) es += __shfl_xor(es, o, 64);
+            l[r] = l[r] * a + es;
+            m[r] = m_new;
+#pragma unroll
+            for (int kk = 0; kk < DPL; ++kk) O[r][kk] *= a;
+            if (sl == 0) Es[w][r][sp] = e;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int r = 0; r < RM; ++r) {
+            if (r >= R) break;
+            float ev[16];
+#pragma unroll
+            for (int j4 = 0; j4 < 4; ++j4) *(float4*)&ev[4 * j4] = *(const float4*)&Es[w][r][4 * j4];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (j < nb) {
+#pragma unroll
+                    for (int kk = 0; kk < DPL; ++kk) O[r][kk] = __builtin_fmaf(ev[j], vv[j][kk], O[r][kk]);
+                }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // the wave's partial results, then the merge in wave order
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+        if (r >= R) break;
+#pragma unroll
+        for (int kk = 0; kk < DPL; ++kk) Ow[w][r][DPL * lane + kk] = O[r][kk];
+        if (lane == 0) {
+            mw[w][r] = m[r];
+            lw[w][r] = l[r];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < R * HD; i += kWT) {
+        const int r = i / HD, d = i - r * HD;
+        float M = -INFINITY;
+        for (int v = 0; v < kWW; ++v) M = fmaxf(M, mw[v][r]);
+        float L = 0.f, o = 0.f;
+        for (int v = 0; v < kWW; ++v) {
+            if (mw[v][r] == -INFINITY) continue;  // a wave without positions
+            const float f = expf(mw[v][r] - M);
+            L = __builtin_fmaf(lw[v][r], f, L);
+            o = __builtin_fmaf(Ow[v][r][d], f, o);
+        }
+        out[(size_t)t * ldo + (g * R + r) * HD + d] = o / L;
     }
 }
 
@@ -673,9 +870,12 @@ extern "C" size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim) 
     return (size_t)kMaxTokAttn * n_heads * kNCMax * (head_dim + 32) * sizeof(float);
 }
 
+extern "C" int orc_attn_wg_limit(void) { return kWGMax; }
+
 extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
                                  const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kc, float* d_vc,
-                                 int ctx, int pos_limit, float* d_out, int ldo, void* d_work, orc_stream_t s) {
+                                 int ctx, int pos_floor, int pos_limit, float* d_out, int ldo, void* d_work,
+                                 orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
     if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || (!d_pos && (pos_off < 0 || pos_off + n_tok > ctx)) ||
         ldqkv < (n_heads + 2 * n_kv) * head_dim || ldqkv % 4 || ldo % 4 || !d_qkv || !d_rope || !d_kc || !d_vc ||
@@ -686,33 +886,48 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
     if (n_tok > kMaxTokAttn) return set_error(ORC_E_UNSUPPORTED, "attn_fused: at most 16 tokens per launch");
     if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_fused: head_dim must be 64 or 128");
     if (pos_limit < 1 || pos_limit > ctx) return set_error(ORC_E_INVALID, "attn_fused: pos_limit must be in [1, ctx]");
+    if (pos_floor < 0 || pos_floor >= pos_limit)
+        return set_error(ORC_E_INVALID, "attn_fused: pos_floor must be in [0, pos_limit)");
     hipStream_t st = resolve_stream(s);
-    // the grid covers the most chunks a token needs: the tokens' own
-    // positions (host position) or any position below pos_limit (device
-    // position); one chunk per token needs no merge launch
-    int nch = 1;
+    // which paths the tokens can take: their own positions (host position)
+    // or any position in [pos_floor, pos_limit) (device position); the split
+    // grid covers the most chunks such a position needs
+    bool short_ctx = false;
+    int nch = 0;
     if (!d_pos) {
-        for (int t = 0; t < n_tok; ++t) nch = std::max(nch, n_chunks(pos_off + t + 1));
+        for (int t = 0; t < n_tok; ++t) {
+            const int P = pos_off + t + 1;
+            if (P <= kWGMax) short_ctx = true;
+            else nch = std::max(nch, n_chunks(P));
+        }
     } else {
-        for (int P = 1; P <= pos_limit && nch < kNCMax; ++P) nch = std::max(nch, n_chunks(P));
+        short_ctx = pos_floor + 1 <= kWGMax;
+        for (int P = std::max(kWGMax, pos_floor) + 1; P <= pos_limit && nch < kNCMax; ++P)
+            nch = std::max(nch, n_chunks(P));
     }
-    const dim3 grid(nch, n_kv, n_tok);
+    const int R = n_heads / n_kv;
     float* w = (float*)d_work;
-    if (head_dim == 64) {
-        hipLaunchKernelGGL(k_attn_split<64>, grid, dim3(kSW), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off,
-                           (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
-        ORC_LAUNCH_CHECK();
-        if (nch > 1)
-            hipLaunchKernelGGL(k_attn_merge<64>, dim3(n_kv, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos, pos_off,
+    auto launch = [&](auto hd_tag) {
+        constexpr int HD = decltype(hd_tag)::value;
+        if (short_ctx) {
+            const dim3 blk(wg_waves<HD>() * 64);
+            if (R <= 4)
+                hipLaunchKernelGGL((k_attn_wg<HD, 4>), dim3(n_kv, n_tok), blk, 0, st, d_qkv, ldqkv, n_heads, n_kv,
+                                   d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+            else
+                hipLaunchKernelGGL((k_attn_wg<HD, 8>), dim3(n_kv, n_tok), blk, 0, st, d_qkv, ldqkv, n_heads, n_kv,
+                                   d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+            ORC_LAUNCH_CHECK();
+        }
+        if (nch > 0) {
+            hipLaunchKernelGGL(k_attn_split<HD>, dim3(nch, n_kv, n_tok), dim3(kSW), 0, st, d_qkv, ldqkv, n_heads, n_kv,
+                               d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
+            ORC_LAUNCH_CHECK();
+            hipLaunchKernelGGL(k_attn_merge<HD>, dim3(n_kv, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos, pos_off,
                                ctx, (const float*)w, d_out, ldo);
-    } else {
-        hipLaunchKernelGGL(k_attn_split<128>, grid, dim3(kSW), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off,
-                           (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
-        ORC_LAUNCH_CHECK();
-        if (nch > 1)
-            hipLaunchKernelGGL(k_attn_merge<128>, dim3(n_kv, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos, pos_off,
-                               ctx, (const float*)w, d_out, ldo);
-    }
-    ORC_LAUNCH_CHECK();
-    return ORC_OK;
+            ORC_LAUNCH_CHECK();
+        }
+        return ORC_OK;
+    };
+    return head_dim == 64 ? launch(std::integral_constant<int, 64>{}) : launch(std::integral_constant<int, 128>{});
 }

@@ -222,9 +222,11 @@ int Model::chunk_dev(const int32_t* d_ids, int n, const int32_t* d_pos, int sp, 
                      d_x_, D, QKV, L.attn_norm, ORC_EPI_STORE, s));
         // RoPE + KV store (model.cpp:401-408), attention (model.cpp:410-435)
         if (fused_attn_) {  // one launch: rotate, store K/V, attend
-            const int lim = d_pos && pos_limit_ > 0 && pos_limit_ < C ? pos_limit_ : C;
+            const bool band = d_pos && pos_limit_ > 0;  // a capture that declared its positions
+            const int lim = band && pos_limit_ < C ? pos_limit_ : C;
+            const int flo = band && pos_floor_ < lim ? pos_floor_ : 0;
             CK(orc_attn_fused_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc, vc,
-                                 C, lim, d_attn_, NQ, d_attn_ws_, s));
+                                 C, flo, lim, d_attn_, NQ, d_attn_ws_, s));
         } else {
             CK(orc_rope_kv_store_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc,
                                     vc, C, s));

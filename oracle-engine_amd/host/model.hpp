@@ -77,7 +77,12 @@ public:
     // Bound (1..ctx_len, 0 = ctx_len) on every position a device-position
     // pass reaches, for the passes recorded while it is set: it sizes their
     // attention grids. Results do not depend on it.
-    void set_pos_limit(int limit) { pos_limit_ = limit; }
+    // Bounds on the device positions of the passes being captured (a graph
+    // replays them at later positions): floor <= position < limit; 0, 0: none.
+    void set_pos_band(int floor, int limit) {
+        pos_floor_ = floor;
+        pos_limit_ = limit;
+    }
     float* d_logits() const { return d_logits_; }
     const char* last_error() const { return err_.c_str(); }
 
@@ -100,7 +105,7 @@ private:
     bool loaded_ = false;
     uint64_t uid_ = 0;
     bool fused_attn_ = false;  // one-launch RoPE + KV store + attention supports this shape
-    int pos_limit_ = 0;
+    int pos_floor_ = 0, pos_limit_ = 0;
     std::vector<Layer> layers_;
     Mat embd_, head_;
     const float* out_norm_ = nullptr;

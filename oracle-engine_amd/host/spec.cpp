@@ -17,10 +17,12 @@ DecodeSession::DecodeSession(int max_tokens, int max_k) : max_tokens_(max_tokens
 }
 
 DecodeSession::~DecodeSession() {
-    drop(greedy_g_);
-    drop(spec_g_);
-    drop(eng_g_);
-    drop(smp_g_);
+    for (int i = 0; i < kBands; ++i) {
+        drop(greedy_g_[i]);
+        drop(spec_g_[i]);
+        drop(eng_g_[i]);
+        drop(smp_g_[i]);
+    }
     orc_free(d_p_);
     orc_free(d_q_);
     orc_free(d_samp_);
@@ -49,17 +51,37 @@ static int graph_limit(int need, int ctx) {
     return std::min(lim, ctx);
 }
 
-// Sets the position bound of the models for the passes being captured and
-// clears it again when the capture is done.
-struct LimitScope {
-    Model *a, *b;
-    LimitScope(Model& x, Model* y, int lim) : a(&x), b(y) {
-        a->set_pos_limit(lim);
-        if (b) b->set_pos_limit(lim);
+// Band of a replay whose positions lie in [p_lo, p_hi]: 0 when all attend to
+// at most T = orc_attn_wg_limit() positions (p < T), 2 when none does, 1 when
+// they straddle T; the limit of bands 1 and 2 is the run's.
+DecodeSession::Band DecodeSession::band_of(int p_lo, int p_hi, int run_lim, int ctx) {
+    const int T = orc_attn_wg_limit();
+    if (p_hi < T) return {0, 0, std::min(T, ctx)};
+    if (p_lo >= T) return {2, T, run_lim};
+    return {1, 0, run_lim};
+}
+
+DecodeSession::Captured& DecodeSession::slot(Captured (&set)[kBands], const Band& b, uint64_t a, uint64_t bb, int k) {
+    Captured& c = set[b.idx];
+    if (c.a != a || c.b != bb || c.k != k || c.floor != b.floor || c.lim != b.lim || !c.g) {
+        drop(c);
+        c.floor = b.floor;
+        c.lim = b.lim;
     }
-    ~LimitScope() {
-        a->set_pos_limit(0);
-        if (b) b->set_pos_limit(0);
+    return c;
+}
+
+// Sets the position band of the models for the passes being captured and
+// clears it again when the capture is done.
+struct BandScope {
+    Model *a, *b;
+    BandScope(Model& x, Model* y, int floor, int lim) : a(&x), b(y) {
+        a->set_pos_band(floor, lim);
+        if (b) b->set_pos_band(floor, lim);
+    }
+    ~BandScope() {
+        a->set_pos_band(0, 0);
+        if (b) b->set_pos_band(0, 0);
     }
 };
 
@@ -73,22 +95,26 @@ static int abort_capture(int rc) {
 // One captured greedy step: forward at *d_pos with input d_tok[0], argmax
 // into d_tok[1], then append / advance on the device.
 int DecodeSession::greedy_graphed(Model& m, int pos, int32_t first, int n_gen, int32_t* out) {
-    const int lim = graph_limit(pos + n_gen + 1, (int)m.cfg.ctx_len);
-    if (greedy_g_.a != m.uid() || greedy_g_.lim != lim || !greedy_g_.g) {
-        drop(greedy_g_);
-        LimitScope ls(m, nullptr, lim);
-        greedy_g_.lim = lim;
-        if (int rc = orc_graph_begin(nullptr)) return rc;
-        if (int rc = m.forward_dev_at(d_tok_, 1, d_pos_, 0, true, d_tok_ + 1)) return abort_capture(rc);
-        if (int rc = orc_decode_advance(d_tok_, d_hist_, d_pos_, d_pos_ + 1, nullptr)) return abort_capture(rc);
-        if (int rc = orc_graph_end(nullptr, &greedy_g_.g)) return rc;
-        greedy_g_.a = m.uid();
-    }
+    const int ctx = (int)m.cfg.ctx_len;
+    const int run_lim = graph_limit(pos + n_gen + 1, ctx);
     const int32_t state[2] = {pos, 0};
     if (int rc = orc_memcpy_h2d(d_pos_, state, 8, nullptr)) return rc;
     if (int rc = orc_memcpy_h2d(d_tok_, &first, 4, nullptr)) return rc;
-    for (int s = 0; s < n_gen; ++s)
-        if (int rc = orc_graph_launch(greedy_g_.g, nullptr)) return rc;
+    for (int s = 0; s < n_gen; ++s) {
+        const Band b = band_of(pos + s, pos + s, run_lim, ctx);
+        Captured& c = slot(greedy_g_, b, m.uid(), 0, 1);
+        if (!c.g) {
+            BandScope bs(m, nullptr, b.floor, b.lim);
+            if (int rc = orc_graph_begin(nullptr)) return rc;
+            if (int rc = m.forward_dev_at(d_tok_, 1, d_pos_, 0, true, d_tok_ + 1)) return abort_capture(rc);
+            if (int rc = orc_decode_advance(d_tok_, d_hist_, d_pos_, d_pos_ + 1, nullptr)) return abort_capture(rc);
+            if (int rc = orc_graph_end(nullptr, &c.g)) return rc;
+            c.a = m.uid();
+            c.b = 0;
+            c.k = 1;
+        }
+        if (int rc = orc_graph_launch(c.g, nullptr)) return rc;
+    }
     if (int rc = orc_memcpy_d2h(out, d_hist_, (size_t)n_gen * 4, nullptr)) return rc;
     return n_gen;
 }
@@ -99,31 +125,33 @@ int DecodeSession::greedy_graphed(Model& m, int pos, int32_t first, int n_gen, i
 // proposal was accepted.
 int DecodeSession::spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx,
                                 int32_t* out, SpecStats& S) {
-    const int lim = graph_limit(pos + n_gen + k + 2, ctx);
-    if (spec_g_.a != tgt.uid() || spec_g_.b != dft.uid() || spec_g_.k != k || spec_g_.lim != lim || !spec_g_.g) {
-        drop(spec_g_);
-        LimitScope ls(tgt, &dft, lim);
-        spec_g_.lim = lim;
-        if (int rc = orc_graph_begin(nullptr)) return rc;
-        for (int i = 0; i < k; ++i)
-            if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1)) return abort_capture(rc);
-        if (int rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, d_tgt_)) return abort_capture(rc);
-        if (int rc = orc_spec_accept_greedy_at(d_tgt_, d_vin_ + 1, k, d_acc_, d_pos_, d_vin_, nullptr))
-            return abort_capture(rc);
-        if (int rc = orc_graph_end(nullptr, &spec_g_.g)) return rc;
-        if (int rc = orc_graph_begin(nullptr)) return rc;
-        if (int rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr)) return abort_capture(rc);
-        if (int rc = orc_graph_end(nullptr, &spec_g_.fill)) return rc;
-        spec_g_.a = tgt.uid();
-        spec_g_.b = dft.uid();
-        spec_g_.k = k;
-    }
+    const int run_lim = graph_limit(pos + n_gen + k + 2, ctx);
     if (int rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr)) return rc;
     if (int rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr)) return rc;
     std::vector<int32_t> h(k + 3);
     int ng = 0;
     while (ng < n_gen && pos + k + 1 <= ctx) {
-        if (int rc = orc_graph_launch(spec_g_.g, nullptr)) return rc;
+        // the round's passes reach positions pos .. pos + k (the refill included)
+        const Band b = band_of(pos, pos + k, run_lim, ctx);
+        Captured& c = slot(spec_g_, b, tgt.uid(), dft.uid(), k);
+        if (!c.g) {
+            BandScope bs(tgt, &dft, b.floor, b.lim);
+            if (int rc = orc_graph_begin(nullptr)) return rc;
+            for (int i = 0; i < k; ++i)
+                if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))
+                    return abort_capture(rc);
+            if (int rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, d_tgt_)) return abort_capture(rc);
+            if (int rc = orc_spec_accept_greedy_at(d_tgt_, d_vin_ + 1, k, d_acc_, d_pos_, d_vin_, nullptr))
+                return abort_capture(rc);
+            if (int rc = orc_graph_end(nullptr, &c.g)) return rc;
+            if (int rc = orc_graph_begin(nullptr)) return rc;
+            if (int rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr)) return abort_capture(rc);
+            if (int rc = orc_graph_end(nullptr, &c.fill)) return rc;
+            c.a = tgt.uid();
+            c.b = dft.uid();
+            c.k = k;
+        }
+        if (int rc = orc_graph_launch(c.g, nullptr)) return rc;
         if (int rc = orc_memcpy_d2h(h.data(), d_acc_, (size_t)(k + 3) * 4, nullptr)) return rc;
         const int a = h[0];
         S.proposed += k;
@@ -139,7 +167,7 @@ int DecodeSession::spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, i
             }
         }
         if (a == k && !capped)
-            if (int rc = orc_graph_launch(spec_g_.fill, nullptr)) return rc;
+            if (int rc = orc_graph_launch(c.fill, nullptr)) return rc;
         pos += a + 1;
     }
     orc_stream_sync(nullptr);
@@ -258,35 +286,37 @@ int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, in
     if (rc) return rc;
     int pos = n_prompt - 1;
 
-    const int lim = graph_limit(pos + n_gen + k + 2, ctx);
-    if (graphs_ && (eng_g_.a != tgt.uid() || eng_g_.b != dft.uid() || eng_g_.k != k || eng_g_.lim != lim || !eng_g_.g)) {
-        drop(eng_g_);
-        LimitScope ls(tgt, &dft, lim);
-        eng_g_.lim = lim;
-        if ((rc = orc_graph_begin(nullptr))) return rc;
-        for (int i = 0; i < k; ++i)
-            if ((rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))) return abort_capture(rc);
-        if ((rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, nullptr))) return abort_capture(rc);
-        if ((rc = orc_spec_accept_engine(d_samp_, tgt.d_logits(), V, V, d_vin_ + 1, k, 0, d_budget_, d_eout_, d_pos_,
-                                         d_vin_, nullptr)))
-            return abort_capture(rc);
-        if ((rc = orc_graph_end(nullptr, &eng_g_.g))) return rc;
-        if ((rc = orc_graph_begin(nullptr))) return rc;
-        if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) return abort_capture(rc);
-        if ((rc = orc_graph_end(nullptr, &eng_g_.fill))) return rc;
-        eng_g_.a = tgt.uid();
-        eng_g_.b = dft.uid();
-        eng_g_.k = k;
-    }
+    const int run_lim = graph_limit(pos + n_gen + k + 2, ctx);
     const int32_t next = ids[n_prompt - 1];
     if ((rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr))) return rc;
     if ((rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr))) return rc;
     if ((rc = orc_memcpy_h2d(d_budget_, &n_gen, 4, nullptr))) return rc;
     std::vector<int32_t> h(k + 5);
     int ng = 0;
+    Captured* c = nullptr;
     while (ng < n_gen && pos + k + 1 <= ctx) {
         if (graphs_) {
-            if ((rc = orc_graph_launch(eng_g_.g, nullptr))) return rc;
+            const Band b = band_of(pos, pos + k, run_lim, ctx);  // positions pos .. pos + k this round
+            c = &slot(eng_g_, b, tgt.uid(), dft.uid(), k);
+            if (!c->g) {
+                BandScope bs(tgt, &dft, b.floor, b.lim);
+                if ((rc = orc_graph_begin(nullptr))) return rc;
+                for (int i = 0; i < k; ++i)
+                    if ((rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1)))
+                        return abort_capture(rc);
+                if ((rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, nullptr))) return abort_capture(rc);
+                if ((rc = orc_spec_accept_engine(d_samp_, tgt.d_logits(), V, V, d_vin_ + 1, k, 0, d_budget_, d_eout_,
+                                                 d_pos_, d_vin_, nullptr)))
+                    return abort_capture(rc);
+                if ((rc = orc_graph_end(nullptr, &c->g))) return rc;
+                if ((rc = orc_graph_begin(nullptr))) return rc;
+                if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) return abort_capture(rc);
+                if ((rc = orc_graph_end(nullptr, &c->fill))) return rc;
+                c->a = tgt.uid();
+                c->b = dft.uid();
+                c->k = k;
+            }
+            if ((rc = orc_graph_launch(c->g, nullptr))) return rc;
         } else {
             for (int i = 0; i < k; ++i)
                 if ((rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))) return rc;
@@ -304,7 +334,7 @@ int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, in
         for (int i = 0; i < emitted && ng < n_gen; ++i) out[ng++] = h[4 + i];
         if (h[3] && ng < n_gen) {  // every proposal accepted: the draft lacks d_{k-1} (engine.cpp:230)
             if (graphs_) {
-                if ((rc = orc_graph_launch(eng_g_.fill, nullptr))) return rc;
+                if ((rc = orc_graph_launch(c->fill, nullptr))) return rc;
             } else if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) {
                 return rc;
             }
@@ -347,7 +377,7 @@ int DecodeSession::spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, i
         orc_free(d_q_);
         d_p_ = d_q_ = nullptr;
         pq_cap_ = 0;
-        drop(smp_g_);
+        for (Captured& c : smp_g_) drop(c);
         if (int rc = orc_malloc((void**)&d_p_, need * 4)) return rc;
         if (int rc = orc_malloc((void**)&d_q_, need * 4)) return rc;
         pq_cap_ = need;
@@ -357,32 +387,34 @@ int DecodeSession::spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, i
     if (rc) return rc;
     int pos = n_prompt - 1;
 
-    const int lim = graph_limit(pos + n_gen + k + 2, ctx);
-    if (graphs_ && (smp_g_.a != tgt.uid() || smp_g_.b != dft.uid() || smp_g_.k != k || smp_g_.lim != lim || !smp_g_.g)) {
-        drop(smp_g_);
-        LimitScope ls(tgt, &dft, lim);
-        smp_g_.lim = lim;
-        if ((rc = orc_graph_begin(nullptr))) return rc;
-        if ((rc = sampled_round(tgt, dft, k, V))) return abort_capture(rc);
-        if ((rc = orc_graph_end(nullptr, &smp_g_.g))) return rc;
-        if ((rc = orc_graph_begin(nullptr))) return rc;
-        if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) return abort_capture(rc);
-        if ((rc = orc_graph_end(nullptr, &smp_g_.fill))) return rc;
-        smp_g_.a = tgt.uid();
-        smp_g_.b = dft.uid();
-        smp_g_.k = k;
-    }
+    const int run_lim = graph_limit(pos + n_gen + k + 2, ctx);
     const int32_t next = ids[n_prompt - 1];
     if ((rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr))) return rc;
     if ((rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr))) return rc;
     if ((rc = orc_memcpy_h2d(d_budget_, &n_gen, 4, nullptr))) return rc;
     std::vector<int32_t> h(k + 5);
     int ng = 0;
+    Captured* c = nullptr;
     while (ng < n_gen && pos + k + 1 <= ctx) {
-        if (graphs_)
-            rc = orc_graph_launch(smp_g_.g, nullptr);
-        else
+        if (graphs_) {
+            const Band b = band_of(pos, pos + k, run_lim, ctx);  // positions pos .. pos + k this round
+            c = &slot(smp_g_, b, tgt.uid(), dft.uid(), k);
+            if (!c->g) {
+                BandScope bs(tgt, &dft, b.floor, b.lim);
+                if ((rc = orc_graph_begin(nullptr))) return rc;
+                if ((rc = sampled_round(tgt, dft, k, V))) return abort_capture(rc);
+                if ((rc = orc_graph_end(nullptr, &c->g))) return rc;
+                if ((rc = orc_graph_begin(nullptr))) return rc;
+                if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) return abort_capture(rc);
+                if ((rc = orc_graph_end(nullptr, &c->fill))) return rc;
+                c->a = tgt.uid();
+                c->b = dft.uid();
+                c->k = k;
+            }
+            rc = orc_graph_launch(c->g, nullptr);
+        } else {
             rc = sampled_round(tgt, dft, k, V);
+        }
         if (rc) return rc;
         if ((rc = orc_memcpy_d2h(h.data(), d_eout_, (size_t)(k + 5) * 4, nullptr))) return rc;
         const int emitted = h[0];
@@ -393,7 +425,7 @@ int DecodeSession::spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, i
         for (int i = 0; i < emitted && ng < n_gen; ++i) out[ng++] = h[4 + i];
         if (h[3] && ng < n_gen) {  // every proposal accepted: the draft lacks x_{k-1}
             if (graphs_) {
-                if ((rc = orc_graph_launch(smp_g_.fill, nullptr))) return rc;
+                if ((rc = orc_graph_launch(c->fill, nullptr))) return rc;
             } else if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) {
                 return rc;
             }

@@ -37,10 +37,12 @@ public:
     // after kernel timing was switched on, to include its event nodes).
     void set_graphs(bool on) {
         graphs_ = on;
-        drop(greedy_g_);
-        drop(spec_g_);
-        drop(eng_g_);
-        drop(smp_g_);
+        for (int i = 0; i < kBands; ++i) {
+            drop(greedy_g_[i]);
+            drop(spec_g_[i]);
+            drop(eng_g_[i]);
+            drop(smp_g_[i]);
+        }
     }
     bool graphs() const { return graphs_; }
 
@@ -81,10 +83,19 @@ private:
     struct Captured {
         uint64_t a = 0, b = 0;  // model uids
         int k = -1;
-        int lim = 0;            // bound on the positions the graph's passes reach
+        int floor = 0, lim = 0;  // floor <= every position the graph's passes reach < lim
         orc_graph_t g = nullptr, fill = nullptr;
     };
-    Captured greedy_g_, spec_g_, eng_g_, smp_g_;
+    // One graph per position band of a loop (the attention kernels a replay
+    // needs depend on which side of orc_attn_wg_limit() its positions lie).
+    static constexpr int kBands = 3;
+    struct Band {
+        int idx, floor, lim;
+    };
+    static Band band_of(int p_lo, int p_hi, int run_lim, int ctx);
+    // the slot of band b, emptied when it holds another capture
+    Captured& slot(Captured (&set)[kBands], const Band& b, uint64_t a, uint64_t bb, int k);
+    Captured greedy_g_[kBands], spec_g_[kBands], eng_g_[kBands], smp_g_[kBands];
     float* d_p_ = nullptr;  // target distributions, k+1 rows
     float* d_q_ = nullptr;  // draft distributions, k rows
     size_t pq_cap_ = 0;     // floats in each of d_p_ / d_q_

@@ -104,12 +104,13 @@ def test_gemm_batch_invariant(dev, qt, n_out, n_in):
         assert np.array_equal(got.view(np.uint32), single[:nt].view(np.uint32)), nt
 
 
-def test_gemm_fused_epilogues(dev):
-    print("[gpu] fused epilogues", flush=True)
+@pytest.mark.parametrize("n_in", [512, 3072])  # 3072: the streamed-weight kernel
+def test_gemm_fused_epilogues(dev, n_in):
+    print(f"[gpu] fused epilogues n_in={n_in}", flush=True)
     import orc
 
     rng = np.random.default_rng(11)
-    n_in, nq, nk, ff = 512, 256, 128, 384
+    nq, nk, ff = 256, 128, 384
     wq, wk, wv = (dev.upload(rand_blocks(ol.Q4_K, n * n_in, rng)) for n in (nq, nk, nk))
     bq = dev.upload(rng.normal(0, 0.1, nq).astype(np.float32))
     normw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
@@ -134,17 +135,18 @@ def test_gemm_fused_epilogues(dev):
         for got, want in ((Y[:, :nq], ref[0]), (Y[:, nq:nq + nk], ref[1]), (Y[:, nq + nk:], ref[2])):
             assert np.allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
         # SwiGLU: silu(gate) * up
-        wg, wu = (dev.upload(rand_blocks(ol.Q6_K, ff * n_in, rng)) for _ in range(2))
-        g = _gemm(dev, ol.Q6_K, wg, nt, ff, n_in, X)
-        u = _gemm(dev, ol.Q6_K, wu, nt, ff, n_in, X)
-        dh = dev.alloc(nt * ff * 4)
-        segs2 = (orc.Seg * 2)(orc.Seg(wg.ptr, ff, dh.ptr, None), orc.Seg(wu.ptr, ff, None, None))
-        segs2[1].d_y = dh.ptr
-        dev.check(dev.L.orc_gemm_fused(ol.Q6_K, segs2, 2, nt, n_in, dx.ptr, n_in, ff, None, C.c_float(0),
-                                       orc.EPI_SWIGLU, None))
-        h = dh.read(np.float32).reshape(nt, ff)
-        want = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
-        assert np.allclose(h, want, rtol=1e-5, atol=1e-6)
+        for st in (ol.Q6_K, ol.Q4_K):
+            wg, wu = (dev.upload(rand_blocks(st, ff * n_in, rng)) for _ in range(2))
+            g = _gemm(dev, st, wg, nt, ff, n_in, X)
+            u = _gemm(dev, st, wu, nt, ff, n_in, X)
+            dh = dev.alloc(nt * ff * 4)
+            segs2 = (orc.Seg * 2)(orc.Seg(wg.ptr, ff, dh.ptr, None), orc.Seg(wu.ptr, ff, None, None))
+            segs2[1].d_y = dh.ptr
+            dev.check(dev.L.orc_gemm_fused(st, segs2, 2, nt, n_in, dx.ptr, n_in, ff, None, C.c_float(0),
+                                           orc.EPI_SWIGLU, None))
+            h = dh.read(np.float32).reshape(nt, ff)
+            want = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
+            assert np.allclose(h, want, rtol=1e-5, atol=1e-6), st
         # residual accumulate
         res = rng.normal(0, 1, (nt, nk)).astype(np.float32)
         dr = dev.upload(res)
@@ -305,21 +307,29 @@ def _attn_ws(dev, H, KVH, hd):
     return dev.alloc(dev.L.orc_attn_fused_workspace(H, KVH, hd))
 
 
-@pytest.mark.parametrize("H,KVH,hd,sp,nt,devpos,lim",
-                         [(24, 8, 128, 0, 1, False, 0), (24, 8, 128, 200, 1, True, 0), (24, 8, 128, 127, 5, True, 140),
-                          (28, 4, 128, 700, 7, False, 0), (14, 2, 64, 31, 9, True, 512), (32, 8, 64, 1000, 1, False, 0),
-                          (24, 8, 128, 1300, 5, True, 1400), (24, 8, 128, 62, 5, False, 0),
-                          (28, 4, 128, 2045, 9, True, 0), (14, 2, 64, 4100, 16, False, 0),
-                          (24, 8, 128, 505, 9, True, 520), (24, 8, 128, 380, 5, True, 512)])
-def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim):
+@pytest.mark.parametrize("H,KVH,hd,sp,nt,devpos,lim,flo",
+                         [(24, 8, 128, 0, 1, False, 0, 0), (24, 8, 128, 200, 1, True, 0, 0),
+                          (24, 8, 128, 127, 5, True, 140, 0), (28, 4, 128, 700, 7, False, 0, 0),
+                          (14, 2, 64, 31, 9, True, 512, 0), (32, 8, 64, 1000, 1, False, 0, 0),
+                          (24, 8, 128, 1300, 5, True, 1400, 0), (24, 8, 128, 62, 5, False, 0, 0),
+                          (28, 4, 128, 2045, 9, True, 0, 0), (14, 2, 64, 4100, 16, False, 0, 0),
+                          (24, 8, 128, 505, 9, True, 520, 0), (24, 8, 128, 380, 5, True, 512, 0),
+                          (24, 8, 128, 1020, 9, True, 1100, 0), (14, 2, 64, 1019, 9, False, 0, 0),
+                          (24, 8, 128, 100, 5, True, 256, 0), (24, 8, 128, 251, 5, True, 256, 0),
+                          (24, 8, 128, 250, 9, True, 512, 0), (24, 8, 128, 256, 5, True, 512, 256),
+                          (24, 8, 128, 300, 9, True, 512, 256), (14, 2, 64, 253, 9, False, 0, 0),
+                          (28, 4, 128, 1500, 5, True, 2048, 256)])
+def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim, flo):
     """Fused RoPE + KV store + attention equals the oracle's rope then
     attention over the prefilled cache plus the new rows; the new K/V rows
     land in the cache; the QKV rows are left as they were. Cases cross chunk
-    boundaries (64 positions per chunk up to 2048, then wider chunks) and a
-    second call on the same workspace repeats the first's outputs. lim: the
-    bound on the positions of a device-position call (0: the context), which
-    sizes its grid."""
-    print(f"[gpu] attn_fused H={H} KVH={KVH} hd={hd} sp={sp} nt={nt} devpos={devpos} lim={lim}", flush=True)
+    boundaries (64 positions per chunk up to 2048, then wider chunks) and the
+    switch between the one-workgroup path and the split (256 positions), and
+    a second call on the same workspace repeats the first's outputs. lim, flo:
+    the bounds flo <= position < lim declared by a device-position call (lim
+    0: the context), which select its kernels and size their grids."""
+    print(f"[gpu] attn_fused H={H} KVH={KVH} hd={hd} sp={sp} nt={nt} devpos={devpos} lim={lim} flo={flo}", flush=True)
+    assert dev.L.orc_attn_wg_limit() == 256
     rng = np.random.default_rng(sp * 7 + nt)
     base = 500000.0
     ctx = max(sp + nt + 5, lim)
@@ -336,11 +346,11 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim):
 
     def run():
         if devpos:
-            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, dp.ptr, 3, dt.ptr, dK.ptr, dV.ptr, ctx, lim,
-                                              dO.ptr, H * hd, ws.ptr, None))
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, dp.ptr, 3, dt.ptr, dK.ptr, dV.ptr, ctx, flo,
+                                              lim, dO.ptr, H * hd, ws.ptr, None))
         else:
-            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, ctx,
-                                              dO.ptr, H * hd, ws.ptr, None))
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, 0,
+                                              ctx, dO.ptr, H * hd, ws.ptr, None))
         return dO.read(np.float32).reshape(nt, H * hd)
 
     got = run()
@@ -366,7 +376,8 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim):
 
 
 @pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 250, 5), (14, 2, 64, 2040, 9), (28, 4, 128, 60, 7),
-                                            (24, 8, 128, 508, 9)])
+                                            (24, 8, 128, 508, 9), (28, 4, 128, 1019, 9), (14, 2, 64, 3, 16),
+                                            (24, 8, 128, 252, 9), (14, 2, 64, 250, 9)])
 def test_attn_fused_batch_invariant(dev, H, KVH, hd, sp, nt):
     """One n-token call equals n one-token calls at the following positions
     bit for bit (the verify pass of a speculative round equals decode)."""
@@ -384,12 +395,12 @@ def test_attn_fused_batch_invariant(dev, H, KVH, hd, sp, nt):
         dK, dV = dev.upload(K), dev.upload(V)
         dO = dev.alloc(nt * H * hd * 4)
         if n == nt:
-            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, ctx,
-                                              dO.ptr, H * hd, ws.ptr, None))
+            dev.check(dev.L.orc_attn_fused_at(dq.ptr, ld, nt, H, KVH, hd, None, sp, dt.ptr, dK.ptr, dV.ptr, ctx, 0,
+                                              ctx, dO.ptr, H * hd, ws.ptr, None))
         else:
             for t in range(nt):
                 dev.check(dev.L.orc_attn_fused_at(dq.at(t * ld * 4), ld, 1, H, KVH, hd, None, sp + t, dt.ptr, dK.ptr,
-                                                  dV.ptr, ctx, ctx, dO.at(t * H * hd * 4), H * hd, ws.ptr, None))
+                                                  dV.ptr, ctx, 0, ctx, dO.at(t * H * hd * 4), H * hd, ws.ptr, None))
         outs.append((dO.read(np.float32), dK.read(np.float32), dV.read(np.float32)))
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
