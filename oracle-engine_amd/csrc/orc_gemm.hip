@@ -590,14 +590,15 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
 }
 
 // ── matrix-core path (Q4_K, Q6_K) ────────────────────────────────────────────
-// Activations are the MFMA's A operand (16 token rows, the batch's tokens and
-// padding), weights the B operand (16 weight rows of a tile), so D[token][row]
-// lands with one weight row per lane: lane l holds D[4 (l/16) + i][l % 16].
-// Each activation x' (x times the norm weight times a per-token power of two
-// that keeps it inside the fp16 range) is split as hi = fp16(x'),
-// lo = fp16(x' - hi); hi + lo carries ~22 bits and every product with a
-// weight code is exact in fp32, so D matches an fp32 dot product to fp32
-// rounding.
+// Activations are the MFMA's A operand, weights the B operand (16 weight rows
+// of a tile), so D[a row][weight row] lands with one weight row per lane:
+// lane l holds D[4 (l/16) + i][l % 16]. Each activation x' (x times the norm
+// weight times a per-token power of two that keeps it inside the fp16 range)
+// is split as hi = fp16(x'), lo = fp16(x' - hi); hi + lo carries ~22 bits and
+// every product with a weight code is exact in fp32. A launch has at most 8
+// tokens, so A row t holds token t's hi halves and row 8 + t its lo halves:
+// one MFMA takes both, and the two rows' sums are added once per tile
+// (lanes l and l + 32), which matches an fp32 dot product to fp32 rounding.
 // A unit is half a superblock (128 values) of one row, in four 32-value
 // slices of one v_mfma_f32_16x16x32_f16 each; lane group c (lanes 16c..16c+15)
 // holds values 8c..8c+7 of a slice, the same for both types:
@@ -607,8 +608,7 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
 //  * Q6_K: a slice spans two 16-value sub-blocks whose int8 scales do not
 //    fit the code exactly (sc * (q - 32) up to 4096), so the scaled code is
 //    split into hi = fp16(sc (q - 32)) and lo = sc (q - 32) - hi (exact,
-//    |lo| <= 1): hi x hi + lo x hi + hi x lo per slice (the lo x lo term,
-//    2^-22 of a product, is dropped), d scales the chain.
+//    |lo| <= 1): one MFMA per code half and slice, d scales the chain.
 // The eight waves of a workgroup split a tile's units into fixed contiguous
 // ranges and their partial sums are added in wave order, so a (token, row)
 // result does not depend on the token count: a (k+1)-token verify equals k+1
@@ -625,7 +625,8 @@ constexpr int kMixK = 256;  // k_mmq type parameter: Q4_K and Q6_K segments in o
 // consecutive halves when two dwords are unpacked into fp16 pairs)
 __device__ __forceinline__ int perm8(int j) { return (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1); }
 
-// A entries: per unit, per (slice, lane group, token), 8 hi then 8 lo halves
+// A entries: per unit, per (slice, lane group, half (hi, lo), token), 8 halves;
+// kABytes per (slice, lane group, token)
 constexpr int kASlices = 4, kABytes = 32;
 
 // A entry of element kk (0..255) of superblock b: unit u, slice i, lane
@@ -699,50 +700,59 @@ struct MCtx {
 
 template <int NT> constexpr int ntp() { return (NT + 3) & ~3; }
 
-// The lane's A entries of a unit (all four slices, token lane % 16) and the
-// 2^-e of its tokens 4c + i; every LDS read under one branch, all in flight.
-template <int NT>
-__device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h8v (&ah)[4], h8v (&al)[4],
-                                       float4& es) {
-    const int c = lane >> 4, t = lane & 15;
-    u32x4 h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = l[i] = u32x4{0u, 0u, 0u, 0u};
-    es = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < NT) {
-        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + (size_t)(c * NT + t) * kABytes;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            h[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * kABytes);
-            l[i] = *(const u32x4*)(ap + (size_t)i * 4 * NT * kABytes + 16);
-        }
-    }
-    if (4 * c < NT) es = *(const float4*)(m.esc + u * ntp<NT>() + 4 * c);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        ah[i] = __builtin_bit_cast(h8v, h[i]);
-        al[i] = __builtin_bit_cast(h8v, l[i]);
-    }
+// Byte offset of A entry (slice i, lane group c, half hl, token t) in a unit.
+template <int NT> __device__ __forceinline__ int a_off(int i, int c, int hl, int t) {
+    return (((i * 4 + c) * 2 + hl) * NT + t) * 16;
 }
 
-// Q4_K unit of TR tiles with the lane's A entries given: one scale-folded
-// chain per tile, then acc += d 2^-e D - sum over the unit's sub-blocks of
-// dmin m sum(x g).
+// The lane's A entries of a unit (all four slices; lane row r = lane % 16:
+// hi of token r, or lo of token r - 8) and the 2^-e of the tokens of its D
+// rows, 4 (c % 2) + i; every LDS read under one branch, all in flight.
+template <int NT>
+__device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h8v (&a)[4], float4& es) {
+    static_assert(NT <= 8, "hi and lo rows of at most 8 tokens");
+    const int c = lane >> 4, r = lane & 15, t = r & 7, tb = 4 * (c & 1);
+    u32x4 h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h[i] = u32x4{0u, 0u, 0u, 0u};
+    es = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < NT) {
+        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + a_off<NT>(0, c, r >> 3, t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 0, 0));
+    }
+    if (tb < NT) es = *(const float4*)(m.esc + u * ntp<NT>() + tb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = __builtin_bit_cast(h8v, h[i]);
+}
+
+// Adds the lo rows' sums to the hi rows' (lanes l and l + 32): afterwards
+// lanes 0..31 hold the tile's results for tokens 4 (l / 16) + i.
+template <int TR> __device__ __forceinline__ void fold_lo(f4v (&acc)[TR]) {
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[tr][e] += __shfl_xor(acc[tr][e], 32, 64);
+}
+
+// Q4_K unit of TR tiles with the lane's A entries given: scale-folded codes
+// (slices alternating between two chains), then acc += d 2^-e D, minus, on
+// the hi rows only, the sum over the unit's sub-blocks of dmin m sum(x g).
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int lane, const MCtx& m, const h8v (&ah)[4],
-                                             const h8v (&al)[4], float4 es, f4v (&acc)[TR]) {
-    const int c = lane >> 4, h = u & 1;
+__device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int lane, const MCtx& m, const h8v (&a)[4],
+                                             float4 es, f4v (&acc)[TR]) {
+    const int c = lane >> 4, h = u & 1, tb = 4 * (c & 1);
     float4 s4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * c < NT) {
+    if (c < 2 && tb < NT) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s4[i] = *(const float4*)(m.sx + min(4 * c + i, NT - 1) * m.sx_stride + 4 * u);
+        for (int i = 0; i < 4; ++i) s4[i] = *(const float4*)(m.sx + min(tb + i, NT - 1) * m.sx_stride + 4 * u);
     }
     const float esv[4] = {es.x, es.y, es.z, es.w};
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
-        f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // hi and lo halves in independent chains
+        f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // even and odd slices in independent chains
         float mm[4];
         const float dmin = h2f(M[tr].a.x >> 16);
 #pragma unroll
@@ -761,8 +771,10 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
 #pragma unroll
             for (int k = 0; k < 4; ++k) bq[k] = as_u32(__builtin_elementwise_fma(as_h2(r[k]), scv, off));
             const h8v b = __builtin_bit_cast(h8v, bq);
-            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], b, D, 0, 0, 0);
-            Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, Dl, 0, 0, 0);
+            if (i & 1)
+                Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, Dl, 0, 0, 0);
+            else
+                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, D, 0, 0, 0);
         }
         D += Dl;
         const float d = h2f(M[tr].a.x & 0xFFFFu);
@@ -782,22 +794,22 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
 template <int NT, int TR>
 __device__ __forceinline__ void mmq_unit_q4k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
-    h8v ah[4], al[4];
+    h8v a[4];
     float4 es;
-    a_load<NT>(u, ua, lane, m, ah, al, es);
-    mmq_core_q4k<NT, TR>(M, u, lane, m, ah, al, es, acc);
+    a_load<NT>(u, ua, lane, m, a, es);
+    mmq_core_q4k<NT, TR>(M, u, lane, m, a, es, acc);
 }
 
 // Q6_K unit of TR tiles with the lane's A entries given: scale-folded hi /
-// lo codes, one chain per tile, acc += d 2^-e D.
+// lo codes in two chains, acc += d 2^-e D.
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, const h8v (&ah)[4], const h8v (&al)[4],
-                                             float4 es, f4v (&acc)[TR]) {
+__device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, const h8v (&a)[4], float4 es,
+                                             f4v (&acc)[TR]) {
     const int c = lane >> 4;
     const float esv[4] = {es.x, es.y, es.z, es.w};
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
-        f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // hi and lo activation halves in independent chains
+        f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // hi and lo code halves in independent chains
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // 6-bit codes of the lane's 8 values of slice i (stored + 32)
@@ -821,9 +833,8 @@ __device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, con
                 bl[k] = as_u32(__builtin_elementwise_fma(v, sc2, -hi));  // exact remainder
             }
             const h8v bhi = __builtin_bit_cast(h8v, bh), blo = __builtin_bit_cast(h8v, bl);
-            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bhi, D, 0, 0, 0);
-            Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bhi, Dl, 0, 0, 0);
-            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], blo, D, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bhi, D, 0, 0, 0);
+            Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], blo, Dl, 0, 0, 0);
         }
         D += Dl;
         const float d = h2f(M[tr].e);
@@ -836,10 +847,10 @@ __device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, con
 template <int NT, int TR>
 __device__ __forceinline__ void mmq_unit_q6k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
                                              f4v (&acc)[TR]) {
-    h8v ah[4], al[4];
+    h8v a[4];
     float4 es;
-    a_load<NT>(u, ua, lane, m, ah, al, es);
-    mmq_core_q6k<NT, TR>(M, lane, ah, al, es, acc);
+    a_load<NT>(u, ua, lane, m, a, es);
+    mmq_core_q6k<NT, TR>(M, lane, a, es, acc);
 }
 
 // DPP reductions inside one 16-lane row (fixed order): the quad sum, then the
@@ -1051,9 +1062,9 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                     hi[perm8(e)] = he;
                     lo[perm8(e)] = (_Float16)(w[e] - (float)he);
                 }
-                uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u + (size_t)((i * 4 + cc) * NT + t) * kABytes;
-                *(h8v*)ap = hi;
-                *(h8v*)(ap + 16) = lo;
+                uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u;
+                *(h8v*)(ap + a_off<NT>(i, cc, 0, t)) = hi;
+                *(h8v*)(ap + a_off<NT>(i, cc, 1, t)) = lo;
                 if (SX && (lane & 3) == 0) sx[t * sx_stride + (k0 >> 5)] = s8;
             }
         }
@@ -1134,6 +1145,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                     }
                 }
         }
+        fold_lo<TR>(acc);
         if (multi_win && first_tile) write_red();
         first_tile = false;
         const int this_tile = tile;
