@@ -647,12 +647,17 @@ __device__ __forceinline__ u32x4 ldg16(const uint8_t* p) { return *(g16p)p; }
 __device__ __forceinline__ u32x2 ldg8(const uint8_t* p) { return *(g8p)p; }
 __device__ __forceinline__ uint32_t ldg2(const uint8_t* p) { return *(g2p)p; }
 
-// Q4_K (scale, min) of sub-block 4h + k (h = 0, 1 and k = 0..3),
-// branch-free (core/gguf_parser.cpp:1085-1093).
-__device__ __forceinline__ void q4k_sm(int h, int k, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc, uint32_t& mn) {
-    const uint32_t b0 = (s0 >> (8 * k)) & 0xFFu, b1 = (s1 >> (8 * k)) & 0xFFu, b2 = (s2 >> (8 * k)) & 0xFFu;
-    sc = h ? ((b2 & 0xFu) | ((b0 >> 6) << 4)) : (b0 & 63u);
-    mn = h ? ((b2 >> 4) | ((b1 >> 6) << 4)) : (b1 & 63u);
+// Q4_K 6-bit scales and minimums of sub-blocks 4h .. 4h + 3 (h = 0, 1), one
+// per byte of sc4 / mn4, from the 12 scale bytes s0 | s1 | s2
+// (core/gguf_parser.cpp:1085-1093); branch-free, h selects by mask.
+__device__ __forceinline__ void q4k_unit_sm(int h, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc4,
+                                            uint32_t& mn4) {
+    const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, mn_lo = s1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    const uint32_t msk = 0u - (uint32_t)(h & 1);
+    sc4 = sc_lo ^ ((sc_lo ^ sc_hi) & msk);
+    mn4 = mn_lo ^ ((mn_lo ^ mn_hi) & msk);
 }
 
 // Loaded bytes of one unit of one row for lane group c (either type).
@@ -755,10 +760,11 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
         f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // even and odd slices in independent chains
         float mm[4];
         const float dmin = h2f(M[tr].a.x >> 16);
+        uint32_t sc4, mn4;
+        q4k_unit_sm(h, M[tr].a.y, M[tr].b.x, M[tr].b.y, sc4, mn4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint32_t sc, mn;
-            q4k_sm(h, i, M[tr].a.y, M[tr].b.x, M[tr].b.y, sc, mn);
+            const uint32_t sc = (sc4 >> (8 * i)) & 0xFFu, mn = (mn4 >> (8 * i)) & 0xFFu;
             mm[i] = dmin * (float)mn;
             // codes as fp16 1024 + q, then (1024 + q) sc - 1024 sc = sc q with one rounding (exact)
             const u32x2 src = (i >> 1) ? M[tr].d : M[tr].c;
