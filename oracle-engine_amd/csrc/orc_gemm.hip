@@ -647,6 +647,19 @@ __device__ __forceinline__ u32x4 ldg16(const uint8_t* p) { return *(g16p)p; }
 __device__ __forceinline__ u32x2 ldg8(const uint8_t* p) { return *(g8p)p; }
 __device__ __forceinline__ uint32_t ldg2(const uint8_t* p) { return *(g2p)p; }
 
+// Constants held in registers: a VOP3 operation such as v_and_or_b32 takes no
+// literal, so (x & mask) | magic is one operation only with both in registers.
+__device__ __forceinline__ uint32_t sreg(uint32_t c) {
+    uint32_t r;
+    asm("s_mov_b32 %0, %1" : "=s"(r) : "n"(c));
+    return r;
+}
+__device__ __forceinline__ uint32_t vreg(uint32_t c) {
+    uint32_t r;
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "n"(c));
+    return r;
+}
+
 // Q4_K 6-bit scales and minimums of sub-blocks 4h .. 4h + 3 (h = 0, 1), one
 // per byte of sc4 / mn4, from the 12 scale bytes s0 | s1 | s2
 // (core/gguf_parser.cpp:1085-1093); branch-free, h selects by mask.
@@ -771,8 +784,9 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
             const int sh = 4 * (i & 1);
             const _Float16 f = (_Float16)(float)sc;
             const h2v scv{f, f}, off{(_Float16)(-1024.f * (float)sc), (_Float16)(-1024.f * (float)sc)};
-            const uint32_t r[4] = {((src.x >> sh) & 0x000F000Fu) | 0x64006400u, ((src.x >> (sh + 8)) & 0x000F000Fu) | 0x64006400u,
-                                   ((src.y >> sh) & 0x000F000Fu) | 0x64006400u, ((src.y >> (sh + 8)) & 0x000F000Fu) | 0x64006400u};
+            const uint32_t m4 = sreg(0x000F000Fu), mg = vreg(0x64006400u);
+            const uint32_t r[4] = {((src.x >> sh) & m4) | mg, ((src.x >> (sh + 8)) & m4) | mg, ((src.y >> sh) & m4) | mg,
+                                   ((src.y >> (sh + 8)) & m4) | mg};
             u32x4 bq;
 #pragma unroll
             for (int k = 0; k < 4; ++k) bq[k] = as_u32(__builtin_elementwise_fma(as_h2(r[k]), scv, off));
