@@ -421,44 +421,47 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
     int g = blockIdx.x + gridDim.x * wave;
     Unit<QT, ROWS> U[UPL];
     RowSet<ROWS> R;
-    if (g < p.n_groups) {  // first batch of the first row group: in flight while x is staged
-        map_rows<ROWS, RG>(p, g, slot, R);
-#pragma unroll
-        for (int i = 0; i < UPL; ++i) {
-            const int u = li + LPR * i;
-            U[i].load(R.rp, u < p.units ? u : 0);
-        }
-    }
 
-    // stage x: all loads first, then LDS stores and per-16 sums (4-lane shuffle)
+    // stage x: the loads of a pass of x (and of the norm weights) go out
+    // first, then (first pass) the first batch of weights, which stays in
+    // flight while x is stored to LDS with its per-16 sums (4-lane shuffle)
     const bool norm = p.norm_w != nullptr;
     float ss[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) ss[t] = 0.f;
     const int q4 = kn / 4;
+    auto load_pass = [&](int b0, float4 (&v)[NT][4], float4 (&gw)[4]) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        ss[t] = 0.f;
-        const float* src = p.x + (size_t)t * p.ldx;
-        for (int b0 = 0; b0 < q4; b0 += 4 * kQWG) {
-            float4 v[4];
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const int i = b0 + m * kQWG + tid;
-                v[m] = i < q4 ? *(const float4*)(src + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[t][m] = i < q4 ? *(const float4*)(p.x + (size_t)t * p.ldx + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
+        if (norm) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const int i = b0 + m * kQWG + tid;
-                float4 a = v[m];
+                gw[m] = i < q4 ? *(const float4*)(p.norm_w + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    auto store_pass = [&](int b0, const float4 (&v)[NT][4], const float4 (&gw)[4]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int i = b0 + m * kQWG + tid;
+                float4 a = v[t][m];
                 if (norm && i < q4) {
                     ss[t] = __builtin_fmaf(a.x, a.x, ss[t]);
                     ss[t] = __builtin_fmaf(a.y, a.y, ss[t]);
                     ss[t] = __builtin_fmaf(a.z, a.z, ss[t]);
                     ss[t] = __builtin_fmaf(a.w, a.w, ss[t]);
-                    const float4 gw = *(const float4*)(p.norm_w + 4 * i);
-                    a.x *= gw.x;
-                    a.y *= gw.y;
-                    a.z *= gw.z;
-                    a.w *= gw.w;
+                    a.x *= gw[m].x;
+                    a.y *= gw[m].y;
+                    a.z *= gw[m].z;
+                    a.w *= gw[m].w;
                 }
                 float s16 = (a.x + a.y) + (a.z + a.w);
                 s16 += __shfl_xor(s16, 1, 64);
@@ -468,6 +471,22 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
                     if ((tid & 3) == 0) sx[t * sx_stride + i / 4] = s16;
                 }
             }
+    };
+    {
+        float4 v[NT][4], gw[4];
+        load_pass(0, v, gw);
+        if (g < p.n_groups) {  // first batch of the first row group
+            map_rows<ROWS, RG>(p, g, slot, R);
+#pragma unroll
+            for (int i = 0; i < UPL; ++i) {
+                const int u = li + LPR * i;
+                U[i].load(R.rp, u < p.units ? u : 0);
+            }
+        }
+        store_pass(0, v, gw);
+        for (int b0 = 4 * kQWG; b0 < q4; b0 += 4 * kQWG) {
+            load_pass(b0, v, gw);
+            store_pass(b0, v, gw);
         }
     }
     if (norm) {
