@@ -1,0 +1,79 @@
+"""The C4 workload at full size: the
+Qwen2.5-7B-shape Q4_K_M target with QKV bias and its Qwen2.5-0.5B-shape Q8_0
+draft, run through the Engine's stochastic speculative loop
+(core/engine.cpp:100-240) with k = 6, temperature 0.8, top-p 0.95, top-k 40,
+repeat penalty 1.1 over the last 64 tokens and seed 4242 for 512 tokens:
+the device's token stream and its accepted / proposed / target-pass counts
+equal the REFERENCE's.
+
+The expected stream is tests/golden/c4_ref.npz, written by
+tests/golden/make_golden_c4.py from the reference build; the models are
+regenerated here by bin/synth_gguf and checked against the stored SHA-256.
+"""
+import hashlib
+import os
+import subprocess
+import time
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, SYNTH
+
+pytestmark = pytest.mark.gpu
+FIX_PATH = os.path.join(GOLDEN, "c4_ref.npz")
+
+
+def _sha(path):
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 22), b""):
+            h.update(chunk)
+    return h.hexdigest()
+
+
+@pytest.fixture(scope="module")
+def c4(tmp_path_factory):
+    import orc
+
+    if not os.path.exists(FIX_PATH):
+        pytest.skip("tests/golden/c4_ref.npz not written (tests/golden/make_golden_c4.py)")
+    fix = np.load(FIX_PATH)
+    d = os.environ.get("ORC_MODEL_DIR") or str(tmp_path_factory.mktemp("c4"))
+    os.makedirs(d, exist_ok=True)
+    paths = {}
+    for m in ("c4", "c4d"):
+        p = os.path.join(d, f"{m}.gguf")
+        if not os.path.exists(p):
+            # a 4.7 GB model takes minutes to write: report progress meanwhile
+            with open(p + ".log", "wb") as log:
+                proc = subprocess.Popen([SYNTH, m, p + ".tmp"], stdout=log, stderr=log)
+                t0 = time.time()
+                while True:
+                    try:
+                        proc.wait(timeout=15)
+                        break
+                    except subprocess.TimeoutExpired:
+                        print(f"[gpu] writing {m}: {time.time() - t0:.0f} s", flush=True)
+            assert proc.returncode == 0, open(p + ".log").read()
+            os.replace(p + ".tmp", p)
+        assert _sha(p) == bytes(fix[f"sha/{m}"]).decode(), f"{p} differs from the model the reference ran"
+        paths[m] = p
+    print("[gpu] loading c4 + c4d", flush=True)
+    tgt, dft = orc.Model(paths["c4"], 4096), orc.Model(paths["c4d"], 4096)
+    yield fix, tgt, dft
+    tgt.close()
+    dft.close()
+
+
+def test_c4_engine_spec_stream_and_stats_match_reference(c4):
+    fix, tgt, dft = c4
+    k = int(fix["k"][0])
+    temp, top_p, top_k, pen, last, seed = fix["sampler"]
+    n_gen = len(fix["espec_tokens"])
+    print(f"[gpu] c4 Engine stochastic spec k={k}, {n_gen} tokens", flush=True)
+    toks, st = tgt.spec_engine(dft, fix["prompt"], n_gen, k, float(temp), float(top_p), int(top_k), float(pen),
+                               int(last), int(seed))
+    assert np.array_equal(toks, fix["espec_tokens"])
+    acc, prop, passes = (int(v) for v in fix["espec_stats"])
+    assert (st["accepted"], st["proposed"], st["passes"]) == (acc, prop, passes)
