@@ -119,56 +119,105 @@ int DecodeSession::greedy_graphed(Model& m, int pos, int32_t first, int n_gen, i
     return n_gen;
 }
 
-// One captured round: k draft steps at *d_pos + i, the (k+1)-token verify at
-// *d_pos, acceptance (which advances *d_pos and writes the next input into
-// d_vin[0]). A second graph refills the draft KV at *d_pos - 1 when every
-// proposal was accepted.
-int DecodeSession::spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx,
-                                int32_t* out, SpecStats& S) {
+// The speculative-greedy loop (benchmark/bench_engine.cpp:310-356). A round
+// at position pos drafts ndt = min(k, ctx - 1 - pos) tokens, verifies the
+// ndt + 1 inputs in one target pass and emits the accepted drafts, then the
+// mismatch, or, when every draft was accepted and pos + ndt + 1 < ctx - 1,
+// the bonus token (and refills the draft's KV at pos + ndt); the loop runs
+// while pos < ctx - 1. Rounds with ndt = k replay one captured graph (k draft
+// steps at *d_pos + i, the (k+1)-token verify at *d_pos, acceptance, which
+// advances *d_pos and writes the next input into d_vin[0]; a second graph
+// refills the draft); the shorter rounds at the end of the context run from
+// the host at host positions.
+int DecodeSession::spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int32_t* out,
+                               SpecStats& S) {
+    const int tctx = (int)tgt.cfg.ctx_len, ctx = (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len);
     const int run_lim = graph_limit(pos + n_gen + k + 2, ctx);
-    if (int rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr)) return rc;
-    if (int rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr)) return rc;
-    std::vector<int32_t> h(k + 3);
+    std::vector<int32_t> h(k + 3), ids(k + 2);
+    bool dev_state = false;  // *d_pos / d_vin[0] hold pos / next
     int ng = 0;
-    while (ng < n_gen && pos + k + 1 <= ctx) {
-        // the round's passes reach positions pos .. pos + k (the refill included)
-        const Band b = band_of(pos, pos + k, run_lim, ctx);
-        Captured& c = slot(spec_g_, b, tgt.uid(), dft.uid(), k);
-        if (!c.g) {
-            BandScope bs(tgt, &dft, b.floor, b.lim);
-            if (int rc = orc_graph_begin(nullptr)) return rc;
-            for (int i = 0; i < k; ++i)
-                if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))
+    while (ng < n_gen && pos < tctx - 1) {
+        const int ndt = std::min(k, ctx - 1 - pos);
+        if (ndt < 1) break;
+        const bool graphed = graphs_ && ndt == k;
+        Captured* c = nullptr;
+        int a;
+        const int32_t* em;  // the round's target argmaxes from the first emitted token on
+        if (graphed) {
+            // the round's passes reach positions pos .. pos + k (the refill included)
+            const Band b = band_of(pos, pos + k, run_lim, ctx);
+            c = &slot(spec_g_, b, tgt.uid(), dft.uid(), k);
+            if (!c->g) {
+                BandScope bs(tgt, &dft, b.floor, b.lim);
+                if (int rc = orc_graph_begin(nullptr)) return rc;
+                for (int i = 0; i < k; ++i)
+                    if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))
+                        return abort_capture(rc);
+                if (int rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, d_tgt_)) return abort_capture(rc);
+                if (int rc = orc_spec_accept_greedy_at(d_tgt_, d_vin_ + 1, k, d_acc_, d_pos_, d_vin_, nullptr))
                     return abort_capture(rc);
-            if (int rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, d_tgt_)) return abort_capture(rc);
-            if (int rc = orc_spec_accept_greedy_at(d_tgt_, d_vin_ + 1, k, d_acc_, d_pos_, d_vin_, nullptr))
-                return abort_capture(rc);
-            if (int rc = orc_graph_end(nullptr, &c.g)) return rc;
-            if (int rc = orc_graph_begin(nullptr)) return rc;
-            if (int rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr)) return abort_capture(rc);
-            if (int rc = orc_graph_end(nullptr, &c.fill)) return rc;
-            c.a = tgt.uid();
-            c.b = dft.uid();
-            c.k = k;
+                if (int rc = orc_graph_end(nullptr, &c->g)) return rc;
+                if (int rc = orc_graph_begin(nullptr)) return rc;
+                if (int rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr)) return abort_capture(rc);
+                if (int rc = orc_graph_end(nullptr, &c->fill)) return rc;
+                c->a = tgt.uid();
+                c->b = dft.uid();
+                c->k = k;
+            }
+            if (!dev_state) {
+                if (int rc = orc_memcpy_h2d(d_pos_, &pos, 4, nullptr)) return rc;
+                if (int rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr)) return rc;
+                dev_state = true;
+            }
+            if (int rc = orc_graph_launch(c->g, nullptr)) return rc;
+            if (int rc = orc_memcpy_d2h(h.data(), d_acc_, (size_t)(k + 3) * 4, nullptr)) return rc;
+            a = h[0];
+            em = h.data() + 2;
+        } else {
+            if (int rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr)) return rc;
+            dev_state = false;
+            // (a) ndt greedy draft proposals; draft step i writes d_i into d_vin[i+1]
+            for (int i = 0; i < ndt; ++i)
+                if (int rc = dft.forward_dev(d_vin_ + i, 1, pos + i, true, d_vin_ + i + 1)) return rc;
+            // (b) one (ndt+1)-token verify pass of the target over [next, d0 .. d_{ndt-1}]
+            if (int rc = tgt.forward_dev(d_vin_, ndt + 1, pos, true, d_tgt_)) return rc;
+            // (c) acceptance on the device; ids and count to the host
+            if (int rc = orc_spec_accept_greedy(d_tgt_, d_vin_ + 1, ndt, d_acc_, nullptr)) return rc;
+            int32_t acc[2];
+            if (int rc = orc_memcpy_d2h(ids.data(), d_tgt_, (size_t)(ndt + 1) * 4, nullptr)) return rc;
+            if (int rc = orc_memcpy_d2h(acc, d_acc_, 8, nullptr)) return rc;
+            a = acc[0];
+            em = ids.data();
         }
-        if (int rc = orc_graph_launch(c.g, nullptr)) return rc;
-        if (int rc = orc_memcpy_d2h(h.data(), d_acc_, (size_t)(k + 3) * 4, nullptr)) return rc;
-        const int a = h[0];
-        S.proposed += k;
+        S.proposed += ndt;
         S.passes++;
         S.rounds++;
-        bool capped = false;
-        for (int i = 0; i <= a; ++i) {
-            out[ng++] = h[2 + i];
-            if (i < a) S.accepted++;
-            if (ng >= n_gen) {
-                capped = true;
-                break;
+        // em[0 .. a-1] are the accepted drafts, em[a] the mismatch or the bonus
+        bool stop = false;
+        for (int i = 0; i < a && !stop; ++i) {
+            out[ng++] = em[i];
+            S.accepted++;
+            stop = ng >= n_gen;
+        }
+        if (!stop) {
+            if (a < ndt) {
+                out[ng++] = em[a];
+                next = em[a];
+            } else if (pos + ndt + 1 < tctx - 1) {
+                out[ng++] = em[ndt];
+                next = em[ndt];
+                // every proposal accepted: the draft still lacks d_{ndt-1} at pos + ndt
+                if (graphed) {
+                    if (int rc = orc_graph_launch(c->fill, nullptr)) return rc;
+                } else if (int rc = dft.forward_dev(d_vin_ + ndt, 1, pos + ndt, false, nullptr)) {
+                    return rc;
+                }
+            } else {
+                stop = true;  // the bonus falls at the end of the context: the loop ends here
             }
         }
-        if (a == k && !capped)
-            if (int rc = orc_graph_launch(c.fill, nullptr)) return rc;
         pos += a + 1;
+        if (stop) break;
     }
     orc_stream_sync(nullptr);
     return ng;
@@ -202,45 +251,10 @@ int DecodeSession::spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, in
     if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return ORC_E_INVALID;  // bench_engine.cpp:290-293
     SpecStats local;
     SpecStats& S = st ? *st : local;
-    int pos = n_prompt - 1, ng = 0;
+    const int pos = n_prompt - 1;
     int32_t next = prompt[n_prompt - 1];
     if (next < 0 || next >= (int32_t)tgt.cfg.n_vocab) next = 0;
-    const int ctx = (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len);
-    if (graphs_) return spec_graphed(tgt, dft, pos, next, n_gen, k, ctx, out, S);
-    std::vector<int32_t> ids(k + 2);
-    while (ng < n_gen && pos + k + 1 <= ctx) {
-        if (int rc = orc_memcpy_h2d(d_vin_, &next, 4, nullptr)) return rc;
-        // (a) k greedy draft proposals; draft step i writes d_i into d_vin[i+1]
-        for (int i = 0; i < k; ++i)
-            if (int rc = dft.forward_dev(d_vin_ + i, 1, pos + i, true, d_vin_ + i + 1)) return rc;
-        S.proposed += k;
-        // (b) one (k+1)-token verify pass of the target over [next, d0 .. d_{k-1}]
-        if (int rc = tgt.forward_dev(d_vin_, k + 1, pos, true, d_tgt_)) return rc;
-        S.passes++;
-        S.rounds++;
-        // (c) acceptance on the device; ids and count to the host
-        if (int rc = orc_spec_accept_greedy(d_tgt_, d_vin_ + 1, k, d_acc_, nullptr)) return rc;
-        int32_t acc[2];
-        if (int rc = orc_memcpy_d2h(ids.data(), d_tgt_, (size_t)(k + 1) * 4, nullptr)) return rc;
-        if (int rc = orc_memcpy_d2h(acc, d_acc_, 8, nullptr)) return rc;
-        const int a = acc[0];
-        // emitted tokens are tgt[0..a]: a accepted draft tokens, then the
-        // mismatch or the bonus token, capped at n_gen
-        bool capped = false;
-        for (int i = 0; i <= a; ++i) {
-            out[ng++] = ids[i];
-            if (i < a) S.accepted++;
-            if (ng >= n_gen) { capped = true; break; }
-        }
-        next = ids[a];
-        if (a == k && !capped) {
-            // all accepted: the draft still lacks d_{k-1} at position pos+k
-            if (int rc = dft.forward_dev(d_vin_ + k, 1, pos + k, false, nullptr)) return rc;
-        }
-        pos += a + 1;
-    }
-    orc_stream_sync(nullptr);
-    return ng;
+    return spec_rounds(tgt, dft, pos, next, n_gen, k, out, S);
 }
 
 // engine.cpp:115-125: reset both models, prefill prompt[0 .. n-2] on each
@@ -294,8 +308,16 @@ int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, in
     std::vector<int32_t> h(k + 5);
     int ng = 0;
     Captured* c = nullptr;
-    while (ng < n_gen && pos + k + 1 <= ctx) {
-        if (graphs_) {
+    // engine.cpp:140-240: a round drafts ndt = min(k, ctx - 1 - pos) tokens and
+    // samples the bonus (an extra target position pos + ndt) only while
+    // pos + ndt < ctx - 1; the loop runs while pos < ctx - 1. Rounds with
+    // ndt = k replay the captured graphs.
+    const int tctx = (int)tgt.cfg.ctx_len;
+    while (ng < n_gen && pos < tctx - 1) {
+        const int ndt = std::min(k, ctx - 1 - pos);
+        if (ndt < 1) break;
+        const bool graphed = graphs_ && ndt == k;
+        if (graphed) {
             const Band b = band_of(pos, pos + k, run_lim, ctx);  // positions pos .. pos + k this round
             c = &slot(eng_g_, b, tgt.uid(), dft.uid(), k);
             if (!c->g) {
@@ -318,24 +340,33 @@ int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, in
             }
             if ((rc = orc_graph_launch(c->g, nullptr))) return rc;
         } else {
-            for (int i = 0; i < k; ++i)
+            for (int i = 0; i < ndt; ++i)
                 if ((rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, d_vin_ + i + 1))) return rc;
-            if ((rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, nullptr))) return rc;
-            if ((rc = orc_spec_accept_engine(d_samp_, tgt.d_logits(), V, V, d_vin_ + 1, k, 0, d_budget_, d_eout_,
+            if ((rc = tgt.forward_dev_at(d_vin_, ndt + 1, d_pos_, 0, true, nullptr))) return rc;
+            if ((rc = orc_spec_accept_engine(d_samp_, tgt.d_logits(), V, V, d_vin_ + 1, ndt, 0, d_budget_, d_eout_,
                                              d_pos_, d_vin_, nullptr)))
                 return rc;
         }
-        if ((rc = orc_memcpy_d2h(h.data(), d_eout_, (size_t)(k + 5) * 4, nullptr))) return rc;
-        const int emitted = h[0];
+        if ((rc = orc_memcpy_d2h(h.data(), d_eout_, (size_t)(ndt + 5) * 4, nullptr))) return rc;
+        int emitted = h[0], passes = h[2];
+        // a bonus at the end of the context is not sampled by the reference:
+        // its token and target pass are dropped and the loop ends
+        const bool bonus = h[3] && emitted == ndt + 1;
+        const bool at_end = bonus && pos + ndt >= tctx - 1;
+        if (at_end) {
+            --emitted;
+            --passes;
+        }
         S.accepted += h[1];
-        S.proposed += k;
-        S.passes += h[2];
+        S.proposed += ndt;
+        S.passes += passes;
         S.rounds++;
         for (int i = 0; i < emitted && ng < n_gen; ++i) out[ng++] = h[4 + i];
-        if (h[3] && ng < n_gen) {  // every proposal accepted: the draft lacks d_{k-1} (engine.cpp:230)
-            if (graphs_) {
+        if (at_end) break;
+        if (h[3] && ng < n_gen) {  // every proposal accepted: the draft lacks d_{ndt-1} (engine.cpp:230)
+            if (graphed) {
                 if ((rc = orc_graph_launch(c->fill, nullptr))) return rc;
-            } else if ((rc = dft.forward_dev_at(d_vin_ + k, 1, d_pos_, -1, false, nullptr))) {
+            } else if ((rc = dft.forward_dev_at(d_vin_ + ndt, 1, d_pos_, -1, false, nullptr))) {
                 return rc;
             }
         }

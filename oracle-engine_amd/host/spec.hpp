@@ -107,6 +107,5 @@ private:
                       std::vector<int32_t>& ids);
     int sampled_round(Model& tgt, Model& dft, int k, int V);
     int greedy_graphed(Model& m, int pos, int32_t first, int n_gen, int32_t* out);
-    int spec_graphed(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int ctx, int32_t* out,
-                     SpecStats& S);
+    int spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int32_t* out, SpecStats& S);
 };

@@ -2,7 +2,9 @@
 Qwen2.5-7B-shape Q4_K_M target with QKV bias and its Qwen2.5-0.5B-shape Q8_0
 draft, run through the Engine's stochastic speculative loop
 (core/engine.cpp:100-240) with k = 6, temperature 0.8, top-p 0.95, top-k 40,
-repeat penalty 1.1 over the last 64 tokens and seed 4242 for 512 tokens:
+repeat penalty 1.1 over the last 64 tokens and seed 4242 for 240 tokens (the
+reference's Model holds 512 positions, core/model.cpp:64, so 512 generated
+tokens after a 256-id prompt cannot run there):
 the device's token stream and its accepted / proposed / target-pass counts
 equal the REFERENCE's.
 

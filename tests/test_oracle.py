@@ -385,3 +385,37 @@ def test_sampled_spec_first_token_is_target_distributed(oracle, models_dir):
     chi2 = ((counts[keep] - exp) ** 2 / exp).sum()
     # 4 degrees of freedom: P(chi2 > 23.5) = 1e-4
     assert chi2 < 23.5, (chi2, counts[keep], exp)
+
+
+CTX_END = np.load(os.path.join(GOLDEN, "ctx_end_ref.npz"))
+
+
+@pytest.mark.parametrize("k", [2, 3, 4])
+def test_spec_greedy_at_context_end_matches_reference(oracle, models_dir, k):
+    """The batched speculative-greedy loop run into the 512-position context
+    end (fewer than k drafts, bonus withheld at the last position) gives the
+    reference's stream and counts (tests/golden/ctx_end_ref.npz)."""
+    for m in ("t-q4k", "t-q4k-d"):
+        h = hashlib.sha256(open(models_dir / f"{m}.gguf", "rb").read()).hexdigest()
+        assert h == bytes(CTX_END[f"sha/{m}"]).decode(), m
+    tgt = ol.OracleModel(oracle, str(models_dir / "t-q4k.gguf"))
+    dft = ol.OracleModel(oracle, str(models_dir / "t-q4k-d.gguf"))
+    toks, st = tgt.spec_greedy(dft, CTX_END[f"spec/k{k}/prompt"], 64, k)
+    assert len(toks) < 64
+    assert np.array_equal(toks, CTX_END[f"spec/k{k}/tokens"])
+    assert [st["accepted"], st["proposed"], st["passes"]] == list(CTX_END[f"spec/k{k}/stats"])
+
+
+def test_engine_spec_at_context_end_matches_reference(oracle, models_dir):
+    tgt = ol.OracleModel(oracle, str(models_dir / "t-qwen.gguf"))
+    dft = ol.OracleModel(oracle, str(models_dir / "t-qwen-d.gguf"))
+    s = oracle.L.orco_sampler_new(0.8, 0.95, 40, 1.1, 64, 4242)
+    prompt = np.ascontiguousarray(CTX_END["espec/prompt"], np.int32)
+    out = np.zeros(64, np.int32)
+    st = np.zeros(3, np.int64)
+    n = oracle.L.orco_spec_engine(tgt.h, dft.h, ol.iptr(prompt), prompt.size, 40, 3, s, ol.iptr(out),
+                                  st.ctypes.data_as(ol._lp))
+    oracle.L.orco_sampler_free(s)
+    assert n < 40
+    assert np.array_equal(out[:n], CTX_END["espec/tokens"])
+    assert list(st) == list(CTX_END["espec/stats"])
