@@ -28,6 +28,16 @@ summary in profiles/.
 cpu_baseline: the reference implementation (oracle/_ref, built from the
 reference's sources) on the same two models, bounded sample: prompt 8 ids,
 16 generated tokens, k = 4.
+gemv_microbench: quantized one-token GEMVs (16384 x 8192) back to back over
+more than 640 MB of distinct weight matrices in rotation (beyond the 256 MB
+Infinity Cache), per type, timed by the same dispatch events.
+
+--workload c4 / c5 run BASELINE.json configs[3] / configs[4] instead (the
+bench line stays quoted on C3): C4 = the Engine's stochastic speculative
+loop (each step a whole Engine call, prefill included, reported beside it);
+C5 = speculative greedy after an 8191-id prefill into a 16384-position cache,
+with the verify passes' GQA KV-read GB/s and weight-GEMM GB/s reported
+separately (verify_split).
 """
 import argparse
 import json
@@ -95,17 +105,88 @@ def measured_traffic(kernel):
     return None, None
 
 
+# The bench line is quoted on C3 (BASELINE.json's metric config); C4 and C5
+# (configs[3], configs[4]) run with --workload for their own measurements.
+WORKLOADS = {
+    "c3": dict(tgt="c2", dft="c3d", n_prompt=128, n_gen=256, k=4, ctx=2048, mode="greedy", prompt_seed=1234,
+               desc="C3 spec greedy: 3B-shape Q4_K_M target + 8-layer Q8_0 draft"),
+    "c4": dict(tgt="c4", dft="c4d", n_prompt=256, n_gen=512, k=6, ctx=4096, mode="engine", prompt_seed=4321,
+               desc="C4 Engine stochastic spec: 7B-shape Q4_K_M target (QKV bias) + 0.5B-shape Q8_0 draft, "
+                    "T 0.8, top-p 0.95, top-k 40, repeat penalty 1.1 over 64, seed 4242"),
+    "c5": dict(tgt="c5", dft="c4d", n_prompt=8192, n_gen=512, k=8, ctx=16384, mode="greedy", prompt_seed=8192,
+               desc="C5 long-context spec greedy: 7B-shape all-Q6_K target + 0.5B-shape Q8_0 draft"),
+}
+SAMPLER = (0.8, 0.95, 40, 1.1, 64, 4242)  # T, top-p, top-k, repeat penalty, repeat_last, seed (C4)
+PROF_FAMILIES = (2, 8, 12, 14, 256, 300, 301, 302)
+FAMILY_NAMES = {**TYPE_NAMES, 300: "attn k_attn_wg", 301: "attn k_attn_split", 302: "attn k_attn_merge"}
+
+
+def family_label(ty, nt):
+    return f"k_gemm {FAMILY_NAMES[ty]} n_tok={nt}" if ty < 300 else f"{FAMILY_NAMES[ty]} n_tok={nt}"
+
+
+def gemv_microbench(dev, n_out=16384, n_in=8192, rotate_mb=640, rounds=6):
+    """Quantized GEMV bandwidth at scale: one-token GEMVs of n_out x n_in
+    matrices back to back over at least rotate_mb MB of distinct weight
+    matrices in rotation (more than the 256 MB Infinity Cache holds), timed
+    per launch with the dispatch's own HIP events. Bytes = weight blocks +
+    x + y per launch."""
+    import ctypes as C
+
+    L = dev.L
+    rng = np.random.default_rng(7)
+    x = dev.upload(rng.standard_normal(n_in).astype(np.float32))
+    y = dev.alloc(4 * n_out)
+    out = []
+    # GGML type, block bytes, byte offsets of the fp16 scales inside a block
+    for ty, bb, scales in ((8, 34, (0,)), (12, 144, (0, 2)), (14, 210, (208,)), (2, 18, (0,))):
+        rb = L.orc_row_bytes(ty, n_in)
+        mb = rb * n_out
+        m = max(2, -(-(rotate_mb << 20) // mb))
+        blocks = np.frombuffer(rng.bytes(mb), np.uint8).reshape(-1, bb).copy()
+        for o in scales:  # finite scales: random fp16 in [0, 1e-3)
+            blocks[:, o:o + 2] = (rng.random(len(blocks)) * 1e-3).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        w = dev.alloc(m * mb)
+        for i in range(m):
+            w.write(blocks, i * mb)
+        del blocks
+        for _ in range(2):  # warm-up round: first-launch costs stay out of the timing
+            for i in range(m):
+                dev.check(L.orc_gemm(ty, w.ptr + i * mb, 1, n_out, n_in, x.ptr, n_in, y.ptr, n_out, None))
+        dev.sync()
+        L.orc_prof_enable(1)
+        for _ in range(rounds):
+            for i in range(m):
+                dev.check(L.orc_gemm(ty, w.ptr + i * mb, 1, n_out, n_in, x.ptr, n_in, y.ptr, n_out, None))
+        dev.sync()
+        dev.check(L.orc_prof_accumulate())
+        n, ms, by = C.c_int64(), C.c_double(), C.c_double()
+        L.orc_prof_read(ty, 1, C.byref(n), C.byref(ms), C.byref(by))
+        L.orc_prof_enable(0)
+        w.free()
+        gbs = by.value / (ms.value * 1e-3) / 1e9
+        out.append({"type": TYPE_NAMES[ty], "shape": [n_out, n_in], "matrix_mb": round(mb / 1e6, 1),
+                    "rotating_mb": round(m * mb / 1e6, 1), "launches": n.value,
+                    "avg_us": round(1e3 * ms.value / n.value, 2), "gbs": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"gemv microbench {TYPE_NAMES[ty]}: {out[-1]['avg_us']} us per {mb / 1e6:.1f} MB launch, "
+            f"{gbs:.0f} GB/s over {m * mb / 1e6:.0f} MB rotating")
+    x.free()
+    y.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--n-gen", type=int, default=256)
-    ap.add_argument("--n-prompt", type=int, default=128)
-    ap.add_argument("--k", type=int, default=4)
-    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3",
+                    help="c3 (the metric's config, default), c4 or c5")
+    ap.add_argument("--n-gen", type=int, default=0, help="generated tokens (default: the workload's)")
     ap.add_argument("--models-dir", default=os.environ.get("ORC_MODEL_DIR", "/tmp/orc_models"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemv-micro", action="store_true", help="skip the rotating-weights GEMV bandwidth run")
     ap.add_argument("--no-prof", action="store_true", help="skip the live per-kernel event timing")
     ap.add_argument("--prof-tokens", type=int, default=64, help="tokens generated by the kernel timing pass")
     ap.add_argument("--no-graphs", action="store_true",
@@ -118,14 +199,16 @@ def main():
         print(f"bench.py measures one GPU only (got --gpus {a.gpus}); this build has no multi-GPU path.",
               file=sys.stderr)
         sys.exit(2)
+    W = WORKLOADS[a.workload]
+    n_gen, k, n_prompt, ctx = a.n_gen or W["n_gen"], W["k"], W["n_prompt"], W["ctx"]
 
     import orc
 
-    tgt_path = ensure_model("c2", a.models_dir)
-    dft_path = ensure_model("c3d", a.models_dir)
+    tgt_path = ensure_model(W["tgt"], a.models_dir)
+    dft_path = ensure_model(W["dft"], a.models_dir)
     dev = orc.Device(0)
     name, n_cu, hbm = dev.info()
-    log(f"device {name}, {n_cu} CUs, {hbm / 1e9:.0f} GB")
+    log(f"device {name}, {n_cu} CUs, {hbm / 1e9:.0f} GB; workload {a.workload}")
     if a.calib_copy_mb > 0:
         nb = a.calib_copy_mb << 20
         src, dst = dev.alloc(nb), dev.alloc(nb)
@@ -137,100 +220,135 @@ def main():
         src.free()
         dst.free()
     t0 = time.time()
-    tgt = orc.Model(tgt_path, a.ctx)
-    dft = orc.Model(dft_path, a.ctx)
+    tgt = orc.Model(tgt_path, ctx)
+    dft = orc.Model(dft_path, ctx)
     log(f"loaded target ({tgt.weight_bytes() / 1e9:.3f} GB/token) and draft ({dft.weight_bytes() / 1e9:.3f} "
         f"GB/token) in {time.time() - t0:.1f}s")
-    prompt = np.random.default_rng(1234).integers(0, tgt.n_vocab, a.n_prompt).astype(np.int32)
+    prompt = np.random.default_rng(W["prompt_seed"]).integers(0, tgt.n_vocab, n_prompt).astype(np.int32)
     if a.no_graphs:
         orc.load_host_lib().orch_set_graphs(0)
+    engine = W["mode"] == "engine"
 
-    greedy = tgt.greedy(prompt, a.n_gen, prefill=True)  # reference stream for the exactness check
-    toks, st = tgt.spec_greedy(dft, prompt, a.n_gen, a.k, prefill=True)  # prefills both models
-    exact = bool(np.array_equal(toks, greedy))
+    def run(n, prefill):
+        if engine:  # Engine::generate prefills both models on every call (core/engine.cpp:115-125)
+            return tgt.spec_engine(dft, prompt, n, k, *SAMPLER)
+        return tgt.spec_greedy(dft, prompt, n, k, prefill=prefill)
+
+    # exactness: spec greedy must reproduce the target's greedy stream; the
+    # Engine loop samples, so its stream must reproduce itself (fixed seed)
+    greedy = None if engine else tgt.greedy(prompt, n_gen, prefill=True)
+    toks, st = run(n_gen, True)  # prefills both models
+    expect = toks if engine else greedy
+    exact = bool(np.array_equal(toks, expect))
     # the reference implementation's own streams on these models (tests/golden/c3_ref.npz)
     ref_identical = None
     fix_path = os.path.join(ROOT, "tests", "golden", "c3_ref.npz")
-    if os.path.exists(fix_path):
+    if a.workload == "c3" and os.path.exists(fix_path):
         fix = np.load(fix_path)
-        if (a.n_prompt, a.n_gen, a.k) == (len(fix["prompt"]), len(fix["spec_tokens"]), int(fix["k"][0])) and \
+        if (n_prompt, n_gen, k) == (len(fix["prompt"]), len(fix["spec_tokens"]), int(fix["k"][0])) and \
                 np.array_equal(prompt, fix["prompt"]):
             ref_identical = bool(np.array_equal(greedy, fix["greedy_tokens"]) and
                                  np.array_equal(toks, fix["spec_tokens"]) and
                                  (st["accepted"], st["proposed"], st["passes"]) == tuple(int(v) for v in fix["spec_stats"]))
     for _ in range(a.warmup):
-        toks, st = tgt.spec_greedy(dft, prompt, a.n_gen, a.k, prefill=False)
-        exact &= bool(np.array_equal(toks, greedy))
+        toks, st = run(n_gen, False)
+        exact &= bool(np.array_equal(toks, expect))
 
     L, H = orc.load_hip_lib(), orc.load_host_lib()
-    tot = {"accepted": 0, "proposed": 0, "passes": 0, "rounds": 0}
+    tot = {"accepted": 0, "proposed": 0, "passes": 0}
     H.orch_sync()
     t0 = time.perf_counter()
     for _ in range(a.steps):
-        toks, st = tgt.spec_greedy(dft, prompt, a.n_gen, a.k, prefill=False)
-        exact &= bool(np.array_equal(toks, greedy))
+        toks, st = run(n_gen, False)
+        exact &= bool(np.array_equal(toks, expect))
         for key in tot:
             tot[key] += st[key]
     H.orch_sync()
     dt = time.perf_counter() - t0
-    value = a.steps * a.n_gen / dt
+    value = a.steps * n_gen / dt
+    prefill_ms = None
+    if engine:  # the prefill each Engine call repeats, timed on its own
+        H.orch_sync()
+        tp = time.perf_counter()
+        tgt.forward_batch(prompt[:-1], 0, logits=False)
+        dft.forward_batch(prompt[:-1], 0, logits=False)
+        H.orch_sync()
+        prefill_ms = 1e3 * (time.perf_counter() - tp)
 
     roofline, fams = None, []
     if not a.no_prof:
         import ctypes as C
 
         # Kernel timing pass right after the timed region: the same spec
-        # rounds launched from the host, every GEMM launch carrying start /
-        # stop HIP events taken from its own dispatch on its stream.
+        # rounds launched from the host, every GEMM (and host-positioned
+        # attention) launch carrying start / stop HIP events taken from its
+        # own dispatch on its stream.
         L.orc_prof_enable(1)
         H.orch_set_graphs(0)
-        tp = time.perf_counter()
         try:
-            ptoks, pst = tgt.spec_greedy(dft, prompt, a.prof_tokens, a.k, prefill=False)
-            exact &= bool(np.array_equal(ptoks, greedy[:len(ptoks)]))
+            ptoks, pst = run(a.prof_tokens, False)
+            exact &= bool(np.array_equal(ptoks, expect[:len(ptoks)]))
             H.orch_sync()
             if L.orc_prof_accumulate():
                 raise orc.OrcError(L.orc_last_error().decode())
         except orc.OrcError as e:
             log(f"kernel timing pass failed: {e}")
             pst = None
-        prof_dt = time.perf_counter() - tp
         L.orc_prof_enable(0)
         H.orch_set_graphs(0 if a.no_graphs else 1)
-        for ty in ((2, 8, 12, 14, 256) if pst else ()):
-            for nt in range(1, 6):
+        for ty in (PROF_FAMILIES if pst else ()):
+            for nt in range(1, 17):
                 n, ms, by = C.c_int64(), C.c_double(), C.c_double()
                 L.orc_prof_read(ty, nt, C.byref(n), C.byref(ms), C.byref(by))
                 if n.value:
-                    fams.append({"kernel": f"k_gemm {TYPE_NAMES[ty]} n_tok={nt}", "launches": n.value,
-                                 "ms": ms.value, "bytes": by.value, "gbs": by.value / (ms.value * 1e-3) / 1e9})
+                    fams.append({"kernel": family_label(ty, nt), "launches": n.value, "ms": ms.value,
+                                 "bytes": by.value, "gbs": by.value / (ms.value * 1e-3) / 1e9})
         fams.sort(key=lambda f: -f["ms"])
-        if fams:
-            f = fams[0]
-            traffic, traffic_src = measured_traffic(f["kernel"])
+        gemms = [f for f in fams if f["kernel"].startswith("k_gemm")]
+        if gemms:
+            f = gemms[0]
+            traffic, traffic_src = measured_traffic(f["kernel"]) if a.workload == "c3" else (None, None)
             roofline = {"bound": "hbm", "achieved": round(f["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(f["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                         "traffic_source": traffic_src, "kernel": f["kernel"],
                         "avg_launch_us": round(1e3 * f["ms"] / f["launches"], 3),
                         "bytes_per_launch": round(f["bytes"] / f["launches"]),
-                        "timing": f"start/stop HIP events of each launch's dispatch over {pst['rounds']} "
+                        "timing": f"start/stop HIP events of each launch's dispatch over {a.prof_tokens} tokens of "
                                   f"host-launched spec rounds"}
 
-    cpu = None if a.no_cpu_baseline else cpu_baseline(tgt_path, dft_path, prompt, a.k)
+    micro = None if a.no_gemv_micro else gemv_microbench(dev)
+    cpu = None if (a.no_cpu_baseline or a.workload != "c3") else cpu_baseline(tgt_path, dft_path, prompt, k)
     out = {
         "metric": "spec-decode tok/s (3B Q4_K, k=4); quant-GEMV HBM GB/s vs peak",
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(1e3 * dt / a.steps, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (random-init N(0,0.02) GGUF, uniform random prompt ids)",
-        "config": {"workload": "C3 spec greedy: 3B-shape Q4_K_M target + 8-layer Q8_0 draft",
-                   "k": a.k, "prompt": a.n_prompt, "gen_tokens": a.n_gen, "ctx": a.ctx},
+        "config": {"workload": W["desc"], "k": k, "prompt": n_prompt, "gen_tokens": n_gen, "ctx": ctx},
         "acceptance": round(tot["accepted"] / max(1, tot["proposed"]), 4),
-        "target_passes_per_token": round(tot["passes"] / max(1, a.steps * a.n_gen), 4),
-        "exact_vs_greedy": exact, "reference_stream_identical": ref_identical,
+        "target_passes_per_token": round(tot["passes"] / max(1, a.steps * n_gen), 4),
+        "exact_vs_greedy" if not engine else "stream_reproducible": exact,
+        "reference_stream_identical": ref_identical,
         "roofline": roofline, "cpu_baseline": cpu,
+        "gemv_microbench": micro,
         "kernel_families": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in f.items()} for f in fams],
     }
+    if engine:
+        out["prefill_ms"] = round(prefill_ms, 2)
+        out["value_note"] = ("each step is a whole Engine call: the prefill of both models (prefill_ms) plus "
+                             f"{n_gen} generated tokens")
+    if a.workload == "c5":
+        kv = [f for f in fams if f["kernel"].startswith("attn k_attn_split") and f["kernel"].endswith(f"={k + 1}")]
+        mg = [f for f in fams if f["kernel"].startswith("attn k_attn_merge") and f["kernel"].endswith(f"={k + 1}")]
+        wt = [f for f in fams if f["kernel"].startswith("k_gemm Q6_K")]  # C5's target is all Q6_K, the draft Q8_0
+        if kv and wt:
+            kvb, kvms = sum(f["bytes"] for f in kv), sum(f["ms"] for f in kv + mg)
+            wb, wms = sum(f["bytes"] for f in wt), sum(f["ms"] for f in wt)
+            out["verify_split"] = {
+                "kv_read_gbs": round(kvb / (kvms * 1e-3) / 1e9, 1), "kv_bytes": kvb, "kv_ms": round(kvms, 3),
+                "weight_gemm_gbs": round(wb / (wms * 1e-3) / 1e9, 1), "weight_bytes": wb, "weight_ms": round(wms, 3),
+                "note": f"{k + 1}-token verify passes of the timing pass: GQA attention (split + merge; K and V "
+                        f"of every cached position counted once per layer) vs the target's weight GEMMs"}
     print(json.dumps(out), flush=True)
 
 

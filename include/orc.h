@@ -141,11 +141,19 @@ int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n_segs, int 
  * GEMM launch made outside stream capture carries a start and a stop HIP
  * event (hipExtLaunchKernelGGL: both take the timestamps of the kernel's own
  * dispatch on its stream) and its algorithmic HBM bytes (weight blocks + x +
- * y) are noted. Once the work has run, orc_prof_accumulate adds every launch's
- * elapsed time to its record; orc_prof_read sums the records of one kernel
- * family (type < 0: all types; n_tok 0: all token counts). orc_prof_enable:
+ * y) are noted; so does every attention launch of orc_attn_fused_at with
+ * host positions (families ORC_PROF_ATTN_WG / _SPLIT / _MERGE; bytes = the K
+ * and V rows its tokens read, counted once, + QKV rows in + rows out; the
+ * merge is noted with 0 bytes). Once the work has run, orc_prof_accumulate
+ * adds every launch's elapsed time to its record; orc_prof_read sums the
+ * records of one kernel family (type = a GGML type id, 256 for mixed
+ * Q4_K + Q6_K launches, or an attention family; type < 0: all families;
+ * n_tok 0: all token counts). orc_prof_enable:
  * 1 = on and clear all records, 2 = on keeping them, 0 = off (accumulate is
  * then a no-op); returns the previous state. */
+#define ORC_PROF_ATTN_WG 300
+#define ORC_PROF_ATTN_SPLIT 301
+#define ORC_PROF_ATTN_MERGE 302
 int orc_prof_enable(int on);
 int orc_prof_accumulate(void);
 int orc_prof_read(int type, int n_tok, int64_t* launches, double* total_ms, double* total_bytes);

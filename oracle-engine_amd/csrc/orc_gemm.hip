@@ -1488,19 +1488,8 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
         q.n_tok = std::min(ntmax, p.n_tok - t0);
         q.x = p.x + (size_t)t0 * p.ldx;
         for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
-        ProfRec rec{};
         LaunchEvents ev;
-        if (g_prof_on) {  // host launches only: a captured launch carries no events
-            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-            (void)hipStreamIsCapturing(s, &cs);
-            if (cs == hipStreamCaptureStatusNone && (rec.a = prof_event()) && (rec.b = prof_event())) {
-                ev.start = rec.a;
-                ev.stop = rec.b;
-                rec.type = type;
-                rec.nt = q.n_tok;
-                rec.bytes = gemm_bytes(q, q.n_tok);
-            }
-        }
+        if (g_prof_on) prof_arm(s, type, q.n_tok, gemm_bytes(q, q.n_tok), &ev.start, &ev.stop);
         int rc;
         switch (type) {
             case ORC_Q4_K: rc = mmq_type_launch<ORC_Q4_K>(q, s, ev); break;
@@ -1511,9 +1500,23 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
         }
         if (rc) return rc;
-        if (ev.start) g_prof.push_back(rec);
     }
     return ORC_OK;
+}
+
+bool prof_arm(hipStream_t s, int family, int n_tok, double bytes, hipEvent_t* start, hipEvent_t* stop) {
+    if (!g_prof_on) return false;  // host launches only: a captured launch carries no events
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    (void)hipStreamIsCapturing(s, &cs);
+    ProfRec rec{};
+    if (cs != hipStreamCaptureStatusNone || !(rec.a = prof_event()) || !(rec.b = prof_event())) return false;
+    rec.type = family;
+    rec.nt = n_tok;
+    rec.bytes = bytes;
+    g_prof.push_back(rec);
+    *start = rec.a;
+    *stop = rec.b;
+    return true;
 }
 
 }  // namespace orc

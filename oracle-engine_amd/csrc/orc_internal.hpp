@@ -16,6 +16,14 @@ bool initialized();
 int gemm_device_init(int device);
 void gemm_device_release();
 
+// Live kernel timing (orc_prof_*): when enabled and the stream is not being
+// captured, hands out a start / stop event pair for one launch and records
+// it under (family, n_tok) with the launch's algorithmic bytes; returns false
+// (events untouched) otherwise. Families: the GGML weight type of a GEMM, or
+// one of the attention ids below.
+constexpr int kProfAttnWG = ORC_PROF_ATTN_WG, kProfAttnSplit = ORC_PROF_ATTN_SPLIT, kProfAttnMerge = ORC_PROF_ATTN_MERGE;
+bool prof_arm(hipStream_t s, int family, int n_tok, double bytes, hipEvent_t* start, hipEvent_t* stop);
+
 #define ORC_HIP_CHECK(expr)                                                                       \
     do {                                                                                          \
         hipError_t e_ = (expr);                                                                   \

@@ -7,6 +7,7 @@
 // (core/model.cpp:595-626), and the acceptance step of the batched spec loop
 // (benchmark/bench_engine.cpp:337-355).
 #include "orc_internal.hpp"
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 #include <type_traits>
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(HD) void k_attn_combine(int n_tok, int n_heads, con
 //    (the next launch, so no fence is needed) merges the chunks in chunk
 //    order: O = sum_c O_c e^(m_c - M) / sum_c l_c e^(m_c - M). A token whose
 //    positions fit one chunk gets its output written directly.
-constexpr int kSW = 256, kSB = 64, kNCMax = 32, kRMax = 8, kMaxTokAttn = 16;
+constexpr int kSW = 256, kSB = 64, kNCMax = 256, kRMax = 8, kMaxTokAttn = 16;
 
 __host__ __device__ inline int chunk_positions(int P) {
     const int per = (P + kNCMax - 1) / kNCMax;
@@ -226,6 +227,10 @@ __host__ __device__ inline int n_chunks(int P) { return (P + chunk_positions(P) 
 // most two passes of its waves); longer ones the split over workgroups plus
 // the merge, which keeps more CUs streaming K and V.
 constexpr int kWGMax = 256;
+
+struct LaunchEv {
+    hipEvent_t a = nullptr, b = nullptr;
+};
 // waves of a k_attn_wg workgroup (the register budget of head_dim 128 allows 8)
 template <int HD> constexpr int wg_waves() { return HD == 128 ? 8 : 16; }
 
@@ -446,42 +451,63 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
     }
 }
 
-// Merge of the chunk partials of k_attn_split: one workgroup per (kv head,
-// token), chunks in chunk order. Tokens with a single chunk were written
-// directly and are skipped.
+// Merge of the chunk partials of k_attn_split: one workgroup per (query
+// head, token). Every thread loads one chunk's (m, l) and forms e^(m_c - M)
+// in parallel (M = the maximum, which no order changes); the sums then run in
+// chunk order, L in one lane and each output dimension in one lane, so the
+// result is that of a serial merge: O = sum_c O_c e^(m_c - M) / sum_c l_c
+// e^(m_c - M). Tokens with a single chunk were written directly and are
+// skipped.
 template <int HD>
 __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const int* d_pos, int pos_off, int ctx,
                                                     const float* work, float* out, int ldo) {
     constexpr int PS = part_stride<HD>();
-    __shared__ float sf[kRMax][kNCMax];  // e^(m_c - M) per head and chunk
-    __shared__ float sL[kRMax];
-    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int R = n_heads / n_kv;
+    static_assert(kNCMax == kSW, "one chunk per thread");
+    static_assert(HD < kSW, "a lane outside the output dimensions sums L");
+    __shared__ float sf[kNCMax], sl[kNCMax];  // e^(m_c - M), l_c
+    __shared__ float smax[kSW / 64], sL;
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int R = n_heads / n_kv, g = h / R, r = h - g * R;
     const int pt = start_position(d_pos, pos_off) + t;
     if (pt < 0 || pt >= ctx) return;
     const int P = pt + 1, nch = n_chunks(P);
     if (P <= kWGMax || nch == 1) return;
-    const float* part = work + ((size_t)t * n_kv + g) * kNCMax * R * PS;
-    if (tid < R) {
-        const int r = tid;
-        float M = -INFINITY;
-        for (int c = 0; c < nch; ++c) M = fmaxf(M, part[((size_t)c * R + r) * PS + HD]);
+    const size_t cs = (size_t)R * PS;  // floats from one chunk's row of this head to the next chunk's
+    const float* part = work + ((size_t)t * n_kv + g) * kNCMax * cs + (size_t)r * PS;
+    float mc = -INFINITY;
+    if (tid < nch) {
+        mc = part[tid * cs + HD];
+        sl[tid] = part[tid * cs + HD + 1];
+    }
+    float M = mc;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) smax[w] = M;
+    __syncthreads();
+    M = smax[0];
+#pragma unroll
+    for (int i = 1; i < kSW / 64; ++i) M = fmaxf(M, smax[i]);
+    if (tid < nch) sf[tid] = expf(mc - M);
+    __syncthreads();
+    if (tid == HD) {
         float L = 0.f;
-        for (int c = 0; c < nch; ++c) {
-            const float* pr = part + ((size_t)c * R + r) * PS;
-            const float f = expf(pr[HD] - M);
-            sf[r][c] = f;
-            L = __builtin_fmaf(pr[HD + 1], f, L);
+        for (int c = 0; c < nch; ++c) L = __builtin_fmaf(sl[c], sf[c], L);
+        sL = L;
+    }
+    float O = 0.f;
+    if (tid < HD) {
+        int c = 0;
+        for (; c + 8 <= nch; c += 8) {  // eight loads in flight, then the eight FMAs in chunk order
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = part[(c + j) * cs + tid];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) O = __builtin_fmaf(v[j], sf[c + j], O);
         }
-        sL[r] = L;
+        for (; c < nch; ++c) O = __builtin_fmaf(part[c * cs + tid], sf[c], O);
     }
     __syncthreads();
-    for (int i = tid; i < R * HD; i += kSW) {
-        const int r = i / HD, d = i - r * HD;
-        float O = 0.f;
-        for (int c = 0; c < nch; ++c) O = __builtin_fmaf(part[((size_t)c * R + r) * PS + d], sf[r][c], O);
-        out[(size_t)t * ldo + (g * R + r) * HD + d] = O / sL[r];
-    }
+    if (tid < HD) out[(size_t)t * ldo + h * HD + tid] = O / sL;
 }
 
 // ── short contexts: all chunks of a (kv head, token) in one workgroup ───────
@@ -902,29 +928,55 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
         }
     } else {
         short_ctx = pos_floor + 1 <= kWGMax;
-        for (int P = std::max(kWGMax, pos_floor) + 1; P <= pos_limit && nch < kNCMax; ++P)
-            nch = std::max(nch, n_chunks(P));
+        // up to kSB * kNCMax positions the chunks are kSB long and n_chunks
+        // grows with P, so the band's last position needs the most
+        if (pos_limit <= kSB * kNCMax)
+            nch = pos_limit > kWGMax ? n_chunks(pos_limit) : 0;
+        else
+            for (int P = std::max(kWGMax, pos_floor) + 1; P <= pos_limit && nch < kNCMax; ++P)
+                nch = std::max(nch, n_chunks(P));
     }
     const int R = n_heads / n_kv;
     float* w = (float*)d_work;
+    // live timing (host positions only): algorithmic bytes of a launch = the
+    // K and V rows of the positions its tokens read, once (the verify tokens
+    // share them), + the QKV rows in + the attention rows out
+    double kv_bytes[2] = {0, 0};  // [k_attn_wg, k_attn_split]
+    if (!d_pos) {
+        const double io = 4.0 * n_tok * ((double)(n_heads + 2 * n_kv) * head_dim + (double)n_heads * head_dim);
+        const int pmax = pos_off + n_tok;
+        kv_bytes[0] = 8.0 * n_kv * head_dim * std::min(pmax, kWGMax) + io;
+        kv_bytes[1] = 8.0 * n_kv * head_dim * pmax + io;
+    }
+    auto armed = [&](int fam, double bytes, LaunchEv& ev) {
+        return !d_pos && prof_arm(st, fam, n_tok, bytes, &ev.a, &ev.b);
+    };
     auto launch = [&](auto hd_tag) {
         constexpr int HD = decltype(hd_tag)::value;
+        LaunchEv ev;
         if (short_ctx) {
-            const dim3 blk(wg_waves<HD>() * 64);
+            const dim3 blk(wg_waves<HD>() * 64), grid(n_kv, n_tok);
+            const bool tm = armed(kProfAttnWG, kv_bytes[0], ev);
             if (R <= 4)
-                hipLaunchKernelGGL((k_attn_wg<HD, 4>), dim3(n_kv, n_tok), blk, 0, st, d_qkv, ldqkv, n_heads, n_kv,
-                                   d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+                hipExtLaunchKernelGGL((k_attn_wg<HD, 4>), grid, blk, 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr,
+                                      0, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc,
+                                      d_vc, ctx, d_out, ldo);
             else
-                hipLaunchKernelGGL((k_attn_wg<HD, 8>), dim3(n_kv, n_tok), blk, 0, st, d_qkv, ldqkv, n_heads, n_kv,
-                                   d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+                hipExtLaunchKernelGGL((k_attn_wg<HD, 8>), grid, blk, 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr,
+                                      0, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc,
+                                      d_vc, ctx, d_out, ldo);
             ORC_LAUNCH_CHECK();
         }
         if (nch > 0) {
-            hipLaunchKernelGGL(k_attn_split<HD>, dim3(nch, n_kv, n_tok), dim3(kSW), 0, st, d_qkv, ldqkv, n_heads, n_kv,
-                               d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
+            bool tm = armed(kProfAttnSplit, kv_bytes[1], ev);
+            hipExtLaunchKernelGGL(k_attn_split<HD>, dim3(nch, n_kv, n_tok), dim3(kSW), 0, st, tm ? ev.a : nullptr,
+                                  tm ? ev.b : nullptr, 0, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off,
+                                  (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
             ORC_LAUNCH_CHECK();
-            hipLaunchKernelGGL(k_attn_merge<HD>, dim3(n_kv, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos, pos_off,
-                               ctx, (const float*)w, d_out, ldo);
+            tm = armed(kProfAttnMerge, 0.0, ev);
+            hipExtLaunchKernelGGL(k_attn_merge<HD>, dim3(n_heads, n_tok), dim3(kSW), 0, st, tm ? ev.a : nullptr,
+                                  tm ? ev.b : nullptr, 0, n_heads, n_kv, d_pos, pos_off, ctx, (const float*)w, d_out,
+                                  ldo);
             ORC_LAUNCH_CHECK();
         }
         return ORC_OK;
