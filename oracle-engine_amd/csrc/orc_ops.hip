@@ -256,7 +256,8 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
     __shared__ __align__(16) float Qs[kRMax][HD];
     __shared__ float S[kRMax][kSB];
     __shared__ float st_m[kRMax], st_l[kRMax], st_a[kRMax];
-    __shared__ __align__(16) float red[NPS][HD];
+    constexpr int kRB = 4;  // heads per pass of the final reduction
+    __shared__ __align__(16) float red[kRB][NPS][HD];
     const int c = blockIdx.x, g = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const int R = n_heads / n_kv;
     const int start = start_position(d_pos, pos_off);
@@ -427,22 +428,27 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
     // this chunk's partial row
     const bool single = nch == 1;
     float* part = work + ((size_t)t * n_kv + g) * kNCMax * R * PS;
+    // heads in batches of kRB through the LDS; each sum runs over k = 0..NPS-1
 #pragma unroll
-    for (int r = 0; r < kRMax; ++r) {
-        if (r >= R) break;
+    for (int r0 = 0; r0 < kRMax; r0 += kRB) {
+        if (r0 >= R) break;
         __syncthreads();
-        *(float4*)&red[ps][4 * col] = acc[r];
+#pragma unroll
+        for (int j = 0; j < kRB; ++j)
+            if (r0 + j < R) *(float4*)&red[j][ps][4 * col] = acc[r0 + j];
         __syncthreads();
-        if (tid < HD) {
+        for (int i = tid; i < kRB * HD; i += kSW) {
+            const int j = i / HD, dd = i - j * HD, r = r0 + j;
+            if (r >= R) break;
             float o = 0.f;
 #pragma unroll
-            for (int k = 0; k < NPS; ++k) o += red[k][tid];
+            for (int k = 0; k < NPS; ++k) o += red[j][k][dd];
             if (single) {
-                out[(size_t)t * ldo + (g * R + r) * HD + tid] = o / st_l[r];
+                out[(size_t)t * ldo + (g * R + r) * HD + dd] = o / st_l[r];
             } else {
                 float* pr = part + ((size_t)c * R + r) * PS;
-                pr[tid] = o;
-                if (tid == 0) {
+                pr[dd] = o;
+                if (dd == 0) {
                     pr[HD] = st_m[r];
                     pr[HD + 1] = st_l[r];
                 }
@@ -453,19 +459,24 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
 
 // Merge of the chunk partials of k_attn_split: one workgroup per (query
 // head, token). Every thread loads one chunk's (m, l) and forms e^(m_c - M)
-// in parallel (M = the maximum, which no order changes); the sums then run in
-// chunk order, L in one lane and each output dimension in one lane, so the
-// result is that of a serial merge: O = sum_c O_c e^(m_c - M) / sum_c l_c
-// e^(m_c - M). Tokens with a single chunk were written directly and are
-// skipped.
+// in parallel (M = the maximum, which no order changes). The sums
+// O = sum_c O_c e^(m_c - M) and L = sum_c l_c e^(m_c - M) then run in chunk
+// order: up to kSerialMerge chunks in one lane per output dimension (L in
+// one more lane); above, the kSW / HD lanes of a dimension each take a
+// contiguous quarter (head_dim 64) or half (128) of the chunks and their
+// sums are added in range order. Either way the order depends on the
+// token's position alone. Tokens with a single chunk were written directly
+// and are skipped.
+constexpr int kSerialMerge = 32;
 template <int HD>
 __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const int* d_pos, int pos_off, int ctx,
                                                     const float* work, float* out, int ldo) {
-    constexpr int PS = part_stride<HD>();
+    constexpr int PS = part_stride<HD>(), S = kSW / HD;
     static_assert(kNCMax == kSW, "one chunk per thread");
-    static_assert(HD < kSW, "a lane outside the output dimensions sums L");
+    static_assert(S >= 2, "a lane outside the output dimensions sums L in serial merges");
     __shared__ float sf[kNCMax], sl[kNCMax];  // e^(m_c - M), l_c
-    __shared__ float smax[kSW / 64], sL;
+    __shared__ float smax[kSW / 64], sLq[S];
+    __shared__ __align__(16) float so[S][HD];
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int R = n_heads / n_kv, g = h / R, r = h - g * R;
     const int pt = start_position(d_pos, pos_off) + t;
@@ -489,25 +500,47 @@ __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const
     for (int i = 1; i < kSW / 64; ++i) M = fmaxf(M, smax[i]);
     if (tid < nch) sf[tid] = expf(mc - M);
     __syncthreads();
-    if (tid == HD) {
-        float L = 0.f;
-        for (int c = 0; c < nch; ++c) L = __builtin_fmaf(sl[c], sf[c], L);
-        sL = L;
+    const bool serial = nch <= kSerialMerge;
+    const int d = tid % HD, q = tid / HD;
+    int c0 = 0, c1 = nch;  // this lane's chunk range
+    if (!serial) {
+        c0 = q * nch / S;
+        c1 = (q + 1) * nch / S;
+    } else if (q) {
+        c1 = 0;
     }
     float O = 0.f;
-    if (tid < HD) {
-        int c = 0;
-        for (; c + 8 <= nch; c += 8) {  // eight loads in flight, then the eight FMAs in chunk order
+    {
+        int c = c0;
+        for (; c + 8 <= c1; c += 8) {  // eight loads in flight, then the eight FMAs in chunk order
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = part[(c + j) * cs + tid];
+            for (int j = 0; j < 8; ++j) v[j] = part[(c + j) * cs + d];
 #pragma unroll
             for (int j = 0; j < 8; ++j) O = __builtin_fmaf(v[j], sf[c + j], O);
         }
-        for (; c < nch; ++c) O = __builtin_fmaf(part[c * cs + tid], sf[c], O);
+        for (; c < c1; ++c) O = __builtin_fmaf(part[c * cs + d], sf[c], O);
     }
+    if (serial ? tid == HD : d == 0) {  // L over all chunks, or over this lane group's range
+        const int l0 = serial ? 0 : c0, l1 = serial ? nch : c1;
+        float L = 0.f;
+        for (int c = l0; c < l1; ++c) L = __builtin_fmaf(sl[c], sf[c], L);
+        sLq[serial ? 0 : q] = L;
+    }
+    if (!serial) so[q][d] = O;
     __syncthreads();
-    if (tid < HD) out[(size_t)t * ldo + h * HD + tid] = O / sL;
+    if (tid < HD) {
+        float L = sLq[0];
+        if (!serial) {
+            O = so[0][d];
+#pragma unroll
+            for (int i = 1; i < S; ++i) {
+                O += so[i][d];
+                L += sLq[i];
+            }
+        }
+        out[(size_t)t * ldo + h * HD + d] = O / L;
+    }
 }
 
 // ── short contexts: all chunks of a (kv head, token) in one workgroup ───────
