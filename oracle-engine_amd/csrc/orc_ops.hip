@@ -239,6 +239,37 @@ template <int HD> constexpr int wg_waves() { return HD == 128 ? 8 : 16; }
 __device__ __forceinline__ float rot_lo(float a, float b, float2 cs) { return __builtin_fmaf(a, cs.x, -(b * cs.y)); }
 __device__ __forceinline__ float rot_hi(float a, float b, float2 cs) { return __builtin_fmaf(b, cs.x, a * cs.y); }
 
+// Rotates the R query heads of kv head g (token t at position pt) into
+// Qs[r][d] with NTH threads; every load of a thread's entries is issued
+// before the first is used.
+template <int HD, int RM, int NTH>
+__device__ __forceinline__ void rope_q_lds(float (&Qs)[RM][HD], const float* qkv, int ldqkv, int t, int g, int R, int pt,
+                                           const float2* rope, int tid) {
+    constexpr int half = HD / 2, QI = (RM * HD + NTH - 1) / NTH;
+    const float* qt = qkv + (size_t)t * ldqkv + (size_t)g * R * HD;
+    const float2* cr = rope + (size_t)pt * half;
+    float a[QI], b[QI];
+    float2 cs[QI];
+#pragma unroll
+    for (int j = 0; j < QI; ++j) {
+        const int i = tid + j * NTH;
+        if (i < R * HD) {
+            const int r = i / HD, d = i - r * HD, dl = d < half ? d : d - half;
+            a[j] = qt[r * HD + dl];
+            b[j] = qt[r * HD + dl + half];
+            cs[j] = cr[dl];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < QI; ++j) {
+        const int i = tid + j * NTH;
+        if (i < R * HD) {
+            const int r = i / HD, d = i - r * HD;
+            Qs[r][d] = d < half ? rot_lo(a[j], b[j], cs[j]) : rot_hi(a[j], b[j], cs[j]);
+        }
+    }
+}
+
 // floats per partial row: O[HD], m, l, padded to whole 128-byte lines
 template <int HD> constexpr int part_stride() { return HD + 32; }
 
@@ -326,12 +357,7 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
         kc[o] = v;
         vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
     }
-    for (int i = tid; i < R * HD; i += kSW) {
-        const int r = i / HD, d = i - r * HD;
-        const float* qr = qkv + (size_t)t * ldqkv + (size_t)(g * R + r) * HD;
-        const float2* cs = rope + (size_t)pt * half;
-        Qs[r][d] = d < half ? rot_lo(qr[d], qr[d + half], cs[d]) : rot_hi(qr[d - half], qr[d], cs[d - half]);
-    }
+    rope_q_lds<HD, kRMax, kSW>(Qs, qkv, ldqkv, t, g, R, pt, rope, tid);
     if (tid < kRMax) {
         st_m[tid] = -INFINITY;
         st_l[tid] = 0.f;
@@ -588,12 +614,7 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
         kc[o] = v;
         vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
     }
-    for (int i = tid; i < R * HD; i += kWT) {
-        const int r = i / HD, d = i - r * HD;
-        const float* qr = qkv + (size_t)t * ldqkv + (size_t)(g * R + r) * HD;
-        const float2* cs = rope + (size_t)pt * half;
-        Qs[r][d] = d < half ? rot_lo(qr[d], qr[d + half], cs[d]) : rot_hi(qr[d - half], qr[d], cs[d - half]);
-    }
+    rope_q_lds<HD, RM, kWT>(Qs, qkv, ldqkv, t, g, R, pt, rope, tid);
     const int CPW = (P + kWW - 1) / kWW;
     const int p0 = w * CPW, p1 = min(P, p0 + CPW);
 
