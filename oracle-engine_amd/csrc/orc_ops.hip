@@ -239,14 +239,15 @@ template <int HD> constexpr int wg_waves() { return HD == 128 ? 8 : 16; }
 __device__ __forceinline__ float rot_lo(float a, float b, float2 cs) { return __builtin_fmaf(a, cs.x, -(b * cs.y)); }
 __device__ __forceinline__ float rot_hi(float a, float b, float2 cs) { return __builtin_fmaf(b, cs.x, a * cs.y); }
 
-// Rotates the R query heads of kv head g (token t at position pt) into
-// Qs[r][d] with NTH threads; every load of a thread's entries is issued
+// Rotates the nh query heads h0 .. h0 + nh - 1 of token t (at position pt)
+// into Qs[r][d] with NTH threads; every load of a thread's entries is issued
 // before the first is used.
 template <int HD, int RM, int NTH>
-__device__ __forceinline__ void rope_q_lds(float (&Qs)[RM][HD], const float* qkv, int ldqkv, int t, int g, int R, int pt,
-                                           const float2* rope, int tid) {
+__device__ __forceinline__ void rope_q_lds(float (&Qs)[RM][HD], const float* qkv, int ldqkv, int t, int h0, int nh,
+                                           int pt, const float2* rope, int tid) {
     constexpr int half = HD / 2, QI = (RM * HD + NTH - 1) / NTH;
-    const float* qt = qkv + (size_t)t * ldqkv + (size_t)g * R * HD;
+    const int R = nh;
+    const float* qt = qkv + (size_t)t * ldqkv + (size_t)h0 * HD;
     const float2* cr = rope + (size_t)pt * half;
     float a[QI], b[QI];
     float2 cs[QI];
@@ -357,7 +358,7 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
         kc[o] = v;
         vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
     }
-    rope_q_lds<HD, kRMax, kSW>(Qs, qkv, ldqkv, t, g, R, pt, rope, tid);
+    rope_q_lds<HD, kRMax, kSW>(Qs, qkv, ldqkv, t, g * R, R, pt, rope, tid);
     if (tid < kRMax) {
         st_m[tid] = -INFINITY;
         st_l[tid] = 0.f;
@@ -569,9 +570,11 @@ __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const
     }
 }
 
-// ── short contexts: all chunks of a (kv head, token) in one workgroup ───────
+// ── short contexts: all positions of a (query heads, token) in one workgroup ─
 // Tokens attending to at most kWGMax positions: one workgroup of kWW waves per
-// (kv head g, token t). Wave w takes positions [w CPW, (w + 1) CPW) with
+// (RM query heads of kv head g, token t); the launch uses RM = 1, so the
+// per-pass chains carry one head and the grid holds n_heads x n_tok
+// workgroups (each head's arithmetic is the same whatever RM is). Wave w takes positions [w CPW, (w + 1) CPW) with
 // CPW = ceil(P / waves), a function of the position alone (so an n-token call
 // still equals n one-token calls bit for bit), in passes of 16: four lanes
 // per position form the scores (K rows from the cache, or for the batch's
@@ -590,9 +593,11 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
     __shared__ __align__(16) float Es[kWW][RM][16];  // a pass's exp(s - m) per wave, head, position
     __shared__ __align__(16) float Ow[kWW][RM][HD];
     __shared__ float mw[kWW][RM], lw[kWW][RM];
-    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    // workgroup = (kv head g, heads r0 .. r0 + RH - 1 of its group, token t)
+    const int R = n_heads / n_kv, nbh = (R + RM - 1) / RM;
+    const int g = blockIdx.x / nbh, r0 = (blockIdx.x - g * nbh) * RM, RH = min(RM, R - r0);
+    const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int R = n_heads / n_kv;
     const int start = start_position(d_pos, pos_off);
     const int pt = start + t;
     if (pt < 0 || pt >= ctx) return;  // outside the cache (graph replays past the end): nothing to do
@@ -604,8 +609,9 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
     const float* vg = vc + (size_t)g * ctx * HD;
     const int sp = lane >> 2, sl = lane & 3;
 
-    // this token's K (rotated) and V at pt go to the cache
-    if (tid < HD) {
+    // this token's K (rotated) and V at pt go to the cache, from the group's
+    // first workgroup
+    if (r0 == 0 && tid < HD) {
         const float* kr = qkv + (size_t)t * ldqkv + kvh;
         const float2* cs = rope + (size_t)pt * half;
         const int d = tid;
@@ -614,7 +620,7 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
         kc[o] = v;
         vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
     }
-    rope_q_lds<HD, RM, kWT>(Qs, qkv, ldqkv, t, g, R, pt, rope, tid);
+    rope_q_lds<HD, RM, kWT>(Qs, qkv, ldqkv, t, g * R + r0, RH, pt, rope, tid);
     const int CPW = (P + kWW - 1) / kWW;
     const int p0 = w * CPW, p1 = min(P, p0 + CPW);
 
@@ -679,7 +685,7 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
         load_k(k, b0 + sp, sp < nb);
 #pragma unroll
         for (int r = 0; r < RM; ++r) {
-            if (r >= R) break;
+            if (r >= RH) break;
             float sc = 0.f;
 #pragma unroll
             for (int j = 0; j < FL; ++j) {
@@ -711,7 +717,7 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int r = 0; r < RM; ++r) {
-            if (r >= R) break;
+            if (r >= RH) break;
             float ev[16];
 #pragma unroll
             for (int j4 = 0; j4 < 4; ++j4) *(float4*)&ev[4 * j4] = *(const float4*)&Es[w][r][4 * j4];
@@ -729,7 +735,7 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
     // the wave's partial results, then the merge in wave order
 #pragma unroll
     for (int r = 0; r < RM; ++r) {
-        if (r >= R) break;
+        if (r >= RH) break;
 #pragma unroll
         for (int kk = 0; kk < DPL; ++kk) Ow[w][r][DPL * lane + kk] = O[r][kk];
         if (lane == 0) {
@@ -738,7 +744,7 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
         }
     }
     __syncthreads();
-    for (int i = tid; i < R * HD; i += kWT) {
+    for (int i = tid; i < RH * HD; i += kWT) {
         const int r = i / HD, d = i - r * HD;
         float M = -INFINITY;
         for (int v = 0; v < kWW; ++v) M = fmaxf(M, mw[v][r]);
@@ -749,7 +755,7 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
             L = __builtin_fmaf(lw[v][r], f, L);
             o = __builtin_fmaf(Ow[v][r][d], f, o);
         }
-        out[(size_t)t * ldo + (g * R + r) * HD + d] = o / L;
+        out[(size_t)t * ldo + (g * R + r0 + r) * HD + d] = o / L;
     }
 }
 
@@ -990,7 +996,6 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
             for (int P = std::max(kWGMax, pos_floor) + 1; P <= pos_limit && nch < kNCMax; ++P)
                 nch = std::max(nch, n_chunks(P));
     }
-    const int R = n_heads / n_kv;
     float* w = (float*)d_work;
     // live timing (host positions only): algorithmic bytes of a launch = the
     // K and V rows of the positions its tokens read, once (the verify tokens
@@ -1009,16 +1014,12 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
         constexpr int HD = decltype(hd_tag)::value;
         LaunchEv ev;
         if (short_ctx) {
-            const dim3 blk(wg_waves<HD>() * 64), grid(n_kv, n_tok);
+            // one workgroup per (query head, token)
+            const dim3 blk(wg_waves<HD>() * 64), grid(n_heads, n_tok);
             const bool tm = armed(kProfAttnWG, kv_bytes[0], ev);
-            if (R <= 4)
-                hipExtLaunchKernelGGL((k_attn_wg<HD, 4>), grid, blk, 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr,
-                                      0, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc,
-                                      d_vc, ctx, d_out, ldo);
-            else
-                hipExtLaunchKernelGGL((k_attn_wg<HD, 8>), grid, blk, 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr,
-                                      0, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc,
-                                      d_vc, ctx, d_out, ldo);
+            hipExtLaunchKernelGGL((k_attn_wg<HD, 1>), grid, blk, 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr, 0,
+                                  d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx,
+                                  d_out, ldo);
             ORC_LAUNCH_CHECK();
         }
         if (nch > 0) {
