@@ -231,8 +231,8 @@ constexpr int kWGMax = 256;
 struct LaunchEv {
     hipEvent_t a = nullptr, b = nullptr;
 };
-// waves of a k_attn_wg workgroup (the register budget of head_dim 128 allows 8)
-template <int HD> constexpr int wg_waves() { return HD == 128 ? 8 : 16; }
+// waves of a k_attn_wg workgroup (head_dim 128: twelve, the most whose registers need no spill)
+template <int HD> constexpr int wg_waves() { return HD == 128 ? 12 : 16; }
 
 // rotate-half of the pair (a = x[i], b = x[i + hd/2]) by (cos, sin) = cs, with
 // one fixed rounding sequence wherever a row is rotated
