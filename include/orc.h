@@ -205,10 +205,10 @@ int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv,
  * orc_rope_kv_store followed by orc_attn_gqa up to fp32 rounding; a token's
  * result does not depend on n_tok. At most 8 query heads per kv head and 16
  * tokens per call; head_dim 64 or 128; 16-byte aligned rows.
- * A token attending to at most orc_attn_wg_limit() positions is computed by
- * one workgroup per kv head; a longer one's positions are split over up to
- * 32 chunks (64 positions each up to 2048) whose partial results a second
- * launch merges: d_work holds orc_attn_fused_workspace(n_heads, n_kv,
+ * A token attending to at most orc_attn_wg_limit() (512) positions is
+ * computed by one workgroup per query head; a longer one's positions are
+ * split over up to 256 chunks (64 positions each up to 16384) whose partial
+ * results a second launch merges: d_work holds orc_attn_fused_workspace(n_heads, n_kv,
  * head_dim) bytes, 16-byte aligned; calls that share a workspace must not
  * overlap. With device positions, every token position p of the call (or of
  * a captured graph replaying it at later device positions) must satisfy

@@ -223,10 +223,11 @@ __host__ __device__ inline int chunk_positions(int P) {
 }
 __host__ __device__ inline int n_chunks(int P) { return (P + chunk_positions(P) - 1) / chunk_positions(P); }
 
-// Tokens attending to at most kWGMax positions take k_attn_wg (one launch, at
-// most two passes of its waves); longer ones the split over workgroups plus
-// the merge, which keeps more CUs streaming K and V.
-constexpr int kWGMax = 256;
+// Tokens attending to at most kWGMax positions take k_attn_wg (one launch,
+// one workgroup per query head, at most three passes of its waves); longer
+// ones the split over workgroups plus the merge, which keeps more CUs
+// streaming K and V.
+constexpr int kWGMax = 512;
 
 struct LaunchEv {
     hipEvent_t a = nullptr, b = nullptr;

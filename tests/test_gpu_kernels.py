@@ -320,19 +320,21 @@ def _attn_ws(dev, H, KVH, hd):
                           (24, 8, 128, 300, 9, True, 512, 256), (14, 2, 64, 253, 9, False, 0, 0),
                           (28, 4, 128, 1500, 5, True, 2048, 256), (28, 4, 128, 8400, 9, False, 0, 0),
                           (14, 2, 64, 16370, 9, True, 16384, 8192), (14, 2, 64, 16380, 9, True, 16400, 16000),
-                          (14, 2, 64, 20000, 3, False, 0, 0)])
+                          (14, 2, 64, 20000, 3, False, 0, 0), (24, 8, 128, 508, 9, True, 1024, 0),
+                          (24, 8, 128, 512, 5, True, 1024, 512), (28, 4, 128, 400, 9, True, 1024, 300),
+                          (14, 2, 64, 509, 9, False, 0, 0)])
 def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim, flo):
     """Fused RoPE + KV store + attention equals the oracle's rope then
     attention over the prefilled cache plus the new rows; the new K/V rows
     land in the cache; the QKV rows are left as they were. Cases cross chunk
     boundaries (64 positions per chunk up to 16384, then wider chunks; merges
     of more than 32 chunks split over lane groups) and the
-    switch between the one-workgroup path and the split (256 positions), and
+    switch between the one-workgroup path and the split (512 positions), and
     a second call on the same workspace repeats the first's outputs. lim, flo:
     the bounds flo <= position < lim declared by a device-position call (lim
     0: the context), which select its kernels and size their grids."""
     print(f"[gpu] attn_fused H={H} KVH={KVH} hd={hd} sp={sp} nt={nt} devpos={devpos} lim={lim} flo={flo}", flush=True)
-    assert dev.L.orc_attn_wg_limit() == 256
+    assert dev.L.orc_attn_wg_limit() == 512
     rng = np.random.default_rng(sp * 7 + nt)
     base = 500000.0
     ctx = max(sp + nt + 5, lim)
@@ -381,7 +383,7 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim, flo):
 @pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 250, 5), (14, 2, 64, 2040, 9), (28, 4, 128, 60, 7),
                                             (24, 8, 128, 508, 9), (28, 4, 128, 1019, 9), (14, 2, 64, 3, 16),
                                             (24, 8, 128, 252, 9), (14, 2, 64, 250, 9), (28, 4, 128, 8400, 9),
-                                            (14, 2, 64, 16380, 9)])
+                                            (14, 2, 64, 16380, 9), (28, 4, 128, 505, 9), (24, 8, 128, 380, 9)])
 def test_attn_fused_batch_invariant(dev, H, KVH, hd, sp, nt):
     """One n-token call equals n one-token calls at the following positions
     bit for bit (the verify pass of a speculative round equals decode)."""
