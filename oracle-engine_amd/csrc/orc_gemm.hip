@@ -637,7 +637,13 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int kMWG = 512, kMW = kMWG / 64;
-constexpr int kMmqMaxNT = 8;
+// Tokens per launch: up to 8 as stacked hi / lo rows of one A tile (rows
+// 0-7 the hi halves of tokens 0-7, rows 8-15 their lo halves); 9 to 16 as
+// two A tiles (the hi halves of tokens 0-15, and their lo halves) against
+// the same B: every (token, row) sum is formed by the same operations in
+// the same order either way. Whole-tile (tall) launches stay at 8.
+constexpr int kMmqMaxNT = 16, kMmqTallNT = 8;
+template <int NT> constexpr bool mmq_wide() { return NT > 8; }
 constexpr int kMixK = 256;  // k_mmq type parameter: Q4_K and Q6_K segments in one launch
 
 // code permutation of one 8-value run (bytes 0,2 / 1,3 / 4,6 / 5,7 land in
@@ -742,25 +748,34 @@ template <int NT> __device__ __forceinline__ int a_off(int i, int c, int hl, int
     return (((i * 4 + c) * 2 + hl) * NT + t) * 16;
 }
 
-// The lane's A entries of a unit (all four slices; lane row r = lane % 16:
-// hi of token r, or lo of token r - 8) and the 2^-e of the tokens of its D
-// rows, 4 (c % 2) + i; every LDS read under one branch, all in flight.
+// The lane's A entries of a unit (all four slices; lane row r = lane % 16)
+// and the 2^-e of the tokens of its D rows; every LDS read under one
+// branch, all in flight. Up to 8 tokens: row r is the hi half of token r or
+// the lo half of token r - 8, D rows are tokens 4 (c % 2) + i. 9 to 16
+// tokens: a holds the hi and al the lo half of token r, D rows are tokens
+// 4 c + i.
 template <int NT>
-__device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h8v (&a)[4], float4& es) {
-    static_assert(NT <= 8, "hi and lo rows of at most 8 tokens");
-    const int c = lane >> 4, r = lane & 15, t = r & 7, tb = 4 * (c & 1);
-    u32x4 h[4];
+__device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h8v (&a)[4], h8v (&al)[4], float4& es) {
+    constexpr bool W = mmq_wide<NT>();
+    const int c = lane >> 4, r = lane & 15, t = W ? r : r & 7, tb = W ? 4 * c : 4 * (c & 1);
+    u32x4 h[4], l[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 4; ++i) h[i] = l[i] = u32x4{0u, 0u, 0u, 0u};
     es = make_float4(0.f, 0.f, 0.f, 0.f);
     if (t < NT) {
-        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + a_off<NT>(0, c, r >> 3, t);
+        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + a_off<NT>(0, c, W ? 0 : r >> 3, t);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 0, 0));
+        for (int i = 0; i < 4; ++i) {
+            h[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 0, 0));
+            if constexpr (W) l[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 1, 0));
+        }
     }
     if (tb < NT) es = *(const float4*)(m.esc + u * ntp<NT>() + tb);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = __builtin_bit_cast(h8v, h[i]);
+    for (int i = 0; i < 4; ++i) {
+        a[i] = __builtin_bit_cast(h8v, h[i]);
+        al[i] = __builtin_bit_cast(h8v, l[i]);
+    }
 }
 
 // Adds the lo rows' sums to the hi rows' (lanes l and l + 32): afterwards
@@ -777,12 +792,13 @@ template <int TR> __device__ __forceinline__ void fold_lo(f4v (&acc)[TR]) {
 // the hi rows only, the sum over the unit's sub-blocks of dmin m sum(x g).
 template <int NT, int TR>
 __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int lane, const MCtx& m, const h8v (&a)[4],
-                                             float4 es, f4v (&acc)[TR]) {
-    const int c = lane >> 4, h = u & 1, tb = 4 * (c & 1);
+                                             const h8v (&al)[4], float4 es, f4v (&acc)[TR], f4v (&acl)[TR]) {
+    constexpr bool W = mmq_wide<NT>();
+    const int c = lane >> 4, h = u & 1, tb = W ? 4 * c : 4 * (c & 1);
     float4 s4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c < 2 && tb < NT) {
+    if ((W || c < 2) && tb < NT) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s4[i] = *(const float4*)(m.sx + min(tb + i, NT - 1) * m.sx_stride + 4 * u);
     }
@@ -790,6 +806,7 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
         f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // even and odd slices in independent chains
+        f4v E = D, El = D;                         // the same for the lo tile (9-16 tokens)
         float mm[4];
         const float dmin = h2f(M[tr].a.x >> 16);
         uint32_t sc4, mn4;
@@ -810,12 +827,16 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
 #pragma unroll
             for (int k = 0; k < 4; ++k) bq[k] = as_u32(__builtin_elementwise_fma(as_h2(r[k]), scv, off));
             const h8v b = __builtin_bit_cast(h8v, bq);
-            if (i & 1)
+            if (i & 1) {
                 Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, Dl, 0, 0, 0);
-            else
+                if constexpr (W) El = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, El, 0, 0, 0);
+            } else {
                 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, D, 0, 0, 0);
+                if constexpr (W) E = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b, E, 0, 0, 0);
+            }
         }
         D += Dl;
+        if constexpr (W) E += El;
         const float d = h2f(M[tr].a.x & 0xFFFFu);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -825,6 +846,15 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
             a = __builtin_fmaf(-mm[2], s4[e].z, a);
             a = __builtin_fmaf(-mm[3], s4[e].w, a);
             acc[tr][e] = a;
+            if constexpr (W) {
+                // the lo rows take the minimum terms with zero sums, as stacked lo rows do
+                float b = __builtin_fmaf(d * esv[e], E[e], acl[tr][e]);
+                b = __builtin_fmaf(-mm[0], 0.f, b);
+                b = __builtin_fmaf(-mm[1], 0.f, b);
+                b = __builtin_fmaf(-mm[2], 0.f, b);
+                b = __builtin_fmaf(-mm[3], 0.f, b);
+                acl[tr][e] = b;
+            }
         }
     }
 }
@@ -832,23 +862,25 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
 // Q4_K unit of TR tiles, A entries from the LDS.
 template <int NT, int TR>
 __device__ __forceinline__ void mmq_unit_q4k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
-                                             f4v (&acc)[TR]) {
-    h8v a[4];
+                                             f4v (&acc)[TR], f4v (&acl)[TR]) {
+    h8v a[4], al[4];
     float4 es;
-    a_load<NT>(u, ua, lane, m, a, es);
-    mmq_core_q4k<NT, TR>(M, u, lane, m, a, es, acc);
+    a_load<NT>(u, ua, lane, m, a, al, es);
+    mmq_core_q4k<NT, TR>(M, u, lane, m, a, al, es, acc, acl);
 }
 
 // Q6_K unit of TR tiles with the lane's A entries given: scale-folded hi /
 // lo codes in two chains, acc += d 2^-e D.
 template <int NT, int TR>
-__device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, const h8v (&a)[4], float4 es,
-                                             f4v (&acc)[TR]) {
+__device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, const h8v (&a)[4], const h8v (&al)[4],
+                                             float4 es, f4v (&acc)[TR], f4v (&acl)[TR]) {
+    constexpr bool W = mmq_wide<NT>();
     const int c = lane >> 4;
     const float esv[4] = {es.x, es.y, es.z, es.w};
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
         f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // hi and lo code halves in independent chains
+        f4v E = D, El = D;                         // the same for the lo tile (9-16 tokens)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // 6-bit codes of the lane's 8 values of slice i (stored + 32)
@@ -874,22 +906,30 @@ __device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, con
             const h8v bhi = __builtin_bit_cast(h8v, bh), blo = __builtin_bit_cast(h8v, bl);
             D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bhi, D, 0, 0, 0);
             Dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], blo, Dl, 0, 0, 0);
+            if constexpr (W) {
+                E = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bhi, E, 0, 0, 0);
+                El = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], blo, El, 0, 0, 0);
+            }
         }
         D += Dl;
+        if constexpr (W) E += El;
         const float d = h2f(M[tr].e);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[tr][e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
+        for (int e = 0; e < 4; ++e) {
+            acc[tr][e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
+            if constexpr (W) acl[tr][e] = __builtin_fmaf(d * esv[e], E[e], acl[tr][e]);
+        }
     }
 }
 
 // Q6_K unit of TR tiles, A entries from the LDS.
 template <int NT, int TR>
 __device__ __forceinline__ void mmq_unit_q6k(const MUnit (&M)[TR], int u, int ua, int lane, const MCtx& m,
-                                             f4v (&acc)[TR]) {
-    h8v a[4];
+                                             f4v (&acc)[TR], f4v (&acl)[TR]) {
+    h8v a[4], al[4];
     float4 es;
-    a_load<NT>(u, ua, lane, m, a, es);
-    mmq_core_q6k<NT, TR>(M, lane, a, es, acc);
+    a_load<NT>(u, ua, lane, m, a, al, es);
+    mmq_core_q6k<NT, TR>(M, lane, a, al, es, acc, acl);
 }
 
 // DPP reductions inside one 16-lane row (fixed order): the quad sum, then the
@@ -1155,9 +1195,9 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
         for (int tr = 0; tr < TR; ++tr) rpn[tr] = rp[tr];
         if (next < n_tiles) tile_rows(next, rpn);
         const int ttn = next < n_tiles ? tile_type(next) : tt;
-        f4v acc[TR];
+        f4v acc[TR], acl[TR];  // acl: the lo tile of 9-16 token launches
 #pragma unroll
-        for (int tr = 0; tr < TR; ++tr) acc[tr] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (int tr = 0; tr < TR; ++tr) acc[tr] = acl[tr] = f4v{0.f, 0.f, 0.f, 0.f};
         for (int ub = k0u; ub < k1u; ub += UW) {
 #pragma unroll
             for (int k = 0; k < UW; ++k)
@@ -1172,9 +1212,9 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                         }
                     }
                     if (tt == ORC_Q4_K)
-                        mmq_unit_q4k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc);
+                        mmq_unit_q4k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc, acl);
                     else
-                        mmq_unit_q6k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc);
+                        mmq_unit_q6k<NT, TR>(buf[k], ub + k, aslot(ub + k, wb), lane, mc, acc, acl);
                     if (ub + k + UW < k1u) {
 #pragma unroll
                         for (int tr = 0; tr < TR; ++tr) buf[k][tr].load(tt, rp[tr], ub + k + UW, c);
@@ -1184,7 +1224,14 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                     }
                 }
         }
-        fold_lo<TR>(acc);
+        if constexpr (mmq_wide<NT>()) {  // hi + lo, the sum fold_lo forms across lanes
+#pragma unroll
+            for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[tr][e] += acl[tr][e];
+        } else {
+            fold_lo<TR>(acc);
+        }
         if (multi_win && first_tile) write_red();
         first_tile = false;
         const int this_tile = tile;
@@ -1364,11 +1411,38 @@ static size_t mmq_lds(int type, int nt, int kn, int tr, int hs) {
 
 static bool mmq_type(int type) { return type == ORC_Q4_K || type == ORC_Q6_K || type == kMixK; }
 
-// tokens per launch: up to kMmqMaxNT as long as one unit per wave fits
-static int mmq_max_tokens(int type, int n_in) {
-    int nt = kMmqMaxNT;
-    while (nt > 1 && mmq_lds(type, nt, n_in, 2, 1) > g_lds_max) --nt;
-    return mmq_lds(type, nt, n_in, 2, 1) <= g_lds_max ? nt : 0;
+// Whole-tile mode (each wave owns whole tiles, every unit of a row staged):
+// chosen by the shape alone, at kMmqTallNT tokens, so a shape takes the same
+// mode (and reduction order) at every token count.
+static bool mmq_tall(int type, const QmvParams& p) {
+    const bool two = type != kMixK && (p.epi == ORC_EPI_SWIGLU || (type == ORC_Q4_K && p.n_rows >= 32 * g_n_cu));
+    const int rows_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.n_rows;
+    return type != kMixK && rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU &&
+           mmq_lds(type, kMmqTallNT, p.n_in, two ? 2 : 1, 0) <= g_lds_max;
+}
+
+// Units per staging window when a wave's range of per_wave units is staged
+// in nwin windows. A window shorter than the range is a whole number of
+// four-unit passes: lane row c then stages units c, c + 4, ... of the range
+// in that order whatever the window, so the RMSNorm's per-lane sums of x^2
+// (and the norm) do not depend on the window size, which the token count
+// sets.
+static int mmq_window(int per_wave, int nwin) {
+    const int hs = (per_wave + nwin - 1) / nwin;
+    return hs >= per_wave ? hs : (hs + 3) & ~3;
+}
+
+// tokens per launch: up to kMmqMaxNT (kMmqTallNT in whole-tile mode) as long
+// as the smallest staging window (one four-unit pass per wave) fits, with the
+// launch's tiles per wave (two for SwiGLU pairs and tall Q4_K matrices)
+static int mmq_max_tokens(int type, const QmvParams& p) {
+    const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
+    const int hs = std::min(per_wave, 4);
+    const bool two = type != kMixK && (p.epi == ORC_EPI_SWIGLU || (type == ORC_Q4_K && p.n_rows >= 32 * g_n_cu));
+    const int tr = two ? 2 : 1;
+    int nt = mmq_tall(type, p) ? kMmqTallNT : kMmqMaxNT;
+    while (nt > 1 && mmq_lds(type, nt, p.n_in, tr, hs) > g_lds_max) --nt;
+    return mmq_lds(type, nt, p.n_in, tr, hs) <= g_lds_max ? nt : 0;
 }
 
 template <int QT, int NT, int TR, int UW, int SW, bool KS1>
@@ -1383,7 +1457,7 @@ static int mmq_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& ev)
     if (!KS1) {
         const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
         for (int nwin = 1; nwin <= per_wave; ++nwin) {
-            p.hs = (per_wave + nwin - 1) / nwin;
+            p.hs = mmq_window(per_wave, nwin);
             if (mmq_lds(QT, NT, p.n_in, TR, p.hs) <= g_lds_max) break;
         }
     }
@@ -1407,23 +1481,33 @@ template <int QT, int NT>
 static int mmq_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
     const bool two = QT != kMixK && (p.epi == ORC_EPI_SWIGLU || (QT == ORC_Q4_K && p.n_rows >= 32 * g_n_cu));
-    const int rows_out = p.epi == ORC_EPI_SWIGLU ? p.rows[0] : p.n_rows;
-    // whole-tile mode only where every unit fits the LDS at the largest token
-    // count, so the mode (and the reduction order) depends on the shape alone;
-    // never for mixed launches (their segments are split-tile sized)
-    const bool tall = QT != kMixK && rows_out / (two ? 32 : 16) >= 2 * kMW * g_n_cu && p.epi != ORC_EPI_SWIGLU &&
-                      mmq_lds(QT, kMmqMaxNT, p.n_in, two ? 2 : 1, 0) <= g_lds_max;
+    // whole-tile mode by the shape alone (never for mixed launches: their
+    // segments are split-tile sized)
+    const bool tall = mmq_tall(QT, p);
     // (ring depth and staging width change no result; two-tile and wide-batch
     // shapes keep them small enough that nothing spills)
     if constexpr (QT != kMixK) {
-        if (tall) return two ? mmq_shape<QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<QT, NT, 1, 6, 4, true>(p, s, ev);
-        if (two) return mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev);
+        if constexpr (NT <= kMmqTallNT) {
+            if (tall)
+                return two ? mmq_shape<QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<QT, NT, 1, 6, 4, true>(p, s, ev);
+        } else if (tall) {
+            return set_error(ORC_E_INVALID, "gemm: more than 8 tokens in a whole-tile launch");
+        }
+        if constexpr (mmq_wide<NT>()) {  // the lo tile's registers leave room for a ring of two
+            if (two) return mmq_shape<QT, NT, 2, 2, 4, false>(p, s, ev);
+        } else {
+            if (two) return mmq_shape<QT, NT, 2, 3, 4, false>(p, s, ev);
+        }
     }
-    if (per_wave <= 3) return mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
-    if constexpr (NT > 4) return mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
-    else {
-        if (per_wave <= 4) return mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
-        return mmq_shape<QT, NT, 1, 4, 8, false>(p, s, ev);
+    if constexpr (mmq_wide<NT>()) {
+        return mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
+    } else {
+        if (per_wave <= 3) return mmq_shape<QT, NT, 1, 3, 4, false>(p, s, ev);
+        if constexpr (NT > 4) return mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
+        else {
+            if (per_wave <= 4) return mmq_shape<QT, NT, 1, 4, 4, false>(p, s, ev);
+            return mmq_shape<QT, NT, 1, 4, 8, false>(p, s, ev);
+        }
     }
 }
 
@@ -1438,7 +1522,15 @@ static int mmq_type_launch(const QmvParams& p, hipStream_t s, const LaunchEvents
         case 6: return mmq_nt<QT, 6>(p, s, ev);
         case 7: return mmq_nt<QT, 7>(p, s, ev);
         case 8: return mmq_nt<QT, 8>(p, s, ev);
-        default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..8");
+        case 9: return mmq_nt<QT, 9>(p, s, ev);
+        case 10: return mmq_nt<QT, 10>(p, s, ev);
+        case 11: return mmq_nt<QT, 11>(p, s, ev);
+        case 12: return mmq_nt<QT, 12>(p, s, ev);
+        case 13: return mmq_nt<QT, 13>(p, s, ev);
+        case 14: return mmq_nt<QT, 14>(p, s, ev);
+        case 15: return mmq_nt<QT, 15>(p, s, ev);
+        case 16: return mmq_nt<QT, 16>(p, s, ev);
+        default: return set_error(ORC_E_UNSUPPORTED, "n_tok chunk must be 1..16");
     }
 }
 
@@ -1479,7 +1571,7 @@ static double gemm_bytes(const QmvParams& p, int nt) {
 static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
     p.units = p.n_in / elems_per_unit(type);
     const bool mm = mmq_type(type);
-    const int ntmax = mm ? mmq_max_tokens(type, p.n_in) : max_tokens(type, p.n_in);
+    const int ntmax = mm ? mmq_max_tokens(type, p) : max_tokens(type, p.n_in);
     if (ntmax < 1) return set_error(ORC_E_UNSUPPORTED, "gemm: n_in too large for the activations to fit LDS");
     // tokens are processed in chunks of at most ntmax; chunking never changes a
     // (token,row) result because the reduction order is independent of n_tok

@@ -90,16 +90,19 @@ def test_gemv_vs_exact(dev, oracle, qt, n_out, n_in):
 
 
 @pytest.mark.parametrize("qt,n_out,n_in", [(ol.Q4_K, 200, 3072), (ol.Q6_K, 77, 8192), (ol.Q8_0, 90, 896),
-                                           (ol.Q4_0, 33, 2048), (ol.Q6_K, 24, 18944), (ol.Q8_0, 40000, 896)])
+                                           (ol.Q4_0, 33, 2048), (ol.Q6_K, 24, 18944), (ol.Q8_0, 40000, 896),
+                                           (ol.Q4_K, 8192, 3072), (ol.Q6_K, 70000, 1024)])
 def test_gemm_batch_invariant(dev, qt, n_out, n_in):
-    """verify(n)[t] is bit-identical to the decode GEMV of token t, n = 1..12."""
+    """verify(n)[t] is bit-identical to the decode GEMV of token t, n = 1..16
+    (the matrix-core kernel: up to 8 tokens as stacked hi / lo rows, 9-16 as
+    two tiles; whole-tile shapes chunked by 8)."""
     print(f"[gpu] gemm invariance type={qt} {n_out}x{n_in}", flush=True)
     rng = np.random.default_rng(3)
     raw = rand_blocks(qt, n_out * n_in, rng)
     wd = dev.upload(raw)
-    X = rng.normal(0, 1, (12, n_in)).astype(np.float32)
-    single = np.stack([_gemm(dev, qt, wd, 1, n_out, n_in, X[t:t + 1])[0] for t in range(12)])
-    for nt in (2, 5, 7, 9, 12):
+    X = rng.normal(0, 1, (16, n_in)).astype(np.float32)
+    single = np.stack([_gemm(dev, qt, wd, 1, n_out, n_in, X[t:t + 1])[0] for t in range(16)])
+    for nt in (2, 5, 7, 9, 12, 16):
         got = _gemm(dev, qt, wd, nt, n_out, n_in, X[:nt])
         assert np.array_equal(got.view(np.uint32), single[:nt].view(np.uint32)), nt
 
@@ -115,7 +118,7 @@ def test_gemm_fused_epilogues(dev, n_in):
     bq = dev.upload(rng.normal(0, 0.1, nq).astype(np.float32))
     normw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
     dnorm = dev.upload(normw)
-    for nt in (1, 4):
+    for nt in (1, 4, 11):
         X = rng.normal(0, 1, (nt, n_in)).astype(np.float32)
         dx = dev.upload(X)
         # reference composition: rmsnorm kernel, then plain GEMMs, bias on the host
@@ -162,7 +165,7 @@ def test_gemm_fused_epilogues(dev, n_in):
                                                   (8192, (160, 96), (ol.Q6_K, ol.Q4_K), False)])
 def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
     """One launch over Q4_K and Q6_K segments (a Q4_K_M layer's Q|K|V) gives
-    every segment's rows bit for bit as the per-type launches do, for 1..8
+    every segment's rows bit for bit as the per-type launches do, for 1..16
     tokens, with the RMSNorm prologue and QKV bias."""
     import orc
 
@@ -173,7 +176,7 @@ def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
     g = dev.upload(rng.uniform(0.5, 1.5, n_in).astype(np.float32))
     ld = sum(rows)
     offs = np.cumsum((0,) + rows)[:-1]
-    for nt in (1, 5, 8):
+    for nt in (1, 5, 8, 9, 16):
         dx = dev.upload(rng.normal(0, 1, (nt, n_in)).astype(np.float32))
         dy, dz = dev.alloc(nt * ld * 4), dev.alloc(nt * ld * 4)
         segs = (orc.Seg * len(rows))(*[orc.Seg(w.ptr, r, dy.ptr + int(o) * 4, b.ptr if b else None)
@@ -194,18 +197,19 @@ def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
                                       None, C.c_float(0), orc.EPI_STORE, None) != 0
 
 
-@pytest.mark.parametrize("qt,epi", [(ol.Q4_K, "norm"), (ol.Q6_K, "swiglu"), (ol.Q4_K, "accum")])
-def test_gemm_staging_windows(dev, oracle, qt, epi):
+@pytest.mark.parametrize("qt,epi,nt", [(ol.Q4_K, "norm", 8), (ol.Q6_K, "swiglu", 8), (ol.Q4_K, "accum", 8),
+                                       (ol.Q6_K, "swiglu", 9), (ol.Q4_K, "norm", 16), (ol.Q6_K, "accum", 12)])
+def test_gemm_staging_windows(dev, oracle, qt, epi, nt):
     """Rows too long for every token's activations to fit the LDS at once
     (n_in = 18944) are staged in windows: with the RMSNorm prologue, the
     SwiGLU pair and the residual epilogue, over more tiles than workgroups (so
-    windows are restaged for later tiles), 8 tokens equal 8 one-token calls bit
-    for bit and match float64 within 2e-6 of sum |w x|."""
+    windows are restaged for later tiles), nt tokens equal nt one-token calls
+    bit for bit and match float64 within 2e-6 of sum |w x|."""
     import orc
 
-    print(f"[gpu] gemm staging windows type={qt} epi={epi}", flush=True)
+    print(f"[gpu] gemm staging windows type={qt} epi={epi} nt={nt}", flush=True)
     rng = np.random.default_rng(19)
-    n_in, n_out, nt = 18944, 16 * 300, 8
+    n_in, n_out = 18944, 16 * 300
     raw = rand_blocks(qt, (2 if epi == "swiglu" else 1) * n_out * n_in, rng)
     wd = dev.upload(raw)
     X = rng.normal(0, 1, (nt, n_in)).astype(np.float32)
