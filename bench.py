@@ -28,6 +28,9 @@ summary in profiles/.
 cpu_baseline: the reference implementation (oracle/_ref, built from the
 reference's sources) on the same two models, bounded sample: prompt 8 ids,
 16 generated tokens, k = 4.
+target_greedy_tok_s: the target alone decoding the same tokens greedily
+(graph replay, after the same prefill): at C3 that is the C2 workload
+(BASELINE.json configs[1]).
 gemv_microbench: quantized one-token GEMVs (16384 x 8192) back to back over
 more than 640 MB of distinct weight matrices in rotation (beyond the 256 MB
 Infinity Cache), per type, timed by the same dispatch events.
@@ -255,6 +258,14 @@ def main():
         exact &= bool(np.array_equal(toks, expect))
 
     L, H = orc.load_hip_lib(), orc.load_host_lib()
+    greedy_tok_s = None
+    if not engine:  # the target alone, greedy (C3's target is C2), KV from the prefill
+        H.orch_sync()
+        tg = time.perf_counter()
+        g2 = tgt.greedy(prompt, n_gen, prefill=False)
+        H.orch_sync()
+        greedy_tok_s = n_gen / (time.perf_counter() - tg)
+        exact &= bool(np.array_equal(g2, greedy))
     tot = {"accepted": 0, "proposed": 0, "passes": 0}
     H.orch_sync()
     t0 = time.perf_counter()
@@ -328,6 +339,7 @@ def main():
         "acceptance": round(tot["accepted"] / max(1, tot["proposed"]), 4),
         "target_passes_per_token": round(tot["passes"] / max(1, a.steps * n_gen), 4),
         "exact_vs_greedy" if not engine else "stream_reproducible": exact,
+        "target_greedy_tok_s": None if greedy_tok_s is None else round(greedy_tok_s, 2),
         "reference_stream_identical": ref_identical,
         "roofline": roofline, "cpu_baseline": cpu,
         "gemv_microbench": micro,
