@@ -31,7 +31,8 @@ reference's sources) on the same two models, bounded sample: prompt 8 ids,
 target_greedy_tok_s: the target alone decoding the same tokens greedily
 (graph replay, after the same prefill): at C3 that is the C2 workload
 (BASELINE.json configs[1]).
-gemv_microbench: quantized one-token GEMVs (16384 x 8192) back to back over
+gemv_microbench: quantized one-token GEMVs (16384 x 8192; Q8_0 both as GGUF
+blocks and regrouped into the aligned Q8_0_X8 layout) back to back over
 more than 640 MB of distinct weight matrices in rotation (beyond the 256 MB
 Infinity Cache), per type, timed by the same dispatch events.
 
@@ -59,7 +60,7 @@ sys.path.insert(0, os.path.join(PKG, "python"))
 SYNTH = os.path.join(PKG, "bin", "synth_gguf")
 REF_DRIVER = os.path.join(ROOT, "oracle", "_ref", "ref_driver")
 HBM_PEAK_GBS = 8000.0
-TYPE_NAMES = {2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K", 256: "Q4_K|Q6_K"}
+TYPE_NAMES = {2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K", 256: "Q4_K|Q6_K", 258: "Q8_0_X8"}
 
 
 def log(msg):
@@ -120,7 +121,7 @@ WORKLOADS = {
                desc="C5 long-context spec greedy: 7B-shape all-Q6_K target + 0.5B-shape Q8_0 draft"),
 }
 SAMPLER = (0.8, 0.95, 40, 1.1, 64, 4242)  # T, top-p, top-k, repeat penalty, repeat_last, seed (C4)
-PROF_FAMILIES = (2, 8, 12, 14, 256, 300, 301, 302)
+PROF_FAMILIES = (2, 8, 12, 14, 256, 258, 300, 301, 302)
 FAMILY_NAMES = {**TYPE_NAMES, 300: "attn k_attn_wg", 301: "attn k_attn_split", 302: "attn k_attn_merge"}
 
 
@@ -142,7 +143,8 @@ def gemv_microbench(dev, n_out=16384, n_in=8192, rotate_mb=640, rounds=6):
     y = dev.alloc(4 * n_out)
     out = []
     # GGML type, block bytes, byte offsets of the fp16 scales inside a block
-    for ty, bb, scales in ((8, 34, (0,)), (12, 144, (0, 2)), (14, 210, (208,)), (2, 18, (0,))):
+    # (258: the Q8_0 blocks regrouped in place into the aligned Q8_0_X8 layout the models use)
+    for ty, bb, scales in ((258, 34, (0,)), (8, 34, (0,)), (12, 144, (0, 2)), (14, 210, (208,)), (2, 18, (0,))):
         rb = L.orc_row_bytes(ty, n_in)
         mb = rb * n_out
         m = max(2, -(-(rotate_mb << 20) // mb))
@@ -153,6 +155,8 @@ def gemv_microbench(dev, n_out=16384, n_in=8192, rotate_mb=640, rounds=6):
         for i in range(m):
             w.write(blocks, i * mb)
         del blocks
+        if ty == 258:
+            dev.check(L.orc_q8_0_regroup(w.ptr, m * mb // 272, None))
         for _ in range(2):  # warm-up round: first-launch costs stay out of the timing
             for i in range(m):
                 dev.check(L.orc_gemm(ty, w.ptr + i * mb, 1, n_out, n_in, x.ptr, n_in, y.ptr, n_out, None))

@@ -43,6 +43,13 @@ extern "C" {
 #define ORC_Q8_0 8
 #define ORC_Q4_K 12
 #define ORC_Q6_K 14
+/* Device layout of Q8_0 weights regrouped by orc_q8_0_regroup (no GGML
+ * counterpart): every 8 consecutive blocks of a row (272 bytes) hold their 8
+ * fp16 scales first (16 bytes), then their 8 x 32 int8 codes (256 bytes), so
+ * every code load is 16-byte aligned. Same bytes per row as Q8_0; rows of a
+ * multiple of 256 values. The GEMM entry points take it as a weight type and
+ * give results bit-identical to the same matrix as Q8_0. */
+#define ORC_Q8_0_X8 258
 
 typedef void* orc_stream_t; /* a hipStream_t */
 typedef void* orc_graph_t;  /* an instantiated hipGraphExec_t */
@@ -84,6 +91,11 @@ int orc_event_elapsed_ms(orc_event_t start, orc_event_t stop, float* ms);
 /* ── quant codecs ────────────────────────────────────────────────────────── */
 /* Bytes of one row of n_el elements of `type` (core/gguf_parser.cpp:61-75). */
 int64_t orc_row_bytes(int type, int64_t n_el);
+/* Regroups n_blocks8 groups of 8 consecutive Q8_0 blocks (272 bytes each,
+ * e.g. n_rows * n_in / 256 for a matrix whose rows hold a multiple of 256
+ * values) in place into the ORC_Q8_0_X8 layout. Apply once per matrix; the
+ * matrix is then used with type ORC_Q8_0_X8 only. */
+int orc_q8_0_regroup(void* d_w, int64_t n_blocks8, orc_stream_t stream);
 /* Dequantize n_el contiguous elements to fp32, bit-exact with the reference
  * codecs: fp16/Q4_0/Q8_0/Q4_K/Q6_K (core/gguf_parser.cpp:1002-1154,
  * dequantize_into :420-441). */

@@ -45,6 +45,7 @@ namespace orc {
 // LPR: lanes per row slot; EPU: values per unit; PP: LDS padding period.
 template <int QT> struct QTr;
 template <> struct QTr<ORC_Q8_0> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
+template <> struct QTr<ORC_Q8_0_X8> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
 template <> struct QTr<ORC_Q4_0> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
 template <> struct QTr<ORC_Q4_K> { static constexpr int EPU = 32, PP = 64, LPR = 32; };
 template <> struct QTr<ORC_Q6_K> { static constexpr int EPU = 64, PP = 64, LPR = 16; };
@@ -282,6 +283,22 @@ template <int ROWS> struct Unit<ORC_Q8_0, ROWS> {
 #pragma unroll
             for (int r = 0; r < ROWS; ++r)
                 acc[r][t] = __builtin_fmaf(h2f(dh[r]), __builtin_fmaf(-128.f, sx32, S[r][t]), acc[r][t]);
+        }
+    }
+};
+
+// ORC_Q8_0_X8: block u is code run u % 8 of the 272-byte group u / 8 (8
+// fp16 scales, then 8 x 32 codes): the same values as Q8_0, loaded with
+// aligned 16-byte reads; the arithmetic is Q8_0's.
+template <int ROWS> struct Unit<ORC_Q8_0_X8, ROWS> : Unit<ORC_Q8_0, ROWS> {
+    __device__ __forceinline__ void load(const uint8_t* const (&rp)[ROWS], int u) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const uint8_t* grp = rp[r] + (size_t)(u >> 3) * 272;
+            this->dh[r] = *(const uint16_t*)(grp + 2 * (u & 7));
+            const u32x4* q = (const u32x4*)(grp + 16 + 32 * (u & 7));
+            this->q0[r] = q[0];
+            this->q1[r] = q[1];
         }
     }
 };
@@ -1328,7 +1345,7 @@ int gemm_device_init(int device) {
 void gemm_device_release() {}
 
 static int elems_per_unit(int type) { return type == ORC_Q6_K ? 64 : 32; }
-static int block_elems(int type) { return type == ORC_Q4_K || type == ORC_Q6_K ? 256 : 32; }
+static int block_elems(int type) { return type == ORC_Q4_K || type == ORC_Q6_K || type == ORC_Q8_0_X8 ? 256 : 32; }
 static int pad_period(int type) { return type == ORC_Q4_K || type == ORC_Q6_K ? 64 : 32; }
 
 static size_t qmv_lds(int type, int nt, int kn) {
@@ -1588,6 +1605,7 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
             case ORC_Q6_K: rc = mmq_type_launch<ORC_Q6_K>(q, s, ev); break;
             case kMixK: rc = mmq_type_launch<kMixK>(q, s, ev); break;
             case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s, ev); break;
+            case ORC_Q8_0_X8: rc = launch_type<ORC_Q8_0_X8>(q, s, ev); break;
             case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, s, ev); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
         }
@@ -1658,21 +1676,49 @@ extern "C" int64_t orc_row_bytes(int type, int64_t n) {
         case ORC_F16: return n * 2;
         case ORC_Q4_0: return n % 32 ? -1 : n / 32 * 18;
         case ORC_Q8_0: return n % 32 ? -1 : n / 32 * 34;
+        case ORC_Q8_0_X8: return n % 256 ? -1 : n / 32 * 34;
         case ORC_Q4_K: return n % 256 ? -1 : n / 256 * 144;
         case ORC_Q6_K: return n % 256 ? -1 : n / 256 * 210;
         default: return -1;
     }
 }
 
+// One thread per 272-byte group: the 8 blocks are read whole before the
+// group is rewritten, and no other thread touches it, so the change is in
+// place.
+__global__ __launch_bounds__(256) void k_q8_0_regroup(uint8_t* w, int64_t n8) {
+    const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gi >= n8) return;
+    uint8_t* g = w + gi * 272;
+    uint16_t d[8];
+    u32x4 q[16];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const uint8_t* blk = g + 34 * b;
+        d[b] = (uint16_t)ld2(blk);
+        q[2 * b] = ld16(blk + 2);
+        q[2 * b + 1] = ld16(blk + 18);
+    }
+    asm volatile("" ::: "memory");  // every read of the group before the first write
+    uint16_t* ds = (uint16_t*)g;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) ds[b] = d[b];
+    u32x4* qs = (u32x4*)(g + 16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qs[i] = q[i];
+}
+
 static int check_gemm_shape(int type, int n_tok, int n_in, const float* x, int ldx, int ldy, const void* w) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0)
+    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q8_0_X8 && type != ORC_Q4_0)
         return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
     if (n_tok < 1 || n_in <= 0 || n_in % block_elems(type))
         return set_error(ORC_E_INVALID, "gemm: n_in must be a positive multiple of the block size");
     if (!x || !w || ldx < n_in || ldx % 4 || ldy < 1)
         return set_error(ORC_E_INVALID, "gemm: bad pointers or strides (ldx >= n_in, ldx % 4 == 0)");
     if (((uintptr_t)x & 15) != 0) return set_error(ORC_E_INVALID, "gemm: x must be 16-byte aligned");
+    if (type == ORC_Q8_0_X8 && ((uintptr_t)w & 15))
+        return set_error(ORC_E_INVALID, "gemm: Q8_0_X8 weights must be 16-byte aligned");
     return ORC_OK;
 }
 
@@ -1710,6 +1756,8 @@ extern "C" int orc_gemm_fused(int type, const orc_seg* segs, int n_segs, int n_t
     int total = 0;
     for (int i = 0; i < n_segs; ++i) {
         if (!segs[i].d_w || !segs[i].d_y || segs[i].n_out <= 0) return set_error(ORC_E_INVALID, "gemm_fused: bad segment");
+        if (type == ORC_Q8_0_X8 && ((uintptr_t)segs[i].d_w & 15))
+            return set_error(ORC_E_INVALID, "gemm: Q8_0_X8 weights must be 16-byte aligned");
         p.w[i] = (const uint8_t*)segs[i].d_w;
         p.y[i] = segs[i].d_y;
         p.bias[i] = segs[i].d_bias;
@@ -1771,4 +1819,17 @@ extern "C" int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n
     p.eps = eps;
     p.epi = epilogue;
     return gemm_dispatch(p, kMixK, resolve_stream(stream));
+}
+
+extern "C" int orc_q8_0_regroup(void* d_w, int64_t n_blocks8, orc_stream_t stream) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_w || n_blocks8 < 0 || ((uintptr_t)d_w & 15))
+        return set_error(ORC_E_INVALID, "q8_0_regroup: null or not 16-byte aligned weights");
+    if (n_blocks8 == 0) return ORC_OK;
+    const int64_t nb = (n_blocks8 + 255) / 256;
+    if (nb > 0x7fffffff) return set_error(ORC_E_INVALID, "q8_0_regroup: too many groups");
+    hipLaunchKernelGGL(k_q8_0_regroup, dim3((unsigned)nb), dim3(256), 0, resolve_stream(stream), (uint8_t*)d_w,
+                       n_blocks8);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
 }

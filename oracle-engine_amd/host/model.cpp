@@ -108,6 +108,22 @@ bool Model::load(const std::string& path, int ctx_len) {
         }
     }
 
+    // Q8_0 matrices whose rows hold a multiple of 256 values are regrouped
+    // once into the aligned ORC_Q8_0_X8 layout (same bytes, same results);
+    // the token embedding keeps the GGUF layout for the row gather
+    {
+        std::vector<Mat*> ms{&head_};
+        for (Layer& L : layers_)
+            for (Mat* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down}) ms.push_back(m);
+        for (Mat* m : ms) {
+            if (m->type != ORC_Q8_0 || m->n_in % 256 || m->d == embd_.d || ((uintptr_t)m->d & 15)) continue;
+            if (orc_q8_0_regroup((void*)m->d, (int64_t)m->n_out * (m->n_in / 256), nullptr))
+                return fail(std::string("q8_0 regroup: ") + orc_last_error());
+            m->type = ORC_Q8_0_X8;
+        }
+        orc_stream_sync(nullptr);
+    }
+
     // device buffers
     const int B = kMaxBatch, C = (int)cfg.ctx_len, QKV = NQ + 2 * NKV;
     auto alloc = [&](void** p, size_t n) { return orc_malloc(p, n) == 0; };

@@ -17,6 +17,7 @@ BIN_DIR = os.path.join(PKG, "bin")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 EPI_STORE, EPI_ACCUM, EPI_SWIGLU = 0, 1, 2
+Q8_0_X8 = 258  # ORC_Q8_0_X8: Q8_0 regrouped by orc_q8_0_regroup
 
 _vp = C.c_void_p
 _fp = C.POINTER(C.c_float)
@@ -57,6 +58,7 @@ ABI = [
     ("orc_event_record", C.c_int, [_vp, _vp]),
     ("orc_event_elapsed_ms", C.c_int, [_vp, _vp, C.POINTER(C.c_float)]),
     ("orc_row_bytes", C.c_int64, [C.c_int, C.c_int64]),
+    ("orc_q8_0_regroup", C.c_int, [_vp, C.c_int64, _vp]),
     ("orc_dequant", C.c_int, [C.c_int, _vp, C.c_int64, _vp, _vp]),
     ("orc_embed", C.c_int, [C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp]),
     ("orc_gemm", C.c_int, [C.c_int, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp]),

@@ -452,3 +452,58 @@ def test_error_paths(dev):
     assert b"ctx" in dev.L.orc_last_error() or b"context" in dev.L.orc_last_error()
     with pytest.raises(orc.OrcError):
         dev.check(dev.L.orc_dequant(13, d.ptr, 256, d.ptr, None))
+
+
+def _x8_layout(raw, n_out, n_in):
+    """The ORC_Q8_0_X8 bytes of a Q8_0 matrix: per 8 blocks, their fp16 scales,
+    then their 32-byte code runs."""
+    b = raw.reshape(n_out * n_in // 256, 8, 34)
+    return np.concatenate([b[:, :, :2].reshape(-1, 16), b[:, :, 2:].reshape(-1, 256)], axis=1).reshape(-1)
+
+
+@pytest.mark.parametrize("n_out,n_in", [(90, 3072), (1024, 8192), (40000, 3072), (8192, 256)])
+def test_q8_0_regroup_gemm_bit_identical(dev, n_out, n_in):
+    """orc_q8_0_regroup writes the 8-block grouped layout in place, and a GEMM
+    over it (1..5 tokens; plain, the LM-head-tall shape, and fused norm /
+    SwiGLU / residual / bias epilogues) equals the same GEMM over the Q8_0
+    blocks bit for bit."""
+    import orc
+
+    print(f"[gpu] q8_0 regroup {n_out}x{n_in}", flush=True)
+    rng = np.random.default_rng(n_out + n_in)
+    raw = rand_blocks(ol.Q8_0, n_out * n_in, rng)
+    wq, wx = dev.upload(raw), dev.upload(raw)
+    dev.check(dev.L.orc_q8_0_regroup(wx.ptr, n_out * n_in // 256, None))
+    dev.sync()
+    assert np.array_equal(wx.read(np.uint8), _x8_layout(raw, n_out, n_in))
+    assert dev.L.orc_row_bytes(orc.Q8_0_X8, n_in) == n_in // 32 * 34
+    X = rng.normal(0, 1, (5, n_in)).astype(np.float32)
+    for nt in (1, 2, 5):
+        a = _gemm(dev, ol.Q8_0, wq, nt, n_out, n_in, X[:nt])
+        b = _gemm(dev, orc.Q8_0_X8, wx, nt, n_out, n_in, X[:nt])
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), nt
+    if n_out % 2 or n_out > 20000:
+        return
+    half = n_out // 2
+    rb = n_in // 32 * 34
+    g = dev.upload(rng.uniform(0.5, 1.5, n_in).astype(np.float32))
+    bias = dev.upload(rng.normal(0, 0.1, n_out).astype(np.float32))
+    for nt in (1, 4):
+        dx = dev.upload(X[:nt])
+        res = rng.normal(0, 1, (nt, n_out)).astype(np.float32)
+        outs = []
+        for ty, w in ((ol.Q8_0, wq), (orc.Q8_0_X8, wx)):
+            got = []
+            dy = dev.upload(res)  # residual epilogue with norm and bias
+            segs = (orc.Seg * 1)(orc.Seg(w.ptr, n_out, dy.ptr, bias.ptr))
+            dev.check(dev.L.orc_gemm_fused(ty, segs, 1, nt, n_in, dx.ptr, n_in, n_out, g.ptr, C.c_float(1e-5),
+                                           orc.EPI_ACCUM, None))
+            got.append(dy.read(np.float32))
+            dz = dev.alloc(nt * half * 4)  # SwiGLU pair with norm
+            segs = (orc.Seg * 2)(orc.Seg(w.ptr, half, dz.ptr, None), orc.Seg(w.ptr + half * rb, half, dz.ptr, None))
+            dev.check(dev.L.orc_gemm_fused(ty, segs, 2, nt, n_in, dx.ptr, n_in, half, g.ptr, C.c_float(1e-5),
+                                           orc.EPI_SWIGLU, None))
+            got.append(dz.read(np.float32))
+            outs.append(got)
+        for a, b in zip(*outs):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), nt
