@@ -272,6 +272,42 @@ __device__ __forceinline__ void rope_q_lds(float (&Qs)[RM][HD], const float* qkv
     }
 }
 
+// rope_q_lds in two steps: load issues every load of the thread's entries,
+// store rotates them into Qs (same arithmetic), so other loads can be issued
+// in between.
+template <int HD, int RM, int NTH> struct QRot {
+    static constexpr int half = HD / 2, QI = (RM * HD + NTH - 1) / NTH;
+    float a[QI], b[QI];
+    float2 cs[QI];
+    int R = 0;
+    __device__ __forceinline__ void load(const float* qkv, int ldqkv, int t, int h0, int nh, int pt,
+                                         const float2* rope, int tid) {
+        R = nh;
+        const float* qt = qkv + (size_t)t * ldqkv + (size_t)h0 * HD;
+        const float2* cr = rope + (size_t)pt * half;
+#pragma unroll
+        for (int j = 0; j < QI; ++j) {
+            const int i = tid + j * NTH;
+            if (i < R * HD) {
+                const int r = i / HD, d = i - r * HD, dl = d < half ? d : d - half;
+                a[j] = qt[r * HD + dl];
+                b[j] = qt[r * HD + dl + half];
+                cs[j] = cr[dl];
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float (&Qs)[RM][HD], int tid) const {
+#pragma unroll
+        for (int j = 0; j < QI; ++j) {
+            const int i = tid + j * NTH;
+            if (i < R * HD) {
+                const int r = i / HD, d = i - r * HD;
+                Qs[r][d] = d < half ? rot_lo(a[j], b[j], cs[j]) : rot_hi(a[j], b[j], cs[j]);
+            }
+        }
+    }
+};
+
 // floats per partial row: O[HD], m, l, padded to whole 128-byte lines
 template <int HD> constexpr int part_stride() { return HD + 32; }
 
@@ -623,7 +659,9 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
         kc[o] = v;
         vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
     }
-    rope_q_lds<HD, RM, kWT>(Qs, qkv, ldqkv, t, g * R + r0, RH, pt, rope, tid);
+    // the query heads' loads go out first (rotated into the LDS below)
+    QRot<HD, RM, kWT> qrot;
+    qrot.load(qkv, ldqkv, t, g * R + r0, RH, pt, rope, tid);
     const int CPW = (P + kWW - 1) / kWW;
     const int p0 = w * CPW, p1 = min(P, p0 + CPW);
 
@@ -663,17 +701,16 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
 #pragma unroll
         for (int k = 0; k < DPL; ++k) O[r][k] = 0.f;
     }
-    __syncthreads();  // Qs written
-    for (int b0 = p0; b0 < p1; b0 += 16) {
-        const int nb = min(16, p1 - b0);
-        // V of the pass's positions, this lane's DPL dims, first
-        float vv[16][DPL];
+    // V of a pass's positions (this lane's DPL dims) and its K rows
+    float vv[16][DPL];
+    float4 k[FL];
+    auto load_pass = [&](int b0, int nb) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int p = b0 + j;
             const float* src = p < start ? vg + (size_t)p * HD : qkv + (size_t)(p - start) * ldqkv + vvh;
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) vv[j][k] = 0.f;
+            for (int kk = 0; kk < DPL; ++kk) vv[j][kk] = 0.f;
             if (j < nb) {
                 if constexpr (DPL == 2) {
                     const float2 v2 = *(const float2*)(src + 2 * lane);
@@ -684,8 +721,15 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
                 }
             }
         }
-        float4 k[FL];
         load_k(k, b0 + sp, sp < nb);
+    };
+    // the first pass's loads are in flight while the query heads are rotated
+    if (p0 < p1) load_pass(p0, min(16, p1 - p0));
+    qrot.store(Qs, tid);
+    __syncthreads();  // Qs written
+    for (int b0 = p0; b0 < p1; b0 += 16) {
+        const int nb = min(16, p1 - b0);
+        if (b0 != p0) load_pass(b0, nb);
 #pragma unroll
         for (int r = 0; r < RM; ++r) {
             if (r >= RH) break;
