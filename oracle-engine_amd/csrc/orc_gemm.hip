@@ -811,27 +811,25 @@ template <int NT, int TR>
 __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int lane, const MCtx& m, const h8v (&a)[4],
                                              const h8v (&al)[4], float4 es, f4v (&acc)[TR], f4v (&acl)[TR]) {
     constexpr bool W = mmq_wide<NT>();
-    const int c = lane >> 4, h = u & 1, tb = W ? 4 * c : 4 * (c & 1);
-    float4 s4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if ((W || c < 2) && tb < NT) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s4[i] = *(const float4*)(m.sx + min(tb + i, NT - 1) * m.sx_stride + 4 * u);
-    }
+    const int c = lane >> 4, h = u & 1, r = lane & 15;
+    // A operand of the minimum term (one 16x16x4 fp32 MFMA per tile): lane
+    // (c, r) holds token r's sum of x g over sub-block 4u + c; zero on the
+    // lo rows of stacked launches and past the last token
+    constexpr int NA = W ? NT : (NT < 8 ? NT : 8);
+    const float sxa = r < NA ? m.sx[r * m.sx_stride + 4 * u + c] : 0.f;
     const float esv[4] = {es.x, es.y, es.z, es.w};
 #pragma unroll
     for (int tr = 0; tr < TR; ++tr) {
         f4v D = f4v{0.f, 0.f, 0.f, 0.f}, Dl = D;  // even and odd slices in independent chains
         f4v E = D, El = D;                         // the same for the lo tile (9-16 tokens)
-        float mm[4];
         const float dmin = h2f(M[tr].a.x >> 16);
         uint32_t sc4, mn4;
         q4k_unit_sm(h, M[tr].a.y, M[tr].b.x, M[tr].b.y, sc4, mn4);
+        // B operand: minus dmin m of sub-block 4u + c of the lane's row
+        const float bm = -(dmin * (float)((mn4 >> (8 * c)) & 0xFFu));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t sc = (sc4 >> (8 * i)) & 0xFFu, mn = (mn4 >> (8 * i)) & 0xFFu;
-            mm[i] = dmin * (float)mn;
+            const uint32_t sc = (sc4 >> (8 * i)) & 0xFFu;
             // codes as fp16 1024 + q, then (1024 + q) sc - 1024 sc = sc q with one rounding (exact)
             const u32x2 src = (i >> 1) ? M[tr].d : M[tr].c;
             const int sh = 4 * (i & 1);
@@ -855,24 +853,15 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
         D += Dl;
         if constexpr (W) E += El;
         const float d = h2f(M[tr].a.x & 0xFFFFu);
+        f4v t;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            float a = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
-            a = __builtin_fmaf(-mm[0], s4[e].x, a);
-            a = __builtin_fmaf(-mm[1], s4[e].y, a);
-            a = __builtin_fmaf(-mm[2], s4[e].z, a);
-            a = __builtin_fmaf(-mm[3], s4[e].w, a);
-            acc[tr][e] = a;
-            if constexpr (W) {
-                // the lo rows take the minimum terms with zero sums, as stacked lo rows do
-                float b = __builtin_fmaf(d * esv[e], E[e], acl[tr][e]);
-                b = __builtin_fmaf(-mm[0], 0.f, b);
-                b = __builtin_fmaf(-mm[1], 0.f, b);
-                b = __builtin_fmaf(-mm[2], 0.f, b);
-                b = __builtin_fmaf(-mm[3], 0.f, b);
-                acl[tr][e] = b;
-            }
+            t[e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
+            // the lo tile of 9-16 token launches takes no minimum term
+            if constexpr (W) acl[tr][e] = __builtin_fmaf(d * esv[e], E[e], acl[tr][e]);
         }
+        // acc = t - sum over the unit's four sub-blocks of dmin m sum(x g)
+        acc[tr] = __builtin_amdgcn_mfma_f32_16x16x4f32(sxa, bm, t, 0, 0, 0);
     }
 }
 
