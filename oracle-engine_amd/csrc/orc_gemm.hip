@@ -766,28 +766,29 @@ template <int NT> __device__ __forceinline__ int a_off(int i, int c, int hl, int
 }
 
 // The lane's A entries of a unit (all four slices; lane row r = lane % 16)
-// and the 2^-e of the tokens of its D rows; every LDS read under one
-// branch, all in flight. Up to 8 tokens: row r is the hi half of token r or
-// the lo half of token r - 8, D rows are tokens 4 (c % 2) + i. 9 to 16
-// tokens: a holds the hi and al the lo half of token r, D rows are tokens
-// 4 c + i.
+// and the 2^-e of the tokens of its D rows, all LDS reads in flight. Up to
+// 8 tokens: row r is the hi half of token r or the lo half of token r - 8,
+// D rows are tokens 4 (c % 2) + i. 9 to 16 tokens: a holds the hi and al
+// the lo half of token r, D rows are tokens 4 c + i.
+// Rows of tokens past n_tok read whatever the neighbouring entries hold
+// (always inside the workgroup's LDS: the esc, red and part arrays follow
+// the A entries). An MFMA's D row depends only on the same A row, the hi
+// and lo rows folded together belong to one token, and every epilogue
+// drops rows of tokens >= n_tok, so those values reach no output; reading
+// them unmasked saves zeroing 16 registers per unit.
 template <int NT>
 __device__ __forceinline__ void a_load(int u, int ua, int lane, const MCtx& m, h8v (&a)[4], h8v (&al)[4], float4& es) {
     constexpr bool W = mmq_wide<NT>();
     const int c = lane >> 4, r = lane & 15, t = W ? r : r & 7, tb = W ? 4 * c : 4 * (c & 1);
     u32x4 h[4], l[4];
+    const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + a_off<NT>(0, c, W ? 0 : r >> 3, t);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = l[i] = u32x4{0u, 0u, 0u, 0u};
-    es = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < NT) {
-        const uint8_t* ap = m.abase + (size_t)ua * m.a_stride_u + a_off<NT>(0, c, W ? 0 : r >> 3, t);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            h[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 0, 0));
-            if constexpr (W) l[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 1, 0));
-        }
+    for (int i = 0; i < 4; ++i) {
+        h[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 0, 0));
+        if constexpr (W) l[i] = *(const u32x4*)(ap + a_off<NT>(i, 0, 1, 0));
+        else l[i] = u32x4{0u, 0u, 0u, 0u};
     }
-    if (tb < NT) es = *(const float4*)(m.esc + u * ntp<NT>() + tb);
+    es = *(const float4*)(m.esc + u * ntp<NT>() + tb);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         a[i] = __builtin_bit_cast(h8v, h[i]);
