@@ -805,6 +805,12 @@ template <int TR> __device__ __forceinline__ void fold_lo(f4v (&acc)[TR]) {
         for (int e = 0; e < 4; ++e) acc[tr][e] += __shfl_xor(acc[tr][e], 32, 64);
 }
 
+// D entries e of a lane that can hold a token below n_tok: lane row c holds
+// tokens 4 (c % 2) + e of stacked launches (4 c + e of wide ones), so below
+// 4 tokens entries e >= n_tok belong to no token and are not scaled (they
+// stay zero and reach no output).
+template <int NT> constexpr int kDRows = (!mmq_wide<NT>() && NT < 4) ? NT : 4;
+
 // Q4_K unit of TR tiles with the lane's A entries given: scale-folded codes
 // (slices alternating between two chains), then acc += d 2^-e D, minus, on
 // the hi rows only, the sum over the unit's sub-blocks of dmin m sum(x g).
@@ -854,9 +860,9 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
         D += Dl;
         if constexpr (W) E += El;
         const float d = h2f(M[tr].a.x & 0xFFFFu);
-        f4v t;
+        f4v t = acc[tr];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < kDRows<NT>; ++e) {
             t[e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
             // the lo tile of 9-16 token launches takes no minimum term
             if constexpr (W) acl[tr][e] = __builtin_fmaf(d * esv[e], E[e], acl[tr][e]);
@@ -922,7 +928,7 @@ __device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, con
         if constexpr (W) E += El;
         const float d = h2f(M[tr].e);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < kDRows<NT>; ++e) {
             acc[tr][e] = __builtin_fmaf(d * esv[e], D[e], acc[tr][e]);
             if constexpr (W) acl[tr][e] = __builtin_fmaf(d * esv[e], E[e], acl[tr][e]);
         }
