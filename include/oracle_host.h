@@ -73,6 +73,19 @@ double orch_weight_bytes(const orch_model* m, int logits);
 /* Block the host until all device work of the library has finished. */
 int orch_sync(void);
 
+/* The model's GGUFParser drop-ins on host buffers (model.gguf() in C++):
+ * n_tok = 1: GGUFParser::gemv_q_range(tensor, out, x, j0, j1, n_in) — out[j]
+ * for j in [j0, j1) (core/gguf_parser.cpp:868-911); n_tok > 1 (j0 = 0):
+ * GGUFParser::gemm_q(tensor, out, x, n_tok, j1, n_in) — out[t * j1 + j]
+ * (core/gguf_parser.cpp:919-997). They read the tensor in the layout its HBM
+ * bytes hold after Model::load (orch_gguf_device_type: the GGML type, or
+ * ORC_Q8_0_X8 = 258 for a regrouped Q8_0 matrix). */
+int orch_gguf_device_type(const orch_model* m, const char* tensor);
+int orch_gguf_gemm(orch_model* m, const char* tensor, const float* x, int n_tok, int j0, int j1, float* out);
+/* GGUFParser::dequantize_row (core/gguf_parser.cpp:443-482): row `row` of the
+ * tensor as fp32 into out (shape[0] floats), bit-exact. */
+int orch_gguf_dequant_row(orch_model* m, const char* tensor, int64_t row, float* out);
+
 #ifdef __cplusplus
 }
 #endif

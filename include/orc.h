@@ -98,7 +98,8 @@ int64_t orc_row_bytes(int type, int64_t n_el);
 int orc_q8_0_regroup(void* d_w, int64_t n_blocks8, orc_stream_t stream);
 /* Dequantize n_el contiguous elements to fp32, bit-exact with the reference
  * codecs: fp16/Q4_0/Q8_0/Q4_K/Q6_K (core/gguf_parser.cpp:1002-1154,
- * dequantize_into :420-441). */
+ * dequantize_into :420-441); also ORC_Q8_0_X8 (n_el a multiple of 256 from
+ * the start of a regrouped row), with the values of the Q8_0 blocks it holds. */
 int orc_dequant(int type, const void* d_w, int64_t n_el, float* d_y, orc_stream_t stream);
 /* Embedding gather: y[t][:] = dequant(row ids[t] of an [n_in, n_rows] table);
  * ids outside [0, n_rows) read row 0 (model.cpp:352-358, 549-558 +
@@ -258,8 +259,9 @@ int orc_spec_accept_greedy_at(const int32_t* d_tgt_ids, const int32_t* d_draft_i
  * std::mt19937 is (the reference passes a 64-bit seed that the engine
  * truncates, sampler.cpp:7-8), the parameters of SamplerParams
  * (sampler.hpp:16-22) and the history, initialised with n_hist recorded ids.
- * top_k 0 = all tokens (exact up to 16384 tokens, the 16384 most probable
- * beyond); repeat_last < 2048. */
+ * top_k 0 = all tokens, for vocabularies of at most 16384 tokens: with such
+ * a state, orc_sample / orc_spec_accept_engine / orc_transform_probs on a
+ * larger vocabulary return ORC_E_UNSUPPORTED; repeat_last < 2048. */
 size_t orc_sampler_state_bytes(void);
 int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty, int repeat_last,
                      uint64_t seed, const int32_t* d_hist, int n_hist, orc_stream_t stream);

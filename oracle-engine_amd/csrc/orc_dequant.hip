@@ -25,6 +25,13 @@ __device__ __forceinline__ void dequant32(int type, const uint8_t* w, int64_t g,
             for (int i = 0; i < 32; ++i) out[i] = d * (float)(int8_t)b[2 + i];
             break;
         }
+        case ORC_Q8_0_X8: {  // block g&7 of the 272-byte group g>>3: scale at 2*(g&7), codes at 16+32*(g&7)
+            const uint8_t* grp = w + (g >> 3) * 272;
+            const float d = h2f(ld2(grp + 2 * (g & 7)));
+            const uint8_t* q = grp + 16 + 32 * (g & 7);
+            for (int i = 0; i < 32; ++i) out[i] = d * (float)(int8_t)q[i];
+            break;
+        }
         case ORC_Q4_0: {
             const uint8_t* b = w + g * 18;
             const float d = h2f(ld2(b));
@@ -102,8 +109,9 @@ static bool dq_type_ok(int t) {
 
 extern "C" int orc_dequant(int type, const void* d_w, int64_t n_el, float* d_y, orc_stream_t stream) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (!dq_type_ok(type)) return set_error(ORC_E_UNSUPPORTED, "dequant: unsupported type " + std::to_string(type));
-    const int be = (type == ORC_Q4_K || type == ORC_Q6_K) ? 256 : 32;
+    if (!dq_type_ok(type) && type != ORC_Q8_0_X8)
+        return set_error(ORC_E_UNSUPPORTED, "dequant: unsupported type " + std::to_string(type));
+    const int be = (type == ORC_Q4_K || type == ORC_Q6_K || type == ORC_Q8_0_X8) ? 256 : 32;
     if (n_el <= 0 || n_el % be || !d_w || !d_y) return set_error(ORC_E_INVALID, "dequant: bad size or pointer");
     if ((uintptr_t)d_y & 15) return set_error(ORC_E_INVALID, "dequant: output must be 16-byte aligned");
     const int64_t groups = n_el / 32;

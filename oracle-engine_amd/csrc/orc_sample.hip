@@ -17,8 +17,9 @@
 //    bit patterns order like the values), then the candidates (p >= the k-th
 //    value) are sorted by (p desc, index asc) with a bitonic sort in LDS;
 //    at most 16384 candidates (top_k = 0, "all tokens" in the reference, is
-//    exact for vocabularies up to that size and keeps the 16384 most probable
-//    tokens beyond it);
+//    exact for vocabularies up to that size; the entry points refuse a
+//    larger vocabulary with ORC_E_UNSUPPORTED for a state initialised with
+//    top_k = 0, since the nucleus could then need more candidates);
 //  * top-p cut at cumulative >= top_p, r = u * total with
 //    u = generate_canonical<float, 24>(mt19937) as libstdc++ forms it, then
 //    r -= p_i until r <= 0 (fallback: the first candidate);
@@ -28,6 +29,8 @@
 #include "orc_internal.hpp"
 
 #include <cstring>
+#include <mutex>
+#include <unordered_set>
 
 namespace orc {
 
@@ -659,6 +662,21 @@ __global__ void k_sampler_history(const DevSampler* s, int32_t* out, int cap, in
 
 using namespace orc;
 
+// Host record of the sampler states initialised with top_k = 0 ("all
+// tokens"): their vocabulary must fit the candidate sort (kCandMax). The
+// state itself is device memory the host never reads back.
+static std::mutex g_all_mu;
+static std::unordered_set<const void*> g_all_tokens;
+
+static int check_vocab(const void* d_state, int n_vocab, const char* who) {
+    if (n_vocab <= kCandMax) return ORC_OK;
+    std::lock_guard<std::mutex> lk(g_all_mu);
+    if (g_all_tokens.count(d_state))
+        return set_error(ORC_E_UNSUPPORTED, std::string(who) + ": top_k = 0 (all tokens) supports vocabularies up to " +
+                                                std::to_string(kCandMax) + " tokens");
+    return ORC_OK;
+}
+
 extern "C" size_t orc_sampler_state_bytes(void) { return sizeof(DevSampler); }
 
 extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty,
@@ -668,6 +686,11 @@ extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, i
     if (!d_state || repeat_last < 0 || repeat_last >= kSampHist / 2 || n_hist < 0 || (n_hist && !d_hist) ||
         top_k < 0 || top_k > kCandMax)
         return set_error(ORC_E_INVALID, "sampler_init: bad args (0 <= top_k <= 16384, repeat_last < 2048)");
+    {
+        std::lock_guard<std::mutex> lk(g_all_mu);
+        if (top_k == 0) g_all_tokens.insert(d_state);
+        else g_all_tokens.erase(d_state);
+    }
     hipLaunchKernelGGL(k_sampler_init, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state,
                        (uint32_t)seed, temperature, top_p, repeat_penalty, top_k, repeat_last, d_hist, n_hist);
     ORC_LAUNCH_CHECK();
@@ -677,6 +700,7 @@ extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, i
 extern "C" int orc_sample(void* d_state, float* d_logits, int n_vocab, int32_t* d_out, orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
     if (!d_state || !d_logits || !d_out || n_vocab <= 0) return set_error(ORC_E_INVALID, "sample: bad args");
+    if (int rc = check_vocab(d_state, n_vocab, "sample")) return rc;
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_logits, n_vocab,
                        d_out);
     ORC_LAUNCH_CHECK();
@@ -708,6 +732,7 @@ extern "C" int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, in
     if (!d_state || !d_logits || !d_out || n_vocab <= 0 || ld < n_vocab || n_draft < 0 || (n_draft && !d_draft) ||
         (max_emit < 1 && !d_budget) || (!d_pos) != (!d_next))
         return set_error(ORC_E_INVALID, "accept_engine: bad args");
+    if (int rc = check_vocab(d_state, n_vocab, "accept_engine")) return rc;
     hipLaunchKernelGGL(k_accept_engine, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_logits,
                        ld, n_vocab, d_draft, n_draft, max_emit, d_budget, d_out, d_pos, d_next);
     ORC_LAUNCH_CHECK();
@@ -720,6 +745,7 @@ extern "C" int orc_transform_probs(const void* d_state, float* d_logits, int ld,
     if (!d_state || !d_logits || !d_p || n_vocab <= 0 || rows < 1 || ld < n_vocab || ldp < n_vocab ||
         extra_base < 0 || ((extra_base + rows > 1) && !d_extra))
         return set_error(ORC_E_INVALID, "transform_probs: bad args");
+    if (int rc = check_vocab(d_state, n_vocab, "transform_probs")) return rc;
     hipLaunchKernelGGL(k_transform, dim3(rows), dim3(kST), 0, resolve_stream(s), (const DevSampler*)d_state,
                        d_logits, ld, n_vocab, d_extra, extra_base, d_p, ldp);
     ORC_LAUNCH_CHECK();

@@ -115,7 +115,7 @@ bool GGUFParser::load(const std::string& path) {
         }
     }
     void* d = nullptr;
-    if (orc_upload(map_ + data_start_, fsize_ - data_start_, &d) != 0) {
+    if (orc_init(0) != 0 || orc_upload(map_ + data_start_, fsize_ - data_start_, &d) != 0) {
         std::fprintf(stderr, "[GGUFParser] upload failed: %s\n", orc_last_error());
         close();
         return false;
@@ -127,6 +127,13 @@ bool GGUFParser::load(const std::string& path) {
 void GGUFParser::close() {
     if (d_data_) orc_free(d_data_);
     d_data_ = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(scr_mu_);
+        if (d_scr_) orc_free(d_scr_);
+        d_scr_ = nullptr;
+        scr_cap_ = 0;
+    }
+    dev_type_.clear();
     if (map_) munmap((void*)map_, fsize_);
     map_ = nullptr;
     if (fd_ >= 0) ::close(fd_);
@@ -169,7 +176,18 @@ bool GGUFParser::parse() {
         std::fprintf(stderr, "[GGUFParser] truncated or corrupt header\n");
         return false;
     }
-    data_start_ = ((uint64_t)(c.p - map_) + 31) & ~uint64_t(31);
+    // The data section starts at the next multiple of general.alignment (32
+    // when absent, the only value the reference supports: gguf_parser.cpp:30,
+    // 196, where the key is ignored; for files that declare 32 or nothing the
+    // two readers agree).
+    uint64_t align = 32;
+    auto al = meta_.find("general.alignment");
+    if (al != meta_.end() && al->second.kind == MetaValue::U32) align = al->second.u32;
+    if (align == 0 || (align & (align - 1)) || align > 65536) {
+        std::fprintf(stderr, "[GGUFParser] general.alignment %llu is not a power of two\n", (unsigned long long)align);
+        return false;
+    }
+    data_start_ = ((uint64_t)(c.p - map_) + align - 1) & ~(align - 1);
     if (data_start_ > fsize_) return false;
     return true;
 }
@@ -242,15 +260,36 @@ std::vector<std::string> GGUFParser::tensor_names() const {
     return v;
 }
 
+// ── device layout ────────────────────────────────────────────────────────────
+int GGUFParser::device_type(const std::string& name) const {
+    auto it = tensors_.find(name);
+    if (it == tensors_.end()) return -1;
+    auto d = dev_type_.find(name);
+    return d != dev_type_.end() ? d->second : (int)it->second.type;
+}
+
+bool GGUFParser::regroup_q8_0(const std::string& name) {
+    auto it = tensors_.find(name);
+    if (it == tensors_.end() || !d_data_ || it->second.type != GGMLType::Q8_0 || dev_type_.count(name)) return false;
+    const TensorInfo& ti = it->second;
+    if (ti.shape.empty() || ti.shape[0] % 256 || ((uintptr_t)tensor_device(name) & 15)) return false;
+    if (orc_q8_0_regroup((void*)tensor_device(name), (int64_t)(ti.n_elems() / 256), nullptr) != 0) return false;
+    dev_type_[name] = ORC_Q8_0_X8;
+    return true;
+}
+
 // ── host-pointer drop-ins, executed on the device ────────────────────────────
-namespace {
-struct DevBuf {
-    void* p = nullptr;
-    explicit DevBuf(size_t n) { orc_malloc(&p, n); }
-    ~DevBuf() { orc_free(p); }
-};
-int type_id(GGMLType t) { return (int)t; }
-}  // namespace
+void* GGUFParser::scratch(size_t bytes) const {
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes > scr_cap_) {
+        if (d_scr_) orc_free(d_scr_);
+        d_scr_ = nullptr;
+        scr_cap_ = 0;
+        if (orc_malloc(&d_scr_, bytes) != 0) return nullptr;
+        scr_cap_ = bytes;
+    }
+    return d_scr_;
+}
 
 void GGUFParser::dequantize_into(const std::string& name, std::vector<float>& out) const {
     auto it = tensors_.find(name);
@@ -264,9 +303,10 @@ void GGUFParser::dequantize_into(const std::string& name, std::vector<float>& ou
         for (uint64_t i = 0; i < n; ++i) { uint32_t f = (uint32_t)s[i] << 16; std::memcpy(&out[i], &f, 4); }
         return;
     }
-    DevBuf y(n * 4);
-    if (orc_dequant(type_id(ti.type), tensor_device(name), (int64_t)n, (float*)y.p, nullptr) == 0)
-        orc_memcpy_d2h(out.data(), y.p, n * 4, nullptr);
+    std::lock_guard<std::mutex> lk(scr_mu_);
+    void* y = scratch(n * 4);
+    if (y && orc_dequant(device_type(name), tensor_device(name), (int64_t)n, (float*)y, nullptr) == 0)
+        orc_memcpy_d2h(out.data(), y, n * 4, nullptr);
 }
 
 std::vector<float> GGUFParser::dequantize(const std::string& name) const {
@@ -288,25 +328,34 @@ void GGUFParser::dequantize_row(const std::string& name, int64_t row, float* out
         for (uint64_t i = 0; i < cols; ++i) { uint32_t f = (uint32_t)s[i] << 16; std::memcpy(&out[i], &f, 4); }
         return;
     }
-    DevBuf y(cols * 4);
-    if (orc_dequant(type_id(ti.type), tensor_device(name) + row * rb, (int64_t)cols, (float*)y.p, nullptr) == 0)
-        orc_memcpy_d2h(out, y.p, cols * 4, nullptr);
+    std::lock_guard<std::mutex> lk(scr_mu_);
+    void* y = scratch(cols * 4);
+    // a row of a regrouped matrix is as long as the file's row and starts a group
+    if (y && orc_dequant(device_type(name), tensor_device(name) + row * rb, (int64_t)cols, (float*)y, nullptr) == 0)
+        orc_memcpy_d2h(out, y, cols * 4, nullptr);
 }
 
-bool GGUFParser::gemm_dev(const TensorInfo& ti, float* out, const float* x, int n_tok, int j0, int j1,
-                          int n_in) const {
-    const int t = type_id(ti.type);
+bool GGUFParser::gemm_dev(const std::string& name, const TensorInfo& ti, float* out, const float* x, int n_tok,
+                          int j0, int j1, int n_in) const {
+    const int t = (int)ti.type;
     if (t != ORC_Q4_0 && t != ORC_Q8_0 && t != ORC_Q4_K && t != ORC_Q6_K) return false;  // reference: false too
     const int n_out = j1 - j0;
     if (n_out <= 0) return true;
-    const int64_t rb = orc_row_bytes(t, n_in);
-    DevBuf dx((size_t)n_tok * n_in * 4), dy((size_t)n_tok * n_out * 4);
-    if (orc_memcpy_h2d(dx.p, x, (size_t)n_tok * n_in * 4, nullptr)) return false;
-    if (orc_gemm(t, tensor_device(ti.name) + (size_t)j0 * rb, n_tok, n_out, n_in, (const float*)dx.p, n_in,
-                 (float*)dy.p, n_out, nullptr))
+    if (n_tok <= 0 || n_in <= 0 || ti.shape.empty() || (uint64_t)n_in != ti.shape[0] || j0 < 0 ||
+        (ti.shape.size() > 1 && (uint64_t)j1 > ti.shape[1]))
+        return false;
+    const int64_t rb = orc_row_bytes(t, n_in);  // a regrouped row has the same length
+    const size_t xb = ((size_t)n_tok * n_in * 4 + 255) & ~size_t(255), yb = (size_t)n_tok * n_out * 4;
+    std::lock_guard<std::mutex> lk(scr_mu_);
+    uint8_t* s = (uint8_t*)scratch(xb + yb);
+    if (!s) return false;
+    float *dx = (float*)s, *dy = (float*)(s + xb);
+    if (orc_memcpy_h2d(dx, x, (size_t)n_tok * n_in * 4, nullptr)) return false;
+    if (orc_gemm(device_type(name), tensor_device(name) + (size_t)j0 * rb, n_tok, n_out, n_in, dx, n_in, dy, n_out,
+                 nullptr))
         return false;
     // gemv_q_range writes out[j0..j1); gemm_q (j0 = 0) writes out[t * n_out + j]
-    return orc_memcpy_d2h(out + j0, dy.p, (size_t)n_tok * n_out * 4, nullptr) == 0;
+    return orc_memcpy_d2h(out + j0, dy, yb, nullptr) == 0;
 }
 
 bool GGUFParser::gemv_q(const std::string& name, float* out, const float* x, int n_out, int n_in) const {
@@ -316,12 +365,43 @@ bool GGUFParser::gemv_q(const std::string& name, float* out, const float* x, int
 bool GGUFParser::gemv_q_range(const std::string& name, float* out, const float* x, int j0, int j1, int n_in) const {
     auto it = tensors_.find(name);
     if (it == tensors_.end()) return false;
-    return gemm_dev(it->second, out, x, 1, j0, j1, n_in);
+    return gemm_dev(name, it->second, out, x, 1, j0, j1, n_in);
 }
 
 bool GGUFParser::gemm_q(const std::string& name, float* out, const float* x, int n_tokens, int n_out,
                         int n_in) const {
     auto it = tensors_.find(name);
     if (it == tensors_.end()) return false;
-    return gemm_dev(it->second, out, x, n_tokens, 0, n_out, n_in);
+    return gemm_dev(name, it->second, out, x, n_tokens, 0, n_out, n_in);
+}
+
+// ── static test hooks: one-shot device buffers (test code, not a hot path) ───
+void GGUFParser::dq_hook(int type, const uint8_t* s, uint64_t n, float* out) {
+    if (!s || !out || !n || orc_init(0) != 0) return;
+    const int64_t in_bytes = orc_row_bytes(type, (int64_t)n);
+    if (in_bytes <= 0) return;
+    void *d_in = nullptr, *d_out = nullptr;
+    if (orc_malloc(&d_in, (size_t)in_bytes) == 0 && orc_malloc(&d_out, n * 4) == 0 &&
+        orc_memcpy_h2d(d_in, s, (size_t)in_bytes, nullptr) == 0 &&
+        orc_dequant(type, d_in, (int64_t)n, (float*)d_out, nullptr) == 0)
+        orc_memcpy_d2h(out, d_out, n * 4, nullptr);
+    orc_free(d_in);
+    orc_free(d_out);
+}
+
+float GGUFParser::dot_hook(int type, const uint8_t* row, int n_cols, const float* x) {
+    if (!row || !x || n_cols <= 0 || orc_init(0) != 0) return 0.f;
+    const int64_t rb = orc_row_bytes(type, n_cols);
+    if (rb <= 0) return 0.f;
+    void *d_w = nullptr, *d_x = nullptr, *d_y = nullptr;
+    float y = 0.f;
+    if (orc_malloc(&d_w, (size_t)rb) == 0 && orc_malloc(&d_x, (size_t)n_cols * 4) == 0 && orc_malloc(&d_y, 4) == 0 &&
+        orc_memcpy_h2d(d_w, row, (size_t)rb, nullptr) == 0 &&
+        orc_memcpy_h2d(d_x, x, (size_t)n_cols * 4, nullptr) == 0 &&
+        orc_gemm(type, d_w, 1, 1, n_cols, (const float*)d_x, n_cols, (float*)d_y, 1, nullptr) == 0)
+        orc_memcpy_d2h(&y, d_y, 4, nullptr);
+    orc_free(d_w);
+    orc_free(d_x);
+    orc_free(d_y);
+    return y;
 }

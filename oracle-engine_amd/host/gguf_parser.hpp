@@ -8,10 +8,15 @@
 // (no dequant-to-float expansion). gemv_q / gemv_q_range / gemm_q /
 // dequantize_row keep their host-pointer signatures for drop-in callers and
 // run on the GPU; the model uses the device pointers directly.
+//
+// A tensor's HBM bytes may be re-laid out once after load (regroup_q8_0); the
+// parser records each tensor's device layout and every device drop-in reads
+// the bytes in that layout, so results stay those of the file's tensor.
 #pragma once
 #include "gguf_types.hpp"
 
 #include <cstdint>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -76,7 +81,16 @@ public:
     const uint8_t* tensor_device(const std::string& name) const;  // HBM bytes
     std::vector<std::string> tensor_names() const;
 
-    // Host-pointer drop-ins of the reference kernels (run on the GPU).
+    // Layout of the tensor's HBM bytes as an orc.h type id: the GGML type of
+    // the file, or ORC_Q8_0_X8 after regroup_q8_0; -1 for an unknown name.
+    int device_type(const std::string& name) const;
+    // Rewrites a Q8_0 matrix's HBM bytes in the aligned ORC_Q8_0_X8 layout
+    // (same bytes per row, same values; rows of a multiple of 256 values,
+    // 16-byte aligned data). Once per tensor; false if not eligible.
+    bool regroup_q8_0(const std::string& name);
+
+    // Host-pointer drop-ins of the reference kernels (run on the GPU; host
+    // buffers in and out, device scratch reused across calls; thread-safe).
     std::vector<float> dequantize(const std::string& name) const;
     void dequantize_into(const std::string& name, std::vector<float>& out) const;
     void dequantize_row(const std::string& name, int64_t row, float* out) const;
@@ -89,6 +103,18 @@ public:
     uint64_t n_meta() const { return meta_.size(); }
     uint64_t file_size() const { return (uint64_t)fsize_; }
     uint64_t data_bytes() const { return fsize_ - data_start_; }
+    // core/gguf_parser.hpp:125: true when the weights were not preloaded and
+    // are served from the file mapping (the Engine then skips its warmup).
+    // Here the data section always lives in HBM once load() succeeds.
+    bool is_mmap_only() const { return d_data_ == nullptr; }
+
+    // Test hooks on synthetic blocks (core/gguf_parser.hpp:128-132), run by
+    // the device codecs / GEMV on host buffers.
+    static void test_dq_q6_k(const uint8_t* s, uint64_t n, float* out) { dq_hook(14, s, n, out); }
+    static void test_dq_q4_k(const uint8_t* s, uint64_t n, float* out) { dq_hook(12, s, n, out); }
+    static void test_dq_q4_0(const uint8_t* s, uint64_t n, float* out) { dq_hook(2, s, n, out); }
+    static float test_dot_q6k(const uint8_t* row, int n_cols, const float* x) { return dot_hook(14, row, n_cols, x); }
+    static float test_dot_q4_0(const uint8_t* row, int n_cols, const float* x) { return dot_hook(2, row, n_cols, x); }
 
 private:
     const uint8_t* map_ = nullptr;
@@ -100,7 +126,15 @@ private:
     uint8_t* d_data_ = nullptr;  // HBM copy of the data section
     std::unordered_map<std::string, MetaValue> meta_;
     std::unordered_map<std::string, TensorInfo> tensors_;
+    std::unordered_map<std::string, int> dev_type_;  // tensors whose HBM layout differs from the file's
+    mutable std::mutex scr_mu_;                      // guards the drop-ins' device scratch
+    mutable void* d_scr_ = nullptr;
+    mutable size_t scr_cap_ = 0;
 
     bool parse();
-    bool gemm_dev(const TensorInfo& ti, float* out, const float* x, int n_tokens, int j0, int j1, int n_in) const;
+    bool gemm_dev(const std::string& name, const TensorInfo& ti, float* out, const float* x, int n_tokens, int j0,
+                  int j1, int n_in) const;
+    void* scratch(size_t bytes) const;  // caller holds scr_mu_
+    static void dq_hook(int type, const uint8_t* s, uint64_t n, float* out);
+    static float dot_hook(int type, const uint8_t* row, int n_cols, const float* x);
 };

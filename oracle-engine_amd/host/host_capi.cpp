@@ -15,12 +15,17 @@ struct orch_model {
 
 namespace {
 thread_local std::string g_load_err;
+// Device scratch and captured graphs of the decode loops: one session per
+// calling thread (created on its first decode call, released when the thread
+// ends), so threads that decode different models never share them. One
+// model must still not be used by two threads at once (its activations and
+// KV cache are single-stream state, as the reference's Model is).
 DecodeSession& session() {
-    static DecodeSession s;  // device scratch for the decode loops, created on first use
+    thread_local DecodeSession s;
     return s;
 }
 int fail(orch_model* h, int rc) {
-    h->err = h->m.last_error()[0] ? h->m.last_error() : orc_last_error();
+    h->err = session().error()[0] ? session().error() : h->m.last_error()[0] ? h->m.last_error() : orc_last_error();
     return rc ? rc : -1;
 }
 }  // namespace
@@ -73,9 +78,11 @@ extern "C" int orch_forward_batch(orch_model* h, const int32_t* toks, int n, int
 }
 
 extern "C" int orch_greedy(orch_model* h, const int32_t* prompt, int np, int n_gen, int32_t* out, int prefill) {
+    if (!h || !prompt || !out) return -1;
+    session().clear_error();
     if (prefill) {
         h->m.reset();
-        session().prefill(h->m, prompt, np);
+        if (int rc = session().prefill(h->m, prompt, np)) return fail(h, rc);
     }
     int rc = session().greedy(h->m, prompt, np, n_gen, out);
     return rc < 0 ? fail(h, rc) : rc;
@@ -83,11 +90,13 @@ extern "C" int orch_greedy(orch_model* h, const int32_t* prompt, int np, int n_g
 
 extern "C" int orch_spec_greedy(orch_model* t, orch_model* d, const int32_t* prompt, int np, int n_gen, int k,
                                 int32_t* out, int64_t* stats, int prefill) {
+    if (!t || !d || !prompt || !out) return -1;
+    session().clear_error();
     if (prefill) {
         t->m.reset();
         d->m.reset();
-        session().prefill(t->m, prompt, np);
-        session().prefill(d->m, prompt, np);
+        if (int rc = session().prefill(t->m, prompt, np)) return fail(t, rc);
+        if (int rc = session().prefill(d->m, prompt, np)) return fail(t, rc);
     }
     SpecStats st;
     int rc = session().spec_greedy(t->m, d->m, prompt, np, n_gen, k, out, &st);
@@ -127,6 +136,7 @@ extern "C" int orch_spec_engine(orch_model* t, orch_model* d, const int32_t* pro
                                 int64_t* stats) {
     if (!t || !d || !prompt || !out || !sampler || !isampler) return -1;
     SpecStats st;
+    session().clear_error();
     const int rc = session().spec_engine(t->m, d->m, prompt, np, n_gen, k, sampler_config(sampler, isampler, seed),
                                          out, &st);
     if (rc < 0) return fail(t, rc);
@@ -143,6 +153,7 @@ extern "C" int orch_spec_sampled(orch_model* t, orch_model* d, const int32_t* pr
                                  int64_t* stats) {
     if (!t || !d || !prompt || !out || !sampler || !isampler) return -1;
     SpecStats st;
+    session().clear_error();
     const int rc = session().spec_sampled(t->m, d->m, prompt, np, n_gen, k, sampler_config(sampler, isampler, seed),
                                           out, &st);
     if (rc < 0) return fail(t, rc);
@@ -152,4 +163,33 @@ extern "C" int orch_spec_sampled(orch_model* t, orch_model* d, const int32_t* pr
         stats[2] = st.passes;
     }
     return rc;
+}
+
+// ── GGUFParser drop-ins of a loaded model (tests of the parser API) ─────────
+extern "C" int orch_gguf_device_type(const orch_model* h, const char* tensor) {
+    return h && tensor ? h->m.gguf().device_type(tensor) : -1;
+}
+
+extern "C" int orch_gguf_gemm(orch_model* h, const char* tensor, const float* x, int n_tok, int j0, int j1,
+                              float* out) {
+    if (!h || !tensor || !x || !out || n_tok < 1) return -1;
+    const GGUFParser& g = h->m.gguf();
+    if (!g.has_tensor(tensor) || g.tensor_info(tensor).shape.size() != 2) {
+        h->err = std::string("no 2-D tensor ") + tensor;
+        return -1;
+    }
+    const int n_in = (int)g.tensor_info(tensor).shape[0];
+    const bool ok = n_tok == 1 ? g.gemv_q_range(tensor, out, x, j0, j1, n_in)
+                  : j0 == 0 ? g.gemm_q(tensor, out, x, n_tok, j1, n_in) : false;
+    if (!ok) {
+        h->err = std::string("gemv_q / gemm_q failed on ") + tensor + ": " + orc_last_error();
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" int orch_gguf_dequant_row(orch_model* h, const char* tensor, int64_t row, float* out) {
+    if (!h || !tensor || !out || !h->m.gguf().has_tensor(tensor)) return -1;
+    h->m.gguf().dequantize_row(tensor, row, out);
+    return 0;
 }

@@ -110,15 +110,24 @@ bool Model::load(const std::string& path, int ctx_len) {
 
     // Q8_0 matrices whose rows hold a multiple of 256 values are regrouped
     // once into the aligned ORC_Q8_0_X8 layout (same bytes, same results);
-    // the token embedding keeps the GGUF layout for the row gather
+    // the token embedding keeps the GGUF layout for the row gather. The
+    // parser records the new layout, so its own drop-ins read it correctly.
     {
-        std::vector<Mat*> ms{&head_};
-        for (Layer& L : layers_)
-            for (Mat* m : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down}) ms.push_back(m);
-        for (Mat* m : ms) {
+        std::vector<std::pair<Mat*, std::string>> ms{{&head_, "output.weight"}};
+        for (uint32_t l = 0; l < cfg.n_layers; ++l) {
+            Layer& L = layers_[l];
+            const std::string b = "blk." + std::to_string(l) + ".";
+            for (auto mn : {std::make_pair(&L.q, "attn_q"), std::make_pair(&L.k, "attn_k"),
+                            std::make_pair(&L.v, "attn_v"), std::make_pair(&L.o, "attn_output"),
+                            std::make_pair(&L.gate, "ffn_gate"), std::make_pair(&L.up, "ffn_up"),
+                            std::make_pair(&L.down, "ffn_down")})
+                ms.push_back({mn.first, b + mn.second + ".weight"});
+        }
+        for (auto& mn : ms) {
+            Mat* m = mn.first;
             if (m->type != ORC_Q8_0 || m->n_in % 256 || m->d == embd_.d || ((uintptr_t)m->d & 15)) continue;
-            if (orc_q8_0_regroup((void*)m->d, (int64_t)m->n_out * (m->n_in / 256), nullptr))
-                return fail(std::string("q8_0 regroup: ") + orc_last_error());
+            if (!gguf_.regroup_q8_0(mn.second))
+                return fail("q8_0 regroup of " + mn.second + ": " + orc_last_error());
             m->type = ORC_Q8_0_X8;
         }
         orc_stream_sync(nullptr);

@@ -120,26 +120,31 @@ int DecodeSession::greedy_graphed(Model& m, int pos, int32_t first, int n_gen, i
 }
 
 // The speculative-greedy loop (benchmark/bench_engine.cpp:310-356). A round
-// at position pos drafts ndt = min(k, ctx - 1 - pos) tokens, verifies the
-// ndt + 1 inputs in one target pass and emits the accepted drafts, then the
-// mismatch, or, when every draft was accepted and pos + ndt + 1 < ctx - 1,
-// the bonus token (and refills the draft's KV at pos + ndt); the loop runs
-// while pos < ctx - 1. Rounds with ndt = k replay one captured graph (k draft
-// steps at *d_pos + i, the (k+1)-token verify at *d_pos, acceptance, which
-// advances *d_pos and writes the next input into d_vin[0]; a second graph
-// refills the draft); the shorter rounds at the end of the context run from
-// the host at host positions.
+// at position pos drafts ndt = min(k, dctx - 1 - pos) tokens (the draft's
+// context), verifies nver = min(ndt + 1, tctx - pos) inputs in one target
+// pass (the target's context) and compares the first min(ndt, nver) drafts;
+// it emits the accepted drafts, then the mismatch, or, when every draft was
+// accepted, the verify pass held a bonus row (nver = ndt + 1) and
+// pos + ndt + 1 < tctx - 1, the bonus token (and refills the draft's KV at
+// pos + ndt); the loop runs while pos < tctx - 1. Rounds with ndt = k and
+// nver = k + 1 replay one captured graph (k draft steps at *d_pos + i, the
+// (k+1)-token verify at *d_pos, acceptance, which advances *d_pos and writes
+// the next input into d_vin[0]; a second graph refills the draft); the
+// shorter rounds at the end of a context run from the host at host
+// positions.
 int DecodeSession::spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, int n_gen, int k, int32_t* out,
                                SpecStats& S) {
-    const int tctx = (int)tgt.cfg.ctx_len, ctx = (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len);
+    const int tctx = (int)tgt.cfg.ctx_len, dctx = (int)dft.cfg.ctx_len, ctx = std::min(tctx, dctx);
     const int run_lim = graph_limit(pos + n_gen + k + 2, ctx);
     std::vector<int32_t> h(k + 3), ids(k + 2);
     bool dev_state = false;  // *d_pos / d_vin[0] hold pos / next
     int ng = 0;
     while (ng < n_gen && pos < tctx - 1) {
-        const int ndt = std::min(k, ctx - 1 - pos);
+        const int ndt = std::min(k, dctx - 1 - pos);
         if (ndt < 1) break;
-        const bool graphed = graphs_ && ndt == k;
+        const int nver = std::min(ndt + 1, tctx - pos);
+        const int ncmp = std::min(ndt, nver);
+        const bool graphed = graphs_ && ndt == k && nver == k + 1;
         Captured* c = nullptr;
         int a;
         const int32_t* em;  // the round's target argmaxes from the first emitted token on
@@ -179,12 +184,12 @@ int DecodeSession::spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, in
             // (a) ndt greedy draft proposals; draft step i writes d_i into d_vin[i+1]
             for (int i = 0; i < ndt; ++i)
                 if (int rc = dft.forward_dev(d_vin_ + i, 1, pos + i, true, d_vin_ + i + 1)) return rc;
-            // (b) one (ndt+1)-token verify pass of the target over [next, d0 .. d_{ndt-1}]
-            if (int rc = tgt.forward_dev(d_vin_, ndt + 1, pos, true, d_tgt_)) return rc;
-            // (c) acceptance on the device; ids and count to the host
-            if (int rc = orc_spec_accept_greedy(d_tgt_, d_vin_ + 1, ndt, d_acc_, nullptr)) return rc;
+            // (b) one nver-token verify pass of the target over [next, d0 .. d_{nver-2}]
+            if (int rc = tgt.forward_dev(d_vin_, nver, pos, true, d_tgt_)) return rc;
+            // (c) acceptance of the first ncmp drafts on the device; ids and count to the host
+            if (int rc = orc_spec_accept_greedy(d_tgt_, d_vin_ + 1, ncmp, d_acc_, nullptr)) return rc;
             int32_t acc[2];
-            if (int rc = orc_memcpy_d2h(ids.data(), d_tgt_, (size_t)(ndt + 1) * 4, nullptr)) return rc;
+            if (int rc = orc_memcpy_d2h(ids.data(), d_tgt_, (size_t)nver * 4, nullptr)) return rc;
             if (int rc = orc_memcpy_d2h(acc, d_acc_, 8, nullptr)) return rc;
             a = acc[0];
             em = ids.data();
@@ -192,7 +197,7 @@ int DecodeSession::spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, in
         S.proposed += ndt;
         S.passes++;
         S.rounds++;
-        // em[0 .. a-1] are the accepted drafts, em[a] the mismatch or the bonus
+        // em[0 .. a-1] are the accepted drafts, em[a] the mismatch or (a = ndt < nver) the bonus
         bool stop = false;
         for (int i = 0; i < a && !stop; ++i) {
             out[ng++] = em[i];
@@ -200,10 +205,10 @@ int DecodeSession::spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, in
             stop = ng >= n_gen;
         }
         if (!stop) {
-            if (a < ndt) {
+            if (a < ncmp) {
                 out[ng++] = em[a];
                 next = em[a];
-            } else if (pos + ndt + 1 < tctx - 1) {
+            } else if (ndt < nver && pos + ndt + 1 < tctx - 1) {
                 out[ng++] = em[ndt];
                 next = em[ndt];
                 // every proposal accepted: the draft still lacks d_{ndt-1} at pos + ndt
@@ -224,17 +229,22 @@ int DecodeSession::spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, in
 }
 
 int DecodeSession::prefill(Model& m, const int32_t* prompt, int n_prompt) {
+    if (n_prompt < 1 || !prompt) return invalid("empty prompt");
+    if (n_prompt > (int)m.cfg.ctx_len)
+        return invalid("prompt of " + std::to_string(n_prompt) + " tokens does not fit the " +
+                       std::to_string(m.cfg.ctx_len) + "-position context");
     if (n_prompt < 2) return 0;
     m.forward_prefill(prompt, n_prompt - 1, 0, nullptr);
+    if (m.last_error()[0]) return invalid(std::string("prefill failed: ") + m.last_error());
     return 0;
 }
 
 // The argmax of step s is written straight into the input slot of step s+1,
 // so the whole chain is enqueued without a host round trip.
 int DecodeSession::greedy(Model& m, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out) {
-    if (n_gen > max_tokens_ || n_prompt < 1) return ORC_E_INVALID;
+    if (n_gen > max_tokens_ || n_prompt < 1) return invalid("greedy: bad prompt or more tokens than the session holds");
     int pos = n_prompt - 1;
-    if (pos + n_gen > (int)m.cfg.ctx_len) return ORC_E_INVALID;
+    if (pos + n_gen > (int)m.cfg.ctx_len) return invalid("greedy: prompt + generated tokens exceed the context");
     int32_t first = prompt[n_prompt - 1];
     if (first < 0 || first >= (int32_t)m.cfg.n_vocab) first = 0;
     if (graphs_) return greedy_graphed(m, pos, first, n_gen, out);
@@ -247,8 +257,9 @@ int DecodeSession::greedy(Model& m, const int32_t* prompt, int n_prompt, int n_g
 
 int DecodeSession::spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                                int32_t* out, SpecStats* st) {
-    if (k < 1 || k > max_k_ || n_prompt < 1) return ORC_E_INVALID;
-    if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return ORC_E_INVALID;  // bench_engine.cpp:290-293
+    if (k < 1 || k > max_k_ || n_prompt < 1) return invalid("spec_greedy: bad k or prompt");
+    if (dft.cfg.n_vocab != tgt.cfg.n_vocab)  // bench_engine.cpp:290-293
+        return invalid("spec_greedy: draft and target vocabularies differ");
     SpecStats local;
     SpecStats& S = st ? *st : local;
     const int pos = n_prompt - 1;
@@ -263,6 +274,8 @@ int DecodeSession::spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, in
 int DecodeSession::begin_sampled(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, const SamplerConfig& sc,
                                  std::vector<int32_t>& ids) {
     const int V = (int)tgt.cfg.n_vocab;
+    if (n_prompt > (int)std::min(tgt.cfg.ctx_len, dft.cfg.ctx_len))
+        return invalid("prompt of " + std::to_string(n_prompt) + " tokens does not fit the context");
     ids.assign(prompt, prompt + n_prompt);
     for (auto& t : ids)
         if (t < 0 || t >= V) t = 0;
@@ -270,7 +283,9 @@ int DecodeSession::begin_sampled(Model& tgt, Model& dft, const int32_t* prompt, 
     dft.reset();
     if (n_prompt > 1) {
         tgt.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
+        if (tgt.last_error()[0]) return invalid(std::string("target prefill failed: ") + tgt.last_error());
         dft.forward_prefill(ids.data(), n_prompt - 1, 0, nullptr);
+        if (dft.last_error()[0]) return invalid(std::string("draft prefill failed: ") + dft.last_error());
     }
     int32_t* d_ph = nullptr;
     if (n_prompt > 1) {
@@ -289,8 +304,12 @@ int DecodeSession::begin_sampled(Model& tgt, Model& dft, const int32_t* prompt, 
 
 int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                                const SamplerConfig& sc, int32_t* out, SpecStats* st) {
-    if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return ORC_E_INVALID;
-    if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return ORC_E_INVALID;
+    if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return invalid("spec_engine: bad k, prompt or length");
+    if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return invalid("spec_engine: draft and target vocabularies differ");
+    // engine.cpp:155-160 lets a draft of a longer context propose tokens the
+    // target can no longer verify; this loop supports draft contexts up to
+    // the target's
+    if (dft.cfg.ctx_len > tgt.cfg.ctx_len) return invalid("spec_engine: draft context longer than the target's");
     SpecStats local;
     SpecStats& S = st ? *st : local;
     const int V = (int)tgt.cfg.n_vocab;
@@ -396,8 +415,8 @@ int DecodeSession::sampled_round(Model& tgt, Model& dft, int k, int V) {
 
 int DecodeSession::spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                                 const SamplerConfig& sc, int32_t* out, SpecStats* st) {
-    if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return ORC_E_INVALID;
-    if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return ORC_E_INVALID;
+    if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return invalid("spec_sampled: bad k, prompt or length");
+    if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return invalid("spec_sampled: draft and target vocabularies differ");
     SpecStats local;
     SpecStats& S = st ? *st : local;
     const int V = (int)tgt.cfg.n_vocab;

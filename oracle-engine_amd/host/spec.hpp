@@ -8,6 +8,7 @@
 #include "model.hpp"
 
 #include <cstdint>
+#include <string>
 #include <vector>
 
 struct SpecStats {
@@ -45,12 +46,20 @@ public:
         }
     }
     bool graphs() const { return graphs_; }
+    // Message of the last argument error a loop reported ("" if none).
+    const char* error() const { return err_.c_str(); }
+    void clear_error() { err_.clear(); }
 
     // Batched prefill of prompt[0 .. n_prompt-2] into the model's KV cache.
+    // ORC_E_INVALID when the prompt does not leave its last token a position
+    // inside the context (n_prompt > ctx_len) or the pass failed.
     int prefill(Model& m, const int32_t* prompt, int n_prompt);
     // n_gen greedy tokens after a prefilled prompt; returns tokens written or <0.
     int greedy(Model& m, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out);
     // Speculative greedy with draft length k after both models are prefilled.
+    // The draft's context bounds the proposals and the target's the verify
+    // width (bench_engine.cpp:313-323), so models of different context
+    // lengths end a run as the reference harness does.
     int spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k, int32_t* out,
                     SpecStats* st);
     // The Engine's stochastic speculative loop (core/engine.cpp:100-240):
@@ -58,6 +67,7 @@ public:
     // in the sampler history), greedy draft proposals, target samples with the
     // device sampler at every verify position, accept while equal.
     // stats: accepted, proposed, target forwards of the reference loop.
+    // The draft's context may not exceed the target's (ORC_E_INVALID).
     int spec_engine(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                     const SamplerConfig& sc, int32_t* out, SpecStats* st);
 
@@ -74,6 +84,11 @@ public:
 private:
     int max_tokens_, max_k_;
     bool graphs_ = true;
+    std::string err_;
+    int invalid(const std::string& m) {
+        err_ = m;
+        return ORC_E_INVALID;
+    }
     int32_t* d_hist_ = nullptr;  // greedy token chain
     int32_t* d_vin_ = nullptr;   // [next, d0 .. d_{k-1}]
     int32_t* d_tgt_ = nullptr;   // verify argmax ids

@@ -200,6 +200,9 @@ HOST_ABI = [
     ("orch_set_graphs", C.c_int, [C.c_int]),
     ("orch_weight_bytes", C.c_double, [_vp, C.c_int]),
     ("orch_sync", C.c_int, []),
+    ("orch_gguf_device_type", C.c_int, [_vp, C.c_char_p]),
+    ("orch_gguf_gemm", C.c_int, [_vp, C.c_char_p, _fp, C.c_int, C.c_int, C.c_int, _fp]),
+    ("orch_gguf_dequant_row", C.c_int, [_vp, C.c_char_p, C.c_int64, _fp]),
 ]
 
 _host = None
@@ -314,3 +317,27 @@ class Model:
 
     def weight_bytes(self, logits=True):
         return self.L.orch_weight_bytes(self.h, int(logits))
+
+    # GGUFParser drop-ins of this model (model.gguf().gemv_q / gemm_q / dequantize_row)
+    def gguf_device_type(self, tensor):
+        return self.L.orch_gguf_device_type(self.h, tensor.encode())
+
+    def gguf_gemv(self, tensor, x, j0=0, j1=None, n_out=None):
+        x = np.ascontiguousarray(x, np.float32)
+        j1 = n_out if j1 is None else j1
+        out = np.zeros(j1, np.float32)
+        self._check(self.L.orch_gguf_gemm(self.h, tensor.encode(), x.ctypes.data_as(_fp), 1, int(j0), int(j1),
+                                          out.ctypes.data_as(_fp)))
+        return out[j0:]
+
+    def gguf_gemm(self, tensor, X, n_out):
+        X = np.ascontiguousarray(X, np.float32)
+        out = np.zeros((X.shape[0], n_out), np.float32)
+        self._check(self.L.orch_gguf_gemm(self.h, tensor.encode(), X.ctypes.data_as(_fp), X.shape[0], 0, int(n_out),
+                                          out.ctypes.data_as(_fp)))
+        return out
+
+    def gguf_dequant_row(self, tensor, row, n_in):
+        out = np.zeros(n_in, np.float32)
+        self._check(self.L.orch_gguf_dequant_row(self.h, tensor.encode(), int(row), out.ctypes.data_as(_fp)))
+        return out

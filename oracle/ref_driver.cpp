@@ -205,7 +205,7 @@ static int usage() {
         "ref_driver gemm <model> <tensor> <X.bin> <ntok> <out.bin>\n"
         "ref_driver greedy <model> <prompt.bin> <n_gen> <tokens.bin> [<logits.bin> <n_steps>]\n"
         "ref_driver batch <model> <tokens.bin> <n_prefill> <n_batch> <logits.bin>\n"
-        "ref_driver spec <target> <draft> <prompt.bin> <n_gen> <k> <tokens.bin>\n"
+        "ref_driver spec <target> <draft> <prompt.bin> <n_gen> <k> <tokens.bin> [<target_ctx> <draft_ctx>]\n"
         "ref_driver espec <target> <draft> <prompt.bin> <n_gen> <k> <temp> <top_p> <top_k> <pen> <last> <seed> <tokens.bin>\n"
         "ref_driver sample <logits.bin> <temp> <top_p> <top_k> <pen> <last> <seed> <history.bin> <n_draws> <out.bin>\n"
         "ref_driver op <rmsnorm|softmax|silu|rope|argmax|dot> ...\n"
@@ -291,9 +291,18 @@ int main(int argc, char** argv) {
         write_bin(argv[6], lg.data(), lg.size());
         return 0;
     }
-    if (cmd == "spec" && argc == 8) {
+    if (cmd == "spec" && (argc == 8 || argc == 10)) {
         Model t, d;
         if (!load_model(t, argv[2]) || !load_model(d, argv[3])) return 1;
+        if (argc == 10) {
+            // contexts below the reference's own 512 positions (core/model.cpp:64;
+            // its per-head scratch is sized for 512, so only smaller values are
+            // safe); spec_greedy's reset() re-sizes the KV caches for them
+            const int tc = std::atoi(argv[8]), dc = std::atoi(argv[9]);
+            if (tc < 2 || tc > 512 || dc < 2 || dc > 512) return usage();
+            t.cfg.ctx_len = (uint32_t)tc;
+            d.cfg.ctx_len = (uint32_t)dc;
+        }
         auto prompt = read_bin<int32_t>(argv[4]);
         SpecStats st;
         auto toks = spec_greedy(t, d, prompt, std::atoi(argv[5]), std::atoi(argv[6]), st);

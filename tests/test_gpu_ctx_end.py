@@ -65,3 +65,26 @@ def test_engine_spec_context_end(cmodels, graphs):
         _graphs(prev)
     assert np.array_equal(toks, FIX["espec/tokens"])
     assert [st["accepted"], st["proposed"], st["passes"]] == list(FIX["espec/stats"])
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+@pytest.mark.parametrize("name", ["draft_longer", "draft_shorter"])
+def test_spec_greedy_unequal_contexts(models_dir, name, graphs):
+    """Target and draft of different context lengths: the draft's bounds the
+    proposals, the target's the verify width (bench_engine.cpp:313-323); when
+    the target's context cuts the verify pass short, the last round compares
+    fewer drafts than it proposed and emits no bonus."""
+    import orc
+
+    tc, dc, k = (int(v) for v in FIX[f"uneq/{name}/cfg"])
+    print(f"[gpu] unequal contexts {name}: target {tc}, draft {dc}, k={k}, graphs={graphs}", flush=True)
+    tgt, dft = orc.Model(models_dir / "t-q4k.gguf", tc), orc.Model(models_dir / "t-q4k-d.gguf", dc)
+    prev = _graphs(graphs)
+    try:
+        toks, st = tgt.spec_greedy(dft, FIX[f"uneq/{name}/prompt"], 64, k)
+    finally:
+        _graphs(prev)
+        tgt.close()
+        dft.close()
+    assert np.array_equal(toks, FIX[f"uneq/{name}/tokens"])
+    assert [st["accepted"], st["proposed"], st["passes"]] == list(FIX[f"uneq/{name}/stats"])
