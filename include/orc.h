@@ -241,6 +241,14 @@ int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int
  * bench_engine.cpp:82-88). d_work needs orc_argmax_workspace() bytes. */
 size_t orc_argmax_workspace(int n_rows, int n);
 int orc_argmax(const float* d_x, int n_rows, int n, int ld, int32_t* d_out, void* d_work, orc_stream_t stream);
+/* orc_argmax without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No reference counterpart. The partials go to a library-owned
+ * 32 KiB device array, one per GPU, set up by orc_init; at most 16 rows per
+ * call (ORC_E_INVALID beyond). Results equal orc_argmax's. It allocates and
+ * clears nothing. Every call on one GPU shares that array: calls that overlap
+ * on one GPU (different streams or threads without ordering) race. */
+int orc_argmax_noalloc(const float* d_x, int n_rows, int n, int ld, int32_t* d_out, orc_stream_t stream);
 
 /* Greedy acceptance of one batched verify round (bench_engine.cpp:337-355):
  * given the verify logits argmax ids tgt[0..n_draft] and the draft ids

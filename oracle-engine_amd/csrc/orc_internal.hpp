@@ -15,6 +15,9 @@ bool initialized();
 // Per-device GEMM state (CU count, LDS limit, split-K workspace), set up by orc_init.
 int gemm_device_init(int device);
 void gemm_device_release();
+// Looks up this device's copy of orc_argmax_noalloc's scratch array (the
+// device must be current); once per device, from orc_init.
+int argmax_noalloc_device_init(int device);
 
 // Live kernel timing (orc_prof_*): when enabled and the stream is not being
 // captured, hands out a start / stop event pair for one launch and records

@@ -10,7 +10,9 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 #include <cfloat>
 
 namespace orc {
@@ -954,6 +956,29 @@ extern "C" int orc_attn_gqa(const float* d_q, int ldq, int n_tok, int n_heads, i
 
 static int argmax_slices(int n) { return std::max(1, std::min(256, (n + kArgBlock - 1) / kArgBlock)); }
 
+// ── allocation-free argmax (orc_argmax_noalloc) ─────────────────────────────
+// The per-slice partial maxima of up to kNoAllocRows rows live in a
+// file-scope device array, one copy per GPU (32 KiB, held until the process
+// ends). Host code never passes the array's name to a kernel: its address on
+// each device is looked up once, with that device current, by
+// argmax_noalloc_device_init (called from orc_init) and kept per device.
+constexpr int kNoAllocRows = 16;
+constexpr int kNoAllocSlices = 256;  // the most slices argmax_slices() makes
+static __device__ __align__(256) VI scratch[kNoAllocRows * kNoAllocSlices];
+static std::mutex g_scratch_mu;
+static std::unordered_map<int, VI*> g_scratch_ptr;  // device -> its copy of `scratch`
+
+int orc::argmax_noalloc_device_init(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr.count(device)) return ORC_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return set_error(ORC_E_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[device] = (VI*)p;
+    return ORC_OK;
+}
+
 extern "C" size_t orc_argmax_workspace(int n_rows, int n) { return (size_t)n_rows * argmax_slices(n) * sizeof(VI); }
 
 extern "C" int orc_argmax(const float* d_x, int n_rows, int n, int ld, int32_t* d_out, void* d_work, orc_stream_t s) {
@@ -964,6 +989,35 @@ extern "C" int orc_argmax(const float* d_x, int n_rows, int n, int ld, int32_t* 
     hipLaunchKernelGGL(k_argmax1, dim3(ns, n_rows), dim3(256), 0, st, d_x, n, ld, ns, (VI*)d_work);
     ORC_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_argmax2, dim3(n_rows), dim3(64), 0, st, (const VI*)d_work, ns, d_out);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+// orc_argmax with its partials in this device's `scratch` instead of a
+// caller workspace: the same two kernels, so the same results. k_argmax1
+// writes every partial k_argmax2 reads, so nothing needs clearing between
+// calls. No allocation, no memset.
+extern "C" int orc_argmax_noalloc(const float* d_x, int n_rows, int n, int ld, int32_t* d_out, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n <= 0 || n_rows <= 0 || ld < n || !d_x || !d_out) return set_error(ORC_E_INVALID, "argmax_noalloc: bad args");
+    if (n_rows > kNoAllocRows)
+        return set_error(ORC_E_INVALID, "argmax_noalloc: at most " + std::to_string(kNoAllocRows) + " rows per call");
+    const int ns = argmax_slices(n);
+    if ((size_t)n_rows * ns > (size_t)kNoAllocRows * kNoAllocSlices)
+        return set_error(ORC_E_INVALID, "argmax_noalloc: partials exceed the scratch");
+    int dev = -1;
+    ORC_HIP_CHECK(hipGetDevice(&dev));
+    VI* w = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        auto it = g_scratch_ptr.find(dev);
+        if (it != g_scratch_ptr.end()) w = it->second;
+    }
+    if (!w) return set_error(ORC_E_NOINIT, "argmax_noalloc: orc_init was not called for the current device");
+    hipStream_t st = resolve_stream(s);
+    hipLaunchKernelGGL(k_argmax1, dim3(ns, n_rows), dim3(256), 0, st, d_x, n, ld, ns, w);
+    ORC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_argmax2, dim3(n_rows), dim3(64), 0, st, (const VI*)w, ns, d_out);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

@@ -50,6 +50,7 @@ extern "C" int orc_init(int device) {
     if (g_stream) (void)hipStreamDestroy(g_stream);
     ORC_HIP_CHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     if (int rc = gemm_device_init(device)) return rc;
+    if (int rc = argmax_noalloc_device_init(device)) return rc;
     g_device = device;
     return ORC_OK;
 }

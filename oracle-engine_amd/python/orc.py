@@ -82,6 +82,7 @@ ABI = [
                                     C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]),
     ("orc_argmax_workspace", C.c_size_t, [C.c_int, C.c_int]),
     ("orc_argmax", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
+    ("orc_argmax_noalloc", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     ("orc_spec_accept_greedy", C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
     ("orc_spec_accept_greedy_at", C.c_int, [_vp, _vp, C.c_int, _vp, _vp, _vp, _vp]),
     ("orc_decode_advance", C.c_int, [_vp, _vp, _vp, _vp, _vp]),
