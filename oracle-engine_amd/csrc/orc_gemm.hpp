@@ -1,0 +1,51 @@
+// Declarations shared by the two quantized GEMM translation units:
+// orc_gemm.hip (vector path for Q8_0 / Q4_0, dispatch, C ABI) and
+// orc_mmq.hip (matrix-core path for Q4_K / Q6_K and mixed launches).
+#pragma once
+#include "orc_internal.hpp"
+
+#include <hip/hip_ext.h>
+
+namespace orc {
+
+// One GEMM launch: up to three weight segments sharing the activations X.
+struct QmvParams {
+    const uint8_t* w[3];
+    float* y[3];
+    const float* bias[3];
+    int rows[3];
+    int n_seg;
+    int n_rows;  // logical rows: sum of the segment rows, or 2 x (gate, up) pairs
+    int units;   // units per row
+    uint64_t row_bytes;
+    const float* x;
+    int ldx, ldy, n_tok, n_in;
+    const float* norm_w;
+    float eps;
+    int epi;
+    int n_groups;
+    int hs;               // matrix-core windowed mode: units of a wave's range staged at a time
+    int seg_type[3];      // matrix-core mixed launches: weight type of each segment
+    uint64_t seg_rb[3];   // and its row bytes
+};
+
+// Kernel timing of one launch: start / stop events taken from its dispatch.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
+// Device properties set by gemm_device_init.
+extern int g_n_cu;
+extern size_t g_lds_max;
+
+// k_mmq type parameter: Q4_K and Q6_K segments in one launch (a Q4_K_M
+// layer's Q|K|V, whose attn_v is Q6_K).
+constexpr int kMixK = 256;
+
+// Matrix-core path (orc_mmq.hip): tokens per launch for this shape (0 if none
+// fit), and one launch of at most that many tokens.
+bool mmq_type(int type);
+int mmq_max_tokens(int type, const QmvParams& p);
+int mmq_launch(int type, const QmvParams& p, hipStream_t s, const LaunchEvents& ev);
+
+}  // namespace orc

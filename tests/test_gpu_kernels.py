@@ -165,8 +165,12 @@ def test_gemm_fused_epilogues(dev, n_in):
                                                   (8192, (160, 96), (ol.Q6_K, ol.Q4_K), False)])
 def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
     """One launch over Q4_K and Q6_K segments (a Q4_K_M layer's Q|K|V) gives
-    every segment's rows bit for bit as the per-type launches do, for 1..16
-    tokens, with the RMSNorm prologue and QKV bias."""
+    every segment's rows as the per-type launches do, for 1..16 tokens, with
+    the RMSNorm prologue and QKV bias. The launches may split K differently
+    (the split follows each launch's row count), so the match is to fp32
+    summation order: 1e-5 of the largest output of the token. Within the
+    mixed launch the tokens are independent: token t of an n-token launch is
+    bit for bit the one-token launch on token t."""
     import orc
 
     print(f"[gpu] gemm mixed n_in={n_in} rows={rows} types={types}", flush=True)
@@ -189,7 +193,17 @@ def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
             dev.check(dev.L.orc_gemm_fused(t, one, 1, nt, n_in, dx.ptr, n_in, ld, g.ptr, C.c_float(1e-5),
                                            orc.EPI_STORE, None))
         got, want = dy.read(np.float32).reshape(nt, ld), dz.read(np.float32).reshape(nt, ld)
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), nt
+        scale = np.abs(want).max(axis=1, keepdims=True)
+        assert np.all(np.abs(got - want) <= 1e-5 * scale), (nt, float(np.abs(got - want).max()))
+        if nt in (5, 16):
+            t = nt - 1
+            d1 = dev.alloc(ld * 4)
+            segs1 = (orc.Seg * len(rows))(*[orc.Seg(w.ptr, r, d1.ptr + int(o) * 4, b.ptr if b else None)
+                                            for w, r, o, b in zip(ws, rows, offs, bs)])
+            dev.check(dev.L.orc_gemm_fused_mixed(ty.ctypes.data_as(C.POINTER(C.c_int32)), segs1, len(rows), 1,
+                                                 n_in, dx.ptr + t * n_in * 4, n_in, ld, g.ptr, C.c_float(1e-5),
+                                                 orc.EPI_STORE, None))
+            assert np.array_equal(d1.read(np.float32).view(np.uint32), got[t].view(np.uint32)), nt
     # error path: a segment that is not a whole number of 16-row tiles
     bad = (orc.Seg * 2)(orc.Seg(ws[0].ptr, 40, dy.ptr, None), orc.Seg(ws[1].ptr, 16, dy.ptr, None))
     ty = np.array(types[:2], np.int32)
