@@ -675,6 +675,10 @@ static int launch_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) 
 
 template <int QT>
 static int launch_type(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
+    if constexpr (QT == ORC_Q4_K || QT == ORC_Q6_K) {  // K-quants: one-token calls only
+        if (p.n_tok != 1) return set_error(ORC_E_UNSUPPORTED, "gemm: K-quant vector path takes one token");
+        return launch_nt<QT, 1>(p, s, ev);
+    }
     switch (p.n_tok) {
         case 1: return launch_nt<QT, 1>(p, s, ev);
         case 2: return launch_nt<QT, 2>(p, s, ev);
@@ -719,9 +723,43 @@ static double gemm_bytes(const QmvParams& p, int nt) {
     return b;
 }
 
+static int gemm_dispatch(QmvParams p, int type, hipStream_t s);
+
+// A one-token launch over Q4_K and Q6_K segments: one vector launch per run
+// of segments of one type, each with the norm prologue.
+static int dispatch_mixed_decode(const QmvParams& p, hipStream_t s) {
+    for (int i0 = 0; i0 < p.n_seg;) {
+        int i1 = i0 + 1;
+        while (i1 < p.n_seg && p.seg_type[i1] == p.seg_type[i0]) ++i1;
+        QmvParams q = p;
+        q.n_seg = i1 - i0;
+        q.n_rows = 0;
+        for (int i = 0; i < 3; ++i) {
+            const int j = i0 + i;
+            const bool in = i < q.n_seg;
+            q.w[i] = in ? p.w[j] : nullptr;
+            q.y[i] = in ? p.y[j] : nullptr;
+            q.bias[i] = in ? p.bias[j] : nullptr;
+            q.rows[i] = in ? p.rows[j] : 0;
+            q.seg_type[i] = in ? p.seg_type[j] : 0;
+            q.seg_rb[i] = in ? p.seg_rb[j] : 0;
+            q.n_rows += q.rows[i];
+        }
+        q.row_bytes = q.seg_rb[0];
+        if (int rc = gemm_dispatch(q, q.seg_type[0], s)) return rc;
+        i0 = i1;
+    }
+    return ORC_OK;
+}
+
 static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
+    // a one-token call (decode) runs on the vector ALUs for every type; the
+    // K-quants take the matrix cores from two tokens up. The choice follows
+    // the call's token count, never a chunk's, so chunking keeps results.
+    const bool decode = p.n_tok == 1;
+    if (decode && type == kMixK) return dispatch_mixed_decode(p, s);
     p.units = p.n_in / elems_per_unit(type);
-    const bool mm = mmq_type(type);
+    const bool mm = mmq_type(type) && !decode;
     const int ntmax = mm ? mmq_max_tokens(type, p) : max_tokens(type, p.n_in);
     if (ntmax < 1) return set_error(ORC_E_UNSUPPORTED, "gemm: n_in too large for the activations to fit LDS");
     // tokens are processed in chunks of at most ntmax; chunking never changes a
@@ -735,8 +773,8 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
         if (g_prof_on) prof_arm(s, type, q.n_tok, gemm_bytes(q, q.n_tok), &ev.start, &ev.stop);
         int rc;
         switch (type) {
-            case ORC_Q4_K:
-            case ORC_Q6_K:
+            case ORC_Q4_K: rc = mm ? mmq_launch(type, q, s, ev) : launch_type<ORC_Q4_K>(q, s, ev); break;
+            case ORC_Q6_K: rc = mm ? mmq_launch(type, q, s, ev) : launch_type<ORC_Q6_K>(q, s, ev); break;
             case kMixK: rc = mmq_launch(type, q, s, ev); break;
             case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s, ev); break;
             case ORC_Q8_0_X8: rc = launch_type<ORC_Q8_0_X8>(q, s, ev); break;

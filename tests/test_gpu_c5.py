@@ -6,7 +6,8 @@ cache and k = 8. The reference's Model fixes its context at 512 positions
 the speculative-greedy loop guarantees at any size: its token stream equals
 the target's own greedy stream (every verify pass here reads ~8.2-8.5 K
 cached positions, so the long-context attention and the 9-token verify
-GEMMs must agree with the one-token decode path bit for bit).
+GEMMs must agree with the one-token decode path: to fp32 rounding, which
+changes no argmax unless two logits tie within it).
 """
 import os
 import subprocess

@@ -1,8 +1,9 @@
 """Parity of the HIP kernels (through the C ABI) against the CPU oracle.
 
 Bars: dequant bit-exact; GEMV within 2e-6 of sum|w*x| of the float64 result
-and 1e-3 relative (norm-wise) of the oracle's fp32 gemv; the n-token GEMM
-bit-identical to n separate GEMVs; elementwise ops within 1e-6 relative.
+and 1e-3 relative (norm-wise) of the oracle's fp32 gemv; the tokens of an
+n-token GEMM independent bit for bit (and, for Q8_0 / Q4_0, bit-identical to n
+separate GEMVs); elementwise ops within 1e-6 relative.
 """
 import ctypes as C
 
@@ -92,19 +93,31 @@ def test_gemv_vs_exact(dev, oracle, qt, n_out, n_in):
 @pytest.mark.parametrize("qt,n_out,n_in", [(ol.Q4_K, 200, 3072), (ol.Q6_K, 77, 8192), (ol.Q8_0, 90, 896),
                                            (ol.Q4_0, 33, 2048), (ol.Q6_K, 24, 18944), (ol.Q8_0, 40000, 896),
                                            (ol.Q4_K, 8192, 3072), (ol.Q6_K, 70000, 1024)])
-def test_gemm_batch_invariant(dev, qt, n_out, n_in):
-    """verify(n)[t] is bit-identical to the decode GEMV of token t, n = 1..16
-    (the matrix-core kernel: up to 8 tokens as stacked hi / lo rows, 9-16 as
-    two tiles; whole-tile shapes chunked by 8)."""
+def test_gemm_batch_invariant(dev, oracle, qt, n_out, n_in):
+    """Tokens of a launch are independent: verify(n)[t] is bit-identical for
+    every n. Q8_0 / Q4_0 run one kernel family for all n, so verify(n)[t] also
+    equals the decode GEMV of token t bit for bit. The K-quants decode one
+    token on the vector ALUs and verify 2..16 on the matrix cores (up to 8
+    tokens as stacked hi / lo rows, 9-16 as two tiles), like the reference,
+    whose gemv_q and gemm_q round differently: decode and verify then agree
+    within 4e-6 of sum |w x|."""
     print(f"[gpu] gemm invariance type={qt} {n_out}x{n_in}", flush=True)
     rng = np.random.default_rng(3)
     raw = rand_blocks(qt, n_out * n_in, rng)
     wd = dev.upload(raw)
     X = rng.normal(0, 1, (16, n_in)).astype(np.float32)
     single = np.stack([_gemm(dev, qt, wd, 1, n_out, n_in, X[t:t + 1])[0] for t in range(16)])
+    kq = qt in (ol.Q4_K, ol.Q6_K)
+    full = _gemm(dev, qt, wd, 16, n_out, n_in, X)
     for nt in (2, 5, 7, 9, 12, 16):
         got = _gemm(dev, qt, wd, nt, n_out, n_in, X[:nt])
-        assert np.array_equal(got.view(np.uint32), single[:nt].view(np.uint32)), nt
+        assert np.array_equal(got.view(np.uint32), full[:nt].view(np.uint32)), nt
+        if not kq:
+            assert np.array_equal(got.view(np.uint32), single[:nt].view(np.uint32)), nt
+    if kq:
+        W = oracle.dequant(qt, raw, n_out * n_in).reshape(n_out, n_in).astype(np.float64)
+        scale = np.abs(X.astype(np.float64)) @ np.abs(W).T
+        assert np.all(np.abs(full - single) <= 4e-6 * scale + 1e-30), np.max(np.abs(full - single) / scale)
 
 
 @pytest.mark.parametrize("n_in", [512, 3072])  # 3072: the streamed-weight kernel
@@ -169,8 +182,8 @@ def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
     the RMSNorm prologue and QKV bias. The launches may split K differently
     (the split follows each launch's row count), so the match is to fp32
     summation order: 1e-5 of the largest output of the token. Within the
-    mixed launch the tokens are independent: token t of an n-token launch is
-    bit for bit the one-token launch on token t."""
+    multi-token mixed launch the tokens are independent: token t of an
+    n-token launch is bit for bit token t of a two-token launch."""
     import orc
 
     print(f"[gpu] gemm mixed n_in={n_in} rows={rows} types={types}", flush=True)
@@ -196,14 +209,15 @@ def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
         scale = np.abs(want).max(axis=1, keepdims=True)
         assert np.all(np.abs(got - want) <= 1e-5 * scale), (nt, float(np.abs(got - want).max()))
         if nt in (5, 16):
-            t = nt - 1
-            d1 = dev.alloc(ld * 4)
-            segs1 = (orc.Seg * len(rows))(*[orc.Seg(w.ptr, r, d1.ptr + int(o) * 4, b.ptr if b else None)
+            t = nt - 2
+            d2 = dev.alloc(2 * ld * 4)
+            segs2 = (orc.Seg * len(rows))(*[orc.Seg(w.ptr, r, d2.ptr + int(o) * 4, b.ptr if b else None)
                                             for w, r, o, b in zip(ws, rows, offs, bs)])
-            dev.check(dev.L.orc_gemm_fused_mixed(ty.ctypes.data_as(C.POINTER(C.c_int32)), segs1, len(rows), 1,
+            dev.check(dev.L.orc_gemm_fused_mixed(ty.ctypes.data_as(C.POINTER(C.c_int32)), segs2, len(rows), 2,
                                                  n_in, dx.ptr + t * n_in * 4, n_in, ld, g.ptr, C.c_float(1e-5),
                                                  orc.EPI_STORE, None))
-            assert np.array_equal(d1.read(np.float32).view(np.uint32), got[t].view(np.uint32)), nt
+            two = d2.read(np.float32).reshape(2, ld)
+            assert np.array_equal(two.view(np.uint32), got[t:t + 2].view(np.uint32)), nt
     # error path: a segment that is not a whole number of 16-row tiles
     bad = (orc.Seg * 2)(orc.Seg(ws[0].ptr, 40, dy.ptr, None), orc.Seg(ws[1].ptr, 16, dy.ptr, None))
     ty = np.array(types[:2], np.int32)
@@ -217,8 +231,9 @@ def test_gemm_staging_windows(dev, oracle, qt, epi, nt):
     """Rows too long for every token's activations to fit the LDS at once
     (n_in = 18944) are staged in windows: with the RMSNorm prologue, the
     SwiGLU pair and the residual epilogue, over more tiles than workgroups (so
-    windows are restaged for later tiles), nt tokens equal nt one-token calls
-    bit for bit and match float64 within 2e-6 of sum |w x|."""
+    windows are restaged for later tiles), the tokens of an nt-token call
+    equal those of two-token calls bit for bit, and they and the one-token
+    (vector) call match float64 within 2e-6 of sum |w x|."""
     import orc
 
     print(f"[gpu] gemm staging windows type={qt} epi={epi} nt={nt}", flush=True)
@@ -247,8 +262,9 @@ def test_gemm_staging_windows(dev, oracle, qt, epi, nt):
         return dy.read(np.float32).reshape(n, n_out)
 
     got = run(0, nt)
-    single = np.concatenate([run(t, 1) for t in range(nt)])
-    assert np.array_equal(got.view(np.uint32), single.view(np.uint32))
+    pairs = np.concatenate([run(t, 2)[:1] for t in range(nt - 1)] + [run(nt - 2, 2)[1:]])
+    assert np.array_equal(got.view(np.uint32), pairs.view(np.uint32))
+    one = run(0, 1)
     W = oracle.dequant(qt, raw, raw.size // ol.row_bytes(qt, n_in) * n_in).reshape(-1, n_in).astype(np.float64)
     Xd = X.astype(np.float64)
     if epi == "norm":
@@ -260,9 +276,11 @@ def test_gemm_staging_windows(dev, oracle, qt, epi, nt):
         want = gt / (1 + np.exp(-gt)) * up
         tol = 3e-6 * (scale[:, :n_out] * np.abs(up) + scale[:, n_out:] * np.abs(gt)) + 1e-30  # |silu'| <= 1.1
         assert np.all(np.abs(got - want) <= tol + 1e-6 * np.abs(want))
+        assert np.all(np.abs(one - want[:1]) <= tol[:1] + 1e-6 * np.abs(want[:1]))
     else:
         want = dot + (res if epi == "accum" else 0)
         assert np.all(np.abs(got - want) <= 2e-6 * scale + 1e-6 * np.abs(want) + 1e-30)
+        assert np.all(np.abs(one - want[:1]) <= 2e-6 * scale[:1] + 1e-6 * np.abs(want[:1]) + 1e-30)
 
 
 def test_rmsnorm(dev, oracle):

