@@ -86,6 +86,45 @@ int orch_gguf_gemm(orch_model* m, const char* tensor, const float* x, int n_tok,
  * tensor as fp32 into out (shape[0] floats), bit-exact. */
 int orch_gguf_dequant_row(orch_model* m, const char* tensor, int64_t row, float* out);
 
+/* ── the rest of the reference's Model surface ─────────────────────────────── */
+/* Model::embed_tokens (core/model.cpp:248-270): embed_dim floats into out. */
+int orch_embed_tokens(orch_model* m, const int32_t* tokens, int n, float* out);
+/* Model::save_state / load_state (core/model.cpp:156-236), the .orkv file. */
+int orch_save_state(orch_model* m, const char* path, int pos);
+int orch_load_state(orch_model* m, const char* path, int* pos);
+/* Model::snapshot_kv / restore_kv (core/model.hpp:103-105) through a handle. */
+typedef struct orch_kv_snapshot orch_kv_snapshot;
+orch_kv_snapshot* orch_snapshot_kv(orch_model* m, int pos);
+int orch_restore_kv(orch_model* m, const orch_kv_snapshot* s);
+int orch_snapshot_pos(const orch_kv_snapshot* s);
+void orch_snapshot_free(orch_kv_snapshot* s);
+/* Model::test_norm_cache_matches (core/model.hpp:119-121): 1 if equal. */
+int orch_norm_cache_matches(orch_model* m);
+
+/* ── namespace ops on host arrays (core/ops.hpp:42-92), run on the GPU ─────── */
+void orch_ops_rmsnorm(float* out, const float* x, const float* w, int n, float eps);
+void orch_ops_matmul(float* out, const float* a, const float* b, int m, int n, int k);
+void orch_ops_matmul_nn(float* out, const float* a, const float* b, int m, int n, int k);
+void orch_ops_silu(float* x, int n);
+void orch_ops_mul(float* out, const float* a, const float* b, int n);
+void orch_ops_add(float* a, const float* b, int n);
+void orch_ops_copy(float* dst, const float* src, int n);
+void orch_ops_softmax(float* x, int n);
+void orch_ops_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim, int pos, float freq_base);
+int orch_ops_argmax(const float* x, int n);
+float orch_ops_dot(const float* a, const float* b, int n);
+
+/* ── Sampler (core/sampler.hpp:24-48) on a device state ──────────────────────── */
+typedef struct orch_sampler orch_sampler;
+orch_sampler* orch_sampler_new(float temperature, float top_p, int top_k, float repeat_pen, int repeat_last,
+                               uint64_t seed);
+void orch_sampler_free(orch_sampler* s);
+int32_t orch_sampler_sample(orch_sampler* s, float* logits, int n_vocab);
+void orch_sampler_record(orch_sampler* s, int32_t id);
+void orch_sampler_reset(orch_sampler* s);
+void orch_sampler_set_params(orch_sampler* s, float temperature, float top_p, int top_k, float repeat_pen,
+                             int repeat_last);
+
 #ifdef __cplusplus
 }
 #endif

@@ -171,6 +171,31 @@ int orc_prof_enable(int on);
 int orc_prof_accumulate(void);
 int orc_prof_read(int type, int n_tok, int64_t* launches, double* total_ms, double* total_bytes);
 
+/* ── free functions on float arrays (namespace ops, core/ops.hpp:42-92) ──── */
+/* Device arrays; fp32; reductions in a fixed order of the device, so results
+ * match the reference's AVX2 loops to fp32 summation order. */
+#define ORC_VEC_MUL 0  /* out = a * b  (ops::mul, ops.cpp:339-354)  */
+#define ORC_VEC_ADD 1  /* out = a + b  (ops::add, ops.cpp:359-374)  */
+#define ORC_VEC_COPY 2 /* out = a      (ops::copy, ops.cpp:379-381) */
+int orc_vec_binary(int op, float* d_out, const float* d_a, const float* d_b, int n, orc_stream_t stream);
+/* x = x / (1 + exp(-x)) in place (ops::silu, ops.cpp:308-334). */
+int orc_vec_silu(float* d_x, int n, orc_stream_t stream);
+/* Row-wise softmax in place of n_rows rows of n, ld floats apart
+ * (ops::softmax, ops.cpp:386-435). */
+int orc_softmax(float* d_x, int n, int n_rows, int ld, orc_stream_t stream);
+/* *d_out = sum a[i] b[i] (ops::dot, ops.cpp:102-143). */
+int orc_dot(const float* d_a, const float* d_b, int n, float* d_out, orc_stream_t stream);
+/* out (m x n) = A (m x k) x B^T with B n x k when b_trans (ops::matmul,
+ * ops.cpp:207-289), else A x B with B k x n (ops::matmul_nn, ops.cpp:294-303). */
+int orc_matmul_f32(float* d_out, const float* d_a, const float* d_b, int m, int n, int k, int b_trans,
+                   orc_stream_t stream);
+/* Rotate-half RoPE of one position (ops::rope, ops.cpp:440-485) in place on
+ * n_heads q heads and n_kv_heads k heads of head_dim values; d_cs holds the
+ * position's head_dim/2 (cos, sin) pairs, computed on the host as the
+ * reference does. */
+int orc_rope_pos(float* d_q, float* d_k, int n_heads, int n_kv_heads, int head_dim, const float* d_cs,
+                 orc_stream_t stream);
+
 /* ── elementwise / attention ─────────────────────────────────────────────── */
 /* out[t] = rmsnorm(x[t]) for n_rows rows of n (ops::rmsnorm, ops.cpp:149-195). */
 int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_rows, float eps, orc_stream_t stream);
@@ -281,6 +306,13 @@ int orc_sample(void* d_state, float* d_logits, int n_vocab, int32_t* d_out, orc_
 int orc_sampler_record(void* d_state, const int32_t* d_tok, int n, orc_stream_t stream);
 /* The last min(cap, size) history entries into d_out, their count into *d_n. */
 int orc_sampler_history(const void* d_state, int32_t* d_out, int cap, int32_t* d_n, orc_stream_t stream);
+/* Sampler::set_params (sampler.hpp:37): new parameters; generator state and
+ * history unchanged (limits as orc_sampler_init). */
+int orc_sampler_set_params(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty,
+                           int repeat_last, orc_stream_t stream);
+/* Sampler::reset (sampler.hpp:34): the history is cleared, the generator
+ * keeps its state. */
+int orc_sampler_clear_history(void* d_state, orc_stream_t stream);
 /* Engine-style stochastic verify (core/engine.cpp:183-232) over the k+1 rows
  * of one batched verify pass (row i = target logits at the i-th verify
  * position, rows ld floats apart; rows are rewritten by sampling): for each

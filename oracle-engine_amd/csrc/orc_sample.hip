@@ -486,6 +486,21 @@ __global__ __launch_bounds__(kST) void k_sample(DevSampler* s, float* lg, int n,
     }
 }
 
+// Sampler::set_params (sampler.hpp:37): new parameters, same generator and
+// history; Sampler::reset (sampler.hpp:34): history cleared, same generator.
+__global__ void k_sampler_set(DevSampler* s, int set, float temp, float top_p, float pen, int top_k, int last) {
+    if (threadIdx.x != 0) return;
+    if (set) {
+        s->temp = temp;
+        s->top_p = top_p;
+        s->pen = pen;
+        s->top_k = top_k;
+        s->last = last;
+    } else {
+        s->nh = 0;
+    }
+}
+
 __global__ void k_sampler_record(DevSampler* s, const int32_t* tok, int n) {
     if (threadIdx.x != 0) return;
     for (int i = 0; i < n; ++i) record_tok(s, tok[i]);
@@ -693,6 +708,31 @@ extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, i
     }
     hipLaunchKernelGGL(k_sampler_init, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state,
                        (uint32_t)seed, temperature, top_p, repeat_penalty, top_k, repeat_last, d_hist, n_hist);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_sampler_set_params(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty,
+                                      int repeat_last, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || repeat_last < 0 || repeat_last >= kSampHist / 2 || top_k < 0 || top_k > kCandMax)
+        return set_error(ORC_E_INVALID, "sampler_set_params: bad args (0 <= top_k <= 16384, repeat_last < 2048)");
+    {
+        std::lock_guard<std::mutex> lk(g_all_mu);
+        if (top_k == 0) g_all_tokens.insert(d_state);
+        else g_all_tokens.erase(d_state);
+    }
+    hipLaunchKernelGGL(k_sampler_set, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state, 1, temperature,
+                       top_p, repeat_penalty, top_k, repeat_last);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_sampler_clear_history(void* d_state, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state) return set_error(ORC_E_INVALID, "sampler_clear_history: null state");
+    hipLaunchKernelGGL(k_sampler_set, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state, 0, 0.f, 0.f, 0.f,
+                       0, 0);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

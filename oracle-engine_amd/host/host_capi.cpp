@@ -2,6 +2,8 @@
 #include "oracle_host.h"
 
 #include "model.hpp"
+#include "ops.hpp"
+#include "sampler.hpp"
 #include "spec.hpp"
 
 #include <cstring>
@@ -192,4 +194,101 @@ extern "C" int orch_gguf_dequant_row(orch_model* h, const char* tensor, int64_t 
     if (!h || !tensor || !out || !h->m.gguf().has_tensor(tensor)) return -1;
     h->m.gguf().dequantize_row(tensor, row, out);
     return 0;
+}
+
+// ── the rest of the Model surface ───────────────────────────────────────────
+extern "C" int orch_embed_tokens(orch_model* h, const int32_t* tokens, int n, float* out) {
+    if (!h || !tokens || !out || n <= 0) return -1;
+    const std::vector<float> e = h->m.embed_tokens(std::vector<int32_t>(tokens, tokens + n));
+    if (e.empty()) return fail(h, -1);
+    std::memcpy(out, e.data(), e.size() * 4);
+    return 0;
+}
+
+extern "C" int orch_save_state(orch_model* h, const char* path, int pos) {
+    return h && path && h->m.save_state(path, pos) ? 0 : -1;
+}
+
+extern "C" int orch_load_state(orch_model* h, const char* path, int* pos) {
+    if (!h || !path || !pos) return -1;
+    return h->m.load_state(path, *pos) ? 0 : -1;
+}
+
+struct orch_kv_snapshot {
+    Model::KVSnapshot s;
+};
+
+extern "C" orch_kv_snapshot* orch_snapshot_kv(orch_model* h, int pos) {
+    if (!h) return nullptr;
+    auto s = std::make_unique<orch_kv_snapshot>();
+    s->s = h->m.snapshot_kv(pos);
+    return s->s.bytes ? s.release() : nullptr;
+}
+
+extern "C" int orch_restore_kv(orch_model* h, const orch_kv_snapshot* s) {
+    if (!h || !s) return -1;
+    h->m.restore_kv(s->s);
+    return h->m.last_error()[0] ? fail(h, -1) : 0;
+}
+
+extern "C" int orch_snapshot_pos(const orch_kv_snapshot* s) { return s ? s->s.pos : -1; }
+extern "C" void orch_snapshot_free(orch_kv_snapshot* s) { delete s; }
+extern "C" int orch_norm_cache_matches(orch_model* h) { return h && h->m.test_norm_cache_matches() ? 1 : 0; }
+
+// ── namespace ops ────────────────────────────────────────────────────────────
+extern "C" void orch_ops_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
+    ops::rmsnorm(out, x, w, n, eps);
+}
+extern "C" void orch_ops_matmul(float* out, const float* a, const float* b, int m, int n, int k) {
+    ops::matmul(out, a, b, m, n, k);
+}
+extern "C" void orch_ops_matmul_nn(float* out, const float* a, const float* b, int m, int n, int k) {
+    ops::matmul_nn(out, a, b, m, n, k);
+}
+extern "C" void orch_ops_silu(float* x, int n) { ops::silu(x, n); }
+extern "C" void orch_ops_mul(float* out, const float* a, const float* b, int n) { ops::mul(out, a, b, n); }
+extern "C" void orch_ops_add(float* a, const float* b, int n) { ops::add(a, b, n); }
+extern "C" void orch_ops_copy(float* dst, const float* src, int n) { ops::copy(dst, src, n); }
+extern "C" void orch_ops_softmax(float* x, int n) { ops::softmax(x, n); }
+extern "C" void orch_ops_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim, int pos,
+                              float freq_base) {
+    ops::rope(q, k, n_heads, n_kv_heads, head_dim, pos, freq_base);
+}
+extern "C" int orch_ops_argmax(const float* x, int n) { return ops::argmax(x, n); }
+extern "C" float orch_ops_dot(const float* a, const float* b, int n) { return ops::dot(a, b, n); }
+
+// ── Sampler ──────────────────────────────────────────────────────────────────
+struct orch_sampler {
+    Sampler s;
+    explicit orch_sampler(const SamplerParams& p, uint64_t seed) : s(p, seed) {}
+};
+
+static SamplerParams sparams(float temperature, float top_p, int top_k, float repeat_pen, int repeat_last) {
+    SamplerParams p;
+    p.temperature = temperature;
+    p.top_p = top_p;
+    p.top_k = top_k;
+    p.repeat_pen = repeat_pen;
+    p.repeat_last = repeat_last;
+    return p;
+}
+
+extern "C" orch_sampler* orch_sampler_new(float temperature, float top_p, int top_k, float repeat_pen,
+                                          int repeat_last, uint64_t seed) {
+    auto h = std::make_unique<orch_sampler>(sparams(temperature, top_p, top_k, repeat_pen, repeat_last), seed);
+    return h->s.device_state() && h->s.error().empty() ? h.release() : nullptr;
+}
+extern "C" void orch_sampler_free(orch_sampler* s) { delete s; }
+extern "C" int32_t orch_sampler_sample(orch_sampler* s, float* logits, int n_vocab) {
+    return s ? s->s.sample(logits, n_vocab) : -1;
+}
+extern "C" void orch_sampler_record(orch_sampler* s, int32_t id) {
+    if (s) s->s.record(id);
+}
+extern "C" void orch_sampler_reset(orch_sampler* s) {
+    if (s) s->s.reset();
+}
+extern "C" void orch_sampler_set_params(orch_sampler* s, float temperature, float top_p, int top_k,
+                                        float repeat_pen, int repeat_last) {
+    if (s) s->s.set_params(sparams(temperature, top_p, top_k, repeat_pen, repeat_last));
 }

@@ -349,6 +349,174 @@ void Model::forward_prefill(const int32_t* tokens, int n, int sp, float* out_log
     orc_stream_sync(nullptr);
 }
 
+// ── embedding, KV snapshot and .orkv files ──────────────────────────────────
+
+std::vector<float> Model::embed_tokens(const std::vector<int32_t>& tokens) {  // model.cpp:248-270
+    if (tokens.empty() || !loaded_) return {};
+    const int D = cfg.embed_dim, n = (int)tokens.size();
+    if (n > (int)cfg.ctx_len) {
+        fail("embed_tokens: more tokens than the context holds");
+        return {};
+    }
+    std::vector<int32_t> ids(tokens);
+    for (auto& t : ids)
+        if (t < 0 || t >= (int32_t)cfg.n_vocab) t = 0;  // model.cpp:352-356
+    std::vector<float> acc((size_t)D, 0.f), xs((size_t)kMaxBatch * D);
+    reset();
+    for (int t0 = 0; t0 < n; t0 += kMaxBatch) {
+        const int m = std::min(kMaxBatch, n - t0);
+        if (orc_memcpy_h2d(d_ids_, ids.data() + t0, (size_t)m * 4, nullptr) ||
+            chunk_dev(d_ids_, m, nullptr, t0, false, nullptr, nullptr) ||
+            orc_memcpy_d2h(xs.data(), d_x_, (size_t)m * D * 4, nullptr)) {
+            fail(std::string("embed_tokens: ") + orc_last_error());
+            reset();
+            return {};
+        }
+        for (int t = 0; t < m; ++t)
+            for (int d = 0; d < D; ++d) acc[d] += xs[(size_t)t * D + d];
+    }
+    const float inv_n = 1.f / n;
+    float norm2 = 0.f;
+    for (int d = 0; d < D; ++d) {
+        acc[d] *= inv_n;
+        norm2 += acc[d] * acc[d];
+    }
+    const float inv_norm = 1.f / (std::sqrt(norm2) + 1e-9f);
+    for (float& v : acc) v *= inv_norm;
+    reset();
+    return acc;
+}
+
+Model::KVSnapshot Model::snapshot_kv(int pos) const {
+    KVSnapshot s;
+    s.pos = pos;
+    if (!loaded_) return s;
+    const size_t bytes = (size_t)cfg.n_layers * cfg.n_kv_total() * cfg.ctx_len * sizeof(float);
+    void *k = nullptr, *v = nullptr;
+    if (orc_malloc(&k, bytes) || orc_malloc(&v, bytes)) {
+        if (k) orc_free(k);
+        std::fprintf(stderr, "[Model] snapshot_kv: %s\n", orc_last_error());
+        return s;
+    }
+    s.k.reset(k, [](void* q) { orc_free(q); });
+    s.v.reset(v, [](void* q) { orc_free(q); });
+    if (orc_memcpy_d2d(k, d_k_, bytes, nullptr) || orc_memcpy_d2d(v, d_v_, bytes, nullptr) ||
+        orc_stream_sync(nullptr)) {
+        std::fprintf(stderr, "[Model] snapshot_kv: %s\n", orc_last_error());
+        return KVSnapshot{nullptr, nullptr, 0, pos};
+    }
+    s.bytes = bytes;
+    return s;
+}
+
+void Model::restore_kv(const KVSnapshot& snap) {
+    err_.clear();
+    const size_t bytes = (size_t)cfg.n_layers * cfg.n_kv_total() * cfg.ctx_len * sizeof(float);
+    if (!loaded_ || !snap.k || !snap.v || snap.bytes != bytes) {
+        fail("restore_kv: the snapshot is empty or of another shape");
+        return;
+    }
+    if (orc_memcpy_d2d(d_k_, snap.k.get(), bytes, nullptr) || orc_memcpy_d2d(d_v_, snap.v.get(), bytes, nullptr) ||
+        orc_stream_sync(nullptr))
+        fail(std::string("restore_kv: ") + orc_last_error());
+}
+
+static constexpr uint32_t kOrkvMagic = 0x564B524Fu;  // "ORKV" little-endian (model.cpp:11-12)
+static constexpr uint32_t kOrkvVersion = 2u;
+static_assert(sizeof(ModelConfig) == 44, "ModelConfig must keep the reference's layout");
+
+// Device KV [layer][kv_head][pos][hd] <-> file [layer][pos][kv_head * hd],
+// one layer at a time through host buffers.
+bool Model::save_state(const std::string& path, int pos) const {  // model.cpp:156-181
+    if (!loaded_) return false;
+    FILE* f = std::fopen(path.c_str(), "wb");
+    if (!f) {
+        std::fprintf(stderr, "[Model] save_state: cannot open %s\n", path.c_str());
+        return false;
+    }
+    const size_t C = cfg.ctx_len, H = cfg.n_kv_heads, hd = cfg.head_dim, per = C * H * hd;
+    const uint32_t ipos = (uint32_t)pos;
+    const uint64_t n = (uint64_t)cfg.n_layers * per;
+    bool ok = std::fwrite(&kOrkvMagic, 4, 1, f) == 1 && std::fwrite(&kOrkvVersion, 4, 1, f) == 1 &&
+              std::fwrite(&cfg, sizeof(ModelConfig), 1, f) == 1 && std::fwrite(&ipos, 4, 1, f) == 1 &&
+              std::fwrite(&n, 8, 1, f) == 1;
+    std::vector<float> dev(per), file(per);
+    for (int which = 0; which < 2 && ok; ++which) {
+        const float* src = which ? d_v_ : d_k_;
+        for (uint32_t l = 0; l < cfg.n_layers && ok; ++l) {
+            ok = orc_memcpy_d2h(dev.data(), src + l * per, per * 4, nullptr) == 0;
+            for (size_t h = 0; ok && h < H; ++h)
+                for (size_t p = 0; p < C; ++p)
+                    std::memcpy(&file[(p * H + h) * hd], &dev[(h * C + p) * hd], hd * 4);
+            ok = ok && std::fwrite(file.data(), 4, per, f) == per;
+        }
+    }
+    std::fclose(f);
+    if (!ok) std::fprintf(stderr, "[Model] save_state: incomplete write to %s\n", path.c_str());
+    return ok;
+}
+
+bool Model::load_state(const std::string& path, int& pos) {  // model.cpp:184-236
+    if (!loaded_) return false;
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    auto bad = [&](const char* why) {
+        std::fprintf(stderr, "[Model] load_state: %s (%s)\n", why, path.c_str());
+        std::fclose(f);
+        return false;
+    };
+    uint32_t magic = 0, ver = 0;
+    if (std::fread(&magic, 4, 1, f) != 1 || std::fread(&ver, 4, 1, f) != 1 || magic != kOrkvMagic ||
+        ver != kOrkvVersion)
+        return bad("not a compatible .orkv file");
+    ModelConfig lc;
+    if (std::fread(&lc, sizeof(ModelConfig), 1, f) != 1) return bad("truncated header");
+    if (lc.n_layers != cfg.n_layers || lc.embed_dim != cfg.embed_dim || lc.ctx_len != cfg.ctx_len ||
+        lc.n_kv_heads != cfg.n_kv_heads || lc.head_dim != cfg.head_dim)
+        return bad("configuration differs from the loaded model (layers/embed/ctx/kv_heads/head_dim)");
+    uint32_t ipos = 0;
+    uint64_t n = 0;
+    if (std::fread(&ipos, 4, 1, f) != 1 || std::fread(&n, 8, 1, f) != 1) return bad("truncated header");
+    const size_t C = cfg.ctx_len, H = cfg.n_kv_heads, hd = cfg.head_dim, per = C * H * hd;
+    if (n != (uint64_t)cfg.n_layers * per) return bad("KV size does not match the configuration");
+    // read everything before touching the device cache (a truncated file
+    // leaves it as it was)
+    std::vector<float> file(2 * n);
+    if (std::fread(file.data(), 4, 2 * n, f) != 2 * n) return bad("truncated KV data");
+    std::fclose(f);
+    std::vector<float> dev(per);
+    for (int which = 0; which < 2; ++which) {
+        float* dst = which ? d_v_ : d_k_;
+        for (uint32_t l = 0; l < cfg.n_layers; ++l) {
+            const float* src = file.data() + (size_t)which * n + (size_t)l * per;
+            for (size_t h = 0; h < H; ++h)
+                for (size_t p = 0; p < C; ++p) std::memcpy(&dev[(h * C + p) * hd], &src[(p * H + h) * hd], hd * 4);
+            if (orc_memcpy_h2d(dst + l * per, dev.data(), per * 4, nullptr))
+                return fail(std::string("load_state: ") + orc_last_error());
+        }
+    }
+    pos = (int)ipos;
+    return true;
+}
+
+bool Model::test_norm_cache_matches() {  // core/model.hpp:119-121
+    if (!loaded_) return false;
+    const int D = cfg.embed_dim;
+    std::vector<float> dev((size_t)D);
+    auto same = [&](const std::string& name, const float* d) {
+        const uint8_t* raw = gguf_.tensor_raw(name);
+        return raw && d && orc_memcpy_d2h(dev.data(), d, (size_t)D * 4, nullptr) == 0 &&
+               std::memcmp(dev.data(), raw, (size_t)D * 4) == 0;
+    };
+    if (!same("output_norm.weight", out_norm_)) return false;
+    for (uint32_t l = 0; l < cfg.n_layers; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        if (!same(b + "attn_norm.weight", layers_[l].attn_norm) || !same(b + "ffn_norm.weight", layers_[l].ffn_norm))
+            return false;
+    }
+    return true;
+}
+
 double Model::weight_bytes(bool logits) const {
     double b = 0;
     auto mb = [](const Mat& m) { return (double)orc_row_bytes(m.type, m.n_in) * m.n_out; };

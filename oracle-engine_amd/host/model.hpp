@@ -15,10 +15,13 @@
 #include "orc.h"
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
-struct ModelConfig {  // core/model.hpp:10-27
+// core/model.hpp:10-27; the same field order and types, so the .orkv
+// header (which stores the struct's bytes) is interchangeable.
+struct ModelConfig {
     uint32_t n_vocab = 0;
     uint32_t n_layers = 0;
     uint32_t n_heads = 0;
@@ -62,6 +65,35 @@ public:
     void reset();
     void warmup();
     const GGUFParser& gguf() const { return gguf_; }
+
+    // core/model.hpp:100 / model.cpp:248-270: the mean over the tokens of the
+    // hidden state after the last layer (before the final norm), L2
+    // normalised (1 / (|acc| + 1e-9)); the KV cache is cleared before and
+    // after. The tokens run as batched passes; the pooling follows the
+    // reference's float order on the host. Empty on error.
+    std::vector<float> embed_tokens(const std::vector<int32_t>& tokens);
+
+    // core/model.hpp:103-105: a copy of the whole KV cache, here in device
+    // memory (a device-to-device copy each way). restore_kv takes only a
+    // snapshot of this model's shape; pos is carried for the caller.
+    struct KVSnapshot {
+        std::shared_ptr<void> k, v;
+        size_t bytes = 0;
+        int pos = 0;
+    };
+    KVSnapshot snapshot_kv(int pos) const;
+    void restore_kv(const KVSnapshot& snap);
+
+    // core/model.hpp:108-116 / model.cpp:156-236: the reference's .orkv file
+    // (magic "ORKV", version 2, the ModelConfig bytes, pos, then the K and V
+    // caches as [layer][pos][kv_head x head_dim] floats), converted from and
+    // to the device layout [layer][kv_head][pos][head_dim]. load_state
+    // rejects the files the reference rejects.
+    bool save_state(const std::string& path, int pos) const;
+    bool load_state(const std::string& path, int& pos);
+
+    // core/model.hpp:120: the norm weights the device reads equal the file's.
+    bool test_norm_cache_matches();
 
     // Device hot path. d_ids: n token ids in HBM at positions start_pos..;
     // when compute_logits, logits of every position go to d_logits() and, if

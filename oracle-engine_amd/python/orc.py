@@ -99,6 +99,14 @@ ABI = [
     ("orc_accept_resample", C.c_int, [_vp, _vp, C.c_int, C.c_int32, C.c_float, C.c_float, _vp, _vp]),
     ("orc_spec_accept_stochastic", C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
                                              _vp, _vp, _vp, _vp]),
+    ("orc_sampler_set_params", C.c_int, [_vp, C.c_float, C.c_float, C.c_int, C.c_float, C.c_int, _vp]),
+    ("orc_sampler_clear_history", C.c_int, [_vp, _vp]),
+    ("orc_vec_binary", C.c_int, [C.c_int, _vp, _vp, _vp, C.c_int, _vp]),
+    ("orc_vec_silu", C.c_int, [_vp, C.c_int, _vp]),
+    ("orc_softmax", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp]),
+    ("orc_dot", C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
+    ("orc_matmul_f32", C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp]),
+    ("orc_rope_pos", C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     ("orc_prof_enable", C.c_int, [C.c_int]),
     ("orc_prof_accumulate", C.c_int, []),
     ("orc_prof_read", C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double),
@@ -204,6 +212,31 @@ HOST_ABI = [
     ("orch_gguf_device_type", C.c_int, [_vp, C.c_char_p]),
     ("orch_gguf_gemm", C.c_int, [_vp, C.c_char_p, _fp, C.c_int, C.c_int, C.c_int, _fp]),
     ("orch_gguf_dequant_row", C.c_int, [_vp, C.c_char_p, C.c_int64, _fp]),
+    ("orch_embed_tokens", C.c_int, [_vp, _ip, C.c_int, _fp]),
+    ("orch_save_state", C.c_int, [_vp, C.c_char_p, C.c_int]),
+    ("orch_load_state", C.c_int, [_vp, C.c_char_p, _ip]),
+    ("orch_snapshot_kv", _vp, [_vp, C.c_int]),
+    ("orch_restore_kv", C.c_int, [_vp, _vp]),
+    ("orch_snapshot_pos", C.c_int, [_vp]),
+    ("orch_snapshot_free", None, [_vp]),
+    ("orch_norm_cache_matches", C.c_int, [_vp]),
+    ("orch_ops_rmsnorm", None, [_fp, _fp, _fp, C.c_int, C.c_float]),
+    ("orch_ops_matmul", None, [_fp, _fp, _fp, C.c_int, C.c_int, C.c_int]),
+    ("orch_ops_matmul_nn", None, [_fp, _fp, _fp, C.c_int, C.c_int, C.c_int]),
+    ("orch_ops_silu", None, [_fp, C.c_int]),
+    ("orch_ops_mul", None, [_fp, _fp, _fp, C.c_int]),
+    ("orch_ops_add", None, [_fp, _fp, C.c_int]),
+    ("orch_ops_copy", None, [_fp, _fp, C.c_int]),
+    ("orch_ops_softmax", None, [_fp, C.c_int]),
+    ("orch_ops_rope", None, [_fp, _fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
+    ("orch_ops_argmax", C.c_int, [_fp, C.c_int]),
+    ("orch_ops_dot", C.c_float, [_fp, _fp, C.c_int]),
+    ("orch_sampler_new", _vp, [C.c_float, C.c_float, C.c_int, C.c_float, C.c_int, C.c_uint64]),
+    ("orch_sampler_free", None, [_vp]),
+    ("orch_sampler_sample", C.c_int32, [_vp, _fp, C.c_int]),
+    ("orch_sampler_record", None, [_vp, C.c_int32]),
+    ("orch_sampler_reset", None, [_vp]),
+    ("orch_sampler_set_params", None, [_vp, C.c_float, C.c_float, C.c_int, C.c_float, C.c_int]),
 ]
 
 _host = None
@@ -342,3 +375,138 @@ class Model:
         out = np.zeros(n_in, np.float32)
         self._check(self.L.orch_gguf_dequant_row(self.h, tensor.encode(), int(row), out.ctypes.data_as(_fp)))
         return out
+
+    def embed_tokens(self, tokens):
+        """Model::embed_tokens (core/model.cpp:248-270)."""
+        t = _i32(tokens)
+        out = np.zeros(self.embed_dim, np.float32)
+        self._check(self.L.orch_embed_tokens(self.h, t.ctypes.data_as(_ip), t.size, out.ctypes.data_as(_fp)))
+        return out
+
+    def save_state(self, path, pos):
+        """Model::save_state (core/model.cpp:156-181): the .orkv file."""
+        self._check(self.L.orch_save_state(self.h, str(path).encode(), int(pos)))
+
+    def load_state(self, path):
+        """Model::load_state (core/model.cpp:184-236); the saved position, or
+        None if the file is missing or incompatible (the reference's false)."""
+        pos = C.c_int(-1)
+        rc = self.L.orch_load_state(self.h, str(path).encode(), C.cast(C.pointer(pos), _ip))
+        return None if rc else pos.value
+
+    def snapshot_kv(self, pos):
+        """Model::snapshot_kv (core/model.hpp:104): a device copy of the KV cache."""
+        h = self.L.orch_snapshot_kv(self.h, int(pos))
+        if not h:
+            raise OrcError("snapshot_kv failed")
+        return KVSnapshot(self.L, h)
+
+    def restore_kv(self, snap):
+        self._check(self.L.orch_restore_kv(self.h, snap.h))
+
+    def norm_cache_matches(self):
+        return bool(self.L.orch_norm_cache_matches(self.h))
+
+
+class KVSnapshot:
+    def __init__(self, L, h):
+        self.L, self.h = L, h
+
+    @property
+    def pos(self):
+        return self.L.orch_snapshot_pos(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.orch_snapshot_free(self.h)
+            self.h = None
+
+
+class Sampler:
+    """Sampler (core/sampler.hpp:24-48) on a device state, host logits."""
+
+    def __init__(self, temperature=0.7, top_p=0.9, top_k=40, repeat_pen=1.1, repeat_last=64, seed=42):
+        self.L = load_host_lib()
+        self.h = self.L.orch_sampler_new(temperature, top_p, int(top_k), repeat_pen, int(repeat_last), int(seed))
+        if not self.h:
+            raise OrcError("Sampler: device state could not be created")
+
+    def sample(self, logits):
+        """Next id; the array is rewritten in place as the reference's is."""
+        assert logits.dtype == np.float32 and logits.flags.c_contiguous
+        return int(self.L.orch_sampler_sample(self.h, logits.ctypes.data_as(_fp), logits.size))
+
+    def record(self, tok):
+        self.L.orch_sampler_record(self.h, int(tok))
+
+    def reset(self):
+        self.L.orch_sampler_reset(self.h)
+
+    def set_params(self, temperature, top_p, top_k, repeat_pen, repeat_last):
+        self.L.orch_sampler_set_params(self.h, temperature, top_p, int(top_k), repeat_pen, int(repeat_last))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.orch_sampler_free(self.h)
+            self.h = None
+
+
+class HostOps:
+    """namespace ops (core/ops.hpp:42-92) on numpy float32 arrays, through
+    liboracle_host (computed on the GPU)."""
+
+    def __init__(self):
+        self.L = load_host_lib()
+
+    @staticmethod
+    def _p(a):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+        return a.ctypes.data_as(_fp)
+
+    def rmsnorm(self, x, w, eps=1e-5):
+        out = np.empty_like(x)
+        self.L.orch_ops_rmsnorm(self._p(out), self._p(x), self._p(w), x.size, eps)
+        return out
+
+    def matmul(self, a, b, nn=False):
+        m, k = a.shape
+        n = b.shape[1] if nn else b.shape[0]
+        out = np.empty((m, n), np.float32)
+        (self.L.orch_ops_matmul_nn if nn else self.L.orch_ops_matmul)(self._p(out), self._p(a), self._p(b), m, n, k)
+        return out
+
+    def silu(self, x):
+        x = x.copy()
+        self.L.orch_ops_silu(self._p(x), x.size)
+        return x
+
+    def mul(self, a, b):
+        out = np.empty_like(a)
+        self.L.orch_ops_mul(self._p(out), self._p(a), self._p(b), a.size)
+        return out
+
+    def add(self, a, b):
+        a = a.copy()
+        self.L.orch_ops_add(self._p(a), self._p(b), a.size)
+        return a
+
+    def copy(self, a):
+        out = np.empty_like(a)
+        self.L.orch_ops_copy(self._p(out), self._p(a), a.size)
+        return out
+
+    def softmax(self, x):
+        x = x.copy()
+        self.L.orch_ops_softmax(self._p(x), x.size)
+        return x
+
+    def rope(self, q, k, n_heads, n_kv, hd, pos, base):
+        q, k = q.copy(), k.copy()
+        self.L.orch_ops_rope(self._p(q), self._p(k), n_heads, n_kv, hd, pos, base)
+        return q, k
+
+    def argmax(self, x):
+        return int(self.L.orch_ops_argmax(self._p(x), x.size))
+
+    def dot(self, a, b):
+        return float(self.L.orch_ops_dot(self._p(a), self._p(b), a.size))

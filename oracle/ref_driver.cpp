@@ -209,7 +209,9 @@ static int usage() {
         "ref_driver espec <target> <draft> <prompt.bin> <n_gen> <k> <temp> <top_p> <top_k> <pen> <last> <seed> <tokens.bin>\n"
         "ref_driver sample <logits.bin> <temp> <top_p> <top_k> <pen> <last> <seed> <history.bin> <n_draws> <out.bin>\n"
         "ref_driver op <rmsnorm|softmax|silu|rope|argmax|dot> ...\n"
-        "ref_driver bench <model> <draft|-> <prompt.bin> <n_gen> <k> <threads>\n");
+        "ref_driver bench <model> <draft|-> <prompt.bin> <n_gen> <k> <threads>\n"
+        "ref_driver embed <model> <tokens.bin> <out.bin>\n"
+        "ref_driver orkv <model> <prompt.bin> <state.orkv> <logits.bin>\n");
     return 2;
 }
 
@@ -385,6 +387,32 @@ int main(int argc, char** argv) {
             return 0;
         }
         return usage();
+    }
+    if (cmd == "embed" && argc == 5) {  // Model::embed_tokens (core/model.cpp:248-270)
+        Model m;
+        if (!load_model(m, argv[2])) return 1;
+        auto toks = read_bin<int32_t>(argv[3]);
+        auto e = m.embed_tokens(toks);
+        write_bin(argv[4], e.data(), e.size());
+        return 0;
+    }
+    if (cmd == "orkv" && argc == 6) {
+        // prefill all but the last prompt id, save_state; then a second Model
+        // loads the file and decodes the last id: its logits
+        Model m;
+        if (!load_model(m, argv[2])) return 1;
+        auto prompt = read_bin<int32_t>(argv[3]);
+        const int n = (int)prompt.size() - 1;
+        m.reset();
+        m.forward_prefill(prompt.data(), n, 0);
+        if (!m.save_state(argv[4], n)) return 1;
+        Model m2;
+        if (!load_model(m2, argv[2])) return 1;
+        int pos = -1;
+        if (!m2.load_state(argv[4], pos) || pos != n) return 1;
+        const float* lg = m2.forward(prompt.back(), pos);
+        write_bin(argv[5], lg, m2.cfg.n_vocab);
+        return 0;
     }
     if (cmd == "bench" && argc == 8) {
 #ifdef _OPENMP
