@@ -26,8 +26,14 @@ family's HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
 runs (scaled by a copy kernel of known size), read from the committed
 summary in profiles/.
 cpu_baseline: the reference implementation (oracle/_ref, built from the
-reference's sources) on the same two models, bounded sample: prompt 8 ids,
-16 generated tokens, k = 4.
+reference's sources) on the same two models and the same 128-id prompt with
+k = 4, bounded sample: its harness protocol timing the first 32 of the 256
+generated tokens (about 10-30 s on the 16 host threads a one-GPU box gives);
+cores = threads used, host_cpus = os.cpu_count().
+Protocol fields (benchmark/bench_engine.cpp:221-263): step_ms_median (the
+median of the K per-step times) and checksum (FNV-1a 64 of the generated
+ids, equal to the reference's for the same stream); prefill_tok_s: the
+target's batched prefill of the prompt.
 target_greedy_tok_s: the target alone decoding the same tokens greedily
 (graph replay, after the same prefill): at C3 that is the C2 workload
 (BASELINE.json configs[1]).
@@ -36,8 +42,10 @@ blocks and regrouped into the aligned Q8_0_X8 layout) back to back over
 more than 640 MB of distinct weight matrices in rotation (beyond the 256 MB
 Infinity Cache), per type, timed by the same dispatch events.
 
---workload c4 / c5 run BASELINE.json configs[3] / configs[4] instead (the
-bench line stays quoted on C3): C4 = the Engine's stochastic speculative
+--workload c1 / c4 / c5 run BASELINE.json configs[0] / configs[3] /
+configs[4] instead (the bench line stays quoted on C3): C1 = greedy decode of
+128 tokens after a 32-id prompt on the 1B-shape Q8_0 model (its own metric,
+cpu_baseline over the whole workload); C4 = the Engine's stochastic speculative
 loop (each step a whole Engine call, prefill included, reported beside it);
 C5 = speculative greedy after an 8191-id prefill into a 16384-position cache,
 with the verify passes' GQA KV-read GB/s and weight-GEMM GB/s reported
@@ -77,23 +85,41 @@ def ensure_model(name, models_dir):
     return path
 
 
-def cpu_baseline(tgt_path, dft_path, prompt, k):
+def fnv1a(ids):
+    """64-bit FNV-1a over the generated ids as uint32 with the reference
+    harness's constants (benchmark/bench_engine.cpp:233-241): its offset basis
+    is 1469598103934665603, one digit short of the standard 14695981039346656037,
+    and is kept so the checksums equal the reference's."""
+    h = 1469598103934665603
+    for x in np.asarray(ids, np.int64):
+        h = ((h ^ (int(x) & 0xFFFFFFFF)) * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    return f"{h:016x}"
+
+
+def cpu_baseline(tgt_path, dft_path, prompt, k, n_gen, label):
+    """The reference build (oracle/_ref) on the same models and prompt: its
+    harness protocol (untimed prefill, timed generation) for n_gen tokens. The
+    box gives one GPU a share of 16 host threads, so at most 16 are used."""
     if not os.path.exists(REF_DRIVER):
         return None
-    threads = min(16, os.cpu_count() or 1)
+    host_cpus = os.cpu_count() or 1
+    threads = min(16, host_cpus)
     p = os.path.join(os.path.dirname(tgt_path), "cpu_prompt.bin")
-    np.ascontiguousarray(prompt[:8], np.int32).tofile(p)
-    log(f"cpu baseline: reference build, {threads} threads, prompt 8, 16 tokens, k={k}")
-    r = subprocess.run([REF_DRIVER, "bench", tgt_path, dft_path, p, "16", str(k), str(threads)],
+    np.ascontiguousarray(prompt, np.int32).tofile(p)
+    log(f"cpu baseline: reference build, {threads} threads, prompt {len(prompt)}, {n_gen} tokens, k={k}")
+    r = subprocess.run([REF_DRIVER, "bench", tgt_path, dft_path or "-", p, str(n_gen), str(k), str(threads)],
                        capture_output=True, text=True, timeout=900)
     m = re.search(r"REF_BENCH (\{.*\})", r.stderr)
     if r.returncode != 0 or not m:
         log(f"cpu baseline failed: {r.stderr[-500:]}")
         return None
     d = json.loads(m.group(1))
-    return {"value": round(d["tok_s"], 4), "unit": "tok/s", "cores": d["threads"], "kind": "reference",
-            "sample": f"reference build (oracle/_ref), same C3 target+draft, prompt 8 ids, {d['tokens']} generated "
-                      f"tokens, k={k}, accepted {d['accepted']}/{d['proposed']}"}
+    return {"value": round(d["tok_s"], 4), "unit": "tok/s", "cores": d["threads"], "host_cpus": host_cpus,
+            "kind": "reference", "checksum": d["checksum"],
+            "sample": f"reference build (oracle/_ref) on the {label} models and prompt ({len(prompt)} ids"
+                      f"{', k=' + str(k) if dft_path else ''}); the first {d['tokens']} generated tokens, timed "
+                      f"after an untimed prefill"
+                      + (f"; accepted {d['accepted']}/{d['proposed']}" if dft_path else "")}
 
 
 def measured_traffic(kernel):
@@ -112,6 +138,8 @@ def measured_traffic(kernel):
 # The bench line is quoted on C3 (BASELINE.json's metric config); C4 and C5
 # (configs[3], configs[4]) run with --workload for their own measurements.
 WORKLOADS = {
+    "c1": dict(tgt="c1", dft=None, n_prompt=32, n_gen=128, k=0, ctx=512, mode="greedy_only", prompt_seed=1234,
+               desc="C1 greedy decode: 1B-shape all-Q8_0 model, tied head"),
     "c3": dict(tgt="c2", dft="c3d", n_prompt=128, n_gen=256, k=4, ctx=2048, mode="greedy", prompt_seed=1234,
                desc="C3 spec greedy: 3B-shape Q4_K_M target + 8-layer Q8_0 draft"),
     "c4": dict(tgt="c4", dft="c4d", n_prompt=256, n_gen=512, k=6, ctx=4096, mode="engine", prompt_seed=4321,
@@ -189,7 +217,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3",
-                    help="c3 (the metric's config, default), c4 or c5")
+                    help="c3 (the metric's config, default), c1, c4 or c5")
     ap.add_argument("--n-gen", type=int, default=0, help="generated tokens (default: the workload's)")
     ap.add_argument("--models-dir", default=os.environ.get("ORC_MODEL_DIR", "/tmp/orc_models"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -212,7 +240,7 @@ def main():
     import orc
 
     tgt_path = ensure_model(W["tgt"], a.models_dir)
-    dft_path = ensure_model(W["dft"], a.models_dir)
+    dft_path = ensure_model(W["dft"], a.models_dir) if W["dft"] else None
     dev = orc.Device(0)
     name, n_cu, hbm = dev.info()
     log(f"device {name}, {n_cu} CUs, {hbm / 1e9:.0f} GB; workload {a.workload}")
@@ -228,28 +256,44 @@ def main():
         dst.free()
     t0 = time.time()
     tgt = orc.Model(tgt_path, ctx)
-    dft = orc.Model(dft_path, ctx)
-    log(f"loaded target ({tgt.weight_bytes() / 1e9:.3f} GB/token) and draft ({dft.weight_bytes() / 1e9:.3f} "
-        f"GB/token) in {time.time() - t0:.1f}s")
+    dft = orc.Model(dft_path, ctx) if dft_path else None
+    log(f"loaded target ({tgt.weight_bytes() / 1e9:.3f} GB/token)" +
+        (f" and draft ({dft.weight_bytes() / 1e9:.3f} GB/token)" if dft else "") + f" in {time.time() - t0:.1f}s")
     prompt = np.random.default_rng(W["prompt_seed"]).integers(0, tgt.n_vocab, n_prompt).astype(np.int32)
     if a.no_graphs:
         orc.load_host_lib().orch_set_graphs(0)
     engine = W["mode"] == "engine"
+    plain = W["mode"] == "greedy_only"
 
     def run(n, prefill):
         if engine:  # Engine::generate prefills both models on every call (core/engine.cpp:115-125)
             return tgt.spec_engine(dft, prompt, n, k, *SAMPLER)
+        if plain:  # the reference harness's greedy decode (benchmark/bench_engine.cpp:221-243)
+            return tgt.greedy(prompt, n, prefill=prefill), {"accepted": 0, "proposed": 0, "passes": n}
         return tgt.spec_greedy(dft, prompt, n, k, prefill=prefill)
 
     # exactness: spec greedy must reproduce the target's greedy stream; the
     # Engine loop samples, so its stream must reproduce itself (fixed seed)
     greedy = None if engine else tgt.greedy(prompt, n_gen, prefill=True)
+    prefill_tok_s = None
+    if not engine:  # the batched prefill of the prompt (all ids but the last), target alone
+        H0 = orc.load_host_lib()
+        H0.orch_sync()
+        tp = time.perf_counter()
+        tgt.forward_batch(prompt[:-1], 0, logits=False)
+        H0.orch_sync()
+        prefill_tok_s = (n_prompt - 1) / (time.perf_counter() - tp)
     toks, st = run(n_gen, True)  # prefills both models
     expect = toks if engine else greedy
     exact = bool(np.array_equal(toks, expect))
     # the reference implementation's own streams on these models (tests/golden/c3_ref.npz)
     ref_identical = None
     fix_path = os.path.join(ROOT, "tests", "golden", "c3_ref.npz")
+    c1_fix = os.path.join(ROOT, "tests", "golden", "c1_ref.npz")
+    if a.workload == "c1" and os.path.exists(c1_fix):
+        fix = np.load(c1_fix)
+        if np.array_equal(prompt, fix["prompt"]) and n_gen == len(fix["greedy_tokens"]):
+            ref_identical = bool(np.array_equal(greedy, fix["greedy_tokens"]))
     if a.workload == "c3" and os.path.exists(fix_path):
         fix = np.load(fix_path)
         if (n_prompt, n_gen, k) == (len(fix["prompt"]), len(fix["spec_tokens"]), int(fix["k"][0])) and \
@@ -263,7 +307,7 @@ def main():
 
     L, H = orc.load_hip_lib(), orc.load_host_lib()
     greedy_tok_s = None
-    if not engine:  # the target alone, greedy (C3's target is C2), KV from the prefill
+    if not engine and not plain:  # the target alone, greedy (C3's target is C2)
         H.orch_sync()
         tg = time.perf_counter()
         g2 = tgt.greedy(prompt, n_gen, prefill=False)
@@ -271,16 +315,20 @@ def main():
         greedy_tok_s = n_gen / (time.perf_counter() - tg)
         exact &= bool(np.array_equal(g2, greedy))
     tot = {"accepted": 0, "proposed": 0, "passes": 0}
+    step_s = []
     H.orch_sync()
     t0 = time.perf_counter()
     for _ in range(a.steps):
-        toks, st = run(n_gen, False)
+        ts = time.perf_counter()
+        toks, st = run(n_gen, False)  # returns after the step's ids reached the host
+        step_s.append(time.perf_counter() - ts)
         exact &= bool(np.array_equal(toks, expect))
         for key in tot:
             tot[key] += st[key]
     H.orch_sync()
     dt = time.perf_counter() - t0
     value = a.steps * n_gen / dt
+    checksum = fnv1a(toks)
     prefill_ms = None
     if engine:  # the prefill each Engine call repeats, timed on its own
         H.orch_sync()
@@ -329,12 +377,17 @@ def main():
                         "avg_launch_us": round(1e3 * f["ms"] / f["launches"], 3),
                         "bytes_per_launch": round(f["bytes"] / f["launches"]),
                         "timing": f"start/stop HIP events of each launch's dispatch over {a.prof_tokens} tokens of "
-                                  f"host-launched spec rounds"}
+                                  f"host-launched rounds of the workload"}
 
     micro = None if a.no_gemv_micro else gemv_microbench(dev)
-    cpu = None if (a.no_cpu_baseline or a.workload != "c3") else cpu_baseline(tgt_path, dft_path, prompt, k)
+    cpu = None
+    if not a.no_cpu_baseline and a.workload in ("c1", "c3"):
+        # bounded sample: C3's full prompt and k, its first 32 tokens (~10-30 s on 16 threads); C1 whole
+        cpu = cpu_baseline(tgt_path, dft_path, prompt, k, 32 if a.workload == "c3" else n_gen, a.workload.upper())
+    metric = ("greedy decode tok/s (1B Q8_0)" if plain else
+              "spec-decode tok/s (3B Q4_K, k=4); quant-GEMV HBM GB/s vs peak")
     out = {
-        "metric": "spec-decode tok/s (3B Q4_K, k=4); quant-GEMV HBM GB/s vs peak",
+        "metric": metric,
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(1e3 * dt / a.steps, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
@@ -343,7 +396,12 @@ def main():
         "acceptance": round(tot["accepted"] / max(1, tot["proposed"]), 4),
         "target_passes_per_token": round(tot["passes"] / max(1, a.steps * n_gen), 4),
         "exact_vs_greedy" if not engine else "stream_reproducible": exact,
+        "step_ms_median": round(1e3 * float(np.median(step_s)), 3),
+        "checksum": checksum,
+        "protocol": "benchmark/bench_engine.cpp:221-263: untimed prefill, warm-up steps discarded, per-step times "
+                    "(median reported beside the mean-based value), FNV-1a 64 of the generated ids",
         "target_greedy_tok_s": None if greedy_tok_s is None else round(greedy_tok_s, 2),
+        "prefill_tok_s": None if prefill_tok_s is None else round(prefill_tok_s, 1),
         "reference_stream_identical": ref_identical,
         "roofline": roofline, "cpu_baseline": cpu,
         "gemv_microbench": micro,
