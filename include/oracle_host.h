@@ -114,6 +114,36 @@ void orch_ops_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim
 int orch_ops_argmax(const float* x, int n);
 float orch_ops_dot(const float* a, const float* b, int n);
 
+/* ── Engine (core/engine.hpp:35-76) and Tokenizer (core/tokenizer.hpp:17-44) ── */
+typedef struct orch_engine orch_engine;
+/* Engine::load, then Engine::load_draft when draft_path is not NULL. */
+orch_engine* orch_engine_new(const char* model_path, const char* draft_path);
+void orch_engine_free(orch_engine* e);
+const char* orch_engine_error(const orch_engine* e);
+/* A fixed sampler seed for the following generate calls. */
+void orch_engine_set_seed(orch_engine* e, uint64_t seed);
+/* Engine::generate over n_msgs (roles[i], contents[i]) with GenParams
+ * {n_predict, temperature, top_p, repeat_penalty, repeat_last_n}. The on_token
+ * pieces go to out as (uint32 byte length, bytes) records; returns the bytes
+ * written, or -1 (the pieces did not fit cap, or the engine failed). */
+int64_t orch_engine_generate(orch_engine* e, const char* const* roles, const char* const* contents, int n_msgs,
+                             int n_predict, float temperature, float top_p, float repeat_penalty, int repeat_last_n,
+                             uint8_t* out, int64_t cap);
+/* Engine::embed: embed_dim floats into out. */
+int orch_engine_embed(orch_engine* e, const char* text, float* out);
+/* A Tokenizer loaded from a GGUF's metadata alone (GGUFParser::load_meta:
+ * no weights uploaded, no GPU needed). */
+typedef struct orch_tokenizer orch_tokenizer;
+orch_tokenizer* orch_tokenizer_load(const char* gguf_path);
+void orch_tokenizer_free(orch_tokenizer* t);
+/* Tokenizer::encode of text (len bytes): ids written (at most cap), or -1. */
+int orch_tok_encode(orch_tokenizer* t, const char* text, int64_t len, int add_bos, int32_t* out, int cap);
+/* Tokenizer::decode_one: the piece's byte length (written up to cap bytes). */
+int orch_tok_decode_one(orch_tokenizer* t, int32_t id, char* out, int cap);
+/* Tokenizer::special_id; bos_id (which = 0) or eos_id (which = 1). */
+int32_t orch_tok_special_id(orch_tokenizer* t, const char* name);
+int32_t orch_tok_bos_eos(orch_tokenizer* t, int which);
+
 /* ── Sampler (core/sampler.hpp:24-48) on a device state ──────────────────────── */
 typedef struct orch_sampler orch_sampler;
 orch_sampler* orch_sampler_new(float temperature, float top_p, int top_k, float repeat_pen, int repeat_last,

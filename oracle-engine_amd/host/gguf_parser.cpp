@@ -89,7 +89,11 @@ void read_value(Cursor& c, uint32_t kind, MetaValue& v) {
 }
 }  // namespace
 
-bool GGUFParser::load(const std::string& path) {
+bool GGUFParser::load(const std::string& path) { return open_file(path, true); }
+
+bool GGUFParser::load_meta(const std::string& path) { return open_file(path, false); }
+
+bool GGUFParser::open_file(const std::string& path, bool upload) {
     close();
     fd_ = ::open(path.c_str(), O_RDONLY);
     if (fd_ < 0) { std::fprintf(stderr, "[GGUFParser] cannot open %s\n", path.c_str()); return false; }
@@ -114,6 +118,7 @@ bool GGUFParser::load(const std::string& path) {
             return false;
         }
     }
+    if (!upload) return true;
     void* d = nullptr;
     if (orc_init(0) != 0 || orc_upload(map_ + data_start_, fsize_ - data_start_, &d) != 0) {
         std::fprintf(stderr, "[GGUFParser] upload failed: %s\n", orc_last_error());

@@ -63,6 +63,10 @@ public:
 
     // Parses and uploads; false (with a message on stderr) on any error.
     bool load(const std::string& path);
+    // Parses the header, metadata and tensor table only, with the weights
+    // left in the file mapping (is_mmap_only(); the device drop-ins then
+    // refuse): enough for a Tokenizer, and needs no GPU.
+    bool load_meta(const std::string& path);
     void close();
     bool is_open() const { return map_ != nullptr; }
 
@@ -132,6 +136,7 @@ private:
     mutable size_t scr_cap_ = 0;
 
     bool parse();
+    bool open_file(const std::string& path, bool upload);
     bool gemm_dev(const std::string& name, const TensorInfo& ti, float* out, const float* x, int n_tokens, int j0,
                   int j1, int n_in) const;
     void* scratch(size_t bytes) const;  // caller holds scr_mu_

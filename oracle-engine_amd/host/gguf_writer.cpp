@@ -163,6 +163,9 @@ void GGUFWriter::add_f32(const std::string& k, float v) {
 void GGUFWriter::add_str_array(const std::string& k, const std::vector<std::string>& v) {
     KV kv; kv.key = k; kv.kind = 9; kv.arr = v; kvs.push_back(kv);
 }
+void GGUFWriter::add_i32_array(const std::string& k, const std::vector<int32_t>& v) {
+    KV kv; kv.key = k; kv.kind = 9; kv.ai = v; kvs.push_back(kv);
+}
 void GGUFWriter::add_tensor(const std::string& name, std::vector<uint64_t> shape, GGMLType type,
                             std::function<void(int64_t, int64_t, uint8_t*)> fill) {
     Tensor t;
@@ -214,9 +217,15 @@ bool GGUFWriter::write(const std::string& path, bool verbose) {
             case 4: o.u32((uint32_t)kv.u); break;
             case 6: o.raw(&kv.f, 4); break;
             case 9:
-                o.u32(8);
-                o.u64(kv.arr.size());
-                for (const auto& s : kv.arr) o.str(s);
+                if (kv.arr.empty() && !kv.ai.empty()) {
+                    o.u32(5);
+                    o.u64(kv.ai.size());
+                    o.raw(kv.ai.data(), kv.ai.size() * 4);
+                } else {
+                    o.u32(8);
+                    o.u64(kv.arr.size());
+                    for (const auto& s : kv.arr) o.str(s);
+                }
                 break;
         }
     }

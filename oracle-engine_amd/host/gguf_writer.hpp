@@ -33,7 +33,8 @@ struct GGUFWriter {
         std::string s;                  // kind 8
         uint64_t u = 0;                 // kinds 4, 10
         float f = 0.f;                  // kind 6
-        std::vector<std::string> arr;   // kind 9 (array of strings)
+        std::vector<std::string> arr;   // kind 9, element type 8 (strings)
+        std::vector<int32_t> ai;        // kind 9, element type 5 (int32), when arr is empty
     };
     struct Tensor {
         std::string name;
@@ -51,6 +52,7 @@ struct GGUFWriter {
     void add_u32(const std::string& k, uint32_t v);
     void add_f32(const std::string& k, float v);
     void add_str_array(const std::string& k, const std::vector<std::string>& v);
+    void add_i32_array(const std::string& k, const std::vector<int32_t>& v);
     void add_tensor(const std::string& name, std::vector<uint64_t> shape, GGMLType type,
                     std::function<void(int64_t, int64_t, uint8_t*)> fill);
     // Writes the file; returns false on an I/O error.

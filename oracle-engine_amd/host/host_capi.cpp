@@ -1,11 +1,13 @@
 // C API of the host library (include/oracle_host.h).
 #include "oracle_host.h"
 
+#include "engine.hpp"
 #include "model.hpp"
 #include "ops.hpp"
 #include "sampler.hpp"
 #include "spec.hpp"
 
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -291,4 +293,98 @@ extern "C" void orch_sampler_reset(orch_sampler* s) {
 extern "C" void orch_sampler_set_params(orch_sampler* s, float temperature, float top_p, int top_k,
                                         float repeat_pen, int repeat_last) {
     if (s) s->s.set_params(sparams(temperature, top_p, top_k, repeat_pen, repeat_last));
+}
+
+// ── Engine and Tokenizer ─────────────────────────────────────────────────────
+struct orch_engine {
+    Engine e;
+    std::string err;
+};
+
+extern "C" orch_engine* orch_engine_new(const char* model_path, const char* draft_path) {
+    auto h = std::make_unique<orch_engine>();
+    if (!model_path || !h->e.load(model_path) || (draft_path && !h->e.load_draft(draft_path))) {
+        g_load_err = h->e.last_error();
+        return nullptr;
+    }
+    return h.release();
+}
+extern "C" void orch_engine_free(orch_engine* e) { delete e; }
+extern "C" const char* orch_engine_error(const orch_engine* e) {
+    return e ? e->e.last_error().c_str() : g_load_err.c_str();
+}
+extern "C" void orch_engine_set_seed(orch_engine* e, uint64_t seed) {
+    if (e) e->e.set_seed(seed);
+}
+
+extern "C" int64_t orch_engine_generate(orch_engine* h, const char* const* roles, const char* const* contents,
+                                        int n_msgs, int n_predict, float temperature, float top_p,
+                                        float repeat_penalty, int repeat_last_n, uint8_t* out, int64_t cap) {
+    if (!h || n_msgs < 0 || (n_msgs && (!roles || !contents)) || !out || cap < 0) return -1;
+    std::vector<Message> msgs;
+    for (int i = 0; i < n_msgs; ++i) msgs.push_back({roles[i], contents[i]});
+    GenParams gp;
+    gp.n_predict = n_predict;
+    gp.temperature = temperature;
+    gp.top_p = top_p;
+    gp.repeat_penalty = repeat_penalty;
+    gp.repeat_last_n = repeat_last_n;
+    int64_t w = 0;
+    bool fit = true;
+    const std::string resp = h->e.generate(msgs, gp, [&](const std::string& p) {
+        const uint32_t n = (uint32_t)p.size();
+        if (w + 4 + (int64_t)n > cap) {
+            fit = false;
+            return;
+        }
+        std::memcpy(out + w, &n, 4);
+        std::memcpy(out + w + 4, p.data(), n);
+        w += 4 + n;
+    });
+    if (!fit) return -1;
+    // a refused prompt is an empty reply, as the reference's; a device failure is an error
+    if (!h->e.last_error().empty() && h->e.last_error() != "prompt too long for the context") return -1;
+    return w;
+}
+
+extern "C" int orch_engine_embed(orch_engine* h, const char* text, float* out) {
+    if (!h || !text || !out) return -1;
+    const std::vector<float> v = h->e.embed(text);
+    if (v.empty()) return -1;
+    std::memcpy(out, v.data(), v.size() * 4);
+    return 0;
+}
+
+struct orch_tokenizer {
+    GGUFParser g;
+    Tokenizer t;
+};
+
+extern "C" orch_tokenizer* orch_tokenizer_load(const char* path) {
+    auto h = std::make_unique<orch_tokenizer>();
+    if (!path || !h->g.load_meta(path) || !h->t.load(h->g)) return nullptr;
+    return h.release();
+}
+extern "C" void orch_tokenizer_free(orch_tokenizer* t) { delete t; }
+
+extern "C" int orch_tok_encode(orch_tokenizer* h, const char* text, int64_t len, int add_bos, int32_t* out, int cap) {
+    if (!h || (len && !text) || len < 0 || !out) return -1;
+    const auto ids = h->t.encode(std::string(text, (size_t)len), add_bos != 0);
+    if ((int64_t)ids.size() > cap) return -1;
+    std::memcpy(out, ids.data(), ids.size() * 4);
+    return (int)ids.size();
+}
+
+extern "C" int orch_tok_decode_one(orch_tokenizer* h, int32_t id, char* out, int cap) {
+    if (!h || !out) return -1;
+    const std::string p = h->t.decode_one(id);
+    std::memcpy(out, p.data(), std::min<size_t>(p.size(), (size_t)std::max(cap, 0)));
+    return (int)p.size();
+}
+
+extern "C" int32_t orch_tok_special_id(orch_tokenizer* h, const char* name) {
+    return h && name ? h->t.special_id(name) : -1;
+}
+extern "C" int32_t orch_tok_bos_eos(orch_tokenizer* h, int which) {
+    return h ? (which ? h->t.eos_id() : h->t.bos_id()) : -1;
 }

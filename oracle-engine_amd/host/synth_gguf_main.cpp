@@ -1,10 +1,11 @@
 // synth_gguf — writes one of the synthetic benchmark/test models.
-//   synth_gguf <preset> <out.gguf> [-v]
+//   synth_gguf <preset> <out.gguf> [-v] [--vocab [--eot-id N]]
 //   synth_gguf --list
 #include "synth_model.hpp"
 
 #include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -14,7 +15,7 @@ int main(int argc, char** argv) {
         return 0;
     }
     if (argc < 3) {
-        std::fprintf(stderr, "usage: synth_gguf <preset> <out.gguf> [-v] | --list\n");
+        std::fprintf(stderr, "usage: synth_gguf <preset> <out.gguf> [-v] [--vocab [--eot-id N]] | --list\n");
         return 2;
     }
     orc::SynthSpec s;
@@ -22,7 +23,16 @@ int main(int argc, char** argv) {
         std::fprintf(stderr, "unknown preset '%s'\n", argv[1]);
         return 2;
     }
-    bool verbose = argc > 3 && std::strcmp(argv[3], "-v") == 0;
+    bool verbose = false;
+    for (int i = 3; i < argc; ++i) {
+        if (std::strcmp(argv[i], "-v") == 0) verbose = true;
+        else if (std::strcmp(argv[i], "--vocab") == 0) s.vocab_stub = true;
+        else if (std::strcmp(argv[i], "--eot-id") == 0 && i + 1 < argc) s.eot_id = std::atoi(argv[++i]);
+        else {
+            std::fprintf(stderr, "unknown option %s\n", argv[i]);
+            return 2;
+        }
+    }
     auto t0 = std::chrono::steady_clock::now();
     std::string tmp = std::string(argv[2]) + ".partial";
     if (!orc::synth_write(s, tmp, verbose) || std::rename(tmp.c_str(), argv[2]) != 0) {

@@ -1,6 +1,7 @@
 #include "synth_model.hpp"
 #include "gguf_writer.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <map>
@@ -117,6 +118,126 @@ std::vector<std::string> synth_preset_names() {
             "t-qwen-d"};
 }
 
+// ── tokenizer stub ──────────────────────────────────────────────────────────
+
+static std::string utf8_of(uint32_t cp) {
+    std::string o;
+    if (cp < 0x80) {
+        o += (char)cp;
+    } else if (cp < 0x800) {
+        o += (char)(0xC0 | (cp >> 6));
+        o += (char)(0x80 | (cp & 0x3F));
+    } else {
+        o += (char)(0xE0 | (cp >> 12));
+        o += (char)(0x80 | ((cp >> 6) & 0x3F));
+        o += (char)(0x80 | (cp & 0x3F));
+    }
+    return o;
+}
+
+// GPT-2's byte -> symbol map (OpenAI's published bytes_to_unicode): printable
+// Latin-1 bytes map to themselves, the other 68 bytes to U+0100 upwards in
+// byte order.
+static std::vector<std::string> byte_symbols() {
+    std::vector<std::string> sym(256);
+    int next = 256;
+    for (int b = 0; b < 256; ++b) {
+        const bool keep = (b >= 33 && b <= 126) || (b >= 0xA1 && b <= 0xAC) || (b >= 0xAE && b <= 0xFF);
+        sym[b] = utf8_of(keep ? (uint32_t)b : (uint32_t)next++);
+    }
+    return sym;
+}
+
+// Text the stub's merges are learned from (spaces attach to the next word,
+// as the reference's pre-tokenizer splits).
+static const char* kStubCorpus =
+    "the quick brown fox jumps over the lazy dog and then the dog sleeps in the sun while the fox runs "
+    "into the green forest where the trees are tall and the river is cold there is a small house near "
+    "the river and the people who live there are kind they speak to the animals and the animals answer "
+    "in their own language the system is an assistant that helps the user the user asks a question and "
+    "the assistant gives an answer with care and patience every answer is short and true";
+
+VocabStub make_vocab_stub(const SynthSpec& s) {
+    VocabStub v;
+    const int V = s.vocab;
+    const std::vector<std::string> sym = byte_symbols();
+    v.tokens.assign(V, std::string());
+    v.types.assign(V, 1);
+    for (int b = 0; b < 256 && b < V; ++b) v.tokens[b] = sym[b];
+    // words of the corpus as symbol sequences
+    std::vector<std::vector<std::string>> words;
+    {
+        std::string cur;
+        auto flush = [&] {
+            if (cur.empty()) return;
+            std::vector<std::string> w;
+            for (unsigned char c : cur) w.push_back(sym[c]);
+            words.push_back(w);
+            cur.clear();
+        };
+        for (const char* p = kStubCorpus; *p; ++p) {
+            if (*p == ' ') flush();
+            cur += *p;
+        }
+        flush();
+    }
+    // greedy pair merges: the most frequent adjacent pair, ties by the smaller key
+    const int n_merge = std::max(0, std::min(300, V - 256 - 32));
+    int next_id = 256;
+    for (int m = 0; m < n_merge; ++m) {
+        std::map<std::string, int> cnt;
+        for (const auto& w : words)
+            for (size_t i = 0; i + 1 < w.size(); ++i) ++cnt[w[i] + " " + w[i + 1]];
+        std::string best;
+        int bc = 0;
+        for (const auto& kv : cnt)
+            if (kv.second > bc) {
+                bc = kv.second;
+                best = kv.first;
+            }
+        if (bc < 2) break;
+        const size_t sp = best.find(' ');
+        const std::string a = best.substr(0, sp), b = best.substr(sp + 1);
+        v.merges.push_back(best);
+        v.tokens[next_id++] = a + b;
+        for (auto& w : words) {
+            std::vector<std::string> o;
+            for (size_t i = 0; i < w.size(); ++i) {
+                if (i + 1 < w.size() && w[i] == a && w[i + 1] == b) {
+                    o.push_back(a + b);
+                    ++i;
+                } else {
+                    o.push_back(w[i]);
+                }
+            }
+            w.swap(o);
+        }
+    }
+    for (int i = next_id; i < V; ++i) v.tokens[i] = "<unused" + std::to_string(i) + ">";
+    // chat special tokens (control type 3) at the architecture's usual ids,
+    // or near the end of a small vocabulary
+    std::vector<std::pair<std::string, int>> sp;
+    const bool qwen = s.arch.rfind("qwen", 0) == 0;
+    if (qwen) {
+        const int base = V >= 151646 ? 151643 : V - 16;
+        sp = {{"<|endoftext|>", base}, {"<|im_start|>", base + 1}, {"<|im_end|>", base + 2}};
+    } else {
+        const int base = V >= 128256 ? 128000 : V - 16;
+        sp = {{"<|begin_of_text|>", base}, {"<|end_of_text|>", base + 1}, {"<|start_header_id|>", base + 6},
+              {"<|end_header_id|>", base + 7}, {"<|eot_id|>", base + 9}};
+    }
+    const std::string eot_name = qwen ? "<|im_end|>" : "<|eot_id|>";
+    for (auto& t : sp) {
+        if (t.first == eot_name && s.eot_id >= 0 && s.eot_id < V) t.second = s.eot_id;
+        v.tokens[t.second] = t.first;
+        v.types[t.second] = 3;
+    }
+    v.bos = sp[0].second;
+    for (const auto& t : sp)
+        if (t.first == eot_name) v.eos = t.second;
+    return v;
+}
+
 bool synth_write(const SynthSpec& s, const std::string& path, bool verbose) {
     GGUFWriter w;
     const std::string a = s.arch;
@@ -133,6 +254,15 @@ bool synth_write(const SynthSpec& s, const std::string& path, bool verbose) {
     w.add_f32(a + ".rope.freq_base", s.rope_theta);
     w.add_f32(a + ".attention.layer_norm_rms_epsilon", s.rms_eps);
     w.add_u32(a + ".vocab_size", (uint32_t)s.vocab);
+    if (s.vocab_stub) {
+        const VocabStub v = make_vocab_stub(s);
+        w.add_str("tokenizer.ggml.model", "gpt2");
+        w.add_str_array("tokenizer.ggml.tokens", v.tokens);
+        w.add_i32_array("tokenizer.ggml.token_type", v.types);
+        w.add_str_array("tokenizer.ggml.merges", v.merges);
+        w.add_u32("tokenizer.ggml.bos_token_id", (uint32_t)v.bos);
+        w.add_u32("tokenizer.ggml.eos_token_id", (uint32_t)v.eos);
+    }
 
     const uint64_t seed = s.seed;
     const int D = s.d_model, NQ = s.n_heads * s.head_dim, NKV = s.n_kv_heads * s.head_dim, FF = s.ffn;

@@ -31,7 +31,24 @@ struct SynthSpec {
     // When true, output.weight holds the same float weights as token_embd
     // (a draft that owns a re-quantized copy of its target's tied head).
     bool head_from_embd = false;
+    // Tokenizer metadata stub (tokenizer.ggml.*): a byte-level BPE vocabulary
+    // the reference's Tokenizer (core/tokenizer.cpp:41-78) loads: the 256
+    // byte symbols, merges learned from a fixed text, the architecture's chat
+    // special tokens, the rest filler. Off by default (the file then equals
+    // the one the reference fixtures were made from).
+    bool vocab_stub = false;
+    // With the stub: the id of the end-of-turn token (<|eot_id|>, qwen2:
+    // <|im_end|>) instead of its usual place; -1 keeps it.
+    int eot_id = -1;
 };
+
+// The stub's tokens, types, merges, bos / eos ids for a spec (exposed for tests).
+struct VocabStub {
+    std::vector<std::string> tokens, merges;
+    std::vector<int32_t> types;
+    int32_t bos = 0, eos = 0;
+};
+VocabStub make_vocab_stub(const SynthSpec& s);
 
 // Named presets: the five benchmark configurations (c1..c5, c3d/c4d drafts)
 // and small test models (t-*). Returns false for an unknown name.

@@ -231,6 +231,20 @@ HOST_ABI = [
     ("orch_ops_rope", None, [_fp, _fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
     ("orch_ops_argmax", C.c_int, [_fp, C.c_int]),
     ("orch_ops_dot", C.c_float, [_fp, _fp, C.c_int]),
+    ("orch_engine_new", _vp, [C.c_char_p, C.c_char_p]),
+    ("orch_engine_free", None, [_vp]),
+    ("orch_engine_error", C.c_char_p, [_vp]),
+    ("orch_engine_set_seed", None, [_vp, C.c_uint64]),
+    ("orch_engine_generate", C.c_int64, [_vp, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_int, C.c_int,
+                                         C.c_float, C.c_float, C.c_float, C.c_int, C.POINTER(C.c_uint8),
+                                         C.c_int64]),
+    ("orch_engine_embed", C.c_int, [_vp, C.c_char_p, _fp]),
+    ("orch_tokenizer_load", _vp, [C.c_char_p]),
+    ("orch_tokenizer_free", None, [_vp]),
+    ("orch_tok_encode", C.c_int, [_vp, C.c_char_p, C.c_int64, C.c_int, _ip, C.c_int]),
+    ("orch_tok_decode_one", C.c_int, [_vp, C.c_int32, C.c_char_p, C.c_int]),
+    ("orch_tok_special_id", C.c_int32, [_vp, C.c_char_p]),
+    ("orch_tok_bos_eos", C.c_int32, [_vp, C.c_int]),
     ("orch_sampler_new", _vp, [C.c_float, C.c_float, C.c_int, C.c_float, C.c_int, C.c_uint64]),
     ("orch_sampler_free", None, [_vp]),
     ("orch_sampler_sample", C.c_int32, [_vp, _fp, C.c_int]),
@@ -449,6 +463,91 @@ class Sampler:
         if getattr(self, "h", None):
             self.L.orch_sampler_free(self.h)
             self.h = None
+
+
+def split_pieces(buf):
+    """(uint32 length, bytes) records -> list of bytes."""
+    out, i = [], 0
+    while i < len(buf):
+        n = int.from_bytes(buf[i:i + 4], "little")
+        out.append(bytes(buf[i + 4:i + 4 + n]))
+        i += 4 + n
+    return out
+
+
+class Tokenizer:
+    """Tokenizer (core/tokenizer.hpp:17-44) from a GGUF's metadata; host only."""
+
+    def __init__(self, path):
+        self.L = load_host_lib()
+        self.h = self.L.orch_tokenizer_load(str(path).encode())
+        if not self.h:
+            raise OrcError(f"cannot load a tokenizer from {path}")
+
+    def encode(self, text, add_bos=True):
+        b = text if isinstance(text, bytes) else text.encode()
+        out = np.zeros(len(b) + 8, np.int32)
+        n = self.L.orch_tok_encode(self.h, b, len(b), int(add_bos), out.ctypes.data_as(_ip), out.size)
+        if n < 0:
+            raise OrcError("encode failed")
+        return out[:n].copy()
+
+    def decode_one(self, tok):
+        buf = C.create_string_buffer(256)
+        n = self.L.orch_tok_decode_one(self.h, int(tok), buf, 256)
+        if n > 256:
+            buf = C.create_string_buffer(n)
+            n = self.L.orch_tok_decode_one(self.h, int(tok), buf, n)
+        return buf.raw[:n]
+
+    def special_id(self, name):
+        return int(self.L.orch_tok_special_id(self.h, name.encode()))
+
+    def bos_eos(self):
+        return int(self.L.orch_tok_bos_eos(self.h, 0)), int(self.L.orch_tok_bos_eos(self.h, 1))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.orch_tokenizer_free(self.h)
+            self.h = None
+
+
+class Engine:
+    """Engine (core/engine.hpp:35-76) on the device path."""
+
+    def __init__(self, model_path, draft_path=None, seed=None):
+        self.L = load_host_lib()
+        self.h = self.L.orch_engine_new(str(model_path).encode(), str(draft_path).encode() if draft_path else None)
+        if not self.h:
+            raise OrcError(f"engine load failed: {self.L.orch_engine_error(None).decode()}")
+        if seed is not None:
+            self.L.orch_engine_set_seed(self.h, int(seed))
+
+    def generate(self, messages, n_predict=256, temperature=0.7, top_p=0.9, repeat_penalty=1.15, repeat_last_n=64):
+        """The on_token pieces (bytes) in order; their concatenation is the reply."""
+        roles = (C.c_char_p * len(messages))(*[r.encode() for r, _ in messages])
+        conts = (C.c_char_p * len(messages))(*[c.encode() for _, c in messages])
+        cap = 64 * (n_predict + 16) + 4096
+        buf = (C.c_uint8 * cap)()
+        n = self.L.orch_engine_generate(self.h, roles, conts, len(messages), n_predict, temperature, top_p,
+                                        repeat_penalty, repeat_last_n, buf, cap)
+        if n < 0:
+            raise OrcError(f"generate failed: {self.L.orch_engine_error(self.h).decode()}")
+        return split_pieces(bytes(buf)[:n])
+
+    def embed(self, text, dim):
+        out = np.zeros(dim, np.float32)
+        if self.L.orch_engine_embed(self.h, text.encode(), out.ctypes.data_as(_fp)):
+            raise OrcError("embed failed")
+        return out
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.orch_engine_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 class HostOps:

@@ -6,8 +6,10 @@
 // (GGUFParser, Model, Sampler, ops); the decode / spec loops below restate the
 // reference harness protocol (benchmark/bench_engine.cpp:221-263, 300-363) and
 // the Engine's stochastic spec loop (core/engine.cpp:150-240) with a fixed seed.
+#include "core/engine.hpp"
 #include "core/gguf_parser.hpp"
 #include "core/model.hpp"
+#include "core/tokenizer.hpp"
 #include "core/ops.hpp"
 #include "core/sampler.hpp"
 
@@ -211,7 +213,10 @@ static int usage() {
         "ref_driver op <rmsnorm|softmax|silu|rope|argmax|dot> ...\n"
         "ref_driver bench <model> <draft|-> <prompt.bin> <n_gen> <k> <threads>\n"
         "ref_driver embed <model> <tokens.bin> <out.bin>\n"
-        "ref_driver orkv <model> <prompt.bin> <state.orkv> <logits.bin>\n");
+        "ref_driver orkv <model> <prompt.bin> <state.orkv> <logits.bin>\n"
+        "ref_driver tokenize <model> <text.bin> <add_bos> <ids.bin>\n"
+        "ref_driver detok <model> <ids.bin> <pieces.bin>\n"
+        "ref_driver engine <model> <draft|-> <n_predict> <temp> <messages.bin> <pieces.bin>\n");
     return 2;
 }
 
@@ -412,6 +417,63 @@ int main(int argc, char** argv) {
         if (!m2.load_state(argv[4], pos) || pos != n) return 1;
         const float* lg = m2.forward(prompt.back(), pos);
         write_bin(argv[5], lg, m2.cfg.n_vocab);
+        return 0;
+    }
+    // pieces.bin: each piece as a uint32 byte length, then its bytes
+    auto write_pieces = [](const char* path, const std::vector<std::string>& ps) {
+        std::vector<uint8_t> out;
+        for (const auto& p : ps) {
+            const uint32_t n = (uint32_t)p.size();
+            out.insert(out.end(), (const uint8_t*)&n, (const uint8_t*)&n + 4);
+            out.insert(out.end(), p.begin(), p.end());
+        }
+        write_bin(path, out.data(), out.size());
+    };
+    if (cmd == "tokenize" && argc == 6) {  // Tokenizer::encode (core/tokenizer.cpp:252-273)
+        GGUFParser g;
+        if (!g.load(argv[2])) return 1;
+        Tokenizer t;
+        if (!t.load(g)) return 1;
+        auto txt = read_bin<char>(argv[3]);
+        auto ids = t.encode(std::string(txt.begin(), txt.end()), std::atoi(argv[4]) != 0);
+        write_bin(argv[5], ids.data(), ids.size());
+        return 0;
+    }
+    if (cmd == "detok" && argc == 5) {  // Tokenizer::decode_one of each id (core/tokenizer.cpp:278-296)
+        GGUFParser g;
+        if (!g.load(argv[2])) return 1;
+        Tokenizer t;
+        if (!t.load(g)) return 1;
+        auto ids = read_bin<int32_t>(argv[3]);
+        std::vector<std::string> ps;
+        for (int32_t id : ids) ps.push_back(t.decode_one(id));
+        write_pieces(argv[4], ps);
+        return 0;
+    }
+    if (cmd == "engine" && argc == 8) {
+        // Engine::generate (core/engine.cpp:83-243) as the reference runs it;
+        // messages.bin: role, NUL, content, NUL, ... ; the on_token pieces
+        Engine e;
+        GenParams gp;
+        gp.n_predict = std::atoi(argv[4]);
+        gp.temperature = (float)std::atof(argv[5]);
+        if (!e.load(argv[2], gp)) return 1;
+        if (std::strcmp(argv[3], "-") != 0 && !e.load_draft(argv[3])) return 1;
+        auto raw = read_bin<char>(argv[6]);
+        std::vector<std::string> f;
+        std::string cur;
+        for (char c : raw) {
+            if (c == 0) { f.push_back(cur); cur.clear(); }
+            else cur += c;
+        }
+        std::vector<Message> msgs;
+        for (size_t i = 0; i + 1 < f.size(); i += 2) msgs.push_back({f[i], f[i + 1]});
+        std::vector<std::string> ps;
+        const std::string resp = e.generate(msgs, gp, [&](const std::string& p) { ps.push_back(p); });
+        std::string joined;
+        for (const auto& p : ps) joined += p;
+        if (joined != resp) { std::fprintf(stderr, "response differs from the streamed pieces\n"); return 1; }
+        write_pieces(argv[7], ps);
         return 0;
     }
     if (cmd == "bench" && argc == 8) {

@@ -7,7 +7,8 @@ core/platform.cpp and bug/logger.cpp, and replaces core/{model,gguf_parser,
 ops}.{hpp,cpp} (and core/sampler.* in the first configuration) with this
 library's headers. Both configurations are checked: with this library's
 Sampler, and with the reference's own core/sampler.cpp calling ops::argmax /
-ops::softmax from this library. The sources are read where they lie under
+ops::softmax from this library. A third build uses this library's own
+Engine and Tokenizer headers as well. The sources are read where they lie under
 /root/reference through a symlink farm in a temporary directory; nothing is
 copied into the repository and nothing built here ships. Skipped when the
 reference tree is absent (the GPU box).
@@ -72,6 +73,23 @@ def _farm(tmp, own_sampler):
     with open(os.path.join(tmp, "main.cpp"), "w") as fh:
         fh.write(MAIN)
     return [r for r in keep if r.endswith(".cpp")] + ["main.cpp"]
+
+
+def test_own_engine_headers_link(tmp_path):
+    """The same caller program against this library's own Engine, Tokenizer,
+    Sampler and ops headers (no reference file at all)."""
+    assert os.path.exists(os.path.join(LIB, "liboracle_host.so")), "build the host library first"
+    core = tmp_path / "core"
+    core.mkdir()
+    for f in OURS + ["sampler.hpp", "engine.hpp", "tokenizer.hpp", "spec.hpp"]:
+        os.symlink(os.path.join(HOST, f), core / f)
+    (tmp_path / "main.cpp").write_text(MAIN)
+    exe = tmp_path / "engine_link"
+    r = subprocess.run(["g++", "-std=c++17", "-O0", "-I", str(tmp_path), "-I", str(core), "-I",
+                        os.path.join(REPO, "include"), str(tmp_path / "main.cpp"), "-o", str(exe), "-L", LIB,
+                        "-loracle_host", "-lorc_hip", f"-Wl,-rpath,{LIB}", "-Wl,--no-undefined"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
 
 
 @pytest.mark.skipif(not os.path.isdir(os.path.join(REF, "core")), reason="reference tree not present")
