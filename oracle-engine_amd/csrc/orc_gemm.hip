@@ -397,6 +397,14 @@ __device__ __forceinline__ void map_rows(const QmvParams& p, int g, int slot, Ro
 // taking turns.
 template <int QT, int NT, int ROWS, int UPL, int WPE, bool PIPE>
 __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) void k_qmv(QmvParams p) {
+    // token block blockIdx.y: tokens [NT y, NT y + NT) of the launch (every block full)
+    if (blockIdx.y) {
+        const size_t ox = (size_t)blockIdx.y * NT * p.ldx, oy = (size_t)blockIdx.y * NT * p.ldy;
+        p.x += ox;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            if (p.y[i]) p.y[i] += oy;
+    }
     using T = QTr<QT>;
     constexpr int LPR = T::LPR, G = 64 / LPR, RG = G * ROWS;
     extern __shared__ float smem[];
@@ -642,14 +650,17 @@ static int launch_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& 
     QmvParams p = p0;
     const int rg = (64 / QTr<QT>::LPR) * ROWS;
     p.n_groups = (p.n_rows + rg - 1) / rg;
-    // persistent grid: WPE/2 workgroups per CU, at most one per row group
-    const int grid = std::max(1, std::min(p.n_groups, (WPE / 2) * g_n_cu));
+    // persistent grid: WPE/2 workgroups per CU, at most one per row group,
+    // times the launch's blocks of exactly NT tokens (the kernel stages and
+    // writes NT rows per block)
+    if (p.tok_block != NT || p.n_tok % NT) return set_error(ORC_E_INVALID, "gemm: token blocks must be whole");
+    const dim3 grid(std::max(1, std::min(p.n_groups, (WPE / 2) * g_n_cu)), p.n_tok / NT);
     const size_t lds = qmv_lds(QT, NT, p.n_in);
     if (lds > g_lds_max) return set_error(ORC_E_UNSUPPORTED, "gemm: activations do not fit LDS");
     if (ev.start)
-        hipExtLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), dim3(grid), dim3(kQWG), lds, s, ev.start, ev.stop, 0, p);
+        hipExtLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), grid, dim3(kQWG), lds, s, ev.start, ev.stop, 0, p);
     else
-        hipLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), dim3(grid), dim3(kQWG), lds, s, p);
+        hipLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), grid, dim3(kQWG), lds, s, p);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }
@@ -676,10 +687,10 @@ static int launch_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) 
 template <int QT>
 static int launch_type(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     if constexpr (QT == ORC_Q4_K || QT == ORC_Q6_K) {  // K-quants: one-token calls only
-        if (p.n_tok != 1) return set_error(ORC_E_UNSUPPORTED, "gemm: K-quant vector path takes one token");
+        if (p.n_tok != 1 || p.tok_block != 1) return set_error(ORC_E_UNSUPPORTED, "gemm: K-quant vector path takes one token");
         return launch_nt<QT, 1>(p, s, ev);
     }
-    switch (p.n_tok) {
+    switch (p.tok_block) {
         case 1: return launch_nt<QT, 1>(p, s, ev);
         case 2: return launch_nt<QT, 2>(p, s, ev);
         case 3: return launch_nt<QT, 3>(p, s, ev);
@@ -762,13 +773,19 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
     const bool mm = mmq_type(type) && !decode;
     const int ntmax = mm ? mmq_max_tokens(type, p) : max_tokens(type, p.n_in);
     if (ntmax < 1) return set_error(ORC_E_UNSUPPORTED, "gemm: n_in too large for the activations to fit LDS");
-    // tokens are processed in chunks of at most ntmax; chunking never changes a
-    // (token,row) result because the reduction order is independent of n_tok
-    for (int t0 = 0; t0 < p.n_tok; t0 += ntmax) {
+    // Tokens go in blocks of ntmax (the second grid dimension of one launch:
+    // every kernel computes exactly its instantiated token count per block),
+    // and the remainder in a second launch of its own size. Blocking never
+    // changes a (token, row) result: the reduction order is independent of
+    // the token count.
+    for (int t0 = 0; t0 < p.n_tok;) {
+        const int left = p.n_tok - t0;
         QmvParams q = p;
-        q.n_tok = std::min(ntmax, p.n_tok - t0);
+        q.tok_block = std::min(ntmax, left);
+        q.n_tok = left >= ntmax ? left / ntmax * ntmax : left;
         q.x = p.x + (size_t)t0 * p.ldx;
         for (int i = 0; i < 3; ++i) q.y[i] = p.y[i] ? p.y[i] + (size_t)t0 * p.ldy : nullptr;
+        t0 += q.n_tok;
         LaunchEvents ev;
         if (g_prof_on) prof_arm(s, type, q.n_tok, gemm_bytes(q, q.n_tok), &ev.start, &ev.stop);
         int rc;

@@ -27,6 +27,7 @@ struct QmvParams {
     int hs;               // matrix-core windowed mode: units of a wave's range staged at a time
     int seg_type[3];      // matrix-core mixed launches: weight type of each segment
     uint64_t seg_rb[3];   // and its row bytes
+    int tok_block;        // tokens per token block (blockIdx.y) of a launch; n_tok counts all blocks
 };
 
 // Kernel timing of one launch: start / stop events taken from its dispatch.

@@ -134,13 +134,13 @@ bool Model::load(const std::string& path, int ctx_len) {
     }
 
     // device buffers
-    const int B = kMaxBatch, C = (int)cfg.ctx_len, QKV = NQ + 2 * NKV;
+    const int B = kMaxBatch, BP = kPrefillBatch, C = (int)cfg.ctx_len, QKV = NQ + 2 * NKV;
     auto alloc = [&](void** p, size_t n) { return orc_malloc(p, n) == 0; };
     const size_t kv = (size_t)cfg.n_layers * NKV * C * sizeof(float);
-    if (!alloc((void**)&d_x_, (size_t)B * D * 4) || !alloc((void**)&d_qkv_, (size_t)B * QKV * 4) ||
-        !alloc((void**)&d_attn_, (size_t)B * NQ * 4) || !alloc((void**)&d_h_, (size_t)B * FF * 4) ||
+    if (!alloc((void**)&d_x_, (size_t)BP * D * 4) || !alloc((void**)&d_qkv_, (size_t)BP * QKV * 4) ||
+        !alloc((void**)&d_attn_, (size_t)BP * NQ * 4) || !alloc((void**)&d_h_, (size_t)BP * FF * 4) ||
         !alloc((void**)&d_logits_, (size_t)B * V * 4) || !alloc((void**)&d_k_, kv) || !alloc((void**)&d_v_, kv) ||
-        !alloc((void**)&d_rope_, (size_t)C * cfg.head_dim * 4) || !alloc((void**)&d_ids_, (size_t)B * 4) ||
+        !alloc((void**)&d_rope_, (size_t)C * cfg.head_dim * 4) || !alloc((void**)&d_ids_, (size_t)BP * 4) ||
         !alloc((void**)&d_am_, (size_t)B * 4) ||
         !alloc(&d_attn_ws_, std::max(orc_attn_workspace(B, cfg.n_heads, cfg.head_dim, C),
                                      orc_attn_fused_workspace(cfg.n_heads, cfg.n_kv_heads, cfg.head_dim))) ||
@@ -246,17 +246,24 @@ int Model::chunk_dev(const int32_t* d_ids, int n, const int32_t* d_pos, int sp, 
         CK(gemm_segs({{&L.q, {d_qkv_, L.bq}}, {&L.k, {d_qkv_ + NQ, L.bk}}, {&L.v, {d_qkv_ + NQ + NKV, L.bv}}}, n,
                      d_x_, D, QKV, L.attn_norm, ORC_EPI_STORE, s));
         // RoPE + KV store (model.cpp:401-408), attention (model.cpp:410-435)
-        if (fused_attn_) {  // one launch: rotate, store K/V, attend
-            const bool band = d_pos && pos_limit_ > 0;  // a capture that declared its positions
-            const int lim = band && pos_limit_ < C ? pos_limit_ : C;
-            const int flo = band && pos_floor_ < lim ? pos_floor_ : 0;
-            CK(orc_attn_fused_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc, vc,
-                                 C, flo, lim, d_attn_, NQ, d_attn_ws_, s));
-        } else {
-            CK(orc_rope_kv_store_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, d_rope_, kc,
-                                    vc, C, s));
-            CK(orc_attn_gqa_at(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp, kc, vc, C,
-                               d_attn_, NQ, d_attn_ws_, s));
+        // in launches of at most kMaxBatch tokens, in order: each stores its
+        // tokens' K / V rows before the next attends to them
+        for (int a0 = 0; a0 < n; a0 += kMaxBatch) {
+            const int an = std::min(kMaxBatch, n - a0);
+            float* qkv = d_qkv_ + (size_t)a0 * QKV;
+            float* att = d_attn_ + (size_t)a0 * NQ;
+            if (fused_attn_) {  // one launch: rotate, store K/V, attend
+                const bool band = d_pos && pos_limit_ > 0;  // a capture that declared its positions
+                const int lim = band && pos_limit_ < C ? pos_limit_ : C;
+                const int flo = band && pos_floor_ < lim ? pos_floor_ : 0;
+                CK(orc_attn_fused_at(qkv, QKV, an, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp + a0,
+                                     d_rope_, kc, vc, C, flo, lim, att, NQ, d_attn_ws_, s));
+            } else {
+                CK(orc_rope_kv_store_at(qkv, QKV, an, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp + a0,
+                                        d_rope_, kc, vc, C, s));
+                CK(orc_attn_gqa_at(qkv, QKV, an, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, d_pos, sp + a0, kc, vc,
+                                   C, att, NQ, d_attn_ws_, s));
+            }
         }
         // x += O attn   (model.cpp:438-444)
         CK(gemm_segs({{&L.o, {d_x_, nullptr}}}, n, d_attn_, NQ, D, nullptr, ORC_EPI_ACCUM, s));
@@ -285,8 +292,9 @@ int Model::forward_dev(const int32_t* d_ids, int n, int sp, bool logits, int32_t
         err_ = "logits for more than kMaxBatch tokens per call";
         return ORC_E_INVALID;
     }
-    for (int t0 = 0; t0 < n; t0 += kMaxBatch) {
-        const int m = std::min(kMaxBatch, n - t0);
+    const int chunk = logits ? kMaxBatch : kPrefillBatch;
+    for (int t0 = 0; t0 < n; t0 += chunk) {
+        const int m = std::min(chunk, n - t0);
         if (int rc = chunk_dev(d_ids + t0, m, nullptr, sp + t0, logits, d_argmax ? d_argmax + t0 : nullptr, s)) {
             err_ = orc_last_error();
             return rc;
@@ -335,8 +343,9 @@ void Model::forward_prefill(const int32_t* tokens, int n, int sp, float* out_log
             std::fprintf(stderr, "[Model] forward_prefill: token id %d out of range, using 0\n", t);
             t = 0;
         }
-    for (int t0 = 0; t0 < n; t0 += kMaxBatch) {
-        const int m = std::min(kMaxBatch, n - t0);
+    const int chunk = out_logits ? kMaxBatch : kPrefillBatch;  // logits rows fit kMaxBatch tokens
+    for (int t0 = 0; t0 < n; t0 += chunk) {
+        const int m = std::min(chunk, n - t0);
         if (orc_memcpy_h2d(d_ids_, ids.data() + t0, (size_t)m * 4, nullptr)) return;
         if (chunk_dev(d_ids_, m, nullptr, sp + t0, out_logits != nullptr, nullptr, nullptr)) {
             err_ = orc_last_error();
@@ -361,10 +370,10 @@ std::vector<float> Model::embed_tokens(const std::vector<int32_t>& tokens) {  //
     std::vector<int32_t> ids(tokens);
     for (auto& t : ids)
         if (t < 0 || t >= (int32_t)cfg.n_vocab) t = 0;  // model.cpp:352-356
-    std::vector<float> acc((size_t)D, 0.f), xs((size_t)kMaxBatch * D);
+    std::vector<float> acc((size_t)D, 0.f), xs((size_t)kPrefillBatch * D);
     reset();
-    for (int t0 = 0; t0 < n; t0 += kMaxBatch) {
-        const int m = std::min(kMaxBatch, n - t0);
+    for (int t0 = 0; t0 < n; t0 += kPrefillBatch) {
+        const int m = std::min(kPrefillBatch, n - t0);
         if (orc_memcpy_h2d(d_ids_, ids.data() + t0, (size_t)m * 4, nullptr) ||
             chunk_dev(d_ids_, m, nullptr, t0, false, nullptr, nullptr) ||
             orc_memcpy_d2h(xs.data(), d_x_, (size_t)m * D * 4, nullptr)) {

@@ -41,7 +41,8 @@ struct ModelConfig {
 class Model {
 public:
     ModelConfig cfg;
-    static constexpr int kMaxBatch = 16;  // tokens per device pass (longer prefills are chunked)
+    static constexpr int kMaxBatch = 16;      // tokens per device pass with logits (verify)
+    static constexpr int kPrefillBatch = 256;  // tokens per device pass without logits (prefill)
 
     Model() = default;
     ~Model();
