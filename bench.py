@@ -149,8 +149,8 @@ WORKLOADS = {
                desc="C5 long-context spec greedy: 7B-shape all-Q6_K target + 0.5B-shape Q8_0 draft"),
 }
 SAMPLER = (0.8, 0.95, 40, 1.1, 64, 4242)  # T, top-p, top-k, repeat penalty, repeat_last, seed (C4)
-PROF_FAMILIES = (2, 8, 12, 14, 256, 258, 300, 301, 302)
-FAMILY_NAMES = {**TYPE_NAMES, 300: "attn k_attn_wg", 301: "attn k_attn_split", 302: "attn k_attn_merge"}
+PROF_FAMILIES = (2, 8, 12, 14, 256, 258, 300, 301, 302, 303)
+FAMILY_NAMES = {**TYPE_NAMES, 300: "attn k_attn_wg", 301: "attn k_attn_split", 302: "attn k_attn_merge", 303: "attn k_attn_mt"}
 
 
 def family_label(ty, nt):
@@ -412,7 +412,8 @@ def main():
         out["value_note"] = ("each step is a whole Engine call: the prefill of both models (prefill_ms) plus "
                              f"{n_gen} generated tokens")
     if a.workload == "c5":
-        kv = [f for f in fams if f["kernel"].startswith("attn k_attn_split") and f["kernel"].endswith(f"={k + 1}")]
+        kv = [f for f in fams if f["kernel"].startswith(("attn k_attn_mt", "attn k_attn_split"))
+              and f["kernel"].endswith(f"={k + 1}")]
         mg = [f for f in fams if f["kernel"].startswith("attn k_attn_merge") and f["kernel"].endswith(f"={k + 1}")]
         wt = [f for f in fams if f["kernel"].startswith("k_gemm Q6_K")]  # C5's target is all Q6_K, the draft Q8_0
         if kv and wt:
@@ -421,7 +422,7 @@ def main():
             out["verify_split"] = {
                 "kv_read_gbs": round(kvb / (kvms * 1e-3) / 1e9, 1), "kv_bytes": kvb, "kv_ms": round(kvms, 3),
                 "weight_gemm_gbs": round(wb / (wms * 1e-3) / 1e9, 1), "weight_bytes": wb, "weight_ms": round(wms, 3),
-                "note": f"{k + 1}-token verify passes of the timing pass: GQA attention (split + merge; K and V "
+                "note": f"{k + 1}-token verify passes of the timing pass: GQA attention (chunk kernels + merge; K and V "
                         f"of every cached position counted once per layer) vs the target's weight GEMMs"}
     print(json.dumps(out), flush=True)
 

@@ -155,7 +155,7 @@ int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n_segs, int 
  * event (hipExtLaunchKernelGGL: both take the timestamps of the kernel's own
  * dispatch on its stream) and its algorithmic HBM bytes (weight blocks + x +
  * y) are noted; so does every attention launch of orc_attn_fused_at with
- * host positions (families ORC_PROF_ATTN_WG / _SPLIT / _MERGE; bytes = the K
+ * host positions (families ORC_PROF_ATTN_WG / _MT / _SPLIT / _MERGE; bytes = the K
  * and V rows its tokens read, counted once, + QKV rows in + rows out; the
  * merge is noted with 0 bytes). Once the work has run, orc_prof_accumulate
  * adds every launch's elapsed time to its record; orc_prof_read sums the
@@ -167,6 +167,7 @@ int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n_segs, int 
 #define ORC_PROF_ATTN_WG 300
 #define ORC_PROF_ATTN_SPLIT 301
 #define ORC_PROF_ATTN_MERGE 302
+#define ORC_PROF_ATTN_MT 303
 int orc_prof_enable(int on);
 int orc_prof_accumulate(void);
 int orc_prof_read(int type, int n_tok, int64_t* launches, double* total_ms, double* total_bytes);

@@ -224,6 +224,8 @@ __host__ __device__ inline int chunk_positions(int P) {
     return (per + kSB - 1) / kSB * kSB;
 }
 __host__ __device__ inline int n_chunks(int P) { return (P + chunk_positions(P) - 1) / chunk_positions(P); }
+// up to kMtMax positions the chunks are kSB long (k_attn_mt); above, wider (k_attn_split)
+constexpr int kMtMax = kSB * kNCMax;
 
 // Tokens attending to at most kWGMax positions take k_attn_wg (one launch,
 // one workgroup per query head, at most three passes of its waves); longer
@@ -337,7 +339,7 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
     const int pt = start + t;
     if (pt < 0 || pt >= ctx) return;  // outside the cache (graph replays past the end): nothing to do
     const int P = pt + 1, CP = chunk_positions(P), nch = n_chunks(P);
-    if (P <= kWGMax || c >= nch) return;  // short contexts: k_attn_wg; grids cover the most chunks any position needs
+    if (P <= kMtMax || c >= nch) return;  // shorter contexts: k_attn_wg, k_attn_mt; grids cover the most chunks any position needs
     const int p0 = c * CP, p1 = min(P, p0 + CP);
     const float scale = 1.f / sqrtf((float)HD);
     const size_t kvh = (size_t)(n_heads + g) * HD, vvh = (size_t)(n_heads + n_kv + g) * HD;
@@ -520,6 +522,254 @@ __global__ __launch_bounds__(kSW) void k_attn_split(const float* qkv, int ldqkv,
                     pr[HD] = st_m[r];
                     pr[HD + 1] = st_l[r];
                 }
+            }
+        }
+    }
+}
+
+// ── positions kWGMax < P <= kMtMax: every token of a launch in one pass ────
+// One workgroup per (chunk of kSB positions, kv head g) forms the partial
+// (O, m, l) of every (token, query head) row that reads the chunk, so each
+// cached K / V byte is read once per launch however many tokens verify. The
+// rows (token-major, NR = tokens x gqa heads, padded to whole 16-row tiles)
+// are a small dense contraction, done on the matrix cores in fp32
+// (v_mfma_f32_16x16x4_f32: fp32 operands and sums):
+//  * scores S = Q K^T: wave w holds the K rows of positions 16w..16w+15 of
+//    the chunk as the B operand (lane group kg = lane / 16 holds dims
+//    [kg HD/8, (kg+1) HD/8) and the same range + HD/2, so the rotate-half
+//    pairs of the batch's own positions rotate in the lane); step m of the
+//    HD/4-step chain sums dim(m, kg) over the four lane groups; A = the
+//    rotated query rows from LDS;
+//  * softmax of each row over the chunk on the VALU (four lanes per row),
+//    e written back over the scores;
+//  * O = E V: wave w owns output dims [w HD/4, (w+1) HD/4); step m of the
+//    16-step chain sums positions kg*16 + m; B = the V rows from the cache
+//    (or the QKV rows of the batch's own positions), A = e from LDS.
+// The order of every sum is fixed by the position and the chunk alone, and a
+// row's result depends on its own query alone (masked positions enter as
+// exact zeros), so an n-token call equals n one-token calls bit for bit.
+// Tokens past kMtMax positions take k_attn_split (wider chunks); each token's
+// path depends on its own position only.
+constexpr int kQPad = 4, kSPad = 4;  // LDS row padding (floats) against bank conflicts
+typedef float mt_f4 __attribute__((ext_vector_type(4)));
+// dynamic LDS floats of k_attn_mt for nr rows: rotated queries, scores / e
+template <int HD> constexpr size_t mt_lds_floats(int nr) {
+    return (size_t)((nr + 15) / 16 * 16) * (HD + kQPad + kSB + kSPad);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kSW) void k_attn_mt(const float* qkv, int ldqkv, int n_tok, int n_heads, int n_kv,
+                                                 const int* d_pos, int pos_off, const float2* rope, float* kc,
+                                                 float* vc, int ctx, float* work) {
+    constexpr int half = HD / 2, E8 = HD / 8, KPL = HD / 4;  // dims per lane-group block; K values per lane
+    constexpr int CT = HD / 64;                              // 16-dim output tiles per wave
+    constexpr int QS = HD + kQPad, SS = kSB + kSPad, PS = part_stride<HD>();
+    static_assert(kSW == 256 && kSB == 64, "four waves, 16 positions each");
+    extern __shared__ __align__(16) float lds[];
+    const int R = n_heads / n_kv;
+    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int w = tid >> 6, ln = tid & 63, li = ln & 15, kg = ln >> 4;
+    const int start = start_position(d_pos, pos_off);
+    const int p0 = c * kSB;
+    // tokens reading this chunk on this path: kWGMax < P_t <= kMtMax,
+    // p0 < P_t, P_t = start + t + 1 <= ctx; they are consecutive
+    const int t_hi = min(n_tok - 1, min(ctx, kMtMax) - 1 - start);
+    const int t_lo = max(0, max(kWGMax, p0) - start);
+    if (t_hi < t_lo) return;
+    const int NR = (t_hi - t_lo + 1) * R, NRP = (NR + 15) & ~15;
+    float* Qs = lds;                   // [NRP][QS]
+    float* S = lds + (size_t)NRP * QS;  // [NRP][SS]
+    const float scale = 1.f / sqrtf((float)HD);
+    const size_t kvh = (size_t)(n_heads + g) * HD, vvh = (size_t)(n_heads + n_kv + g) * HD;
+    const float* kg_c = kc + (size_t)g * ctx * HD;
+    const float* vg_c = vc + (size_t)g * ctx * HD;
+    const int p_end = start + t_hi + 1;  // positions [p0, p_end) hold data the rows read
+
+    // B operand of the scores: K of position p0 + 16w + li, dims [kg E8, +E8) and + half
+    float kb[KPL];
+    {
+        const int p = p0 + 16 * w + li;
+        if (p >= p_end) {
+#pragma unroll
+            for (int i = 0; i < KPL; ++i) kb[i] = 0.f;
+        } else if (p < start) {
+            const float* src = kg_c + (size_t)p * HD + kg * E8;
+#pragma unroll
+            for (int i = 0; i < E8; i += 4) {
+                const float4 lo = *(const float4*)(src + i), hi = *(const float4*)(src + half + i);
+                kb[i] = lo.x, kb[i + 1] = lo.y, kb[i + 2] = lo.z, kb[i + 3] = lo.w;
+                kb[E8 + i] = hi.x, kb[E8 + i + 1] = hi.y, kb[E8 + i + 2] = hi.z, kb[E8 + i + 3] = hi.w;
+            }
+        } else {
+            const float* src = qkv + (size_t)(p - start) * ldqkv + kvh + kg * E8;
+            const float2* cs = rope + (size_t)p * half + kg * E8;
+#pragma unroll
+            for (int i = 0; i < E8; i += 4) {
+                const float4 lo = *(const float4*)(src + i), hi = *(const float4*)(src + half + i);
+                const float4 c01 = *(const float4*)(cs + i), c23 = *(const float4*)(cs + i + 2);
+                const float2 e0{c01.x, c01.y}, e1{c01.z, c01.w}, e2{c23.x, c23.y}, e3{c23.z, c23.w};
+                kb[i] = rot_lo(lo.x, hi.x, e0), kb[i + 1] = rot_lo(lo.y, hi.y, e1);
+                kb[i + 2] = rot_lo(lo.z, hi.z, e2), kb[i + 3] = rot_lo(lo.w, hi.w, e3);
+                kb[E8 + i] = rot_hi(lo.x, hi.x, e0), kb[E8 + i + 1] = rot_hi(lo.y, hi.y, e1);
+                kb[E8 + i + 2] = rot_hi(lo.z, hi.z, e2), kb[E8 + i + 3] = rot_hi(lo.w, hi.w, e3);
+            }
+        }
+    }
+    // B operand of P.V: V[p0 + 16 kg + m][w HD/4 + 16 ct + li]
+    float vb[CT][16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+        const int p = p0 + 16 * kg + m;
+        const float* src = p >= p_end ? nullptr
+                           : p < start ? vg_c + (size_t)p * HD
+                                       : qkv + (size_t)(p - start) * ldqkv + vvh;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) vb[ct][m] = src ? src[w * (HD / 4) + 16 * ct + li] : 0.f;
+    }
+
+    // K (rotated) and V of the tokens whose own position lies in this chunk go to the cache
+    {
+        const int tw = min(t_hi, p0 + kSB - 1 - start) - t_lo + 1;
+        for (int i = tid; i < tw * HD; i += kSW) {
+            const int t = t_lo + i / HD, d = i % HD, pt = start + t;
+            const float* kr = qkv + (size_t)t * ldqkv + kvh;
+            const float2* cs = rope + (size_t)pt * half;
+            const float kv = d < half ? rot_lo(kr[d], kr[d + half], cs[d]) : rot_hi(kr[d - half], kr[d], cs[d - half]);
+            const size_t o = ((size_t)g * ctx + pt) * HD + d;
+            kc[o] = kv;
+            vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
+        }
+    }
+
+    // rotated queries of every row (rope_q_lds's arithmetic): an item is four
+    // dims of the first half of a row and their rotate-half partners; four
+    // items per thread in flight. Padded rows are zero.
+    {
+        constexpr int QD = half / 4;  // items per row
+        for (int i0 = 0; i0 < NRP * QD; i0 += 4 * kSW) {
+            float4 lo[4], hi[4], c01[4], c23[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = i0 + tid + j * kSW, row = i / QD, d = 4 * (i - row * QD);
+                if (row < NR) {
+                    const int ti = row / R, t = t_lo + ti;
+                    const float* qt = qkv + (size_t)t * ldqkv + (size_t)(g * R + row - ti * R) * HD + d;
+                    const float2* cs = rope + (size_t)(start + t) * half + d;
+                    lo[j] = *(const float4*)qt;
+                    hi[j] = *(const float4*)(qt + half);
+                    c01[j] = *(const float4*)cs;
+                    c23[j] = *(const float4*)(cs + 2);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = i0 + tid + j * kSW, row = i / QD, d = 4 * (i - row * QD);
+                if (row < NRP) {
+                    float4 ql = make_float4(0.f, 0.f, 0.f, 0.f), qh = ql;
+                    if (row < NR) {
+                        const float2 e0{c01[j].x, c01[j].y}, e1{c01[j].z, c01[j].w};
+                        const float2 e2{c23[j].x, c23[j].y}, e3{c23[j].z, c23[j].w};
+                        ql = make_float4(rot_lo(lo[j].x, hi[j].x, e0), rot_lo(lo[j].y, hi[j].y, e1),
+                                         rot_lo(lo[j].z, hi[j].z, e2), rot_lo(lo[j].w, hi[j].w, e3));
+                        qh = make_float4(rot_hi(lo[j].x, hi[j].x, e0), rot_hi(lo[j].y, hi[j].y, e1),
+                                         rot_hi(lo[j].z, hi[j].z, e2), rot_hi(lo[j].w, hi[j].w, e3));
+                    }
+                    *(float4*)&Qs[(size_t)row * QS + d] = ql;
+                    *(float4*)&Qs[(size_t)row * QS + half + d] = qh;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // scores of 16-row tiles against this wave's 16 positions
+    for (int rt = 0; rt < NRP / 16; ++rt) {
+        const float* q = Qs + (size_t)(rt * 16 + li) * QS + kg * E8;
+        float qa[KPL];
+#pragma unroll
+        for (int i = 0; i < E8; i += 4) {
+            const float4 lo = *(const float4*)(q + i), hi = *(const float4*)(q + half + i);
+            qa[i] = lo.x, qa[i + 1] = lo.y, qa[i + 2] = lo.z, qa[i + 3] = lo.w;
+            qa[E8 + i] = hi.x, qa[E8 + i + 1] = hi.y, qa[E8 + i + 2] = hi.z, qa[E8 + i + 3] = hi.w;
+        }
+        mt_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < KPL; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[m], kb[m], acc, 0, 0, 0);
+        const int pos = 16 * w + li;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = rt * 16 + 4 * kg + r;
+            if (row < NR) {
+                const int nb = min(kSB, start + t_lo + row / R + 1 - p0);
+                S[(size_t)row * SS + pos] = pos < nb ? acc[r] * scale : -INFINITY;
+            }
+        }
+    }
+    __syncthreads();
+
+    // softmax of each row over the chunk: four lanes per row, sixteen
+    // positions per lane (max and sum in position order, then over the four
+    // lanes by DPP in a fixed order); (m, l) go to the row's partial; padded
+    // rows get e = 0
+    for (int row0 = 0; row0 < NRP; row0 += kSW / 4) {
+        const int row = row0 + (tid >> 2), q4 = tid & 3;
+        if (row < NRP) {  // whole quads: the DPP exchanges stay inside active quads
+            float* sr = S + (size_t)row * SS + 16 * q4;
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const float4 v4 = *(const float4*)(sr + i);
+                x[i] = v4.x, x[i + 1] = v4.y, x[i + 2] = v4.z, x[i + 3] = v4.w;
+            }
+            const int ti = row / R, t = t_lo + ti;
+            const int nb = row < NR ? min(kSB, start + t + 1 - p0) : 0;
+            float mx = x[0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x[i]);
+            mx = fmaxf(mx, dpp<0xB1>(mx));
+            mx = fmaxf(mx, dpp<0x4E>(mx));
+            float l = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                x[i] = 16 * q4 + i < nb ? expf(x[i] - mx) : 0.f;
+                l += x[i];
+            }
+            l = quad_sum(l);
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) *(float4*)(sr + i) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
+            if (q4 == 0 && row < NR) {
+                float* pr = work + (((size_t)t * n_kv + g) * kNCMax * R + (size_t)c * R + (row - ti * R)) * PS;
+                pr[HD] = mx;
+                pr[HD + 1] = l;
+            }
+        }
+    }
+    __syncthreads();
+
+    // O = E V per 16-row tile and this wave's output dims, into the partial rows
+    for (int rt = 0; rt < NRP / 16; ++rt) {
+        const float* e = S + (size_t)(rt * 16 + li) * SS + 16 * kg;
+        float ea[16];
+#pragma unroll
+        for (int m = 0; m < 16; m += 4) {
+            const float4 x = *(const float4*)(e + m);
+            ea[m] = x.x, ea[m + 1] = x.y, ea[m + 2] = x.z, ea[m + 3] = x.w;
+        }
+        mt_f4 acc[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            acc[ct] = mt_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < 16; ++m) acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ea[m], vb[ct][m], acc[ct], 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = rt * 16 + 4 * kg + r;
+            if (row < NR) {
+                const int ti = row / R, t = t_lo + ti;
+                float* pr = work + (((size_t)t * n_kv + g) * kNCMax * R + (size_t)c * R + (row - ti * R)) * PS;
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) pr[w * (HD / 4) + 16 * ct + li] = acc[ct][r];
             }
         }
     }
@@ -1076,38 +1326,38 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
     if (pos_floor < 0 || pos_floor >= pos_limit)
         return set_error(ORC_E_INVALID, "attn_fused: pos_floor must be in [0, pos_limit)");
     hipStream_t st = resolve_stream(s);
-    // which paths the tokens can take: their own positions (host position)
-    // or any position in [pos_floor, pos_limit) (device position); the split
-    // grid covers the most chunks such a position needs
+    // which paths the tokens take: by their own positions (host position) or
+    // for any position in [pos_floor, pos_limit) (device position):
+    // P <= kWGMax k_attn_wg, P <= kMtMax k_attn_mt, above k_attn_split; the
+    // chunk grids cover the most chunks such a position needs
     bool short_ctx = false;
-    int nch = 0;
+    int nch_mt = 0, nch_sp = 0;
     if (!d_pos) {
         for (int t = 0; t < n_tok; ++t) {
             const int P = pos_off + t + 1;
             if (P <= kWGMax) short_ctx = true;
-            else nch = std::max(nch, n_chunks(P));
+            else if (P <= kMtMax) nch_mt = std::max(nch_mt, n_chunks(P));
+            else nch_sp = std::max(nch_sp, n_chunks(P));
         }
     } else {
         short_ctx = pos_floor + 1 <= kWGMax;
-        // up to kSB * kNCMax positions the chunks are kSB long and n_chunks
-        // grows with P, so the band's last position needs the most
-        if (pos_limit <= kSB * kNCMax)
-            nch = pos_limit > kWGMax ? n_chunks(pos_limit) : 0;
-        else
-            for (int P = std::max(kWGMax, pos_floor) + 1; P <= pos_limit && nch < kNCMax; ++P)
-                nch = std::max(nch, n_chunks(P));
+        // below kMtMax, n_chunks grows with P: the band's last position needs the most
+        if (pos_limit > kWGMax && pos_floor + 1 <= kMtMax) nch_mt = n_chunks(std::min(pos_limit, kMtMax));
+        for (int P = std::max(kMtMax, pos_floor) + 1; P <= pos_limit && nch_sp < kNCMax; ++P)
+            nch_sp = std::max(nch_sp, n_chunks(P));
     }
     const int R = n_heads / n_kv;
     float* w = (float*)d_work;
     // live timing (host positions only): algorithmic bytes of a launch = the
     // K and V rows of the positions its tokens read, once (the verify tokens
     // share them), + the QKV rows in + the attention rows out
-    double kv_bytes[2] = {0, 0};  // [k_attn_wg, k_attn_split]
+    double kv_bytes[3] = {0, 0, 0};  // [k_attn_wg, k_attn_mt, k_attn_split]
     if (!d_pos) {
         const double io = 4.0 * n_tok * ((double)(n_heads + 2 * n_kv) * head_dim + (double)n_heads * head_dim);
         const int pmax = pos_off + n_tok;
         kv_bytes[0] = 8.0 * n_kv * head_dim * std::min(pmax, kWGMax) + io;
-        kv_bytes[1] = 8.0 * n_kv * head_dim * pmax + io;
+        kv_bytes[1] = 8.0 * n_kv * head_dim * std::min(pmax, kMtMax) + io;
+        kv_bytes[2] = 8.0 * n_kv * head_dim * pmax + io;
     }
     auto armed = [&](int fam, double bytes, LaunchEv& ev) {
         return !d_pos && prof_arm(st, fam, n_tok, bytes, &ev.a, &ev.b);
@@ -1124,16 +1374,27 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
                                   d_out, ldo);
             ORC_LAUNCH_CHECK();
         }
-        if (nch > 0) {
-            bool tm = armed(kProfAttnSplit, kv_bytes[1], ev);
+        if (nch_mt > 0) {
+            // one workgroup per (chunk, kv head) for all tokens and query heads
+            const bool tm = armed(kProfAttnMt, kv_bytes[1], ev);
+            hipExtLaunchKernelGGL((k_attn_mt<HD>), dim3(nch_mt, n_kv), dim3(kSW),
+                                  mt_lds_floats<HD>(n_tok * R) * sizeof(float), st, tm ? ev.a : nullptr,
+                                  tm ? ev.b : nullptr, 0, d_qkv, ldqkv, n_tok, n_heads, n_kv, d_pos, pos_off,
+                                  (const float2*)d_rope, d_kc, d_vc, ctx, w);
+            ORC_LAUNCH_CHECK();
+        }
+        if (nch_sp > 0) {
             // all query heads of a kv head in one workgroup (one workgroup
-            // per query head measured slower here: 12.1 vs 9.2 us for a
+            // per query head measured slower: 12.1 vs 9.2 us for a
             // 0.5B-draft decode step at 8.4 K positions)
-            hipExtLaunchKernelGGL((k_attn_split<HD, kRMax>), dim3(nch, n_kv * ((R + kRMax - 1) / kRMax), n_tok),
+            const bool tm = armed(kProfAttnSplit, kv_bytes[2], ev);
+            hipExtLaunchKernelGGL((k_attn_split<HD, kRMax>), dim3(nch_sp, n_kv * ((R + kRMax - 1) / kRMax), n_tok),
                                   dim3(kSW), 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr, 0, d_qkv, ldqkv, n_heads,
                                   n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
             ORC_LAUNCH_CHECK();
-            tm = armed(kProfAttnMerge, 0.0, ev);
+        }
+        if (nch_mt > 0 || nch_sp > 0) {
+            const bool tm = armed(kProfAttnMerge, 0.0, ev);
             hipExtLaunchKernelGGL(k_attn_merge<HD>, dim3(n_heads, n_tok), dim3(kSW), 0, st, tm ? ev.a : nullptr,
                                   tm ? ev.b : nullptr, 0, n_heads, n_kv, d_pos, pos_off, ctx, (const float*)w, d_out,
                                   ldo);
