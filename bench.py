@@ -145,6 +145,10 @@ WORKLOADS = {
     "c4": dict(tgt="c4", dft="c4d", n_prompt=256, n_gen=512, k=6, ctx=4096, mode="engine", prompt_seed=4321,
                desc="C4 Engine stochastic spec: 7B-shape Q4_K_M target (QKV bias) + 0.5B-shape Q8_0 draft, "
                     "T 0.8, top-p 0.95, top-k 40, repeat penalty 1.1 over 64, seed 4242"),
+    "c4s": dict(tgt="c4", dft="c4d", n_prompt=256, n_gen=512, k=6, ctx=4096, mode="sampled", prompt_seed=4321,
+                desc="C4 models, speculative sampling (min(1, p/q) acceptance, residual resampling, bonus draw): "
+                     "7B-shape Q4_K_M target (QKV bias) + 0.5B-shape Q8_0 draft, T 0.8, top-p 0.95, top-k 40, "
+                     "repeat penalty 1.1 over 64, seed 4242"),
     "c5": dict(tgt="c5", dft="c4d", n_prompt=8192, n_gen=512, k=8, ctx=16384, mode="greedy", prompt_seed=8192,
                desc="C5 long-context spec greedy: 7B-shape all-Q6_K target + 0.5B-shape Q8_0 draft"),
 }
@@ -262,12 +266,16 @@ def main():
     prompt = np.random.default_rng(W["prompt_seed"]).integers(0, tgt.n_vocab, n_prompt).astype(np.int32)
     if a.no_graphs:
         orc.load_host_lib().orch_set_graphs(0)
-    engine = W["mode"] == "engine"
+    # stochastic loops prefill both models on every call, as Engine::generate
+    # does (core/engine.cpp:115-125)
+    engine = W["mode"] in ("engine", "sampled")
     plain = W["mode"] == "greedy_only"
 
     def run(n, prefill):
-        if engine:  # Engine::generate prefills both models on every call (core/engine.cpp:115-125)
+        if W["mode"] == "engine":
             return tgt.spec_engine(dft, prompt, n, k, *SAMPLER)
+        if W["mode"] == "sampled":
+            return tgt.spec_sampled(dft, prompt, n, k, *SAMPLER)
         if plain:  # the reference harness's greedy decode (benchmark/bench_engine.cpp:221-243)
             return tgt.greedy(prompt, n, prefill=prefill), {"accepted": 0, "proposed": 0, "passes": n}
         return tgt.spec_greedy(dft, prompt, n, k, prefill=prefill)
@@ -409,8 +417,8 @@ def main():
     }
     if engine:
         out["prefill_ms"] = round(prefill_ms, 2)
-        out["value_note"] = ("each step is a whole Engine call: the prefill of both models (prefill_ms) plus "
-                             f"{n_gen} generated tokens")
+        out["value_note"] = (f"each step is a whole {'Engine' if W['mode'] == 'engine' else 'spec_sampled'} call: "
+                             f"the prefill of both models (prefill_ms) plus {n_gen} generated tokens")
     if a.workload == "c5":
         kv = [f for f in fams if f["kernel"].startswith(("attn k_attn_mt", "attn k_attn_split"))
               and f["kernel"].endswith(f"={k + 1}")]

@@ -246,7 +246,9 @@ int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv,
  * tokens per call; head_dim 64 or 128; 16-byte aligned rows.
  * A token attending to at most orc_attn_wg_limit() (512) positions is
  * computed by one workgroup per query head; a longer one's positions are
- * split over up to 256 chunks (64 positions each up to 16384) whose partial
+ * split over up to 256 chunks (64 positions each up to 16384, one workgroup
+ * per chunk and kv head for all tokens of the call, on the matrix cores in
+ * fp32; wider chunks above) whose partial
  * results a second launch merges: d_work holds orc_attn_fused_workspace(n_heads, n_kv,
  * head_dim) bytes, 16-byte aligned; calls that share a workspace must not
  * overlap. With device positions, every token position p of the call (or of
@@ -293,9 +295,10 @@ int orc_spec_accept_greedy_at(const int32_t* d_tgt_ids, const int32_t* d_draft_i
  * std::mt19937 is (the reference passes a 64-bit seed that the engine
  * truncates, sampler.cpp:7-8), the parameters of SamplerParams
  * (sampler.hpp:16-22) and the history, initialised with n_hist recorded ids.
- * top_k 0 = all tokens, for vocabularies of at most 16384 tokens: with such
- * a state, orc_sample / orc_spec_accept_engine / orc_transform_probs on a
- * larger vocabulary return ORC_E_UNSUPPORTED; repeat_last < 2048. */
+ * top_k 0 = all tokens, for vocabularies of at most 16384 tokens when
+ * T > 0 (T <= 0 is the argmax and sorts nothing): with such a state,
+ * orc_sample / orc_spec_accept_engine / orc_transform_probs on a larger
+ * vocabulary return ORC_E_UNSUPPORTED; repeat_last < 2048. */
 size_t orc_sampler_state_bytes(void);
 int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty, int repeat_last,
                      uint64_t seed, const int32_t* d_hist, int n_hist, orc_stream_t stream);

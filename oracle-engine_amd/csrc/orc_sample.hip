@@ -678,8 +678,8 @@ __global__ void k_sampler_history(const DevSampler* s, int32_t* out, int cap, in
 using namespace orc;
 
 // Host record of the sampler states initialised with top_k = 0 ("all
-// tokens"): their vocabulary must fit the candidate sort (kCandMax). The
-// state itself is device memory the host never reads back.
+// tokens") and T > 0: their vocabulary must fit the candidate sort
+// (kCandMax). The state itself is device memory the host never reads back.
 static std::mutex g_all_mu;
 static std::unordered_set<const void*> g_all_tokens;
 
@@ -703,7 +703,7 @@ extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, i
         return set_error(ORC_E_INVALID, "sampler_init: bad args (0 <= top_k <= 16384, repeat_last < 2048)");
     {
         std::lock_guard<std::mutex> lk(g_all_mu);
-        if (top_k == 0) g_all_tokens.insert(d_state);
+        if (top_k == 0 && temperature > 0.f) g_all_tokens.insert(d_state);  // T <= 0 sorts nothing (argmax)
         else g_all_tokens.erase(d_state);
     }
     hipLaunchKernelGGL(k_sampler_init, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state,
@@ -719,7 +719,7 @@ extern "C" int orc_sampler_set_params(void* d_state, float temperature, float to
         return set_error(ORC_E_INVALID, "sampler_set_params: bad args (0 <= top_k <= 16384, repeat_last < 2048)");
     {
         std::lock_guard<std::mutex> lk(g_all_mu);
-        if (top_k == 0) g_all_tokens.insert(d_state);
+        if (top_k == 0 && temperature > 0.f) g_all_tokens.insert(d_state);  // T <= 0 sorts nothing (argmax)
         else g_all_tokens.erase(d_state);
     }
     hipLaunchKernelGGL(k_sampler_set, dim3(1), dim3(64), 0, resolve_stream(s), (DevSampler*)d_state, 1, temperature,

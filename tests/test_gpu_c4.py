@@ -79,3 +79,39 @@ def test_c4_engine_spec_stream_and_stats_match_reference(c4):
     assert np.array_equal(toks, fix["espec_tokens"])
     acc, prop, passes = (int(v) for v in fix["espec_stats"])
     assert (st["accepted"], st["proposed"], st["passes"]) == (acc, prop, passes)
+
+
+def test_c4_spec_sampled_full_size(c4):
+    """Speculative sampling (min(1, p/q) acceptance, residual resampling, bonus
+    draw) at C4 size, where no CPU loop can run: at T = 0 without penalty it is
+    the target's greedy decode (same stream; every proposal accounted for); at
+    C4's sampler settings the stream is a function of the seed alone (graph
+    replay and host launches agree, a second call repeats it) and the counts
+    are consistent. The rule itself is pinned against the oracle loop on the
+    small model pairs (test_gpu_spec_sampling.py)."""
+    import orc
+
+    fix, tgt, dft = c4
+    k = int(fix["k"][0])
+    temp, top_p, top_k, pen, last, seed = fix["sampler"]
+    prompt = fix["prompt"]
+    n = 96
+    print(f"[gpu] c4 spec_sampled T=0 limit k={k}, {n} tokens", flush=True)
+    greedy = tgt.greedy(prompt, n)
+    toks, st = tgt.spec_sampled(dft, prompt, n, k, 0.0, 1.0, 0, 1.0, int(last), int(seed))
+    assert np.array_equal(toks[:n], greedy)
+    assert 0 <= st["accepted"] <= st["proposed"] and st["passes"] >= 1
+    H = orc.load_host_lib()
+    runs = []
+    for graphs in (True, False, True):
+        print(f"[gpu] c4 spec_sampled T={float(temp)} graphs={graphs}", flush=True)
+        prev = H.orch_set_graphs(int(graphs))
+        try:
+            runs.append(tgt.spec_sampled(dft, prompt, n, k, float(temp), float(top_p), int(top_k), float(pen),
+                                         int(last), int(seed)))
+        finally:
+            H.orch_set_graphs(prev)
+    (t0, s0), (t1, s1), (t2, s2) = runs
+    assert np.array_equal(t0, t1) and np.array_equal(t0, t2) and s0 == s1 == s2
+    assert len(t0) >= n and int(t0.min()) >= 0 and int(t0.max()) < tgt.n_vocab
+    assert 0 <= s0["accepted"] <= s0["proposed"] and s0["passes"] * (k + 1) >= len(t0)

@@ -167,7 +167,8 @@ def test_all_tokens_top_k_refuses_large_vocabulary(dev):
 
     V = 20000
     st = dev.alloc(dev.L.orc_sampler_state_bytes())
-    lg = dev.upload(np.random.default_rng(5).normal(size=V).astype(np.float32))
+    x = np.random.default_rng(5).normal(size=V).astype(np.float32)
+    lg = dev.upload(x)
     out = dev.alloc(16)
     dev.check(dev.L.orc_sampler_init(st.ptr, C.c_float(0.8), C.c_float(0.95), 0, C.c_float(1.1), 64, 42, None, 0,
                                      None))
@@ -180,4 +181,10 @@ def test_all_tokens_top_k_refuses_large_vocabulary(dev):
     dev.check(dev.L.orc_sampler_init(st.ptr, C.c_float(0.8), C.c_float(0.95), 40, C.c_float(1.1), 64, 42, None, 0,
                                      None))
     dev.check(dev.L.orc_sample(st.ptr, lg.ptr, V, out.ptr, None))
+    # T = 0 is the argmax (sampler.cpp:50): top_k = 0 sorts nothing then, so any vocabulary works
+    dev.check(dev.L.orc_sampler_init(st.ptr, C.c_float(0.0), C.c_float(0.95), 0, C.c_float(1.0), 64, 42, None, 0,
+                                     None))
+    lg = dev.upload(x)  # orc_sample leaves probabilities in the row it sampled
+    dev.check(dev.L.orc_sample(st.ptr, lg.ptr, V, out.ptr, None))
+    assert int(out.read(np.int32, 1)[0]) == int(np.argmax(x))
     assert 0 <= int(out.read(np.int32, 1)[0]) < V
