@@ -771,6 +771,11 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
     if (decode && type == kMixK) return dispatch_mixed_decode(p, s);
     p.units = p.n_in / elems_per_unit(type);
     const bool mm = mmq_type(type) && !decode;
+    if (mm && mmq_prefill(type, p)) {  // a prefill pass: every token in one launch
+        LaunchEvents ev;
+        if (g_prof_on) prof_arm(s, type, p.n_tok, gemm_bytes(p, p.n_tok), &ev.start, &ev.stop);
+        return mmq_prefill_launch(type, p, s, ev);
+    }
     const int ntmax = mm ? mmq_max_tokens(type, p) : max_tokens(type, p.n_in);
     if (ntmax < 1) return set_error(ORC_E_UNSUPPORTED, "gemm: n_in too large for the activations to fit LDS");
     // Tokens go in blocks of ntmax (the second grid dimension of one launch:

@@ -42,7 +42,7 @@ class Model {
 public:
     ModelConfig cfg;
     static constexpr int kMaxBatch = 16;      // tokens per device pass with logits (verify)
-    static constexpr int kPrefillBatch = 256;  // tokens per device pass without logits (prefill)
+    static constexpr int kPrefillBatch = 1024;  // tokens per device pass without logits (prefill)
 
     Model() = default;
     ~Model();

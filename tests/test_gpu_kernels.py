@@ -120,6 +120,90 @@ def test_gemm_batch_invariant(dev, oracle, qt, n_out, n_in):
         assert np.all(np.abs(full - single) <= 4e-6 * scale + 1e-30), np.max(np.abs(full - single) / scale)
 
 
+@pytest.mark.parametrize("qt,n_out,n_in,nt", [(ol.Q4_K, 300, 3072, 300), (ol.Q6_K, 130, 2048, 256),
+                                              (ol.Q6_K, 200, 18944, 263), (ol.Q4_K, 64, 512, 640),
+                                              (ol.Q4_K, 8192, 3072, 256)])
+def test_gemm_prefill_vs_exact_and_blocks(dev, oracle, qt, n_out, n_in, nt):
+    """Calls of 256 tokens or more on a K-quant matrix run the prefill kernel
+    (64 tokens per workgroup, each weight slice decoded once for all of them):
+    every (token, row) within 2e-6 of sum |w x| of the float64 product and
+    within 4e-6 of the same tokens in 16-token calls (the verify kernel), with
+    partial token and row blocks; a token's row does not depend on the call's
+    other tokens (bit for bit)."""
+    print(f"[gpu] prefill gemm type={qt} {n_out}x{n_in} nt={nt}", flush=True)
+    rng = np.random.default_rng(n_out + nt)
+    raw = rand_blocks(qt, n_out * n_in, rng)
+    wd = dev.upload(raw)
+    X = rng.normal(0, 1, (nt, n_in)).astype(np.float32)
+    full = _gemm(dev, qt, wd, nt, n_out, n_in, X)
+    blocks = np.concatenate([_gemm(dev, qt, wd, min(16, nt - t), n_out, n_in, X[t:t + 16]) for t in range(0, nt, 16)])
+    W = oracle.dequant(qt, raw, n_out * n_in).reshape(n_out, n_in).astype(np.float64)
+    exact = X.astype(np.float64) @ W.T
+    scale = np.abs(X.astype(np.float64)) @ np.abs(W).T
+    assert np.all(np.abs(full - exact) <= 2e-6 * scale + 1e-30), np.max(np.abs(full - exact) / scale)
+    assert np.all(np.abs(full - blocks) <= 4e-6 * scale + 1e-30), np.max(np.abs(full - blocks) / scale)
+    tail = _gemm(dev, qt, wd, 256, n_out, n_in, X[nt - 256:])
+    assert np.array_equal(tail.view(np.uint32), full[nt - 256:].view(np.uint32))
+
+
+def test_gemm_prefill_epilogues(dev):
+    """The prefill kernel's RMSNorm prologue, bias, three output segments,
+    SwiGLU pairs and residual accumulation agree with the verify kernel's
+    (16-token calls of the same fused entry point)."""
+    print("[gpu] prefill gemm epilogues", flush=True)
+    import orc
+
+    rng = np.random.default_rng(17)
+    n_in, nq, nk, ff, nt = 1024, 256, 128, 320, 300
+    X = rng.normal(0, 1, (nt, n_in)).astype(np.float32)
+    dx = dev.upload(X)
+    dnorm = dev.upload(rng.uniform(0.5, 1.5, n_in).astype(np.float32))
+    wq, wk, wv = (dev.upload(rand_blocks(ol.Q4_K, n * n_in, rng)) for n in (nq, nk, nk))
+    bq = dev.upload(rng.normal(0, 0.1, nq).astype(np.float32))
+
+    def both(run, ld, init=None):
+        """run(t0, n, dy) for the whole call and for 16-token calls; returns both outputs"""
+        outs = []
+        for chunk in (nt, 16):
+            dy = dev.upload(init) if init is not None else dev.alloc(nt * ld * 4)
+            for t0 in range(0, nt, chunk):
+                run(t0, min(chunk, nt - t0), dy)
+            outs.append(dy.read(np.float32).reshape(nt, ld))
+        return outs
+
+    ld = nq + 2 * nk
+
+    def qkv(t0, n, dy):
+        yo = dy.ptr + t0 * ld * 4
+        segs = (orc.Seg * 3)(orc.Seg(wq.ptr, nq, yo, bq.ptr), orc.Seg(wk.ptr, nk, yo + nq * 4, None),
+                             orc.Seg(wv.ptr, nk, yo + (nq + nk) * 4, None))
+        dev.check(dev.L.orc_gemm_fused(ol.Q4_K, segs, 3, n, n_in, dx.ptr + t0 * n_in * 4, n_in, ld, dnorm.ptr,
+                                       C.c_float(1e-5), orc.EPI_STORE, None))
+
+    a, b = both(qkv, ld)
+    assert np.allclose(a, b, rtol=0, atol=2e-5 * np.abs(b).max())
+    for st in (ol.Q6_K, ol.Q4_K):
+        wg, wu = (dev.upload(rand_blocks(st, ff * n_in, rng)) for _ in range(2))
+
+        def swiglu(t0, n, dy):
+            yo = dy.ptr + t0 * ff * 4
+            segs = (orc.Seg * 2)(orc.Seg(wg.ptr, ff, yo, None), orc.Seg(wu.ptr, ff, yo, None))
+            dev.check(dev.L.orc_gemm_fused(st, segs, 2, n, n_in, dx.ptr + t0 * n_in * 4, n_in, ff, dnorm.ptr,
+                                           C.c_float(1e-5), orc.EPI_SWIGLU, None))
+
+        a, b = both(swiglu, ff)
+        assert np.allclose(a, b, rtol=1e-5, atol=1e-5 * np.abs(b).max()), st
+    res = rng.normal(0, 1, (nt, nk)).astype(np.float32)
+
+    def accum(t0, n, dy):
+        segs = (orc.Seg * 1)(orc.Seg(wk.ptr, nk, dy.ptr + t0 * nk * 4, None))
+        dev.check(dev.L.orc_gemm_fused(ol.Q4_K, segs, 1, n, n_in, dx.ptr + t0 * n_in * 4, n_in, nk, None,
+                                       C.c_float(0), orc.EPI_ACCUM, None))
+
+    a, b = both(accum, nk, res)
+    assert np.allclose(a, b, rtol=0, atol=2e-5 * np.abs(b).max())
+
+
 @pytest.mark.parametrize("n_in", [512, 3072])  # 3072: the streamed-weight kernel
 def test_gemm_fused_epilogues(dev, n_in):
     print(f"[gpu] fused epilogues n_in={n_in}", flush=True)
