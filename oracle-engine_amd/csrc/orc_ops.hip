@@ -1302,6 +1302,15 @@ extern "C" int orc_decode_advance(int32_t* d_tok, int32_t* d_hist, int32_t* d_po
 }
 
 
+// A timed launch takes its dispatch's start / stop events (hipExtLaunchKernelGGL);
+// every other launch, and so every launch recorded into a graph, is a plain one.
+template <typename K, typename... A>
+static void attn_launch(bool timed, const LaunchEv& ev, K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st,
+                        A... args) {
+    if (timed) hipExtLaunchKernelGGL(kernel, grid, block, lds, st, ev.a, ev.b, 0, args...);
+    else hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+}
+
 extern "C" size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim) {
     if (n_heads <= 0 || n_kv <= 0 || head_dim <= 0) return 0;
     return (size_t)kMaxTokAttn * n_heads * kNCMax * (head_dim + 32) * sizeof(float);
@@ -1369,18 +1378,16 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
             // one workgroup per (query head, token)
             const dim3 blk(wg_waves<HD>() * 64), grid(n_heads, n_tok);
             const bool tm = armed(kProfAttnWG, kv_bytes[0], ev);
-            hipExtLaunchKernelGGL((k_attn_wg<HD, 1>), grid, blk, 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr, 0,
-                                  d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx,
-                                  d_out, ldo);
+            attn_launch(tm, ev, (k_attn_wg<HD, 1>), grid, blk, 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off,
+                        (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
             ORC_LAUNCH_CHECK();
         }
         if (nch_mt > 0) {
             // one workgroup per (chunk, kv head) for all tokens and query heads
             const bool tm = armed(kProfAttnMt, kv_bytes[1], ev);
-            hipExtLaunchKernelGGL((k_attn_mt<HD>), dim3(nch_mt, n_kv), dim3(kSW),
-                                  mt_lds_floats<HD>(n_tok * R) * sizeof(float), st, tm ? ev.a : nullptr,
-                                  tm ? ev.b : nullptr, 0, d_qkv, ldqkv, n_tok, n_heads, n_kv, d_pos, pos_off,
-                                  (const float2*)d_rope, d_kc, d_vc, ctx, w);
+            attn_launch(tm, ev, (k_attn_mt<HD>), dim3(nch_mt, n_kv), dim3(kSW),
+                        mt_lds_floats<HD>(n_tok * R) * sizeof(float), st, d_qkv, ldqkv, n_tok, n_heads, n_kv, d_pos,
+                        pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, w);
             ORC_LAUNCH_CHECK();
         }
         if (nch_sp > 0) {
@@ -1388,16 +1395,15 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
             // per query head measured slower: 12.1 vs 9.2 us for a
             // 0.5B-draft decode step at 8.4 K positions)
             const bool tm = armed(kProfAttnSplit, kv_bytes[2], ev);
-            hipExtLaunchKernelGGL((k_attn_split<HD, kRMax>), dim3(nch_sp, n_kv * ((R + kRMax - 1) / kRMax), n_tok),
-                                  dim3(kSW), 0, st, tm ? ev.a : nullptr, tm ? ev.b : nullptr, 0, d_qkv, ldqkv, n_heads,
-                                  n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo, w);
+            attn_launch(tm, ev, (k_attn_split<HD, kRMax>), dim3(nch_sp, n_kv * ((R + kRMax - 1) / kRMax), n_tok),
+                        dim3(kSW), 0, st, d_qkv, ldqkv, n_heads, n_kv, d_pos, pos_off, (const float2*)d_rope, d_kc,
+                        d_vc, ctx, d_out, ldo, w);
             ORC_LAUNCH_CHECK();
         }
         if (nch_mt > 0 || nch_sp > 0) {
             const bool tm = armed(kProfAttnMerge, 0.0, ev);
-            hipExtLaunchKernelGGL(k_attn_merge<HD>, dim3(n_heads, n_tok), dim3(kSW), 0, st, tm ? ev.a : nullptr,
-                                  tm ? ev.b : nullptr, 0, n_heads, n_kv, d_pos, pos_off, ctx, (const float*)w, d_out,
-                                  ldo);
+            attn_launch(tm, ev, (k_attn_merge<HD>), dim3(n_heads, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos,
+                        pos_off, ctx, (const float*)w, d_out, ldo);
             ORC_LAUNCH_CHECK();
         }
         return ORC_OK;
