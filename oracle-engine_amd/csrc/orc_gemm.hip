@@ -675,8 +675,17 @@ static int launch_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) 
     const bool tall = p.n_rows >= 32768;  // LM heads
     if constexpr (NT == 1) {
         if ((QT == ORC_Q6_K && tall) || pair) return launch_shape<QT, NT, 2, 1, 4>(p, s, ev);
-        // tall matrices whose rows are one batch: row groups double-buffered
-        if (tall && p.units <= QTr<QT>::LPR * 3) return launch_shape<QT, NT, 1, 3, 4, true>(p, s, ev);
+        // units per lane per batch: at most what a row gives a lane (the
+        // clamped extra loads of a shorter row only cost: a 151936 x 896
+        // Q8_0 head took 80 us with three per batch, 41 us with one)
+        const int per_lane = (p.units + QTr<QT>::LPR - 1) / QTr<QT>::LPR;
+        if (tall && per_lane <= 3) {  // rows of one batch: row groups double-buffered
+            if (per_lane == 1) return launch_shape<QT, NT, 1, 1, 4, true>(p, s, ev);
+            if (per_lane == 2) return launch_shape<QT, NT, 1, 2, 4, true>(p, s, ev);
+            return launch_shape<QT, NT, 1, 3, 4, true>(p, s, ev);
+        }
+        if (per_lane == 1) return launch_shape<QT, NT, 1, 1, 4>(p, s, ev);
+        if (per_lane == 2) return launch_shape<QT, NT, 1, 2, 4>(p, s, ev);
         return launch_shape<QT, NT, 1, 3, 4>(p, s, ev);
     } else {
         if (pair || tall) return launch_shape<QT, NT, 2, 1, 2>(p, s, ev);
