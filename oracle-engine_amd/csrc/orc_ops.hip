@@ -775,25 +775,25 @@ __global__ __launch_bounds__(kSW) void k_attn_mt(const float* qkv, int ldqkv, in
     }
 }
 
-// Merge of the chunk partials of k_attn_split: one workgroup per (query
-// head, token). Every thread loads one chunk's (m, l) and forms e^(m_c - M)
-// in parallel (M = the maximum, which no order changes). The sums
-// O = sum_c O_c e^(m_c - M) and L = sum_c l_c e^(m_c - M) then run in chunk
-// order: up to kSerialMerge chunks in one lane per output dimension (L in
-// one more lane); above, the kSW / HD lanes of a dimension each take a
-// contiguous quarter (head_dim 64) or half (128) of the chunks and their
-// sums are added in range order. Either way the order depends on the
-// token's position alone. Tokens with a single chunk were written directly
-// and are skipped.
-constexpr int kSerialMerge = 32;
+// Merge of the chunk partials of k_attn_mt / k_attn_split: one workgroup of
+// kMG threads per (query head, token). Every thread loads one chunk's (m, l)
+// and forms e^(m_c - M) in parallel (M = the maximum, which no order
+// changes). The sums O = sum_c O_c e^(m_c - M) and L = sum_c l_c e^(m_c - M)
+// then run in chunk order: up to kSerialMerge chunks in one lane per output
+// dimension (L in one more lane); above, the kMG / HD lanes of a dimension
+// each take a contiguous range of the chunks (at most eight at C5's 8 K
+// positions: one batch of loads) and their sums are added in range order.
+// Either way the order depends on the token's position alone. Tokens with a
+// single chunk were written directly and are skipped.
+constexpr int kSerialMerge = 8, kMG = 1024;  // serial up to one batch of loads; threads of a merge workgroup
 template <int HD>
-__global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const int* d_pos, int pos_off, int ctx,
+__global__ __launch_bounds__(kMG) void k_attn_merge(int n_heads, int n_kv, const int* d_pos, int pos_off, int ctx,
                                                     const float* work, float* out, int ldo) {
-    constexpr int PS = part_stride<HD>(), S = kSW / HD;
-    static_assert(kNCMax == kSW, "one chunk per thread");
+    constexpr int PS = part_stride<HD>(), S = kMG / HD;
+    static_assert(kNCMax <= kMG, "one chunk per thread");
     static_assert(S >= 2, "a lane outside the output dimensions sums L in serial merges");
     __shared__ float sf[kNCMax], sl[kNCMax];  // e^(m_c - M), l_c
-    __shared__ float smax[kSW / 64], sLq[S];
+    __shared__ float smax[kMG / 64], sLq[S];
     __shared__ __align__(16) float so[S][HD];
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int R = n_heads / n_kv, g = h / R, r = h - g * R;
@@ -815,7 +815,7 @@ __global__ __launch_bounds__(kSW) void k_attn_merge(int n_heads, int n_kv, const
     __syncthreads();
     M = smax[0];
 #pragma unroll
-    for (int i = 1; i < kSW / 64; ++i) M = fmaxf(M, smax[i]);
+    for (int i = 1; i < kMG / 64; ++i) M = fmaxf(M, smax[i]);
     if (tid < nch) sf[tid] = expf(mc - M);
     __syncthreads();
     const bool serial = nch <= kSerialMerge;
@@ -1402,7 +1402,7 @@ extern "C" int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n
         }
         if (nch_mt > 0 || nch_sp > 0) {
             const bool tm = armed(kProfAttnMerge, 0.0, ev);
-            attn_launch(tm, ev, (k_attn_merge<HD>), dim3(n_heads, n_tok), dim3(kSW), 0, st, n_heads, n_kv, d_pos,
+            attn_launch(tm, ev, (k_attn_merge<HD>), dim3(n_heads, n_tok), dim3(kMG), 0, st, n_heads, n_kv, d_pos,
                         pos_off, ctx, (const float*)w, d_out, ldo);
             ORC_LAUNCH_CHECK();
         }
