@@ -735,8 +735,9 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
 // every unit of its rows once: each wave decodes its row tile's slice (the
 // same unit arithmetic as k_mmq: Q4_K scale folded into the codes, Q6_K
 // codes split into exact hi / lo halves) and feeds it to the hi and the lo
-// A tiles of four 16-token tiles, so a weight byte is streamed once per 64
-// tokens instead of once per 16-token block. The activations of the next
+// A tiles of four 16-token tiles (Q6_K: hi x hi, lo x hi and hi x lo; the
+// lo x lo term is below 2^-22 of each product and dropped), so a weight
+// byte is streamed once per 64 tokens instead of once per 16-token block. The activations of the next
 // unit (64 tokens x 128 values) are loaded while this unit's MFMAs run, then
 // split into hi / lo fp16 with a power of two per (unit, token) that keeps
 // them in range (as k_mmq stages them) into the other of two LDS buffers;
@@ -917,19 +918,32 @@ __global__ __launch_bounds__(kPfWG) void k_mmq_pf(QmvParams p) {
                 if constexpr (QT == ORC_Q4_K) bh[rt] = q4k_slice_b(cur[rt], i, sc4[rt]);
                 else q6k_slice_b(cur[rt], i, c, bh[rt], bl[rt]);
             }
+            h8v ah[kPfTT], al[kPfTT];
 #pragma unroll
             for (int tt = 0; tt < kPfTT; ++tt) {
                 const uint8_t* ap = ab + ((i * 4 + c) * 2 * kPfBM + tt * 16 + n) * 16;
-                const h8v ah = *(const h8v*)ap, al = *(const h8v*)(ap + kPfBM * 16);
+                ah[tt] = *(const h8v*)ap;
+                al[tt] = *(const h8v*)(ap + kPfBM * 16);
+            }
+            // each product over every (token tile, row tile) accumulator in
+            // turn, so consecutive MFMAs never wait on each other; Q6_K drops
+            // the lo activations x lo codes term (below 2^-22 of each product)
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
-                    D[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[rt], D[tt][rt], 0, 0, 0);
-                    D[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[rt], D[tt][rt], 0, 0, 0);
-                    if constexpr (QT == ORC_Q6_K) {
-                        D[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[rt], D[tt][rt], 0, 0, 0);
-                        D[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bl[rt], D[tt][rt], 0, 0, 0);
-                    }
-                }
+            for (int tt = 0; tt < kPfTT; ++tt)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    D[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[tt], bh[rt], D[tt][rt], 0, 0, 0);
+#pragma unroll
+            for (int tt = 0; tt < kPfTT; ++tt)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    D[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[tt], bh[rt], D[tt][rt], 0, 0, 0);
+            if constexpr (QT == ORC_Q6_K) {
+#pragma unroll
+                for (int tt = 0; tt < kPfTT; ++tt)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        D[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[tt], bl[rt], D[tt][rt], 0, 0, 0);
             }
         }
         // acc += d 2^-e D (Q4_K: minus the unit's minimum terms, one MFMA)
