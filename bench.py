@@ -153,8 +153,8 @@ WORKLOADS = {
                desc="C5 long-context spec greedy: 7B-shape all-Q6_K target + 0.5B-shape Q8_0 draft"),
 }
 SAMPLER = (0.8, 0.95, 40, 1.1, 64, 4242)  # T, top-p, top-k, repeat penalty, repeat_last, seed (C4)
-PROF_FAMILIES = (2, 8, 12, 14, 256, 258, 300, 301, 302, 303)
-FAMILY_NAMES = {**TYPE_NAMES, 300: "attn k_attn_wg", 301: "attn k_attn_split", 302: "attn k_attn_merge", 303: "attn k_attn_mt"}
+PROF_FAMILIES = (2, 8, 12, 14, 256, 258, 300, 301, 302, 303, 304)
+FAMILY_NAMES = {**TYPE_NAMES, 300: "attn k_attn_wg", 301: "attn k_attn_split", 302: "attn k_attn_merge", 303: "attn k_attn_mt", 304: "attn k_attn_pf"}
 
 
 def family_label(ty, nt):

@@ -155,7 +155,8 @@ int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n_segs, int 
  * event (hipExtLaunchKernelGGL: both take the timestamps of the kernel's own
  * dispatch on its stream) and its algorithmic HBM bytes (weight blocks + x +
  * y) are noted; so does every attention launch of orc_attn_fused_at with
- * host positions (families ORC_PROF_ATTN_WG / _MT / _SPLIT / _MERGE; bytes = the K
+ * host positions (families ORC_PROF_ATTN_WG / _MT / _SPLIT / _MERGE, and
+ * orc_attn_prefill: ORC_PROF_ATTN_PF; bytes = the K
  * and V rows its tokens read, counted once, + QKV rows in + rows out; the
  * merge is noted with 0 bytes). Once the work has run, orc_prof_accumulate
  * adds every launch's elapsed time to its record; orc_prof_read sums the
@@ -168,6 +169,7 @@ int orc_gemm_fused_mixed(const int* types, const orc_seg* segs, int n_segs, int 
 #define ORC_PROF_ATTN_SPLIT 301
 #define ORC_PROF_ATTN_MERGE 302
 #define ORC_PROF_ATTN_MT 303
+#define ORC_PROF_ATTN_PF 304
 int orc_prof_enable(int on);
 int orc_prof_accumulate(void);
 int orc_prof_read(int type, int n_tok, int64_t* launches, double* total_ms, double* total_bytes);
@@ -258,6 +260,17 @@ int orc_attn_gqa_at(const float* d_q, int ldq, int n_tok, int n_heads, int n_kv,
  * may be left unwritten) and sizes their grids by pos_limit. Host-position
  * calls take pos_floor = 0, pos_limit = ctx. */
 size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim);
+/* Prefill form of orc_attn_fused_at (host positions pos_off.., any n_tok, no
+ * workspace): RoPE on q and k, K / V of every token stored in the cache,
+ * causal attention of each token over positions 0..its own, written to
+ * d_out (rows of ldo floats); the same layouts, limits (head_dim 64 / 128,
+ * at most 8 query heads per kv head) and alignment. One workgroup per
+ * (16-token block, kv head) walks the key chunks with an online softmax:
+ * within fp32 rounding of orc_attn_fused_at's results, not equal to them
+ * bit for bit (core/model.cpp:595-626 is the prefill counterpart). */
+int orc_attn_prefill(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim, int pos_off,
+                     const float* d_rope, float* d_kc, float* d_vc, int ctx, float* d_out, int ldo,
+                     orc_stream_t stream);
 int orc_attn_wg_limit(void);
 int orc_attn_fused_at(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
                       const int32_t* d_pos, int pos_off, const float* d_rope, float* d_kcache, float* d_vcache,

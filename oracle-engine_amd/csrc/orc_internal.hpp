@@ -25,7 +25,7 @@ int argmax_noalloc_device_init(int device);
 // (events untouched) otherwise. Families: the GGML weight type of a GEMM, or
 // one of the attention ids below.
 constexpr int kProfAttnWG = ORC_PROF_ATTN_WG, kProfAttnSplit = ORC_PROF_ATTN_SPLIT, kProfAttnMerge = ORC_PROF_ATTN_MERGE,
-              kProfAttnMt = ORC_PROF_ATTN_MT;
+              kProfAttnMt = ORC_PROF_ATTN_MT, kProfAttnPf = ORC_PROF_ATTN_PF;
 bool prof_arm(hipStream_t s, int family, int n_tok, double bytes, hipEvent_t* start, hipEvent_t* stop);
 
 #define ORC_HIP_CHECK(expr)                                                                       \

@@ -775,6 +775,268 @@ __global__ __launch_bounds__(kSW) void k_attn_mt(const float* qkv, int ldqkv, in
     }
 }
 
+// ── prefill attention: 16-token query blocks, no partials ───────────────────
+// orc_attn_prefill (prompt passes, host positions): one workgroup per (block
+// of kPaTok tokens, kv head g) carries the block's kPaTok x gqa rows
+// (token-major) through every kSB-position key chunk up to the block's last
+// position with an online softmax (running max and sum per row in LDS), so
+// there are no partial rows and no merge launch, and a chunk's K / V rows are
+// read once per query block. Per chunk, as in k_attn_mt: scores on fp32
+// MFMA chains (wave w: positions 16w..16w+15 of the chunk), the causal mask
+// (key p <= the row's own position), the softmax update four lanes per row
+// (rows whose chunk is all masked keep their state: factor 1, e = 0), then
+// O = a O + E V on the matrix cores (wave w: output dims [w HD/4, (w+1)
+// HD/4)). The next chunk's K rows are loaded after the scores and its V rows
+// after P.V; the batch's own positions come from the QKV rows, rotated when
+// used. Different rounding from the decode path (one online softmax over all
+// chunks instead of per-chunk partials), as the reference's prefill and
+// decode differ: within fp32 rounding of the exact attention.
+constexpr int kPaTok = 16;
+template <int HD> constexpr size_t pa_lds_bytes(int R) {
+    const size_t nrp = (size_t)kPaTok * R;
+    return (nrp * (HD + kQPad) + 2 * nrp * (kSB + kSPad) + 4 * nrp) * sizeof(float);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kSW) void k_attn_pf(const float* qkv, int ldqkv, int n_tok, int n_heads, int n_kv,
+                                                 int start, const float2* rope, float* kc, float* vc, int ctx,
+                                                 float* out, int ldo) {
+    constexpr int half = HD / 2, E8 = HD / 8, KPL = HD / 4, CT = HD / 64;
+    constexpr int QS = HD + kQPad, SS = kSB + kSPad;
+    static_assert(kSW == 256 && kSB == 64, "four waves, 16 positions each");
+    extern __shared__ __align__(16) float lds[];
+    const int R = n_heads / n_kv;
+    const int t0 = blockIdx.x * kPaTok, g = blockIdx.y, tid = threadIdx.x;
+    const int w = tid >> 6, ln = tid & 63, li = ln & 15, kg = ln >> 4;
+    const int nt = min(kPaTok, n_tok - t0), NR = nt * R, NRP = kPaTok * R;
+    float* Qs = lds;                          // [NRP][QS] rotated queries
+    float* S = Qs + (size_t)NRP * QS;         // [2][NRP][SS] scores, then e (chunk parity)
+    float* m_run = S + 2 * (size_t)NRP * SS;  // [NRP] running max
+    float* l_run = m_run + NRP;               // [NRP] running sum
+    float* a_row = l_run + NRP;               // [2][NRP] rescale factor of the chunk
+    const float scale = 1.f / sqrtf((float)HD);
+    const size_t kvh = (size_t)(n_heads + g) * HD, vvh = (size_t)(n_heads + n_kv + g) * HD;
+    const float* kg_c = kc + (size_t)g * ctx * HD;
+    const float* vg_c = vc + (size_t)g * ctx * HD;
+    const int p_end = start + t0 + nt;  // keys [0, p_end) hold data the rows read
+    const int nch = (p_end + kSB - 1) / kSB;
+
+    // K rows of chunk c (B operand of the scores; lane: position 16w + li,
+    // dims [kg E8, +E8) and + half), raw; rows of the batch's own positions
+    // also carry their rope pairs and are rotated when used
+    float kb[KPL];
+    float2 kcs[E8];
+    bool krot = false;
+    auto load_k = [&](int c) {
+        const int p = c * kSB + 16 * w + li;
+        krot = false;
+        if (p >= p_end) {
+#pragma unroll
+            for (int i = 0; i < KPL; ++i) kb[i] = 0.f;
+            return;
+        }
+        const float* src = p < start ? kg_c + (size_t)p * HD + kg * E8 : qkv + (size_t)(p - start) * ldqkv + kvh + kg * E8;
+#pragma unroll
+        for (int i = 0; i < E8; i += 4) {
+            const float4 lo = *(const float4*)(src + i), hi = *(const float4*)(src + half + i);
+            kb[i] = lo.x, kb[i + 1] = lo.y, kb[i + 2] = lo.z, kb[i + 3] = lo.w;
+            kb[E8 + i] = hi.x, kb[E8 + i + 1] = hi.y, kb[E8 + i + 2] = hi.z, kb[E8 + i + 3] = hi.w;
+        }
+        if (p >= start) {
+            krot = true;
+            const float2* cs = rope + (size_t)p * half + kg * E8;
+#pragma unroll
+            for (int i = 0; i < E8; ++i) kcs[i] = cs[i];
+        }
+    };
+    // V rows of chunk c (B operand of P.V: V[p0 + 16 kg + m][w HD/4 + 16 ct + li])
+    float vb[CT][16];
+    auto load_v = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int p = c * kSB + 16 * kg + m;
+            const float* src = p >= p_end ? nullptr
+                               : p < start ? vg_c + (size_t)p * HD
+                                           : qkv + (size_t)(p - start) * ldqkv + vvh;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) vb[ct][m] = src ? src[w * (HD / 4) + 16 * ct + li] : 0.f;
+        }
+    };
+    load_k(0);
+    load_v(0);
+
+    // K (rotated) and V of the block's tokens go to the cache
+    for (int i = tid; i < nt * HD; i += kSW) {
+        const int t = t0 + i / HD, d = i % HD, pt = start + t;
+        const float* kr = qkv + (size_t)t * ldqkv + kvh;
+        const float2* cs = rope + (size_t)pt * half;
+        const float kv = d < half ? rot_lo(kr[d], kr[d + half], cs[d]) : rot_hi(kr[d - half], kr[d], cs[d - half]);
+        const size_t o = ((size_t)g * ctx + pt) * HD + d;
+        kc[o] = kv;
+        vc[o] = qkv[(size_t)t * ldqkv + vvh + d];
+    }
+    // rotated queries of the block's rows (rope_q_lds's arithmetic; padded rows zero), running state
+    {
+        constexpr int QD = half / 4;
+        for (int i0 = 0; i0 < NRP * QD; i0 += 4 * kSW) {
+            float4 lo[4], hi[4], c01[4], c23[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = i0 + tid + j * kSW, row = i / QD, d = 4 * (i - row * QD);
+                if (row < NR) {
+                    const int ti = row / R, t = t0 + ti;
+                    const float* qt = qkv + (size_t)t * ldqkv + (size_t)(g * R + row - ti * R) * HD + d;
+                    const float2* cs = rope + (size_t)(start + t) * half + d;
+                    lo[j] = *(const float4*)qt;
+                    hi[j] = *(const float4*)(qt + half);
+                    c01[j] = *(const float4*)cs;
+                    c23[j] = *(const float4*)(cs + 2);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = i0 + tid + j * kSW, row = i / QD, d = 4 * (i - row * QD);
+                if (row < NRP) {
+                    float4 ql = make_float4(0.f, 0.f, 0.f, 0.f), qh = ql;
+                    if (row < NR) {
+                        const float2 e0{c01[j].x, c01[j].y}, e1{c01[j].z, c01[j].w};
+                        const float2 e2{c23[j].x, c23[j].y}, e3{c23[j].z, c23[j].w};
+                        ql = make_float4(rot_lo(lo[j].x, hi[j].x, e0), rot_lo(lo[j].y, hi[j].y, e1),
+                                         rot_lo(lo[j].z, hi[j].z, e2), rot_lo(lo[j].w, hi[j].w, e3));
+                        qh = make_float4(rot_hi(lo[j].x, hi[j].x, e0), rot_hi(lo[j].y, hi[j].y, e1),
+                                         rot_hi(lo[j].z, hi[j].z, e2), rot_hi(lo[j].w, hi[j].w, e3));
+                    }
+                    *(float4*)&Qs[(size_t)row * QS + d] = ql;
+                    *(float4*)&Qs[(size_t)row * QS + half + d] = qh;
+                }
+            }
+        }
+        for (int row = tid; row < NRP; row += kSW) {
+            m_run[row] = -INFINITY;
+            l_run[row] = 0.f;
+        }
+    }
+    mt_f4 o[kRMax][CT];  // O of row tile rt (rows 16 rt + 4 kg + r), this wave's columns
+#pragma unroll
+    for (int rt = 0; rt < kRMax; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) o[rt][ct] = mt_f4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+
+    for (int c = 0; c < nch; ++c) {
+        const int b = c & 1, p0 = c * kSB;
+        float* Sb = S + (size_t)b * NRP * SS;
+        if (krot) {  // the batch's own positions: rotate-half with the position's rope pairs
+#pragma unroll
+            for (int i = 0; i < E8; ++i) {
+                const float a = kb[i], h = kb[E8 + i];
+                kb[i] = rot_lo(a, h, kcs[i]);
+                kb[E8 + i] = rot_hi(a, h, kcs[i]);
+            }
+        }
+        // scores of every row tile against this wave's 16 positions, causal mask
+#pragma unroll
+        for (int rt = 0; rt < kRMax; ++rt) {
+            if (rt >= R) break;
+            const float* q = Qs + (size_t)(rt * 16 + li) * QS + kg * E8;
+            float qa[KPL];
+#pragma unroll
+            for (int i = 0; i < E8; i += 4) {
+                const float4 lo = *(const float4*)(q + i), hi = *(const float4*)(q + half + i);
+                qa[i] = lo.x, qa[i + 1] = lo.y, qa[i + 2] = lo.z, qa[i + 3] = lo.w;
+                qa[E8 + i] = hi.x, qa[E8 + i + 1] = hi.y, qa[E8 + i + 2] = hi.z, qa[E8 + i + 3] = hi.w;
+            }
+            mt_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < KPL; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[m], kb[m], acc, 0, 0, 0);
+            const int pos = 16 * w + li;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = rt * 16 + 4 * kg + r;
+                const bool ok = row < NR && p0 + pos <= start + t0 + row / R;
+                Sb[(size_t)row * SS + pos] = ok ? acc[r] * scale : -INFINITY;
+            }
+        }
+        if (c + 1 < nch) load_k(c + 1);
+        __syncthreads();
+        // online softmax update, four lanes per row (sixteen positions each)
+        for (int row0 = 0; row0 < NRP; row0 += kSW / 4) {
+            const int row = row0 + (tid >> 2), q4 = tid & 3;
+            if (row < NRP) {  // whole quads
+                float* sr = Sb + (size_t)row * SS + 16 * q4;
+                float x[16];
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    const float4 v4 = *(const float4*)(sr + i);
+                    x[i] = v4.x, x[i + 1] = v4.y, x[i + 2] = v4.z, x[i + 3] = v4.w;
+                }
+                float mx = x[0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x[i]);
+                mx = fmaxf(mx, dpp<0xB1>(mx));
+                mx = fmaxf(mx, dpp<0x4E>(mx));
+                const float m_old = m_run[row], m_new = fmaxf(m_old, mx);
+                const bool live = m_new != -INFINITY;  // padded rows stay all -inf
+                const float a = live && m_old != -INFINITY ? expf(m_old - m_new) : 0.f;
+                float l = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    x[i] = live && x[i] != -INFINITY ? expf(x[i] - m_new) : 0.f;
+                    l += x[i];
+                }
+                l = quad_sum(l);
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) *(float4*)(sr + i) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
+                if (q4 == 0) {
+                    l_run[row] = __builtin_fmaf(l_run[row], a, l);
+                    m_run[row] = m_new;
+                    a_row[b * NRP + row] = a;
+                }
+            }
+        }
+        __syncthreads();
+        // O = a O + E V
+#pragma unroll
+        for (int rt = 0; rt < kRMax; ++rt) {
+            if (rt >= R) break;
+            const float* e = Sb + (size_t)(rt * 16 + li) * SS + 16 * kg;
+            float ea[16];
+#pragma unroll
+            for (int m = 0; m < 16; m += 4) {
+                const float4 x = *(const float4*)(e + m);
+                ea[m] = x.x, ea[m + 1] = x.y, ea[m + 2] = x.z, ea[m + 3] = x.w;
+            }
+            const float4 av = *(const float4*)&a_row[b * NRP + rt * 16 + 4 * kg];
+            const float ar[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[rt][ct][r] *= ar[r];
+#pragma unroll
+                for (int m = 0; m < 16; ++m)
+                    o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ea[m], vb[ct][m], o[rt][ct], 0, 0, 0);
+            }
+        }
+        if (c + 1 < nch) load_v(c + 1);
+    }
+    __syncthreads();
+    // O / l into the output rows
+#pragma unroll
+    for (int rt = 0; rt < kRMax; ++rt) {
+        if (rt >= R) break;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = rt * 16 + 4 * kg + r;
+            if (row >= NR) continue;
+            const int ti = row / R, t = t0 + ti, h = g * R + row - ti * R;
+            const float L = l_run[row];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+                out[(size_t)t * ldo + (size_t)h * HD + w * (HD / 4) + 16 * ct + li] = o[rt][ct][r] / L;
+        }
+    }
+}
+
 // Merge of the chunk partials of k_attn_mt / k_attn_split: one workgroup of
 // kMG threads per (query head, token). Every thread loads one chunk's (m, l)
 // and forms e^(m_c - M) in parallel (M = the maximum, which no order
@@ -1309,6 +1571,41 @@ static void attn_launch(bool timed, const LaunchEv& ev, K kernel, dim3 grid, dim
                         A... args) {
     if (timed) hipExtLaunchKernelGGL(kernel, grid, block, lds, st, ev.a, ev.b, 0, args...);
     else hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+}
+
+extern "C" int orc_attn_prefill(const float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim,
+                                int pos_off, const float* d_rope, float* d_kc, float* d_vc, int ctx, float* d_out,
+                                int ldo, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n_tok <= 0 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || pos_off < 0 || pos_off + n_tok > ctx ||
+        ldqkv < (n_heads + 2 * n_kv) * head_dim || ldqkv % 4 || ldo % 4 || !d_qkv || !d_rope || !d_kc || !d_vc ||
+        !d_out || ((uintptr_t)d_qkv & 15) || ((uintptr_t)d_kc & 15) || ((uintptr_t)d_vc & 15) ||
+        ((uintptr_t)d_rope & 15) || ((uintptr_t)d_out & 15))
+        return set_error(ORC_E_INVALID, "attn_prefill: bad args");
+    if (n_heads / n_kv > kRMax) return set_error(ORC_E_UNSUPPORTED, "attn_prefill: more than 8 query heads per kv head");
+    if (head_dim != 64 && head_dim != 128) return set_error(ORC_E_UNSUPPORTED, "attn_prefill: head_dim must be 64 or 128");
+    const int R = n_heads / n_kv;
+    hipStream_t st = resolve_stream(s);
+    const dim3 grid((n_tok + kPaTok - 1) / kPaTok, n_kv);
+    double bytes = 0;  // K / V rows of every query block's positions, once per block; QKV rows in, rows out
+    for (int t0 = 0; t0 < n_tok; t0 += kPaTok)
+        bytes += 8.0 * n_kv * head_dim * (pos_off + std::min(n_tok, t0 + kPaTok));
+    bytes += 4.0 * n_tok * ((double)(n_heads + 2 * n_kv) * head_dim + (double)n_heads * head_dim);
+    LaunchEv ev;
+    const bool tm = prof_arm(st, kProfAttnPf, n_tok, bytes, &ev.a, &ev.b);
+    if (head_dim == 64) {
+        const size_t lds = pa_lds_bytes<64>(R);
+        if (lds > 160 * 1024) return set_error(ORC_E_UNSUPPORTED, "attn_prefill: LDS");
+        attn_launch(tm, ev, (k_attn_pf<64>), grid, dim3(kSW), lds, st, d_qkv, ldqkv, n_tok, n_heads, n_kv, pos_off,
+                    (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+    } else {
+        const size_t lds = pa_lds_bytes<128>(R);
+        if (lds > 160 * 1024) return set_error(ORC_E_UNSUPPORTED, "attn_prefill: LDS");
+        attn_launch(tm, ev, (k_attn_pf<128>), grid, dim3(kSW), lds, st, d_qkv, ldqkv, n_tok, n_heads, n_kv, pos_off,
+                    (const float2*)d_rope, d_kc, d_vc, ctx, d_out, ldo);
+    }
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
 }
 
 extern "C" size_t orc_attn_fused_workspace(int n_heads, int n_kv, int head_dim) {

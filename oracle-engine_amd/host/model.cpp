@@ -245,10 +245,16 @@ int Model::chunk_dev(const int32_t* d_ids, int n, const int32_t* d_pos, int sp, 
         // pre-norm + Q|K|V (+bias) -> qkv rows [q | k | v]   (model.cpp:366-388)
         CK(gemm_segs({{&L.q, {d_qkv_, L.bq}}, {&L.k, {d_qkv_ + NQ, L.bk}}, {&L.v, {d_qkv_ + NQ + NKV, L.bv}}}, n,
                      d_x_, D, QKV, L.attn_norm, ORC_EPI_STORE, s));
-        // RoPE + KV store (model.cpp:401-408), attention (model.cpp:410-435)
-        // in launches of at most kMaxBatch tokens, in order: each stores its
-        // tokens' K / V rows before the next attends to them
-        for (int a0 = 0; a0 < n; a0 += kMaxBatch) {
+        // RoPE + KV store (model.cpp:401-408), attention (model.cpp:410-435).
+        // Prefill passes of kPrefillAttnMin tokens or more (host positions):
+        // one launch over the pass (query blocks, online softmax; the
+        // prefill attention of model.cpp:595-626). Otherwise launches of at
+        // most kMaxBatch tokens, in order: each stores its tokens' K / V rows
+        // before the next attends to them.
+        if (fused_attn_ && !d_pos && n >= kPrefillAttnMin) {
+            CK(orc_attn_prefill(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, sp, d_rope_, kc, vc, C,
+                                d_attn_, NQ, s));
+        } else for (int a0 = 0; a0 < n; a0 += kMaxBatch) {
             const int an = std::min(kMaxBatch, n - a0);
             float* qkv = d_qkv_ + (size_t)a0 * QKV;
             float* att = d_attn_ + (size_t)a0 * NQ;

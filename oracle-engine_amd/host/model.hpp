@@ -43,6 +43,9 @@ public:
     ModelConfig cfg;
     static constexpr int kMaxBatch = 16;      // tokens per device pass with logits (verify)
     static constexpr int kPrefillBatch = 1024;  // tokens per device pass without logits (prefill)
+    // Passes of this many tokens or more run orc_attn_prefill (the prompts of
+    // the 127-255-id configurations keep the verify path's attention).
+    static constexpr int kPrefillAttnMin = 256;
 
     Model() = default;
     ~Model();

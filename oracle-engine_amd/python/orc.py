@@ -78,6 +78,8 @@ ABI = [
                                   C.c_int, _vp, C.c_int, _vp, _vp]),
     ("orc_attn_fused_workspace", C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     ("orc_attn_wg_limit", C.c_int, []),
+    ("orc_attn_prefill", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int,
+                                   _vp, C.c_int, _vp]),
     ("orc_attn_fused_at", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp,
                                     C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp]),
     ("orc_argmax_workspace", C.c_size_t, [C.c_int, C.c_int]),

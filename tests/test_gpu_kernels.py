@@ -500,6 +500,60 @@ def test_attn_fused(dev, oracle, H, KVH, hd, sp, nt, devpos, lim, flo):
         assert np.allclose(got[t], want, rtol=2e-5, atol=4e-6), (t, np.abs(got[t] - want).max())
 
 
+@pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 0, 256), (14, 2, 64, 100, 300), (28, 4, 128, 700, 260),
+                                            (24, 8, 128, 3, 40), (32, 4, 64, 1000, 17)])
+def test_attn_prefill(dev, oracle, H, KVH, hd, sp, nt):
+    """The prefill attention (one workgroup per 16-token block and kv head,
+    online softmax over every key chunk, no partials) equals the oracle's
+    rope then causal attention over the prefilled cache plus the new rows
+    (2e-5), agrees with 16-token calls of the decode / verify path (4e-6 of
+    the largest output), stores the same K / V rows, and leaves the QKV rows
+    as they were; partial last blocks, a cache prefix and chunk boundaries
+    included."""
+    print(f"[gpu] attn_prefill H={H} KVH={KVH} hd={hd} sp={sp} nt={nt}", flush=True)
+    rng = np.random.default_rng(sp + nt)
+    base = 500000.0
+    ctx = sp + nt + 3
+    ld = (H + 2 * KVH) * hd
+    qkv = rng.normal(0, 1, (nt, ld)).astype(np.float32)
+    K = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    V = rng.normal(0, 1, (KVH, ctx, hd)).astype(np.float32)
+    dq, dt = dev.upload(qkv), dev.upload(rope_table(ctx, hd, base))
+    outs = []
+    for mode in ("prefill", "blocks"):
+        dK, dV = dev.upload(K), dev.upload(V)
+        dO = dev.alloc(nt * H * hd * 4)
+        if mode == "prefill":
+            dev.check(dev.L.orc_attn_prefill(dq.ptr, ld, nt, H, KVH, hd, sp, dt.ptr, dK.ptr, dV.ptr, ctx, dO.ptr,
+                                             H * hd, None))
+        else:
+            ws = _attn_ws(dev, H, KVH, hd)
+            for t0 in range(0, nt, 16):
+                n = min(16, nt - t0)
+                dev.check(dev.L.orc_attn_fused_at(dq.at(t0 * ld * 4), ld, n, H, KVH, hd, None, sp + t0, dt.ptr,
+                                                  dK.ptr, dV.ptr, ctx, 0, ctx, dO.at(t0 * H * hd * 4), H * hd, ws.ptr,
+                                                  None))
+        outs.append((dO.read(np.float32).reshape(nt, H * hd), dK.read(np.float32).reshape(KVH, ctx, hd),
+                     dV.read(np.float32).reshape(KVH, ctx, hd)))
+    (got, Kc, Vc), (blk, Kb, Vb) = outs
+    assert np.array_equal(dq.read(np.float32).reshape(nt, ld), qkv)
+    assert np.array_equal(Kc, Kb) and np.array_equal(Vc, Vb)
+    assert np.allclose(got, blk, rtol=0, atol=4e-6 * np.abs(blk).max()), np.abs(got - blk).max()
+    kref, vref = K.copy(), V.copy()
+    qs = []
+    for t in range(nt):
+        q, k = oracle.rope(qkv[t, :H * hd], qkv[t, H * hd:(H + KVH) * hd], H, KVH, hd, sp + t, base)
+        qs.append(q)
+        kref[:, sp + t, :] = k.reshape(KVH, hd)
+        vref[:, sp + t, :] = qkv[t, (H + KVH) * hd:].reshape(KVH, hd)
+    assert np.allclose(Kc, kref, rtol=1e-5, atol=2e-6) and np.array_equal(Vc, vref)
+    kc = kref.transpose(1, 0, 2).reshape(ctx, KVH * hd)
+    vc = vref.transpose(1, 0, 2).reshape(ctx, KVH * hd)
+    for t in range(0, nt, max(1, nt // 24)):
+        want = oracle.attention(qs[t], kc, vc, H, KVH, hd, sp + t)
+        assert np.allclose(got[t], want, rtol=2e-5, atol=4e-6), (t, np.abs(got[t] - want).max())
+
+
 @pytest.mark.parametrize("H,KVH,hd,sp,nt", [(24, 8, 128, 250, 5), (14, 2, 64, 2040, 9), (28, 4, 128, 60, 7),
                                             (24, 8, 128, 508, 9), (28, 4, 128, 1019, 9), (14, 2, 64, 3, 16),
                                             (24, 8, 128, 252, 9), (14, 2, 64, 250, 9), (28, 4, 128, 8400, 9),
