@@ -427,8 +427,12 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
     RowSet<ROWS> R;
 
     // stage x: the loads of a pass of x (and of the norm weights) go out
-    // first, then (first pass) the first batch of weights, which stays in
-    // flight while x is stored to LDS with its per-16 sums (4-lane shuffle)
+    // first; x is stored to LDS with its per-16 sums (4-lane shuffle). The
+    // first batch of weights goes out after the staging barrier (late_w):
+    // issued earlier, the weight stream of the CU's waves delays the x reads
+    // queued behind it (measured: 0.4-1.3 us per launch on 1-30 MB
+    // matrices); or (large matrices, row-group pipelining) right after the
+    // first pass of x loads, in flight while x is stored.
     const bool norm = p.norm_w != nullptr;
     float ss[NT];
 #pragma unroll
@@ -479,7 +483,7 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
     {
         float4 v[NT][4], gw[4];
         load_pass(0, v, gw);
-        if (g < p.n_groups) {  // first batch of the first row group
+        if (!p.late_w && g < p.n_groups) {  // first batch of the first row group
             map_rows<ROWS, RG>(p, g, slot, R);
 #pragma unroll
             for (int i = 0; i < UPL; ++i) {
@@ -503,6 +507,14 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
         }
     }
     __syncthreads();
+    if (p.late_w && g < p.n_groups) {
+        map_rows<ROWS, RG>(p, g, slot, R);
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = li + LPR * i;
+            U[i].load(R.rp, u < p.units ? u : 0);
+        }
+    }
     float inv[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -657,6 +669,11 @@ static int launch_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& 
     const dim3 grid(std::max(1, std::min(p.n_groups, (WPE / 2) * g_n_cu)), p.n_tok / NT);
     const size_t lds = qmv_lds(QT, NT, p.n_in);
     if (lds > g_lds_max) return set_error(ORC_E_UNSUPPORTED, "gemm: activations do not fit LDS");
+    // weights after the staging (one ordering or the other: results are the
+    // same); a 53 MB Q8_0 gate+up and the pipelined LM heads keep them early
+    double wbytes = 0;
+    for (int i = 0; i < p.n_seg; ++i) wbytes += (double)p.seg_rb[i] * p.rows[i];
+    p.late_w = !PIPE && wbytes < 40e6;
     if (ev.start)
         hipExtLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), grid, dim3(kQWG), lds, s, ev.start, ev.stop, 0, p);
     else

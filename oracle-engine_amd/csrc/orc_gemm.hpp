@@ -28,6 +28,7 @@ struct QmvParams {
     int seg_type[3];      // matrix-core mixed launches: weight type of each segment
     uint64_t seg_rb[3];   // and its row bytes
     int tok_block;        // tokens per token block (blockIdx.y) of a launch; n_tok counts all blocks
+    int late_w;           // vector path: first weight batch issued after the activations are staged
 };
 
 // Kernel timing of one launch: start / stop events taken from its dispatch.
