@@ -36,6 +36,7 @@
 #include "orc_gemm.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 namespace orc {
@@ -47,6 +48,9 @@ template <> struct QTr<ORC_Q8_0_X8> { static constexpr int EPU = 32, PP = 32, LP
 template <> struct QTr<ORC_Q4_0> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
 template <> struct QTr<ORC_Q4_K> { static constexpr int EPU = 32, PP = 64, LPR = 32; };
 template <> struct QTr<ORC_Q6_K> { static constexpr int EPU = 64, PP = 64, LPR = 16; };
+// one-token mixed launches (Q4_K segments, then Q6_K segments): each row
+// group takes its own type's unit, LPR and row count; both pad every 64 values
+template <> struct QTr<kMixK> { static constexpr int EPU = 32, PP = 64, LPR = 32; };
 
 template <int PP> __device__ __forceinline__ int padx(int k) { return k + 4 * (k / PP); }
 
@@ -342,6 +346,10 @@ template <int ROWS> struct Unit<ORC_Q4_0, ROWS> {
     }
 };
 
+// kMixK instantiates the generic row-group loops, which its launches never
+// run (the mixed loop below takes every group)
+template <int ROWS> struct Unit<kMixK, ROWS> : Unit<ORC_Q4_K, ROWS> {};
+
 // ── the kernel ───────────────────────────────────────────────────────────────
 
 constexpr int kQWG = 512, kQWaves = kQWG / 64;
@@ -387,6 +395,28 @@ __device__ __forceinline__ void map_rows(const QmvParams& p, int g, int slot, Ro
         float* yb = s2 ? spin(p.y[2]) : (s1 ? spin(p.y[1]) : spin(p.y[0]));
         const float* bb = s2 ? spin(p.bias[2]) : (s1 ? spin(p.bias[1]) : spin(p.bias[0]));
         R.rp[r] = w + (size_t)j * p.row_bytes;
+        R.y[r] = yb + j;
+        R.bias[r] = bb ? bb + j : nullptr;
+    }
+}
+
+// Rows of a slot from its first logical row jl0 (store / accumulate
+// epilogues) with rows of rb bytes; rows of the launch past the end, or past
+// jlim, are clamped to row 0 of segment 0 and marked not ok.
+template <int ROWS>
+__device__ __forceinline__ void map_rows_at(const QmvParams& p, int jl0, int jlim, uint64_t rb, RowSet<ROWS>& R) {
+    R.jl0 = jl0;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        int j = jl0 + r;
+        R.ok[r] = j < jlim;
+        bool s1 = R.ok[r] && p.n_seg > 1 && j >= p.rows[0];
+        bool s2 = R.ok[r] && p.n_seg > 2 && j >= p.rows[0] + p.rows[1];
+        j = !R.ok[r] ? 0 : (s2 ? j - p.rows[0] - p.rows[1] : (s1 ? j - p.rows[0] : j));
+        const uint8_t* w = s2 ? spin(p.w[2]) : (s1 ? spin(p.w[1]) : spin(p.w[0]));
+        float* yb = s2 ? spin(p.y[2]) : (s1 ? spin(p.y[1]) : spin(p.y[0]));
+        const float* bb = s2 ? spin(p.bias[2]) : (s1 ? spin(p.bias[1]) : spin(p.bias[0]));
+        R.rp[r] = w + (size_t)j * (R.ok[r] ? rb : 0);
         R.y[r] = yb + j;
         R.bias[r] = bb ? bb + j : nullptr;
     }
@@ -507,7 +537,7 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
         }
     }
     __syncthreads();
-    if (p.late_w && g < p.n_groups) {
+    if (QT != kMixK && p.late_w && g < p.n_groups) {
         map_rows<ROWS, RG>(p, g, slot, R);
 #pragma unroll
         for (int i = 0; i < UPL; ++i) {
@@ -561,6 +591,57 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
                     }
         }
     };
+    if constexpr (QT == kMixK) {
+        // groups [0, g4): Q4_K rows [0, split_rows), 64 / 32 slots of ROWS
+        // rows; then Q6_K rows [split_rows, n_rows), 64 / 16 slots. A group's
+        // type is wave-uniform; each keeps its type's unit, lane split and
+        // slot reduction, so its rows equal the single-type launches' bit
+        // for bit.
+        const int rows4 = p.split_rows, g4 = rows4 / (2 * ROWS);
+        const uint64_t rb4 = (uint64_t)(kn / 256) * 144, rb6 = (uint64_t)(kn / 256) * 210;
+        auto run = [&](auto tag, int gl, int jbase, int jlim, uint64_t rb) {
+            constexpr int UT = decltype(tag)::value, L = QTr<UT>::LPR, RGU = (64 / L) * ROWS;
+            const int sl = lane / L, lli = lane % L, units = kn / QTr<UT>::EPU;
+            RowSet<ROWS> Rr;
+            map_rows_at<ROWS>(p, jbase + gl * RGU + sl * ROWS, jlim, rb, Rr);
+            Unit<UT, ROWS> Uu[UPL];
+            float acc[ROWS][NT];
+            zero(acc);
+            const int nbt = (units + L * UPL - 1) / (L * UPL);
+            for (int bt = 0; bt < nbt; ++bt) {
+#pragma unroll
+                for (int i = 0; i < UPL; ++i) {
+                    const int u = lli + L * (bt * UPL + i);
+                    Uu[i].load(Rr.rp, u < units ? u : 0);
+                }
+#pragma unroll
+                for (int i = 0; i < UPL; ++i) {
+                    const int u = lli + L * (bt * UPL + i);
+                    if (u < units) Uu[i].template compute<NT>(u, c, acc);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    float v = acc[r][t];
+#pragma unroll
+                    for (int o = L / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+                    if (lli == (r * NT + t) % L && Rr.ok[r]) {
+                        v *= inv[t];
+                        if (Rr.bias[r]) v += *Rr.bias[r];
+                        float* dst = Rr.y[r] + (size_t)t * p.ldy;
+                        if (p.epi == ORC_EPI_ACCUM) *dst += v;
+                        else *dst = v;
+                    }
+                }
+        };
+        for (; g < p.n_groups; g += gstride) {
+            if (g < g4) run(std::integral_constant<int, ORC_Q4_K>{}, g, 0, rows4, rb4);
+            else run(std::integral_constant<int, ORC_Q6_K>{}, g - g4, rows4, p.n_rows, rb6);
+        }
+        return;
+    }
     if constexpr (PIPE) {
         Unit<QT, ROWS> V[UPL];
         RowSet<ROWS> R2;
@@ -662,6 +743,8 @@ static int launch_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& 
     QmvParams p = p0;
     const int rg = (64 / QTr<QT>::LPR) * ROWS;
     p.n_groups = (p.n_rows + rg - 1) / rg;
+    // mixed: whole groups of two (Q4_K) and four (Q6_K) rows per slot set
+    if constexpr (QT == kMixK) p.n_groups = p.split_rows / (2 * ROWS) + (p.n_rows - p.split_rows) / (4 * ROWS);
     // persistent grid: WPE/2 workgroups per CU, at most one per row group,
     // times the launch's blocks of exactly NT tokens (the kernel stages and
     // writes NT rows per block)
@@ -673,7 +756,7 @@ static int launch_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& 
     // same); a 53 MB Q8_0 gate+up and the pipelined LM heads keep them early
     double wbytes = 0;
     for (int i = 0; i < p.n_seg; ++i) wbytes += (double)p.seg_rb[i] * p.rows[i];
-    p.late_w = !PIPE && wbytes < 40e6;
+    p.late_w = QT == kMixK || (!PIPE && wbytes < 40e6);
     if (ev.start)
         hipExtLaunchKernelGGL((k_qmv<QT, NT, ROWS, UPL, WPE, PIPE>), grid, dim3(kQWG), lds, s, ev.start, ev.stop, 0, p);
     else
@@ -765,6 +848,27 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s);
 // A one-token launch over Q4_K and Q6_K segments: one vector launch per run
 // of segments of one type, each with the norm prologue.
 static int dispatch_mixed_decode(const QmvParams& p, hipStream_t s) {
+    // Q4_K segments followed by Q6_K segments (a Q4_K_M layer's Q|K|V): one
+    // launch whose row groups take their own type (whole groups of each)
+    int n4 = 0;
+    while (n4 < p.n_seg && p.seg_type[n4] == ORC_Q4_K) ++n4;
+    bool ordered = n4 > 0 && n4 < p.n_seg && p.epi != ORC_EPI_SWIGLU;
+    int rows4 = 0;
+    for (int i = 0; i < p.n_seg; ++i) {
+        if (i >= n4 && p.seg_type[i] != ORC_Q6_K) ordered = false;
+        if (i < n4) rows4 += p.rows[i];
+    }
+    if (ordered && rows4 % 2 == 0 && (p.n_rows - rows4) % 4 == 0 && max_tokens(ORC_Q4_K, p.n_in) >= 1) {
+        QmvParams q = p;
+        q.split_rows = rows4;
+        q.tok_block = 1;
+        LaunchEvents ev;
+        if (g_prof_on) prof_arm(s, kMixK, 1, gemm_bytes(q, 1), &ev.start, &ev.stop);
+        const int per_lane = (p.n_in / 32 + 31) / 32;  // Q4_K units per lane; Q6_K's are no more
+        if (per_lane == 1) return launch_shape<kMixK, 1, 1, 1, 4>(q, s, ev);
+        if (per_lane == 2) return launch_shape<kMixK, 1, 1, 2, 4>(q, s, ev);
+        return launch_shape<kMixK, 1, 1, 3, 4>(q, s, ev);
+    }
     for (int i0 = 0; i0 < p.n_seg;) {
         int i1 = i0 + 1;
         while (i1 < p.n_seg && p.seg_type[i1] == p.seg_type[i0]) ++i1;

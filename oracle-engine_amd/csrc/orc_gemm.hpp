@@ -29,6 +29,7 @@ struct QmvParams {
     uint64_t seg_rb[3];   // and its row bytes
     int tok_block;        // tokens per token block (blockIdx.y) of a launch; n_tok counts all blocks
     int late_w;           // vector path: first weight batch issued after the activations are staged
+    int split_rows;       // vector mixed launches: logical rows of the leading Q4_K segments
 };
 
 // Kernel timing of one launch: start / stop events taken from its dispatch.

@@ -259,6 +259,7 @@ def test_gemm_fused_epilogues(dev, n_in):
 
 @pytest.mark.parametrize("n_in,rows,types,bias", [(3072, (3072, 1024, 1024), (ol.Q4_K, ol.Q4_K, ol.Q6_K), False),
                                                   (512, (448, 64, 64), (ol.Q4_K, ol.Q4_K, ol.Q6_K), True),
+                                                  (3584, (3584, 512, 512), (ol.Q4_K, ol.Q4_K, ol.Q6_K), True),
                                                   (8192, (160, 96), (ol.Q6_K, ol.Q4_K), False)])
 def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
     """One launch over Q4_K and Q6_K segments (a Q4_K_M layer's Q|K|V) gives
@@ -267,7 +268,10 @@ def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
     (the split follows each launch's row count), so the match is to fp32
     summation order: 1e-5 of the largest output of the token. Within the
     multi-token mixed launch the tokens are independent: token t of an
-    n-token launch is bit for bit token t of a two-token launch."""
+    n-token launch is bit for bit token t of a two-token launch. One token
+    over Q4_K segments then Q6_K segments is one vector launch whose row
+    groups each keep their type's unit, lane split and reduction: equal to
+    the per-type launches bit for bit."""
     import orc
 
     print(f"[gpu] gemm mixed n_in={n_in} rows={rows} types={types}", flush=True)
@@ -292,6 +296,8 @@ def test_gemm_mixed_equals_per_type(dev, n_in, rows, types, bias):
         got, want = dy.read(np.float32).reshape(nt, ld), dz.read(np.float32).reshape(nt, ld)
         scale = np.abs(want).max(axis=1, keepdims=True)
         assert np.all(np.abs(got - want) <= 1e-5 * scale), (nt, float(np.abs(got - want).max()))
+        if nt == 1 and types[0] == ol.Q4_K:
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         if nt in (5, 16):
             t = nt - 2
             d2 = dev.alloc(2 * ld * 4)
