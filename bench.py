@@ -26,10 +26,10 @@ family's HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
 runs (scaled by a copy kernel of known size), read from the committed
 summary in profiles/.
 cpu_baseline: the reference implementation (oracle/_ref, built from the
-reference's sources) on the same two models and the same 128-id prompt with
-k = 4, bounded sample: its harness protocol timing the first 32 of the 256
-generated tokens (about 10-30 s on the 16 host threads a one-GPU box gives);
-cores = threads used, host_cpus = os.cpu_count().
+reference's sources) on the whole C3 workload: the same two models, the same
+128-id prompt, k = 4 and all 256 generated tokens, with its harness protocol
+(untimed prefill, timed generation; about 35 s on the 16 host threads a
+one-GPU box gives); cores = threads used, host_cpus = os.cpu_count().
 Protocol fields (benchmark/bench_engine.cpp:221-263): step_ms_median (the
 median of the K per-step times) and checksum (FNV-1a 64 of the generated
 ids, equal to the reference's for the same stream); prefill_tok_s: the
@@ -117,8 +117,8 @@ def cpu_baseline(tgt_path, dft_path, prompt, k, n_gen, label):
     return {"value": round(d["tok_s"], 4), "unit": "tok/s", "cores": d["threads"], "host_cpus": host_cpus,
             "kind": "reference", "checksum": d["checksum"],
             "sample": f"reference build (oracle/_ref) on the {label} models and prompt ({len(prompt)} ids"
-                      f"{', k=' + str(k) if dft_path else ''}); the first {d['tokens']} generated tokens, timed "
-                      f"after an untimed prefill"
+                      f"{', k=' + str(k) if dft_path else ''}); all {d['tokens']} generated tokens of the workload, "
+                      f"timed after an untimed prefill"
                       + (f"; accepted {d['accepted']}/{d['proposed']}" if dft_path else "")}
 
 
@@ -390,8 +390,10 @@ def main():
     micro = None if a.no_gemv_micro else gemv_microbench(dev)
     cpu = None
     if not a.no_cpu_baseline and a.workload in ("c1", "c3"):
-        # bounded sample: C3's full prompt and k, its first 32 tokens (~10-30 s on 16 threads); C1 whole
-        cpu = cpu_baseline(tgt_path, dft_path, prompt, k, 32 if a.workload == "c3" else n_gen, a.workload.upper())
+        # the whole workload: prompt, k and every generated token (C3 ~35 s, C1 ~1 s on 16 threads)
+        cpu = cpu_baseline(tgt_path, dft_path, prompt, k, n_gen, a.workload.upper())
+        if cpu:  # the same workload on both sides: the reference's stream checksum against this run's
+            cpu["checksum_equal"] = cpu["checksum"] == checksum
     metric = ("greedy decode tok/s (1B Q8_0)" if plain else
               "spec-decode tok/s (3B Q4_K, k=4); quant-GEMV HBM GB/s vs peak")
     out = {
