@@ -401,6 +401,10 @@ def main():
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(1e3 * dt / a.steps, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
+        "arithmetic": ("weights as stored GGUF blocks (Q8_0 regrouped 8 blocks at a time at load, same bytes); "
+                       "decode GEMVs and attention in fp32 FMA / fp32 MFMA; K-quant verify GEMMs on fp16 MFMA with "
+                       "exact fp16 weight codes and each activation split into hi + lo fp16 halves (~22 bits), "
+                       "products exact, sums in fp32"),
         "data": "synthetic (random-init N(0,0.02) GGUF, uniform random prompt ids)",
         "config": {"workload": W["desc"], "k": k, "prompt": n_prompt, "gen_tokens": n_gen, "ctx": ctx},
         "acceptance": round(tot["accepted"] / max(1, tot["proposed"]), 4),

@@ -135,6 +135,8 @@ int main(int argc, char** argv) {
     double spec_tps = 0, acc_rate = 0;
     uint64_t spec_csum = 0;
     bool exact = false;
+    SpecStats spec_st;  // counts of the measured speculative run
+    int spec_n_tok = 0;
     if (!a.draft.empty()) {
         Model draft;
         if (!draft.load(a.draft, ctx)) { std::fprintf(stderr, "error: cannot load draft\n"); return 1; }
@@ -157,6 +159,8 @@ int main(int argc, char** argv) {
         }
         spec_csum = fnv(st_toks);
         exact = spec_csum == csum;
+        spec_st = st;
+        spec_n_tok = (int)st_toks.size();
         acc_rate = st.proposed ? 100.0 * st.accepted / st.proposed : 0.0;
         std::printf("speculative (k=%d): %.1f tok/s (x%.2f vs greedy)\n  acceptance : %.1f%% (%ld/%ld)\n"
                     "  passes/tok : %.2f\n  exact      : %s (spec %016llx vs greedy %016llx)\n",
@@ -170,9 +174,12 @@ int main(int argc, char** argv) {
             std::fprintf(f,
                          "{\"engine\": \"ORACLE-mi355x\", \"model\": \"%s\", \"prompt_tokens\": %d, \"gen_tokens\": %d, "
                          "\"generation_tok_s\": %.3f, \"prefill_tok_s\": %.3f, \"gen_checksum\": \"%016llx\", "
-                         "\"spec_tok_s\": %.3f, \"acceptance_pct\": %.3f, \"spec_exact\": %s}\n",
+                         "\"spec_tok_s\": %.3f, \"acceptance_pct\": %.3f, \"spec_exact\": %s, "
+                         "\"spec_checksum\": \"%016llx\", \"accepted\": %ld, \"proposed\": %ld, \"passes\": %ld, "
+                         "\"spec_tokens\": %d}\n",
                          a.model.c_str(), a.n_prompt - 1, a.n_gen, g_med, median(pf), (unsigned long long)csum, spec_tps,
-                         acc_rate, exact ? "true" : "false");
+                         acc_rate, exact ? "true" : "false", (unsigned long long)spec_csum, spec_st.accepted,
+                         spec_st.proposed, spec_st.passes, spec_n_tok);
             std::fclose(f);
         }
     }
