@@ -642,42 +642,38 @@ __global__ __launch_bounds__(kSW) void k_attn_mt(const float* qkv, int ldqkv, in
     }
 
     // rotated queries of every row (rope_q_lds's arithmetic): an item is four
-    // dims of the first half of a row and their rotate-half partners; four
-    // items per thread in flight. Padded rows are zero.
+    // dims of the first half and their rotate-half partners for one token;
+    // its rope pairs are loaded once and applied to the token's R query heads
+    // (every head's loads in flight first). Padded rows are zero.
     {
-        constexpr int QD = half / 4;  // items per row
-        for (int i0 = 0; i0 < NRP * QD; i0 += 4 * kSW) {
-            float4 lo[4], hi[4], c01[4], c23[4];
+        constexpr int QD = half / 4;  // items per token
+        const int ntk = t_hi - t_lo + 1;
+        for (int i = tid; i < ntk * QD; i += kSW) {
+            const int ti = i / QD, d = 4 * (i - ti * QD), t = t_lo + ti;
+            const float* qt = qkv + (size_t)t * ldqkv + (size_t)g * R * HD + d;
+            const float2* cs = rope + (size_t)(start + t) * half + d;
+            const float4 c01 = *(const float4*)cs, c23 = *(const float4*)(cs + 2);
+            float4 lo[kRMax], hi[kRMax];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = i0 + tid + j * kSW, row = i / QD, d = 4 * (i - row * QD);
-                if (row < NR) {
-                    const int ti = row / R, t = t_lo + ti;
-                    const float* qt = qkv + (size_t)t * ldqkv + (size_t)(g * R + row - ti * R) * HD + d;
-                    const float2* cs = rope + (size_t)(start + t) * half + d;
-                    lo[j] = *(const float4*)qt;
-                    hi[j] = *(const float4*)(qt + half);
-                    c01[j] = *(const float4*)cs;
-                    c23[j] = *(const float4*)(cs + 2);
+            for (int h = 0; h < kRMax; ++h)
+                if (h < R) {
+                    lo[h] = *(const float4*)(qt + (size_t)h * HD);
+                    hi[h] = *(const float4*)(qt + (size_t)h * HD + half);
                 }
-            }
+            const float2 e0{c01.x, c01.y}, e1{c01.z, c01.w}, e2{c23.x, c23.y}, e3{c23.z, c23.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = i0 + tid + j * kSW, row = i / QD, d = 4 * (i - row * QD);
-                if (row < NRP) {
-                    float4 ql = make_float4(0.f, 0.f, 0.f, 0.f), qh = ql;
-                    if (row < NR) {
-                        const float2 e0{c01[j].x, c01[j].y}, e1{c01[j].z, c01[j].w};
-                        const float2 e2{c23[j].x, c23[j].y}, e3{c23[j].z, c23[j].w};
-                        ql = make_float4(rot_lo(lo[j].x, hi[j].x, e0), rot_lo(lo[j].y, hi[j].y, e1),
-                                         rot_lo(lo[j].z, hi[j].z, e2), rot_lo(lo[j].w, hi[j].w, e3));
-                        qh = make_float4(rot_hi(lo[j].x, hi[j].x, e0), rot_hi(lo[j].y, hi[j].y, e1),
-                                         rot_hi(lo[j].z, hi[j].z, e2), rot_hi(lo[j].w, hi[j].w, e3));
-                    }
-                    *(float4*)&Qs[(size_t)row * QS + d] = ql;
-                    *(float4*)&Qs[(size_t)row * QS + half + d] = qh;
+            for (int h = 0; h < kRMax; ++h)
+                if (h < R) {
+                    float* qr = Qs + (size_t)(ti * R + h) * QS;
+                    *(float4*)&qr[d] = make_float4(rot_lo(lo[h].x, hi[h].x, e0), rot_lo(lo[h].y, hi[h].y, e1),
+                                                   rot_lo(lo[h].z, hi[h].z, e2), rot_lo(lo[h].w, hi[h].w, e3));
+                    *(float4*)&qr[half + d] = make_float4(rot_hi(lo[h].x, hi[h].x, e0), rot_hi(lo[h].y, hi[h].y, e1),
+                                                          rot_hi(lo[h].z, hi[h].z, e2), rot_hi(lo[h].w, hi[h].w, e3));
                 }
-            }
+        }
+        for (int i = NR * (HD / 4) + tid; i < NRP * (HD / 4); i += kSW) {
+            const int row = i / (HD / 4), d = 4 * (i - row * (HD / 4));
+            *(float4*)&Qs[(size_t)row * QS + d] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
     __syncthreads();
