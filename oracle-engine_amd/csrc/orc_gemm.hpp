@@ -50,6 +50,8 @@ constexpr int kMixK = 256;
 bool mmq_type(int type);
 int mmq_max_tokens(int type, const QmvParams& p);
 int mmq_launch(int type, const QmvParams& p, hipStream_t s, const LaunchEvents& ev);
+// the same for launches whose wave ranges are staged in windows (orc_mmq_win.hip)
+int mmq_launch_windowed(int type, const QmvParams& p, hipStream_t s, const LaunchEvents& ev);
 // Prefill launches (orc_mmq.hip): calls of at least kPfMinTok tokens on one
 // K-quant type run k_mmq_pf, all tokens in one launch.
 constexpr int kPfMinTok = 256;
