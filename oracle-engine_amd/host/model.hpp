@@ -110,11 +110,10 @@ public:
     // caller keeps positions inside the context. n <= kMaxBatch.
     int forward_dev_at(const int32_t* d_ids, int n, const int32_t* d_pos, int pos_off, bool compute_logits,
                        int32_t* d_argmax, orc_stream_t s = nullptr);
-    // Bound (1..ctx_len, 0 = ctx_len) on every position a device-position
-    // pass reaches, for the passes recorded while it is set: it sizes their
-    // attention grids. Results do not depend on it.
-    // Bounds on the device positions of the passes being captured (a graph
-    // replays them at later positions): floor <= position < limit; 0, 0: none.
+    // Bounds on the device positions of the passes recorded while they are set
+    // (a captured graph replays them at later positions): floor <= position <
+    // limit; 0, 0: none. They size the attention grids; results do not depend
+    // on them.
     void set_pos_band(int floor, int limit) {
         pos_floor_ = floor;
         pos_limit_ = limit;
