@@ -42,6 +42,7 @@ template <class T> __device__ __forceinline__ T* spin(T* p) {
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f2v __attribute__((ext_vector_type(2)));
 
 constexpr int kMWG = 512, kMW = kMWG / 64;
 // Tokens per launch: up to 8 as stacked hi / lo rows of one A tile (rows
@@ -77,6 +78,10 @@ typedef const __attribute__((address_space(1))) u16_u* g2p;
 __device__ __forceinline__ u32x4 ldg16(const uint8_t* p) { return *(g16p)p; }
 __device__ __forceinline__ u32x2 ldg8(const uint8_t* p) { return *(g8p)p; }
 __device__ __forceinline__ uint32_t ldg2(const uint8_t* p) { return *(g2p)p; }
+// outputs and biases through the global address space too (flat accesses
+// would also count against the LDS wait counter)
+typedef const __attribute__((address_space(1))) float* gfp;
+typedef __attribute__((address_space(1))) float* gwp;
 
 // Constants held in registers: a VOP3 operation such as v_and_or_b32 takes no
 // literal, so (x & mask) | magic is one operation only with both in registers.
@@ -223,17 +228,22 @@ __device__ __forceinline__ void mmq_core_q4k(const MUnit (&M)[TR], int u, int la
         q4k_unit_sm(h, M[tr].a.y, M[tr].b.x, M[tr].b.y, sc4, mn4);
         // B operand: minus dmin m of sub-block 4u + c of the lane's row
         const float bm = -(dmin * (float)((mn4 >> (8 * c)) & 0xFFu));
+        // code words shifted by one byte, shared by a low-nibble slice and its high-nibble partner
+        const uint32_t s8[4] = {M[tr].c.x >> 8, M[tr].c.y >> 8, M[tr].d.x >> 8, M[tr].d.y >> 8};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t sc = (sc4 >> (8 * i)) & 0xFFu;
-            // codes as fp16 1024 + q, then (1024 + q) sc - 1024 sc = sc q with one rounding (exact)
             const u32x2 src = (i >> 1) ? M[tr].d : M[tr].c;
-            const int sh = 4 * (i & 1);
-            const _Float16 f = (_Float16)(float)sc;
-            const h2v scv{f, f}, off{(_Float16)(-1024.f * (float)sc), (_Float16)(-1024.f * (float)sc)};
-            const uint32_t m4 = sreg(0x000F000Fu), mg = vreg(0x64006400u);
-            const uint32_t r[4] = {((src.x >> sh) & m4) | mg, ((src.x >> (sh + 8)) & m4) | mg, ((src.y >> sh) & m4) | mg,
-                                   ((src.y >> (sh + 8)) & m4) | mg};
+            // low nibbles as fp16 1024 + q: (1024 + q) sc - 1024 sc; high nibbles in
+            // place as 1024 + 16 q: (1024 + 16 q) (sc / 16) - 64 sc; either way sc q
+            // with one rounding (exact: sc q <= 945, sc / 16 and 64 sc exact in fp16)
+            const bool hn = i & 1;
+            const float scs = (float)sc;
+            const _Float16 f = (_Float16)(hn ? scs * 0.0625f : scs), o = (_Float16)(hn ? scs * -64.f : scs * -1024.f);
+            const h2v scv{f, f}, off{o, o};
+            const uint32_t mk = hn ? sreg(0x00F000F0u) : sreg(0x000F000Fu), mg = vreg(0x64006400u);
+            const uint32_t r[4] = {(src.x & mk) | mg, (s8[2 * (i >> 1)] & mk) | mg, (src.y & mk) | mg,
+                                   (s8[2 * (i >> 1) + 1] & mk) | mg};
             u32x4 bq;
 #pragma unroll
             for (int k = 0; k < 4; ++k) bq[k] = as_u32(__builtin_elementwise_fma(as_h2(r[k]), scv, off));
@@ -509,12 +519,15 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
             for (int k = 0; k < GPL; ++k) {
                 const bool in = sum_sq && lane + 64 * k < ng;
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
+                for (int t = 0; t < NT; ++t) {
+                    // the chain over the lane's values, kept only for lanes inside the range
+                    float sq = ssl[t];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        ssl[t] = __builtin_fmaf(in ? v[t][k][e] : 0.f, v[t][k][e], ssl[t]);
-                        v[t][k][e] *= gw[k][e];
-                    }
+                    for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(v[t][k][e], v[t][k][e], sq);
+                    ssl[t] = in ? sq : ssl[t];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[t][k][e] *= gw[k][e];
+                }
             }
         }
 #pragma unroll
@@ -545,12 +558,15 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                 for (int e = 0; e < 8; ++e) w[e] = v[t][k][e] * up;
                 int u, i, cc, j;
                 a_slot(b, k0 & 255, u, i, cc, j);
+                // hi halves converted two at a time, lo from the same rounded halves
                 h8v hi, lo;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const _Float16 he = (_Float16)w[e];
-                    hi[perm8(e)] = he;
-                    lo[perm8(e)] = (_Float16)(w[e] - (float)he);
+                for (int e = 0; e < 8; e += 2) {
+                    const h2v hp = __builtin_convertvector((f2v){w[e], w[e + 1]}, h2v);
+                    hi[perm8(e)] = hp.x;
+                    hi[perm8(e + 1)] = hp.y;
+                    lo[perm8(e)] = (_Float16)(w[e] - (float)hp.x);
+                    lo[perm8(e + 1)] = (_Float16)(w[e + 1] - (float)hp.y);
                 }
                 uint8_t* ap = abase + (size_t)aslot(u, s0) * a_stride_u;
                 *(h8v*)(ap + a_off<NT>(i, cc, 0, t)) = hi;
@@ -661,7 +677,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                     const int j = this_tile * 16 + n;
                     if (j < p.rows[0]) {
                         const float gv = acc[0][i] * inv, uv = acc[TR - 1][i] * inv;
-                        sy0[j + (size_t)tok * p.ldy] = (gv / (1.f + expf(-gv))) * uv;
+                        *(gwp)(sy0 + j + (size_t)tok * p.ldy) = (gv / (1.f + expf(-gv))) * uv;
                     }
                 } else {
 #pragma unroll
@@ -670,10 +686,10 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                         const float* bias;
                         if (orow((this_tile * TR + tr) * 16 + n, y, bias)) {
                             float v = acc[tr][i] * inv;
-                            if (bias) v += *bias;
+                            if (bias) v += *(gfp)bias;
                             float* dst = y + (size_t)tok * p.ldy;
-                            if (p.epi == ORC_EPI_ACCUM) *dst += v;
-                            else *dst = v;
+                            if (p.epi == ORC_EPI_ACCUM) *(gwp)dst += v;
+                            else *(gwp)dst = v;
                         }
                     }
                 }
@@ -701,7 +717,7 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
                 const float inv = inv_rms(tok);
                 if (j < p.rows[0]) {
                     const float gv = gs * inv, uv = us * inv;
-                    sy0[j + (size_t)tok * p.ldy] = (gv / (1.f + expf(-gv))) * uv;
+                    *(gwp)(sy0 + j + (size_t)tok * p.ldy) = (gv / (1.f + expf(-gv))) * uv;
                 }
             }
         } else if (tid < TR * NT * 16) {
@@ -714,10 +730,10 @@ __global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void 
             const float* bias;
             if (orow(jl, y, bias)) {
                 float v = s * inv;
-                if (bias) v += *bias;
+                if (bias) v += *(gfp)bias;
                 float* dst = y + (size_t)tok * p.ldy;
-                if (p.epi == ORC_EPI_ACCUM) *dst += v;
-                else *dst = v;
+                if (p.epi == ORC_EPI_ACCUM) *(gwp)dst += v;
+                else *(gwp)dst = v;
             }
         }
         __syncthreads();
