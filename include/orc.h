@@ -39,6 +39,7 @@ extern "C" {
 /* GGML type ids (core/gguf_parser.hpp:9-24) */
 #define ORC_F32 0
 #define ORC_F16 1
+#define ORC_BF16 30 /* dense weights: F32, F16 and BF16 rows run the vector GEMV */
 #define ORC_Q4_0 2
 #define ORC_Q8_0 8
 #define ORC_Q4_K 12
@@ -97,7 +98,7 @@ int64_t orc_row_bytes(int type, int64_t n_el);
  * matrix is then used with type ORC_Q8_0_X8 only. */
 int orc_q8_0_regroup(void* d_w, int64_t n_blocks8, orc_stream_t stream);
 /* Dequantize n_el contiguous elements to fp32, bit-exact with the reference
- * codecs: fp16/Q4_0/Q8_0/Q4_K/Q6_K (core/gguf_parser.cpp:1002-1154,
+ * codecs: F32/F16/BF16/Q4_0/Q8_0/Q4_K/Q6_K (core/gguf_parser.cpp:1002-1154,
  * dequantize_into :420-441); also ORC_Q8_0_X8 (n_el a multiple of 256 from
  * the start of a regrouped row), with the values of the Q8_0 blocks it holds. */
 int orc_dequant(int type, const void* d_w, int64_t n_el, float* d_y, orc_stream_t stream);
@@ -113,7 +114,10 @@ int orc_embed(int type, const void* d_table, int n_in, int n_rows, const int32_t
  * core/gguf_parser.cpp:868-911); n_tok > 1 is the verify / prefill GEMM
  * (gemm_q, core/gguf_parser.cpp:919-997). The per-(token,row) reduction order
  * does not depend on n_tok, so the verify pass is bit-identical to n_tok
- * separate GEMVs. Supported types: Q4_0, Q8_0, Q4_K, Q6_K. */
+ * separate GEMVs. Supported types: Q4_0, Q8_0, Q4_K, Q6_K, and the dense
+ * F32, F16 and BF16 (n_in a multiple of 32), which the reference runs through
+ * its dequantize + ops::matmul fallback (core/model.cpp:370-381): fp32 FMA
+ * on the exactly widened values, one kernel family at every token count. */
 int orc_gemm(int type, const void* d_w, int n_tok, int n_out, int n_in, const float* d_x, int ldx, float* d_y,
              int ldy, orc_stream_t stream);
 static inline int orc_gemv(int type, const void* d_w, int n_out, int n_in, const float* d_x, float* d_y,
@@ -195,12 +199,14 @@ int orc_matmul_f32(float* d_out, const float* d_a, const float* d_b, int m, int 
 /* Rotate-half RoPE of one position (ops::rope, ops.cpp:440-485) in place on
  * n_heads q heads and n_kv_heads k heads of head_dim values; d_cs holds the
  * position's head_dim/2 (cos, sin) pairs, computed on the host as the
- * reference does. */
+ * reference does. An odd head_dim rotates the pairs (i, i + head_dim/2) and
+ * leaves each head's last value as it is, as the reference does. */
 int orc_rope_pos(float* d_q, float* d_k, int n_heads, int n_kv_heads, int head_dim, const float* d_cs,
                  orc_stream_t stream);
 
 /* ── elementwise / attention ─────────────────────────────────────────────── */
-/* out[t] = rmsnorm(x[t]) for n_rows rows of n (ops::rmsnorm, ops.cpp:149-195). */
+/* out[t] = rmsnorm(x[t]) for n_rows rows of n (ops::rmsnorm, ops.cpp:149-195);
+ * any n >= 1 (pointers 16-byte aligned when n is a multiple of 4). */
 int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_rows, float eps, orc_stream_t stream);
 /* RoPE (rotate-half pairs (i, i+hd/2), theta = pos / base^(2i/hd),
  * ops::rope ops.cpp:440-485) on the q and k columns of n_tok QKV rows laid out
@@ -311,7 +317,10 @@ int orc_spec_accept_greedy_at(const int32_t* d_tgt_ids, const int32_t* d_draft_i
  * top_k 0 = all tokens, for vocabularies of at most 16384 tokens when
  * T > 0 (T <= 0 is the argmax and sorts nothing): with such a state,
  * orc_sample / orc_spec_accept_engine / orc_transform_probs on a larger
- * vocabulary return ORC_E_UNSUPPORTED; repeat_last < 2048. */
+ * vocabulary return ORC_E_UNSUPPORTED. 0 <= repeat_last < 4096 (ORC_E_INVALID
+ * beyond): the penalty over the last repeat_last entries is the reference's
+ * at every such value; from 2048 up the history a full buffer keeps is its
+ * last repeat_last entries (the reference keeps up to 2 * repeat_last). */
 size_t orc_sampler_state_bytes(void);
 int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty, int repeat_last,
                      uint64_t seed, const int32_t* d_hist, int n_hist, orc_stream_t stream);

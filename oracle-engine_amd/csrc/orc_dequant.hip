@@ -8,7 +8,7 @@
 // ── bit-exact dequant (core/gguf_parser.cpp:1029-1154) ───────────────────────
 namespace orc {
 // One thread per 32 consecutive output values; rounding exactly as the
-// reference build: Q4_0/Q8_0/F16 one product or exact conversion, Q4_K
+// reference build: Q4_0/Q8_0/F16/BF16 one product or exact conversion, Q4_K
 // fma(d*sc, q, -(dmin*m)) (the reference's d1*q - m1f contracts to one FMA),
 // Q6_K (d*sc)*q with two roundings.
 __device__ __forceinline__ void dequant32(int type, const uint8_t* w, int64_t g, float* out) {
@@ -18,6 +18,9 @@ __device__ __forceinline__ void dequant32(int type, const uint8_t* w, int64_t g,
             break;
         case ORC_F16:
             for (int i = 0; i < 32; ++i) out[i] = h2f(ld2(w + (g * 32 + i) * 2));
+            break;
+        case ORC_BF16:  // the high half of an fp32 (core/gguf_parser.cpp:1034-1040)
+            for (int i = 0; i < 32; ++i) out[i] = __builtin_bit_cast(float, ld2(w + (g * 32 + i) * 2) << 16);
             break;
         case ORC_Q8_0: {
             const uint8_t* b = w + g * 34;
@@ -104,7 +107,8 @@ __global__ void k_embed(int type, const uint8_t* table, int n_in, int n_rows, ui
 using namespace orc;
 
 static bool dq_type_ok(int t) {
-    return t == ORC_F32 || t == ORC_F16 || t == ORC_Q4_0 || t == ORC_Q8_0 || t == ORC_Q4_K || t == ORC_Q6_K;
+    return t == ORC_F32 || t == ORC_F16 || t == ORC_BF16 || t == ORC_Q4_0 || t == ORC_Q8_0 || t == ORC_Q4_K ||
+           t == ORC_Q6_K;
 }
 
 extern "C" int orc_dequant(int type, const void* d_w, int64_t n_el, float* d_y, orc_stream_t stream) {

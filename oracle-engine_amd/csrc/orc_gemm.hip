@@ -48,6 +48,10 @@ template <> struct QTr<ORC_Q8_0_X8> { static constexpr int EPU = 32, PP = 32, LP
 template <> struct QTr<ORC_Q4_0> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
 template <> struct QTr<ORC_Q4_K> { static constexpr int EPU = 32, PP = 64, LPR = 32; };
 template <> struct QTr<ORC_Q6_K> { static constexpr int EPU = 64, PP = 64, LPR = 16; };
+// dense rows (F32 / F16 / BF16): a unit is 32 consecutive values
+template <> struct QTr<ORC_F32> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
+template <> struct QTr<ORC_F16> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
+template <> struct QTr<ORC_BF16> { static constexpr int EPU = 32, PP = 32, LPR = 32; };
 // one-token mixed launches (Q4_K segments, then Q6_K segments): each row
 // group takes its own type's unit, LPR and row count; both pad every 64 values
 template <> struct QTr<kMixK> { static constexpr int EPU = 32, PP = 64, LPR = 32; };
@@ -345,6 +349,66 @@ template <int ROWS> struct Unit<ORC_Q4_0, ROWS> {
         }
     }
 };
+
+// Dense rows: F32, F16 or BF16 values widened exactly to fp32. The reference
+// runs such matrices through its fallback, dequantize + ops::matmul
+// (core/model.cpp:370-381 and the same pattern for o / gate / up / down /
+// head; core/gguf_parser.cpp:1029-1055 for the conversions).
+template <int QT, int ROWS> struct DenseUnit {
+    static constexpr int WB = QT == ORC_F32 ? 4 : 2;  // bytes per value
+    static constexpr int NV = 2 * WB;                 // 16-byte loads per 32-value unit
+    u32x4 v[ROWS][NV];
+    __device__ __forceinline__ void load(const uint8_t* const (&rp)[ROWS], int u) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const uint8_t* p = rp[r] + (size_t)u * 32 * WB;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) v[r][i] = ld16(p + 16 * i);
+        }
+    }
+    // values 8k .. 8k + 7 of the unit of row r
+    __device__ __forceinline__ void vals8(int r, int k, float* w) const {
+        if constexpr (QT == ORC_F32) {
+            const u32x4 a = v[r][2 * k], b = v[r][2 * k + 1];
+            const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = __builtin_bit_cast(float, q[i]);
+        } else {
+            const u32x4 a = v[r][k];
+            const uint32_t q[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (QT == ORC_F16) {
+                    w[2 * i] = h2f(q[i] & 0xFFFFu);
+                    w[2 * i + 1] = h2f(q[i] >> 16);
+                } else {  // BF16: the high half of an fp32
+                    w[2 * i] = __builtin_bit_cast(float, q[i] << 16);
+                    w[2 * i + 1] = __builtin_bit_cast(float, q[i] & 0xFFFF0000u);
+                }
+            }
+        }
+    }
+    template <int NT>
+    __device__ __forceinline__ void compute(int u, const XCtx& c, float (&acc)[ROWS][NT]) const {
+        const int p0 = padx<32>(u * 32 - c.k0);
+        float S[ROWS][NT];
+        zero(S);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float w[ROWS][8];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) vals8(r, k, w[r]);
+            dot8(w, c, p0 + 8 * k, S);
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[r][t] += S[r][t];
+    }
+};
+template <int ROWS> struct Unit<ORC_F32, ROWS> : DenseUnit<ORC_F32, ROWS> {};
+template <int ROWS> struct Unit<ORC_F16, ROWS> : DenseUnit<ORC_F16, ROWS> {};
+template <int ROWS> struct Unit<ORC_BF16, ROWS> : DenseUnit<ORC_BF16, ROWS> {};
 
 // kMixK instantiates the generic row-group loops, which its launches never
 // run (the mixed loop below takes every group)
@@ -773,6 +837,19 @@ template <int QT, int NT>
 static int launch_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     const bool pair = p.epi == ORC_EPI_SWIGLU;
     const bool tall = p.n_rows >= 32768;  // LM heads
+    if constexpr (QT == ORC_F32 || QT == ORC_F16 || QT == ORC_BF16) {
+        // dense units hold 64-128 bytes per row: one unit per lane in flight
+        // (two for 2-byte values), no row pipelining
+        const int per_lane = (p.units + 31) / 32;
+        if constexpr (NT == 1) {
+            if (pair) return launch_shape<QT, NT, 2, 1, 4>(p, s, ev);
+            if (QT != ORC_F32 && per_lane >= 2) return launch_shape<QT, NT, 1, 2, 4>(p, s, ev);
+            return launch_shape<QT, NT, 1, 1, 4>(p, s, ev);
+        } else {
+            if (pair) return launch_shape<QT, NT, 2, 1, 2>(p, s, ev);
+            return launch_shape<QT, NT, 1, 1, 2>(p, s, ev);
+        }
+    }
     if constexpr (NT == 1) {
         if ((QT == ORC_Q6_K && tall) || pair) return launch_shape<QT, NT, 2, 1, 4>(p, s, ev);
         // units per lane per batch: at most what a row gives a lane (the
@@ -931,6 +1008,9 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
             case ORC_Q8_0: rc = launch_type<ORC_Q8_0>(q, s, ev); break;
             case ORC_Q8_0_X8: rc = launch_type<ORC_Q8_0_X8>(q, s, ev); break;
             case ORC_Q4_0: rc = launch_type<ORC_Q4_0>(q, s, ev); break;
+            case ORC_F32: rc = launch_type<ORC_F32>(q, s, ev); break;
+            case ORC_F16: rc = launch_type<ORC_F16>(q, s, ev); break;
+            case ORC_BF16: rc = launch_type<ORC_BF16>(q, s, ev); break;
             default: return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
         }
         if (rc) return rc;
@@ -998,6 +1078,7 @@ extern "C" int64_t orc_row_bytes(int type, int64_t n) {
     switch (type) {
         case ORC_F32: return n * 4;
         case ORC_F16: return n * 2;
+        case ORC_BF16: return n * 2;
         case ORC_Q4_0: return n % 32 ? -1 : n / 32 * 18;
         case ORC_Q8_0: return n % 32 ? -1 : n / 32 * 34;
         case ORC_Q8_0_X8: return n % 256 ? -1 : n / 32 * 34;
@@ -1034,7 +1115,8 @@ __global__ __launch_bounds__(256) void k_q8_0_regroup(uint8_t* w, int64_t n8) {
 
 static int check_gemm_shape(int type, int n_tok, int n_in, const float* x, int ldx, int ldy, const void* w) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q8_0_X8 && type != ORC_Q4_0)
+    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q8_0_X8 && type != ORC_Q4_0 &&
+        type != ORC_F32 && type != ORC_F16 && type != ORC_BF16)
         return set_error(ORC_E_UNSUPPORTED, "gemm: unsupported weight type " + std::to_string(type));
     if (n_tok < 1 || n_in <= 0 || n_in % block_elems(type))
         return set_error(ORC_E_INVALID, "gemm: n_in must be a positive multiple of the block size");
@@ -1043,6 +1125,8 @@ static int check_gemm_shape(int type, int n_tok, int n_in, const float* x, int l
     if (((uintptr_t)x & 15) != 0) return set_error(ORC_E_INVALID, "gemm: x must be 16-byte aligned");
     if (type == ORC_Q8_0_X8 && ((uintptr_t)w & 15))
         return set_error(ORC_E_INVALID, "gemm: Q8_0_X8 weights must be 16-byte aligned");
+    if (type == ORC_F32 && ((uintptr_t)w & 3))
+        return set_error(ORC_E_INVALID, "gemm: F32 weights must be 4-byte aligned");
     return ORC_OK;
 }
 

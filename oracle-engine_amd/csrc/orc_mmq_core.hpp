@@ -374,8 +374,11 @@ template <class T> __device__ __forceinline__ T* pick3(int s, T* a, T* b, T* c) 
 // KS1 = false: the eight waves of a workgroup split one tile's units (small
 // matrices, where tiles are few); true: each wave owns whole tiles and its
 // ring of loads runs on across them without barriers (tall matrices).
-template <int QT, int NT, int TR, int UW, int SW, bool KS1, bool MW>
-__global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(2))) void k_mmq(QmvParams p) {
+// WPE: waves per SIMD the registers are sized for: 2 (one workgroup per CU),
+// or 4 (two per CU, at most 128 registers) for the kernels that fit them
+// without spills, whose launches then run up to two workgroups per CU.
+template <int QT, int NT, int TR, int UW, int SW, bool KS1, bool MW, int WPE>
+__global__ __launch_bounds__(kMWG) __attribute__((amdgpu_waves_per_eu(WPE))) void k_mmq(QmvParams p) {
     // token block blockIdx.y: tokens [NT y, NT (y + 1)) of the launch. Every
     // block holds exactly NT tokens (the kernel stages and writes NT rows).
     if (blockIdx.y) {
@@ -771,14 +774,14 @@ static int mmq_window(int per_wave, int nwin) {
     return hs >= per_wave ? hs : (hs + 3) & ~3;
 }
 
-template <bool MW, int QT, int NT, int TR, int UW, int SW, bool KS1>
+template <bool MW, int QT, int NT, int TR, int UW, int SW, bool KS1, int WPE = 2>
 static int mmq_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& ev) {
     QmvParams p = p0;
     const bool swiglu = p.epi == ORC_EPI_SWIGLU;
     const int rows_out = swiglu ? p.rows[0] : p.n_rows;
     const int n_tiles = swiglu ? (rows_out + 15) / 16 : (rows_out + 16 * TR - 1) / (16 * TR);
     if (p.tok_block != NT || p.n_tok % NT) return set_error(ORC_E_INVALID, "gemm: token blocks must be whole");
-    const dim3 grid(std::max(1, std::min(KS1 ? (n_tiles + kMW - 1) / kMW : n_tiles, g_n_cu)),
+    const dim3 grid(std::max(1, std::min(KS1 ? (n_tiles + kMW - 1) / kMW : n_tiles, (WPE / 2) * g_n_cu)),
                     p.n_tok / NT);  // the launch's token blocks
     // split-tile mode: the fewest staging windows per wave range that fit
     p.hs = 0;
@@ -797,9 +800,10 @@ static int mmq_shape(const QmvParams& p0, hipStream_t s, const LaunchEvents& ev)
         if (!KS1 && p.hs < (p.n_in / 128 + kMW - 1) / kMW) return mmq_launch_windowed(QT, p0, s, ev);
     }
     if (ev.start)
-        hipExtLaunchKernelGGL((k_mmq<QT, NT, TR, UW, SW, KS1, MW>), grid, dim3(kMWG), lds, s, ev.start, ev.stop, 0, p);
+        hipExtLaunchKernelGGL((k_mmq<QT, NT, TR, UW, SW, KS1, MW, WPE>), grid, dim3(kMWG), lds, s, ev.start, ev.stop, 0,
+                              p);
     else
-        hipLaunchKernelGGL((k_mmq<QT, NT, TR, UW, SW, KS1, MW>), grid, dim3(kMWG), lds, s, p);
+        hipLaunchKernelGGL((k_mmq<QT, NT, TR, UW, SW, KS1, MW, WPE>), grid, dim3(kMWG), lds, s, p);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }
@@ -835,6 +839,13 @@ static int mmq_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     if constexpr (mmq_wide<NT>()) {
         return mmq_shape<MW, QT, NT, 1, 3, 4, false>(p, s, ev);
     } else {
+        // a mixed Q|K|V of three units per wave (n_in 3072: 320 tiles at the
+        // 3B shape) fits two workgroups per CU with a ring of two, so every
+        // tile runs at once (measured at 5 tokens: 13.8 -> 12.4 us per launch)
+        if constexpr (QT == kMixK && !MW) {
+            if (per_wave <= 3 && 2 * mmq_lds(QT, NT, p.n_in, 1, 0) <= 160 * 1024)
+                return mmq_shape<MW, QT, NT, 1, 2, 4, false, 4>(p, s, ev);
+        }
         if (per_wave <= 3) return mmq_shape<MW, QT, NT, 1, 3, 4, false>(p, s, ev);
         if constexpr (NT > 4) return mmq_shape<MW, QT, NT, 1, 4, 4, false>(p, s, ev);
         else {

@@ -18,28 +18,41 @@
 namespace orc {
 
 // ── RMSNorm: one workgroup per row, the same reduction as the GEMM prologue ───
+// Rows of a multiple of 4 floats are read as float4s; any other n (which the
+// reference's scalar tail also takes, core/ops.cpp:149-195) one float per
+// thread and step.
 __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
     __shared__ float red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float4* xr = (const float4*)(x + (size_t)blockIdx.x * n);
+    const bool v4 = (n & 3) == 0;
+    const float* xr = x + (size_t)blockIdx.x * n;
+    float* orow = out + (size_t)blockIdx.x * n;
     float ss = 0.f;
-    for (int i = tid; i < n / 4; i += 256) {
-        float4 v = xr[i];
-        ss = __builtin_fmaf(v.x, v.x, ss);
-        ss = __builtin_fmaf(v.y, v.y, ss);
-        ss = __builtin_fmaf(v.z, v.z, ss);
-        ss = __builtin_fmaf(v.w, v.w, ss);
+    if (v4) {
+        for (int i = tid; i < n / 4; i += 256) {
+            float4 v = ((const float4*)xr)[i];
+            ss = __builtin_fmaf(v.x, v.x, ss);
+            ss = __builtin_fmaf(v.y, v.y, ss);
+            ss = __builtin_fmaf(v.z, v.z, ss);
+            ss = __builtin_fmaf(v.w, v.w, ss);
+        }
+    } else {
+        for (int i = tid; i < n; i += 256) ss = __builtin_fmaf(xr[i], xr[i], ss);
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     const float s = 1.f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)n + eps);
-    float4* o4 = (float4*)(out + (size_t)blockIdx.x * n);
-    const float4* w4 = (const float4*)w;
-    for (int i = tid; i < n / 4; i += 256) {
-        float4 v = xr[i], g = w4[i];
-        o4[i] = make_float4((v.x * s) * g.x, (v.y * s) * g.y, (v.z * s) * g.z, (v.w * s) * g.w);
+    if (v4) {
+        float4* o4 = (float4*)orow;
+        const float4* w4 = (const float4*)w;
+        for (int i = tid; i < n / 4; i += 256) {
+            float4 v = ((const float4*)xr)[i], g = w4[i];
+            o4[i] = make_float4((v.x * s) * g.x, (v.y * s) * g.y, (v.z * s) * g.z, (v.w * s) * g.w);
+        }
+    } else {
+        for (int i = tid; i < n; i += 256) orow[i] = (xr[i] * s) * w[i];
     }
 }
 
@@ -1390,9 +1403,9 @@ using namespace orc;
 extern "C" int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_rows, float eps,
                            orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (n <= 0 || n % 4 || n_rows < 0 || !d_out || !d_x || !d_w) return set_error(ORC_E_INVALID, "rmsnorm: bad args");
-    if (((uintptr_t)d_out | (uintptr_t)d_x | (uintptr_t)d_w) & 15)
-        return set_error(ORC_E_INVALID, "rmsnorm: pointers must be 16-byte aligned");
+    if (n <= 0 || n_rows < 0 || !d_out || !d_x || !d_w) return set_error(ORC_E_INVALID, "rmsnorm: bad args");
+    if (n % 4 == 0 && (((uintptr_t)d_out | (uintptr_t)d_x | (uintptr_t)d_w) & 15))
+        return set_error(ORC_E_INVALID, "rmsnorm: pointers must be 16-byte aligned when n is a multiple of 4");
     if (!n_rows) return ORC_OK;
     hipLaunchKernelGGL(k_rmsnorm, dim3(n_rows), dim3(256), 0, resolve_stream(s), d_out, d_x, d_w, n, eps);
     ORC_LAUNCH_CHECK();

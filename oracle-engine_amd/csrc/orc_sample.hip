@@ -35,7 +35,7 @@
 namespace orc {
 
 constexpr int kST = 1024;          // threads of a sampling workgroup
-constexpr int kSampHist = 4096;    // history capacity (repeat_last <= 2047)
+constexpr int kSampHist = 4096;    // history capacity (repeat_last <= kSampHist - 1)
 constexpr int kCandMax = 16384;    // candidates sorted in LDS (largest top_k; top_k = 0 means this many)
 
 struct DevSampler {
@@ -71,9 +71,14 @@ __device__ float mt_canonical(DevSampler* s) {
 }
 
 __device__ void record_tok(DevSampler* s, int32_t tok) {
-    if (s->nh >= kSampHist) {  // only reachable with repeat_last == 0, where history is never read
-        for (int i = 0; i < kSampHist / 2; ++i) s->hist[i] = s->hist[i + kSampHist / 2];
-        s->nh = kSampHist / 2;
+    // A full buffer keeps its last repeat_last entries (< kSampHist), the only
+    // ones the penalty ever reads; below 2048 the reference's own trim (more
+    // than 2 * repeat_last entries) comes first and this never runs but with
+    // repeat_last == 0, where the history is never read.
+    if (s->nh >= kSampHist) {
+        const int keep = s->last;
+        for (int i = 0; i < keep; ++i) s->hist[i] = s->hist[s->nh - keep + i];
+        s->nh = keep;
     }
     s->hist[s->nh++] = tok;
     if (s->nh > s->last * 2) {
@@ -698,9 +703,9 @@ extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, i
                                 int repeat_last, uint64_t seed, const int32_t* d_hist, int n_hist,
                                 orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (!d_state || repeat_last < 0 || repeat_last >= kSampHist / 2 || n_hist < 0 || (n_hist && !d_hist) ||
+    if (!d_state || repeat_last < 0 || repeat_last >= kSampHist || n_hist < 0 || (n_hist && !d_hist) ||
         top_k < 0 || top_k > kCandMax)
-        return set_error(ORC_E_INVALID, "sampler_init: bad args (0 <= top_k <= 16384, repeat_last < 2048)");
+        return set_error(ORC_E_INVALID, "sampler_init: bad args (0 <= top_k <= 16384, 0 <= repeat_last < 4096)");
     {
         std::lock_guard<std::mutex> lk(g_all_mu);
         if (top_k == 0 && temperature > 0.f) g_all_tokens.insert(d_state);  // T <= 0 sorts nothing (argmax)
@@ -715,8 +720,8 @@ extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, i
 extern "C" int orc_sampler_set_params(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty,
                                       int repeat_last, orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (!d_state || repeat_last < 0 || repeat_last >= kSampHist / 2 || top_k < 0 || top_k > kCandMax)
-        return set_error(ORC_E_INVALID, "sampler_set_params: bad args (0 <= top_k <= 16384, repeat_last < 2048)");
+    if (!d_state || repeat_last < 0 || repeat_last >= kSampHist || top_k < 0 || top_k > kCandMax)
+        return set_error(ORC_E_INVALID, "sampler_set_params: bad args (0 <= top_k <= 16384, 0 <= repeat_last < 4096)");
     {
         std::lock_guard<std::mutex> lk(g_all_mu);
         if (top_k == 0 && temperature > 0.f) g_all_tokens.insert(d_state);  // T <= 0 sorts nothing (argmax)

@@ -174,7 +174,7 @@ extern "C" int orc_matmul_f32(float* d_out, const float* d_a, const float* d_b, 
 extern "C" int orc_rope_pos(float* d_q, float* d_k, int n_heads, int n_kv_heads, int head_dim, const float* d_cs,
                             orc_stream_t s) {
     if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
-    if (n_heads < 0 || n_kv_heads < 0 || head_dim <= 0 || head_dim % 2 || !d_cs || (n_heads && !d_q) ||
+    if (n_heads < 0 || n_kv_heads < 0 || head_dim < 2 || !d_cs || (n_heads && !d_q) ||
         (n_kv_heads && !d_k))
         return set_error(ORC_E_INVALID, "rope_pos: bad args");
     const int n = (n_heads + n_kv_heads) * (head_dim / 2);

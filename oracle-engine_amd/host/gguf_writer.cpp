@@ -143,6 +143,15 @@ bool quantize_any(GGMLType t, const float* x, int64_t n, uint8_t* out) {
                 std::memcpy(out + 2 * i, &h, 2);
             }
             return true;
+        case GGMLType::BF16:  // round to nearest even (finite inputs)
+            for (int64_t i = 0; i < n; ++i) {
+                uint32_t u;
+                std::memcpy(&u, &x[i], 4);
+                u += 0x7FFFu + ((u >> 16) & 1u);
+                const uint16_t h = (uint16_t)(u >> 16);
+                std::memcpy(out + 2 * i, &h, 2);
+            }
+            return true;
         case GGMLType::Q8_0: quantize_q8_0(x, n, out); return true;
         case GGMLType::Q4_0: quantize_q4_0(x, n, out); return true;
         case GGMLType::Q4_K: quantize_q4_k(x, n, out); return true;

@@ -67,19 +67,28 @@ bool Model::load(const std::string& path, int ctx_len) {
         m.n_out = ti.shape.size() > 1 ? (int)ti.shape[1] : 1;
         if (m.n_in != n_in || m.n_out != n_out)
             return fail("tensor " + name + " has an unexpected shape");
-        if (m.type != ORC_Q4_0 && m.type != ORC_Q8_0 && m.type != ORC_Q4_K && m.type != ORC_Q6_K)
+        // quantized blocks, or dense F32 / F16 / BF16 rows (the reference's
+        // dequantize + ops::matmul fallback, core/model.cpp:370-381)
+        if (m.type != ORC_Q4_0 && m.type != ORC_Q8_0 && m.type != ORC_Q4_K && m.type != ORC_Q6_K &&
+            m.type != ORC_F32 && m.type != ORC_F16 && m.type != ORC_BF16)
             return fail("tensor " + name + ": weight type " + ggml_type_name(ti.type) +
-                        " is not supported by the device GEMM (quantized types only)");
+                        " is not supported by the device GEMM");
+        if ((m.type == ORC_F32 || m.type == ORC_F16 || m.type == ORC_BF16) && m.n_in % 32)
+            return fail("tensor " + name + ": dense rows must hold a multiple of 32 values");
         return true;
     };
+    // Norm weights and biases: n floats read from the tensor's first byte
+    // whatever type it declares, as the reference's load_norm_n memcpy's
+    // 4 n raw bytes (core/model.cpp:317-320); the read must stay inside the
+    // data section.
     auto vec = [&](const std::string& name, int n, bool required) -> const float* {
         if (!gguf_.has_tensor(name)) {
             if (required) fail("missing tensor " + name);
             return nullptr;
         }
         const TensorInfo& ti = gguf_.tensor_info(name);
-        if (ti.type != GGMLType::F32 || ti.n_elems() < (uint64_t)n) {
-            fail("tensor " + name + " must be F32 with " + std::to_string(n) + " values");
+        if (ti.offset + 4 * (uint64_t)n > gguf_.data_bytes() || (ti.offset & 3)) {
+            fail("tensor " + name + ": " + std::to_string(n) + " floats from its offset leave the data section");
             return nullptr;
         }
         return (const float*)gguf_.tensor_device(name);

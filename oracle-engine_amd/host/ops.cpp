@@ -125,8 +125,9 @@ void softmax(float* x, int n) {  // ops.cpp:386-435
 
 void rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim, int pos, float freq_base) {
     // ops.cpp:440-485: the position's angles with the reference's float
-    // arithmetic on the host, the rotation on the device
-    if (head_dim <= 0 || head_dim % 2 || n_heads < 0 || n_kv_heads < 0) return;
+    // arithmetic on the host, the rotation on the device; an odd head_dim
+    // rotates the pairs (i, i + head_dim / 2) and leaves the last value
+    if (head_dim < 2 || n_heads < 0 || n_kv_heads < 0) return;
     const int half = head_dim / 2;
     std::vector<float> cs((size_t)2 * half);
     for (int i = 0; i < half; ++i) {

@@ -13,8 +13,12 @@ Sampler::Sampler(const SamplerParams& p, uint64_t seed) : p_(p) {  // sampler.cp
         return;
     }
     if (orc_sampler_init(d_state_, p.temperature, p.top_p, p.top_k, p.repeat_pen, p.repeat_last, seed, nullptr, 0,
-                         nullptr) != ORC_OK)
+                         nullptr) != ORC_OK) {
+        // e.g. repeat_last >= 4096: reported here (error()), and the sampler
+        // is left without a state, so sample() returns -1 and record() does nothing
         fail("init");
+        release();
+    }
 }
 
 Sampler::~Sampler() { release(); }

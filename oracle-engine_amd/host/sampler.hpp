@@ -20,7 +20,10 @@ struct SamplerParams {  // core/sampler.hpp:16-22
 class Sampler {
 public:
     // core/sampler.hpp:26; the seed is truncated to 32 bits as std::mt19937's
-    // constructor does with the reference's 64-bit seed.
+    // constructor does with the reference's 64-bit seed. The device history
+    // holds 4096 ids: repeat_last must be below 4096 (the reference takes any
+    // value); a larger one, or a failed device set-up, is reported here
+    // through error() (and stderr), and sample() then returns -1.
     explicit Sampler(const SamplerParams& p = {}, uint64_t seed = 42);
     ~Sampler();
     Sampler(const Sampler&) = delete;

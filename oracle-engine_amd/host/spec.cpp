@@ -4,16 +4,30 @@
 #include <cstdio>
 
 DecodeSession::DecodeSession(int max_tokens, int max_k) : max_tokens_(max_tokens), max_k_(max_k) {
-    orc_init(0);  // idempotent; the session may be created before any model is loaded
-    orc_malloc((void**)&d_hist_, (size_t)(max_tokens + 2) * 4);
-    orc_malloc((void**)&d_vin_, (size_t)(max_k + 2) * 4);
-    orc_malloc((void**)&d_tgt_, (size_t)(max_k + 2) * 4);
-    orc_malloc((void**)&d_acc_, (size_t)(max_k + 4) * 4);
-    orc_malloc((void**)&d_pos_, 4 * 4);
-    orc_malloc((void**)&d_tok_, 4 * 4);
-    orc_malloc(&d_samp_, orc_sampler_state_bytes());
-    orc_malloc((void**)&d_eout_, (size_t)(max_k + 8) * 4);
-    orc_malloc((void**)&d_budget_, 4);
+    // orc_init is idempotent; the session may be created before any model is
+    // loaded. A failed step leaves the session unusable: every loop then
+    // returns the recorded error instead of launching on null buffers.
+    auto need = [&](int rc, const char* what) {
+        if (rc != ORC_OK && init_rc_ == ORC_OK) {
+            init_rc_ = rc;
+            init_err_ = std::string("DecodeSession: ") + what + ": " + orc_last_error();
+        }
+    };
+    need(orc_init(0), "orc_init");
+    if (max_tokens < 1 || max_k < 1) {
+        init_rc_ = ORC_E_INVALID;
+        init_err_ = "DecodeSession: max_tokens and max_k must be positive";
+        return;
+    }
+    need(orc_malloc((void**)&d_hist_, (size_t)(max_tokens + 2) * 4), "device allocation");
+    need(orc_malloc((void**)&d_vin_, (size_t)(max_k + 2) * 4), "device allocation");
+    need(orc_malloc((void**)&d_tgt_, (size_t)(max_k + 2) * 4), "device allocation");
+    need(orc_malloc((void**)&d_acc_, (size_t)(max_k + 4) * 4), "device allocation");
+    need(orc_malloc((void**)&d_pos_, 4 * 4), "device allocation");
+    need(orc_malloc((void**)&d_tok_, 4 * 4), "device allocation");
+    need(orc_malloc(&d_samp_, orc_sampler_state_bytes()), "device allocation");
+    need(orc_malloc((void**)&d_eout_, (size_t)(max_k + 8) * 4), "device allocation");
+    need(orc_malloc((void**)&d_budget_, 4), "device allocation");
 }
 
 DecodeSession::~DecodeSession() {
@@ -229,6 +243,7 @@ int DecodeSession::spec_rounds(Model& tgt, Model& dft, int pos, int32_t next, in
 }
 
 int DecodeSession::prefill(Model& m, const int32_t* prompt, int n_prompt) {
+    if (init_rc_ != ORC_OK) return unusable();
     if (n_prompt < 1 || !prompt) return invalid("empty prompt");
     if (n_prompt > (int)m.cfg.ctx_len)
         return invalid("prompt of " + std::to_string(n_prompt) + " tokens does not fit the " +
@@ -242,6 +257,7 @@ int DecodeSession::prefill(Model& m, const int32_t* prompt, int n_prompt) {
 // The argmax of step s is written straight into the input slot of step s+1,
 // so the whole chain is enqueued without a host round trip.
 int DecodeSession::greedy(Model& m, const int32_t* prompt, int n_prompt, int n_gen, int32_t* out) {
+    if (init_rc_ != ORC_OK) return unusable();
     if (n_gen > max_tokens_ || n_prompt < 1) return invalid("greedy: bad prompt or more tokens than the session holds");
     int pos = n_prompt - 1;
     if (pos + n_gen > (int)m.cfg.ctx_len) return invalid("greedy: prompt + generated tokens exceed the context");
@@ -257,6 +273,7 @@ int DecodeSession::greedy(Model& m, const int32_t* prompt, int n_prompt, int n_g
 
 int DecodeSession::spec_greedy(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                                int32_t* out, SpecStats* st) {
+    if (init_rc_ != ORC_OK) return unusable();
     if (k < 1 || k > max_k_ || n_prompt < 1) return invalid("spec_greedy: bad k or prompt");
     if (dft.cfg.n_vocab != tgt.cfg.n_vocab)  // bench_engine.cpp:290-293
         return invalid("spec_greedy: draft and target vocabularies differ");
@@ -304,6 +321,7 @@ int DecodeSession::begin_sampled(Model& tgt, Model& dft, const int32_t* prompt, 
 
 int DecodeSession::spec_engine(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                                const SamplerConfig& sc, int32_t* out, SpecStats* st) {
+    if (init_rc_ != ORC_OK) return unusable();
     if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return invalid("spec_engine: bad k, prompt or length");
     if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return invalid("spec_engine: draft and target vocabularies differ");
     // engine.cpp:155-160 lets a draft of a longer context propose tokens the
@@ -415,6 +433,7 @@ int DecodeSession::sampled_round(Model& tgt, Model& dft, int k, int V) {
 
 int DecodeSession::spec_sampled(Model& tgt, Model& dft, const int32_t* prompt, int n_prompt, int n_gen, int k,
                                 const SamplerConfig& sc, int32_t* out, SpecStats* st) {
+    if (init_rc_ != ORC_OK) return unusable();
     if (k < 1 || k > max_k_ || n_prompt < 1 || n_gen < 1) return invalid("spec_sampled: bad k, prompt or length");
     if (dft.cfg.n_vocab != tgt.cfg.n_vocab) return invalid("spec_sampled: draft and target vocabularies differ");
     SpecStats local;

@@ -46,8 +46,11 @@ public:
         }
     }
     bool graphs() const { return graphs_; }
-    // Message of the last argument error a loop reported ("" if none).
+    // Message of the last error a loop reported ("" if none): a bad argument,
+    // or a session whose device set-up failed (every loop then returns that
+    // set-up's code).
     const char* error() const { return err_.c_str(); }
+    bool usable() const { return init_rc_ == ORC_OK; }
     void clear_error() { err_.clear(); }
 
     // Batched prefill of prompt[0 .. n_prompt-2] into the model's KV cache.
@@ -85,6 +88,13 @@ private:
     int max_tokens_, max_k_;
     bool graphs_ = true;
     std::string err_;
+    // set by the constructor when orc_init or a device allocation failed
+    int init_rc_ = ORC_OK;
+    std::string init_err_;
+    int unusable() {
+        err_ = init_err_;
+        return init_rc_;
+    }
     int invalid(const std::string& m) {
         err_ = m;
         return ORC_E_INVALID;

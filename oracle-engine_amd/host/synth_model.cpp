@@ -105,6 +105,11 @@ bool synth_preset(const std::string& name, SynthSpec& s) {
         s.t_default = T::Q4_K; s.t_attn_v = T::Q6_K; s.t_ffn_down = T::Q6_K;
         s.t_embd = T::Q4_K; s.t_output = T::Q6_K; return true;
     }
+    if (name == "t-dense") {  // dense weights: F16 embedding, BF16 head, an all-F32 layer, a raw-F32 norm
+        s = tiny(name); s.tied = false; s.seed = 11;
+        s.t_embd = T::F16; s.t_output = T::BF16; s.f32_layer = 0; s.raw_norm_layer = 1;
+        return true;
+    }
     if (name == "t-qwen-d") {  // independent 1-layer Q8_0 draft for t-qwen (stochastic spec tests)
         s = tiny(name); s.arch = "qwen2"; s.qkv_bias = true; s.tied = true; s.rope_theta = 1000000.f;
         s.n_layers = 1; s.d_model = 256; s.n_heads = 4; s.n_kv_heads = 2; s.ffn = 512; s.seed = 9;
@@ -115,7 +120,7 @@ bool synth_preset(const std::string& name, SynthSpec& s) {
 
 std::vector<std::string> synth_preset_names() {
     return {"c1", "c2", "c3d", "c4", "c4d", "c5", "t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen",
-            "t-qwen-d"};
+            "t-qwen-d", "t-dense"};
 }
 
 // ── tokenizer stub ──────────────────────────────────────────────────────────
@@ -293,23 +298,36 @@ bool synth_write(const SynthSpec& s, const std::string& path, bool verbose) {
         });
     };
 
+    // norm weights 1 + N(0, 0.1^2) stored as F32 bytes under a declared F16
+    // type of 2n values (the same byte count)
+    auto raw_norm = [&](const std::string& name, int n) {
+        w.add_tensor(name, {(uint64_t)(2 * n)}, GGMLType::F16, [seed, name, n](int64_t, int64_t, uint8_t* dst) {
+            const uint64_t key = tensor_key(seed, name);
+            for (int i = 0; i < n; ++i) { float v = 1.f + normal_at(key, (uint64_t)i, 0.1f); std::memcpy(dst + 4 * i, &v, 4); }
+        });
+    };
+
     matrix("token_embd.weight", "token_embd.weight", D, s.vocab, s.t_embd);
     for (int l = 0; l < s.n_layers; ++l) {
         const std::string b = "blk." + std::to_string(l) + ".";
-        ones(b + "attn_norm.weight", D);
-        matrix(b + "attn_q.weight", b + "attn_q.weight", D, NQ, s.t_default);
-        matrix(b + "attn_k.weight", b + "attn_k.weight", D, NKV, s.t_default);
-        matrix(b + "attn_v.weight", b + "attn_v.weight", D, NKV, s.t_attn_v);
+        const bool f32 = l == s.f32_layer;
+        const GGMLType td = f32 ? GGMLType::F32 : s.t_default, tv = f32 ? GGMLType::F32 : s.t_attn_v,
+                       tdn = f32 ? GGMLType::F32 : s.t_ffn_down;
+        if (l == s.raw_norm_layer) raw_norm(b + "attn_norm.weight", D);
+        else ones(b + "attn_norm.weight", D);
+        matrix(b + "attn_q.weight", b + "attn_q.weight", D, NQ, td);
+        matrix(b + "attn_k.weight", b + "attn_k.weight", D, NKV, td);
+        matrix(b + "attn_v.weight", b + "attn_v.weight", D, NKV, tv);
         if (s.qkv_bias) {
             bias(b + "attn_q.bias", NQ);
             bias(b + "attn_k.bias", NKV);
             bias(b + "attn_v.bias", NKV);
         }
-        matrix(b + "attn_output.weight", b + "attn_output.weight", NQ, D, s.t_default);
+        matrix(b + "attn_output.weight", b + "attn_output.weight", NQ, D, td);
         ones(b + "ffn_norm.weight", D);
-        matrix(b + "ffn_gate.weight", b + "ffn_gate.weight", D, FF, s.t_default);
-        matrix(b + "ffn_up.weight", b + "ffn_up.weight", D, FF, s.t_default);
-        matrix(b + "ffn_down.weight", b + "ffn_down.weight", FF, D, s.t_ffn_down);
+        matrix(b + "ffn_gate.weight", b + "ffn_gate.weight", D, FF, td);
+        matrix(b + "ffn_up.weight", b + "ffn_up.weight", D, FF, td);
+        matrix(b + "ffn_down.weight", b + "ffn_down.weight", FF, D, tdn);
     }
     ones("output_norm.weight", D);
     if (!s.tied)

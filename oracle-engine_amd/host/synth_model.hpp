@@ -28,6 +28,11 @@ struct SynthSpec {
     GGMLType t_embd = GGMLType::Q8_0;
     GGMLType t_output = GGMLType::Q8_0;    // only when !tied
     uint64_t seed = 1;
+    // Layer whose seven matrices are all F32 (-1: none), and layer whose
+    // attn_norm is declared F16 with twice the values while its bytes are
+    // the F32 norm weights (1 + N(0, 0.1^2)), which the reference reads as
+    // raw F32 whatever the declared type (core/model.cpp:317-320); -1: none.
+    int f32_layer = -1, raw_norm_layer = -1;
     // When true, output.weight holds the same float weights as token_embd
     // (a draft that owns a re-quantized copy of its target's tied head).
     bool head_from_embd = false;

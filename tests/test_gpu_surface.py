@@ -62,6 +62,36 @@ def test_ops_match_reference(hops):
     assert np.allclose(k, FIX["op/rope_k"], rtol=1e-6, atol=1e-6)
 
 
+def test_ops_any_size(hops):
+    # rmsnorm of a length that is not a multiple of 4 (the reference's scalar
+    # tail, core/ops.cpp:149-195) and rope with an odd head_dim (pairs
+    # (i, i + hd/2), the last value untouched, core/ops.cpp:440-485),
+    # against float64 closed forms
+    print("[gpu] ops at odd sizes", flush=True)
+    rng = np.random.default_rng(12)
+    for n in (1, 3, 5, 3071):
+        x = rng.normal(0, 1, n).astype(np.float32)
+        g = rng.normal(1, 0.1, n).astype(np.float32)
+        xd = x.astype(np.float64)
+        want = xd / np.sqrt((xd * xd).mean() + 1e-5) * g
+        got = hops.rmsnorm(x, g, 1e-5)
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * np.abs(want).max()), (n, np.abs(got - want).max())
+    hd, nh, nk, pos, base = 7, 3, 2, 5, 10000.0
+    q = rng.normal(0, 1, nh * hd).astype(np.float32)
+    k = rng.normal(0, 1, nk * hd).astype(np.float32)
+    gq, gk = hops.rope(q, k, nh, nk, hd, pos, base)
+    half = hd // 2
+    i = np.arange(half)
+    th = pos / np.power(base, 2.0 * i / hd)
+    for got, src, nheads in ((gq, q, nh), (gk, k, nk)):
+        want = src.astype(np.float64).reshape(nheads, hd).copy()
+        a, b = want[:, :half].copy(), want[:, half:2 * half].copy()
+        want[:, :half] = a * np.cos(th) - b * np.sin(th)
+        want[:, half:2 * half] = a * np.sin(th) + b * np.cos(th)
+        assert np.allclose(got.reshape(nheads, hd), want, rtol=1e-5, atol=1e-5)
+        assert np.array_equal(got.reshape(nheads, hd)[:, -1], src.reshape(nheads, hd)[:, -1])
+
+
 def test_ops_closed_forms(hops):
     print("[gpu] ops closed forms", flush=True)
     rng = np.random.default_rng(11)
@@ -125,6 +155,34 @@ def test_sampler_class_matches_reference():
     # set_params: T = 0 makes the next draw the argmax
     a.set_params(0.0, float(P), int(K), 1.0, int(last))
     assert a.sample(lg.copy()) == int(np.argmax(lg))
+
+
+def test_sampler_repeat_window_limits(oracle):
+    """A repeat window of up to 4095 ids penalises exactly as the reference's
+    Sampler (core/sampler.cpp:15-27, 99-105; the CPU oracle restates it) over a
+    history longer than the device buffer; a larger window is refused when the
+    Sampler is built (the C API returns no handle), not later as -1 ids."""
+    import orc
+
+    with pytest.raises(orc.OrcError):
+        orc.Sampler(0.8, 0.95, 40, 1.1, 4096, 3)
+    rng = np.random.default_rng(21)
+    V = 512
+    for last in (3000, 4095):
+        print(f"[gpu] Sampler repeat_last={last}", flush=True)
+        s = orc.Sampler(0.0, 1.0, 40, 1.5, last, 3)  # T = 0: argmax after the penalty
+        o = oracle.L.orco_sampler_new(0.0, 1.0, 40, 1.5, last, 3)
+        hist = rng.integers(0, 40, 9000).astype(np.int32)  # more than the 4096 the device holds
+        for h in hist:
+            s.record(int(h))
+            oracle.L.orco_sampler_record(o, int(h))
+        for trial in range(6):
+            lg = rng.normal(0, 1, V).astype(np.float32)
+            lg[:40] += 3.0  # penalised ids compete for the argmax
+            lo = lg.copy()
+            want = oracle.L.orco_sampler_sample(o, lo.ctypes.data_as(orc._fp), V)
+            assert s.sample(lg.copy()) == want, (last, trial)
+        oracle.L.orco_sampler_free(o)
 
 
 @pytest.mark.parametrize("m", ["t-q8", "t-q4k"])

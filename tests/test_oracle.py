@@ -26,6 +26,9 @@ def test_models_regenerate_identically(models_dir):
     for m in ("t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen", "t-qwen-d"):
         h = hashlib.sha256(open(models_dir / f"{m}.gguf", "rb").read()).hexdigest()
         assert h == bytes(FIX[f"sha/{m}"]).decode(), m
+    dense = np.load(os.path.join(GOLDEN, "dense_ref.npz"))
+    h = hashlib.sha256(open(models_dir / "t-dense.gguf", "rb").read()).hexdigest()
+    assert h == bytes(dense["sha/t-dense"]).decode()
 
 
 # ── codecs ───────────────────────────────────────────────────────────────────
