@@ -283,14 +283,26 @@ def main():
     # exactness: spec greedy must reproduce the target's greedy stream; the
     # Engine loop samples, so its stream must reproduce itself (fixed seed)
     greedy = None if engine else tgt.greedy(prompt, n_gen, prefill=True)
-    prefill_tok_s = None
-    if not engine:  # the batched prefill of the prompt (all ids but the last), target alone
+    prefill_tok_s, prefill_split = None, None
+    if not engine:  # the batched prefill of the prompt (all ids but the last): target, then draft
         H0 = orc.load_host_lib()
         H0.orch_sync()
         tp = time.perf_counter()
         tgt.forward_batch(prompt[:-1], 0, logits=False)
         H0.orch_sync()
-        prefill_tok_s = (n_prompt - 1) / (time.perf_counter() - tp)
+        t_tgt = time.perf_counter() - tp
+        prefill_tok_s = (n_prompt - 1) / t_tgt
+        prefill_split = {"target_ms": round(1e3 * t_tgt, 2)}
+        if dft is not None:
+            tp = time.perf_counter()
+            dft.forward_batch(prompt[:-1], 0, logits=False)
+            H0.orch_sync()
+            t_dft = time.perf_counter() - tp
+            prefill_split["draft_ms"] = round(1e3 * t_dft, 2)
+            prefill_split["draft_tok_s"] = round((n_prompt - 1) / t_dft, 1)
+        # time to first token: the prompt prefills of both models (the first
+        # round then emits the first generated token)
+        prefill_split["both_models_ms"] = round(sum(v for k2, v in prefill_split.items() if k2.endswith("_ms")), 2)
     toks, st = run(n_gen, True)  # prefills both models
     expect = toks if engine else greedy
     exact = bool(np.array_equal(toks, expect))
@@ -416,6 +428,7 @@ def main():
                     "(median reported beside the mean-based value), FNV-1a 64 of the generated ids",
         "target_greedy_tok_s": None if greedy_tok_s is None else round(greedy_tok_s, 2),
         "prefill_tok_s": None if prefill_tok_s is None else round(prefill_tok_s, 1),
+        "prefill": prefill_split,
         "reference_stream_identical": ref_identical,
         "roofline": roofline, "cpu_baseline": cpu,
         "gemv_microbench": micro,

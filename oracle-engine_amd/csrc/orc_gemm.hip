@@ -978,7 +978,9 @@ static int gemm_dispatch(QmvParams p, int type, hipStream_t s) {
     if (decode && type == kMixK) return dispatch_mixed_decode(p, s);
     p.units = p.n_in / elems_per_unit(type);
     const bool mm = mmq_type(type) && !decode;
-    if (mm && mmq_prefill(type, p)) {  // a prefill pass: every token in one launch
+    // a prefill pass (K-quant and Q8_0 calls of kPfMinTok tokens or more):
+    // every token in one launch on the matrix cores
+    if (!decode && (mm || type == ORC_Q8_0 || type == ORC_Q8_0_X8) && mmq_prefill(type, p)) {
         LaunchEvents ev;
         if (g_prof_on) prof_arm(s, type, p.n_tok, gemm_bytes(p, p.n_tok), &ev.start, &ev.stop);
         return mmq_prefill_launch(type, p, s, ev);

@@ -9,6 +9,7 @@
 #include "orc_mmq_core.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace orc {
 
@@ -32,6 +33,11 @@ namespace orc {
 // bit (calls below kPfMinTok tokens, which every verify pass is, keep k_mmq;
 // the reference's own prefill and decode round differently as well).
 constexpr int kPfTT = 4, kPfBM = 16 * kPfTT, kPfW = 8, kPfWG = 64 * kPfW;
+// Internal epilogue of the second of a two-pass SwiGLU (Q8_0 prefill: one
+// row tile per wave keeps the kernel inside its registers): the first pass
+// stored g = gate rows, this one the up rows u: y = silu(y) * u, the fused
+// epilogue's arithmetic.
+constexpr int kEpiSwigluUp = 16;
 constexpr int kPfABuf = 4 * 4 * 2 * kPfBM * 16;  // A bytes per unit: [slice][lane group][hi, lo][token] x 8 halves
 constexpr size_t kPfLds = 2 * kPfABuf + (2 * kPfBM + 2 * kPfBM * 4 + kPfBM) * sizeof(float);
 
@@ -76,10 +82,50 @@ __device__ __forceinline__ void q6k_slice_b(const MUnit& M, int i, int c, h8v& b
     blo = __builtin_bit_cast(h8v, bl);
 }
 
+// Q8_0 unit of 128 values (four 32-value blocks, core/gguf_parser.cpp:
+// 1073-1082) for lane group c: codes 8c .. 8c + 7 of each block and the
+// blocks' four fp16 scales, from the GGUF blocks or the regrouped
+// ORC_Q8_0_X8 groups (the unit is half of a group: scales 4 (u & 1) ..,
+// then their code runs).
+struct Q8Unit {
+    u32x2 q[4];
+    u32x2 s;
+    __device__ __forceinline__ void load(int type, const uint8_t* row, int u, int cg) {
+        if (type == ORC_Q8_0_X8) {
+            const uint8_t* grp = row + (size_t)(u >> 1) * 272;
+            const int b0 = 4 * (u & 1);
+            s = ldg8(grp + 2 * b0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = ldg8(grp + 16 + 32 * (b0 + i) + 8 * cg);
+        } else {
+            const uint8_t* blk = row + (size_t)(4 * u) * 34;
+            s = u32x2{ldg2(blk) | (ldg2(blk + 34) << 16), ldg2(blk + 68) | (ldg2(blk + 102) << 16)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = ldg8(blk + 34 * i + 2 + 8 * cg);
+        }
+    }
+};
+
+// B operand of block i of a Q8_0 unit: its 8 int8 codes, exact in fp16, in
+// the A entries' element order (perm8): code bytes move up by 128 and into
+// the low byte of fp16 1024 + b, then 1152 comes off
+__device__ __forceinline__ h8v q8_slice_b(const Q8Unit& M, int i) {
+    const uint32_t a = M.q[i].x ^ 0x80808080u, b = M.q[i].y ^ 0x80808080u;
+    const uint32_t m = sreg(0x00FF00FFu), mg = vreg(0x64006400u);
+    const uint32_t r[4] = {(a & m) | mg, ((a >> 8) & m) | mg, (b & m) | mg, ((b >> 8) & m) | mg};
+    const h2v off{(_Float16)-1152.f, (_Float16)-1152.f};
+    u32x4 bq;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bq[k] = as_u32(as_h2(r[k]) + off);
+    return __builtin_bit_cast(h8v, bq);
+}
+
 // RT row tiles per wave: 1, or 2 for SwiGLU (a gate tile and its up tile)
 template <int QT, int RT>
 __global__ __launch_bounds__(kPfWG) void k_mmq_pf(QmvParams p) {
-    static_assert(QT == ORC_Q4_K || QT == ORC_Q6_K, "one K-quant type per launch");
+    static_assert(QT == ORC_Q4_K || QT == ORC_Q6_K || QT == ORC_Q8_0 || QT == ORC_Q8_0_X8, "one type per launch");
+    constexpr bool Q8 = QT == ORC_Q8_0 || QT == ORC_Q8_0_X8;
+    using UnitT = std::conditional_t<Q8, Q8Unit, MUnit>;
     extern __shared__ __attribute__((aligned(16))) uint8_t msm[];
     float* esc = (float*)(msm + 2 * kPfABuf);  // [2][token] 2^-e of the unit
     float* sxs = esc + 2 * kPfBM;               // [2][token][sub-block] sums of x g (Q4_K)
@@ -165,7 +211,7 @@ __global__ __launch_bounds__(kPfWG) void k_mmq_pf(QmvParams p) {
         }
     };
 
-    MUnit cur[RT], nxt[RT];
+    UnitT cur[RT], nxt[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) cur[rt].load(QT, rp[rt], 0, c);
     st_load(0);
@@ -190,6 +236,38 @@ __global__ __launch_bounds__(kPfWG) void k_mmq_pf(QmvParams p) {
         for (int tt = 0; tt < kPfTT; ++tt)
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) D[tt][rt] = f4v{0.f, 0.f, 0.f, 0.f};
+        if constexpr (Q8) {
+            // a block per slice, each with its own scale: its two products
+            // (hi and lo activations) are scaled into acc before the next;
+            // one token tile at a time keeps few operands live
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                h8v bq[RT];
+                float dq[RT];
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    bq[rt] = q8_slice_b(cur[rt], i);
+                    const uint32_t sw = (i >> 1) ? cur[rt].s.y : cur[rt].s.x;
+                    dq[rt] = h2f((sw >> (16 * (i & 1))) & 0xFFFFu);
+                }
+#pragma unroll
+                for (int tt = 0; tt < kPfTT; ++tt) {
+                    const uint8_t* ap = ab + ((i * 4 + c) * 2 * kPfBM + tt * 16 + n) * 16;
+                    const h8v ah = *(const h8v*)ap, al = *(const h8v*)(ap + kPfBM * 16);
+                    const float4 es = *(const float4*)&esc[b * kPfBM + tt * 16 + 4 * c];
+                    const float esv[4] = {es.x, es.y, es.z, es.w};
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        f4v z = f4v{0.f, 0.f, 0.f, 0.f};
+                        z = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[rt], z, 0, 0, 0);
+                        z = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[rt], z, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[tt][rt][e] = __builtin_fmaf(dq[rt] * esv[e], z[e], acc[tt][rt][e]);
+                    }
+                }
+            }
+        } else {
         uint32_t sc4[RT], mn4[RT];
         if constexpr (QT == ORC_Q4_K) {
 #pragma unroll
@@ -254,6 +332,7 @@ __global__ __launch_bounds__(kPfWG) void k_mmq_pf(QmvParams p) {
                 }
             }
         }
+        }
         if (u + 1 < U) {
             st_store(u + 1, b ^ 1);  // the other buffer: its readers passed the last barrier
 #pragma unroll
@@ -295,8 +374,14 @@ __global__ __launch_bounds__(kPfWG) void k_mmq_pf(QmvParams p) {
                     const float* bb = pick3(sgi, sb0, sb1, sb2);
                     float v = acc[tt][rt][e] * inv;
                     if (bb) v += bb[jj];
-                    if (p.epi == ORC_EPI_ACCUM) *y += v;
-                    else *y = v;
+                    if (p.epi == ORC_EPI_ACCUM) {
+                        *y += v;
+                    } else if (p.epi == kEpiSwigluUp) {
+                        const float g = *y;
+                        *y = (g / (1.f + expf(-g))) * v;
+                    } else {
+                        *y = v;
+                    }
                 }
             }
         }
@@ -318,7 +403,8 @@ int mmq_max_tokens(int type, const QmvParams& p) {
 }
 
 bool mmq_prefill(int type, const QmvParams& p) {
-    return (type == ORC_Q4_K || type == ORC_Q6_K) && p.n_tok >= kPfMinTok && p.n_in % 128 == 0 &&
+    return (type == ORC_Q4_K || type == ORC_Q6_K || type == ORC_Q8_0 || type == ORC_Q8_0_X8) &&
+           p.n_tok >= kPfMinTok && p.n_in % (type == ORC_Q8_0_X8 ? 256 : 128) == 0 &&
            (p.epi != ORC_EPI_SWIGLU || p.n_seg == 2) && kPfLds <= g_lds_max;
 }
 
@@ -338,7 +424,26 @@ int mmq_prefill_launch(int type, const QmvParams& p, hipStream_t s, const Launch
     if (!mmq_prefill(type, p)) return set_error(ORC_E_INVALID, "gemm: not a prefill launch");
     const bool swiglu = p.epi == ORC_EPI_SWIGLU;
     if (type == ORC_Q4_K) return swiglu ? mmq_pf_shape<ORC_Q4_K, 2>(p, s, ev) : mmq_pf_shape<ORC_Q4_K, 1>(p, s, ev);
-    return swiglu ? mmq_pf_shape<ORC_Q6_K, 2>(p, s, ev) : mmq_pf_shape<ORC_Q6_K, 1>(p, s, ev);
+    if (type == ORC_Q6_K) return swiglu ? mmq_pf_shape<ORC_Q6_K, 2>(p, s, ev) : mmq_pf_shape<ORC_Q6_K, 1>(p, s, ev);
+    // Q8_0: one row tile per wave; SwiGLU in two passes over the output
+    // rows (gate stored, then the up rows' epilogue applies silu(g) * u)
+    auto q8 = [&](const QmvParams& q) {
+        return type == ORC_Q8_0 ? mmq_pf_shape<ORC_Q8_0, 1>(q, s, ev) : mmq_pf_shape<ORC_Q8_0_X8, 1>(q, s, ev);
+    };
+    if (!swiglu) return q8(p);
+    QmvParams g = p;
+    g.epi = ORC_EPI_STORE;
+    g.n_seg = 1;
+    g.n_rows = p.rows[0];
+    g.bias[0] = g.bias[1] = nullptr;
+    g.w[1] = nullptr;
+    g.y[1] = nullptr;
+    g.rows[1] = 0;
+    if (int rc = q8(g)) return rc;
+    QmvParams u = g;
+    u.w[0] = p.w[1];
+    u.epi = kEpiSwigluUp;
+    return q8(u);
 }
 
 int mmq_launch(int type, const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {

@@ -1156,8 +1156,12 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
     __shared__ __align__(16) float Ow[kWW][RM][HD];
     __shared__ float mw[kWW][RM], lw[kWW][RM];
     // workgroup = (kv head g, heads r0 .. r0 + RH - 1 of its group, token t)
-    const int R = n_heads / n_kv, nbh = (R + RM - 1) / RM;
-    const int g = blockIdx.x / nbh, r0 = (blockIdx.x - g * nbh) * RM, RH = min(RM, R - r0);
+    const int R = n_heads / n_kv;
+    // kv head g = blockIdx.x % n_kv: consecutive workgroup ids go to the 8
+    // XCDs in turn, so with 8 kv heads (and a grid width a multiple of 8)
+    // every workgroup reading kv head g's K / V runs on one XCD and shares
+    // its L2 instead of fetching the rows into several
+    const int g = blockIdx.x % n_kv, r0 = (blockIdx.x / n_kv) * RM, RH = min(RM, R - r0);
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int start = start_position(d_pos, pos_off);

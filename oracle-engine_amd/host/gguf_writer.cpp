@@ -213,12 +213,21 @@ bool GGUFWriter::write(const std::string& path, bool verbose) {
     if (!f) return false;
     std::vector<char> buf(1 << 22);
     std::setvbuf(f, buf.data(), _IOFBF, buf.size());
+    const uint64_t al = alignment ? alignment : 32;
+    std::vector<KV> all = kvs;
+    if (al != 32) {
+        KV kv;
+        kv.key = "general.alignment";
+        kv.kind = 4;
+        kv.u = al;
+        all.push_back(kv);
+    }
     Out o{f};
     o.raw("GGUF", 4);
     o.u32(3);
     o.u64(tensors.size());
-    o.u64(kvs.size());
-    for (const KV& kv : kvs) {
+    o.u64(all.size());
+    for (const KV& kv : all) {
         o.str(kv.key);
         o.u32(kv.kind);
         switch (kv.kind) {
@@ -241,7 +250,7 @@ bool GGUFWriter::write(const std::string& path, bool verbose) {
     uint64_t off = 0;
     for (Tensor& t : tensors) {
         t.offset = off;
-        off = (off + t.nbytes + 31) / 32 * 32;
+        off = (off + t.nbytes + al - 1) / al * al;
     }
     for (const Tensor& t : tensors) {
         o.str(t.name);
@@ -250,7 +259,7 @@ bool GGUFWriter::write(const std::string& path, bool verbose) {
         o.u32((uint32_t)t.type);
         o.u64(t.offset);
     }
-    o.pad_to(32);
+    o.pad_to(al);
     const uint64_t data_start = o.pos;
     std::vector<uint8_t> chunk;
     for (const Tensor& t : tensors) {

@@ -5,7 +5,7 @@
 // The layout written here is exactly what the reader expects
 // (core/gguf_parser.cpp:164-324): header, KV metadata, tensor table, data
 // section aligned to 32 bytes from the file start, each tensor aligned to 32
-// inside the data section.
+// inside the data section (or to `alignment`, declared as general.alignment).
 #pragma once
 #include "gguf_types.hpp"
 #include <cstdint>
@@ -47,6 +47,10 @@ struct GGUFWriter {
     };
     std::vector<KV> kvs;
     std::vector<Tensor> tensors;
+    // Data-section and tensor alignment (a power of two). Other than 32 it is
+    // declared as general.alignment, as the GGUF format defines; the
+    // reference's reader supports 32 only (core/gguf_parser.cpp:30, 196).
+    uint64_t alignment = 32;
 
     void add_str(const std::string& k, const std::string& v);
     void add_u32(const std::string& k, uint32_t v);

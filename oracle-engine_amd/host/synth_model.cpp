@@ -105,6 +105,9 @@ bool synth_preset(const std::string& name, SynthSpec& s) {
         s.t_default = T::Q4_K; s.t_attn_v = T::Q6_K; s.t_ffn_down = T::Q6_K;
         s.t_embd = T::Q4_K; s.t_output = T::Q6_K; return true;
     }
+    if (name == "t-q8-a64") {  // t-q8's tensors in a file that declares general.alignment = 64
+        s = tiny("t-q8"); s.alignment = 64; return true;
+    }
     if (name == "t-dense") {  // dense weights: F16 embedding, BF16 head, an all-F32 layer, a raw-F32 norm
         s = tiny(name); s.tied = false; s.seed = 11;
         s.t_embd = T::F16; s.t_output = T::BF16; s.f32_layer = 0; s.raw_norm_layer = 1;
@@ -120,7 +123,7 @@ bool synth_preset(const std::string& name, SynthSpec& s) {
 
 std::vector<std::string> synth_preset_names() {
     return {"c1", "c2", "c3d", "c4", "c4d", "c5", "t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen",
-            "t-qwen-d", "t-dense"};
+            "t-qwen-d", "t-dense", "t-q8-a64"};
 }
 
 // ── tokenizer stub ──────────────────────────────────────────────────────────
@@ -245,6 +248,7 @@ VocabStub make_vocab_stub(const SynthSpec& s) {
 
 bool synth_write(const SynthSpec& s, const std::string& path, bool verbose) {
     GGUFWriter w;
+    w.alignment = s.alignment;
     const std::string a = s.arch;
     w.add_str("general.architecture", a);
     w.add_str("general.name", "orc-synthetic-" + s.name);

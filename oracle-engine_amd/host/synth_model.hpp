@@ -33,6 +33,8 @@ struct SynthSpec {
     // the F32 norm weights (1 + N(0, 0.1^2)), which the reference reads as
     // raw F32 whatever the declared type (core/model.cpp:317-320); -1: none.
     int f32_layer = -1, raw_norm_layer = -1;
+    // general.alignment of the file (32: not declared, the reference's only value)
+    uint32_t alignment = 32;
     // When true, output.weight holds the same float weights as token_embd
     // (a draft that owns a re-quantized copy of its target's tied head).
     bool head_from_embd = false;

@@ -13,6 +13,7 @@ ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "liborc_oracle.so")
 REF_DRIVER = os.path.join(ROOT, "oracle", "_ref", "ref_driver")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
+Q8_0_X8 = 258  # the device's regrouped Q8_0 layout (orc_q8_0_regroup); the oracle reads the GGUF blocks
 BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 _fp = C.POINTER(C.c_float)

@@ -19,7 +19,7 @@ import pytest
 from conftest import SYNTH
 
 pytestmark = pytest.mark.gpu
-N_PROMPT, N_GEN, K, CTX, VOCAB = 8192, 64, 8, 16384, 152064
+N_PROMPT, N_GEN, K, CTX, VOCAB = 8192, 512, 8, 16384, 152064  # the config's 512 generated tokens
 
 
 @pytest.fixture(scope="module")

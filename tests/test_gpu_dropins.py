@@ -188,3 +188,23 @@ def test_all_tokens_top_k_refuses_large_vocabulary(dev):
     dev.check(dev.L.orc_sample(st.ptr, lg.ptr, V, out.ptr, None))
     assert int(out.read(np.int32, 1)[0]) == int(np.argmax(x))
     assert 0 <= int(out.read(np.int32, 1)[0]) < V
+
+
+def test_alignment_64_file_decodes_as_its_32_byte_twin(models_dir):
+    """t-q8-a64 declares general.alignment = 64 (the t-q8 tensors): the
+    device path reads it at the declared alignment, so greedy tokens and the
+    decode logits equal t-q8's bit for bit."""
+    import orc
+
+    print("[gpu] general.alignment = 64", flush=True)
+    prompt = np.array([5, 17, 99, 3, 1000, 42], np.int32)
+    outs = []
+    for name in ("t-q8", "t-q8-a64"):
+        m = orc.Model(models_dir / f"{name}.gguf")
+        toks = m.greedy(prompt, 12)
+        m.reset()
+        m.forward_batch(prompt[:-1], 0, logits=False)
+        outs.append((toks, m.forward(int(prompt[-1]), len(prompt) - 1)))
+        m.close()
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1].view(np.uint32), outs[1][1].view(np.uint32))

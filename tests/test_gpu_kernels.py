@@ -122,22 +122,29 @@ def test_gemm_batch_invariant(dev, oracle, qt, n_out, n_in):
 
 @pytest.mark.parametrize("qt,n_out,n_in,nt", [(ol.Q4_K, 300, 3072, 300), (ol.Q6_K, 130, 2048, 256),
                                               (ol.Q6_K, 200, 18944, 263), (ol.Q4_K, 64, 512, 640),
-                                              (ol.Q4_K, 8192, 3072, 256)])
+                                              (ol.Q4_K, 8192, 3072, 256), (ol.Q8_0, 300, 3072, 300),
+                                              (ol.Q8_0, 200, 896, 263), (ol.Q8_0, 70, 4864, 256),
+                                              (ol.Q8_0_X8, 257, 3072, 256)])
 def test_gemm_prefill_vs_exact_and_blocks(dev, oracle, qt, n_out, n_in, nt):
-    """Calls of 256 tokens or more on a K-quant matrix run the prefill kernel
-    (64 tokens per workgroup, each weight slice decoded once for all of them):
-    every (token, row) within 2e-6 of sum |w x| of the float64 product and
-    within 4e-6 of the same tokens in 16-token calls (the verify kernel), with
-    partial token and row blocks; a token's row does not depend on the call's
-    other tokens (bit for bit)."""
+    """Calls of 256 tokens or more on a K-quant or Q8_0 matrix run the
+    prefill kernel (64 tokens per workgroup, each weight slice decoded once
+    for all of them; Q8_0 from the GGUF blocks or the regrouped Q8_0_X8
+    layout, each block's scale applied to its own products): every (token,
+    row) within 2e-6 of sum |w x| of the float64 product and within 4e-6 of
+    the same tokens in 16-token calls (the verify path), with partial token
+    and row blocks; a token's row does not depend on the call's other tokens
+    (bit for bit)."""
     print(f"[gpu] prefill gemm type={qt} {n_out}x{n_in} nt={nt}", flush=True)
     rng = np.random.default_rng(n_out + nt)
-    raw = rand_blocks(qt, n_out * n_in, rng)
+    x8 = qt == ol.Q8_0_X8
+    raw = rand_blocks(ol.Q8_0 if x8 else qt, n_out * n_in, rng)
     wd = dev.upload(raw)
+    if x8:  # the Q8_0 blocks regrouped in place; the oracle reads the GGUF blocks
+        dev.check(dev.L.orc_q8_0_regroup(wd.ptr, n_out * n_in // 256, None))
     X = rng.normal(0, 1, (nt, n_in)).astype(np.float32)
     full = _gemm(dev, qt, wd, nt, n_out, n_in, X)
     blocks = np.concatenate([_gemm(dev, qt, wd, min(16, nt - t), n_out, n_in, X[t:t + 16]) for t in range(0, nt, 16)])
-    W = oracle.dequant(qt, raw, n_out * n_in).reshape(n_out, n_in).astype(np.float64)
+    W = oracle.dequant(ol.Q8_0 if x8 else qt, raw, n_out * n_in).reshape(n_out, n_in).astype(np.float64)
     exact = X.astype(np.float64) @ W.T
     scale = np.abs(X.astype(np.float64)) @ np.abs(W).T
     assert np.all(np.abs(full - exact) <= 2e-6 * scale + 1e-30), np.max(np.abs(full - exact) / scale)
@@ -182,7 +189,7 @@ def test_gemm_prefill_epilogues(dev):
 
     a, b = both(qkv, ld)
     assert np.allclose(a, b, rtol=0, atol=2e-5 * np.abs(b).max())
-    for st in (ol.Q6_K, ol.Q4_K):
+    for st in (ol.Q6_K, ol.Q4_K, ol.Q8_0):  # Q8_0: SwiGLU in two passes (gate rows, then up)
         wg, wu = (dev.upload(rand_blocks(st, ff * n_in, rng)) for _ in range(2))
 
         def swiglu(t0, n, dy):

@@ -31,6 +31,28 @@ def test_models_regenerate_identically(models_dir):
     assert h == bytes(dense["sha/t-dense"]).decode()
 
 
+def test_alignment_64_file_holds_the_same_tensors(models_dir):
+    """A file declaring general.alignment = 64 (t-q8-a64, the t-q8 tensors):
+    the data section and every tensor start on 64-byte boundaries and each
+    tensor holds exactly t-q8's bytes. The build's parser honours the key, as
+    the GGUF format defines (host/gguf_parser.cpp); the reference ignores it
+    and takes 32 (core/gguf_parser.cpp:30, 196), which for this file starts
+    the data section elsewhere."""
+    import gguf_read
+
+    a64, a32 = models_dir / "t-q8-a64.gguf", models_dir / "t-q8.gguf"
+    t64, t32 = gguf_read.tensors(a64), gguf_read.tensors(a32)
+    assert sorted(t64) == sorted(t32)
+    b64, b32 = open(a64, "rb").read(), open(a32, "rb").read()
+    for name, (ty, shape, off) in t64.items():
+        ty32, shape32, off32 = t32[name]
+        assert (ty, shape) == (ty32, shape32) and off % 64 == 0, name
+        nb = ol.row_bytes(ty, shape[0]) * int(np.prod(shape[1:]))
+        assert b64[off:off + nb] == b32[off32:off32 + nb], name
+    as_ref = gguf_read.tensors(a64, honour_alignment=False)
+    assert any(as_ref[k][2] != t64[k][2] for k in t64)
+
+
 # ── codecs ───────────────────────────────────────────────────────────────────
 @pytest.mark.parametrize("name,qt", [("q4_0", ol.Q4_0), ("q4_k", ol.Q4_K), ("q6_k", ol.Q6_K)])
 def test_dequant_matches_reference_hooks(oracle, name, qt):
@@ -348,6 +370,55 @@ def test_transform_greedy_limit(oracle):
     assert p[np.argmax(lg)] == 1.0 and p.sum() == 1.0
     p = _probs(oracle, lg, 0.8, 1.0, 1)
     assert p[np.argmax(lg)] == 1.0
+
+
+def test_transform_probs_pinned_by_reference_draws(oracle):
+    """orco_transform_probs (the p and q of the min(1, p/q) loop) against the
+    reference Sampler's own draws (tests/golden/transform_ref.npz, written by
+    make_golden_transform.py): for top_p < 1, top_k in {0, 40} and repeat
+    penalties, each reference draw must be the id whose interval of the
+    transform's cumulative probability, in the reference's candidate order
+    (probability descending, core/sampler.cpp:58-86), holds that draw's
+    uniform (mt19937 + generate_canonical, the oracle's engine on the same
+    seed). The history window is the reference's: every draw is recorded
+    (sampler.cpp:95). A wrong kept set, a wrong cut or wrong probabilities put
+    some of the 400 draws per case outside their interval."""
+    ref = np.load(os.path.join(GOLDEN, "transform_ref.npz"))
+    lg, hist = ref["logits"], ref["history"]
+    n_case = len([k for k in ref.files if k.endswith("/draws")])
+    checked = 0
+    for i in range(n_case):
+        T, P, K, pen, last = ref[f"case/{i}/params"]
+        seed = int(ref[f"case/{i}/seed"][0])
+        K, last = int(K), int(last)
+        s = oracle.L.orco_sampler_new(float(T), float(P), K, float(pen), last, seed)
+        for h in hist:
+            oracle.L.orco_sampler_record(s, int(h))
+        kept_sizes = set()
+        for d, want in enumerate(ref[f"case/{i}/draws"]):
+            hb = np.zeros(8192, np.int32)
+            n = oracle.L.orco_sampler_history(s, ol.iptr(hb), hb.size)
+            win = hb[:n][max(0, n - last):] if last > 0 else hb[:0]
+            p = _probs(oracle, lg, float(T), float(P), K, float(pen), win)
+            u = np.float32(np.float32(oracle.L.orco_mt_next(s)) / np.float32(4294967296.0))
+            u = float(min(u, np.nextafter(np.float32(1), np.float32(0))))
+            kept = np.nonzero(p)[0]
+            kept_sizes.add(kept.size)
+            order = kept[np.lexsort((kept, -p[kept].astype(np.float64)))]
+            cum = np.cumsum(p[order].astype(np.float64))
+            j = int(np.searchsorted(cum, u, side="left"))
+            j = min(j, order.size - 1)
+            got = int(order[j])
+            if got != int(want):  # only a draw within float rounding of an interval end may differ
+                jw = int(np.nonzero(order == int(want))[0][0]) if int(want) in order else -1
+                assert jw >= 0, (i, d, "reference id outside the transform's kept set")
+                edge = cum[min(j, jw)]
+                assert abs(edge - u) < 2e-6, (i, d, got, int(want), u, edge)
+            oracle.L.orco_sampler_record(s, int(want))
+            checked += 1
+        oracle.L.orco_sampler_free(s)
+        assert max(kept_sizes) > 1, i  # the cut leaves a real choice in every case
+    assert checked == n_case * 400
 
 
 @pytest.mark.parametrize("k", [2, 4])
