@@ -42,10 +42,11 @@ blocks and regrouped into the aligned Q8_0_X8 layout) back to back over
 more than 640 MB of distinct weight matrices in rotation (beyond the 256 MB
 Infinity Cache), per type, timed by the same dispatch events.
 
---workload c1 / c4 / c5 run BASELINE.json configs[0] / configs[3] /
-configs[4] instead (the bench line stays quoted on C3): C1 = greedy decode of
-128 tokens after a 32-id prompt on the 1B-shape Q8_0 model (its own metric,
-cpu_baseline over the whole workload); C4 = the Engine's stochastic speculative
+--workload c1 / c2 / c4 / c5 run BASELINE.json configs[0] / configs[1] /
+configs[3] / configs[4] instead (the bench line stays quoted on C3): C1 =
+greedy decode of 128 tokens after a 32-id prompt on the 1B-shape Q8_0 model
+(its own metric, cpu_baseline over the whole workload); C2 = greedy decode
+of C3's 256 tokens by C3's target alone (the one-token K-quant GEMVs); C4 = the Engine's stochastic speculative
 loop (each step a whole Engine call, prefill included, reported beside it);
 C5 = speculative greedy after an 8191-id prefill into a 16384-position cache,
 with the verify passes' GQA KV-read GB/s and weight-GEMM GB/s reported
@@ -140,6 +141,8 @@ def measured_traffic(kernel):
 WORKLOADS = {
     "c1": dict(tgt="c1", dft=None, n_prompt=32, n_gen=128, k=0, ctx=512, mode="greedy_only", prompt_seed=1234,
                desc="C1 greedy decode: 1B-shape all-Q8_0 model, tied head"),
+    "c2": dict(tgt="c2", dft=None, n_prompt=128, n_gen=256, k=0, ctx=2048, mode="greedy_only", prompt_seed=1234,
+               desc="C2 greedy decode: the C3 target (3B-shape Q4_K_M, configs[1]) alone"),
     "c3": dict(tgt="c2", dft="c3d", n_prompt=128, n_gen=256, k=4, ctx=2048, mode="greedy", prompt_seed=1234,
                desc="C3 spec greedy: 3B-shape Q4_K_M target + 8-layer Q8_0 draft"),
     "c4": dict(tgt="c4", dft="c4d", n_prompt=256, n_gen=512, k=6, ctx=4096, mode="engine", prompt_seed=4321,
@@ -221,7 +224,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3",
-                    help="c3 (the metric's config, default), c1, c4 or c5")
+                    help="c3 (the metric's config, default), c1, c2, c4, c4s or c5")
     ap.add_argument("--n-gen", type=int, default=0, help="generated tokens (default: the workload's)")
     ap.add_argument("--models-dir", default=os.environ.get("ORC_MODEL_DIR", "/tmp/orc_models"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -314,6 +317,10 @@ def main():
         fix = np.load(c1_fix)
         if np.array_equal(prompt, fix["prompt"]) and n_gen == len(fix["greedy_tokens"]):
             ref_identical = bool(np.array_equal(greedy, fix["greedy_tokens"]))
+    if a.workload == "c2" and os.path.exists(fix_path):  # C3's target: its greedy stream is in the C3 fixture
+        fix = np.load(fix_path)
+        if np.array_equal(prompt, fix["prompt"]) and n_gen == len(fix["greedy_tokens"]):
+            ref_identical = bool(np.array_equal(greedy, fix["greedy_tokens"]))
     if a.workload == "c3" and os.path.exists(fix_path):
         fix = np.load(fix_path)
         if (n_prompt, n_gen, k) == (len(fix["prompt"]), len(fix["spec_tokens"]), int(fix["k"][0])) and \
@@ -401,12 +408,12 @@ def main():
 
     micro = None if a.no_gemv_micro else gemv_microbench(dev)
     cpu = None
-    if not a.no_cpu_baseline and a.workload in ("c1", "c3"):
+    if not a.no_cpu_baseline and a.workload in ("c1", "c2", "c3"):
         # the whole workload: prompt, k and every generated token (C3 ~35 s, C1 ~1 s on 16 threads)
         cpu = cpu_baseline(tgt_path, dft_path, prompt, k, n_gen, a.workload.upper())
         if cpu:  # the same workload on both sides: the reference's stream checksum against this run's
             cpu["checksum_equal"] = cpu["checksum"] == checksum
-    metric = ("greedy decode tok/s (1B Q8_0)" if plain else
+    metric = ({"c1": "greedy decode tok/s (1B Q8_0)", "c2": "greedy decode tok/s (3B Q4_K_M)"}[a.workload] if plain else
               "spec-decode tok/s (3B Q4_K, k=4); quant-GEMV HBM GB/s vs peak")
     out = {
         "metric": metric,

@@ -208,6 +208,14 @@ int orc_rope_pos(float* d_q, float* d_k, int n_heads, int n_kv_heads, int head_d
 /* out[t] = rmsnorm(x[t]) for n_rows rows of n (ops::rmsnorm, ops.cpp:149-195);
  * any n >= 1 (pointers 16-byte aligned when n is a multiple of 4). */
 int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int n, int n_rows, float eps, orc_stream_t stream);
+/* QK-norm (Qwen3; core/model.cpp:390-399, 584-593): ops::rmsnorm over each
+ * head of head_dim values, in place, on the q heads (weights d_qw) and k heads
+ * (weights d_kw; head_dim floats each, shared by the heads) of n_tok QKV rows
+ * [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)] with row stride ldqkv, before
+ * RoPE; eps is the model's attention.layer_norm_rms_epsilon, as the reference
+ * passes cfg.rms_eps there. 1 <= head_dim <= 128. */
+int orc_qk_norm(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim, const float* d_qw,
+                const float* d_kw, float eps, orc_stream_t stream);
 /* RoPE (rotate-half pairs (i, i+hd/2), theta = pos / base^(2i/hd),
  * ops::rope ops.cpp:440-485) on the q and k columns of n_tok QKV rows laid out
  * [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)] with row stride ldqkv, then

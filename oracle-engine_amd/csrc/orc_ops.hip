@@ -56,6 +56,36 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* out, const float* x, con
     }
 }
 
+// ── Per-head RMSNorm of q and k (QK-norm) in place on QKV rows ───────────────
+// One wave per (head, token): rows [q heads | k heads] of each token's QKV row
+// [q (n_heads*hd) | k (n_kv*hd) | v], the q heads scaled by qw, the k heads by
+// kw (head_dim weights each, shared by the heads). Sum of squares as one FMA
+// chain per lane, then a fixed xor-butterfly; out = (x * s) * w, the order of
+// ops::rmsnorm's store.
+__global__ __launch_bounds__(256) void k_qk_norm(float* qkv, int ldqkv, int n_heads, int n_kv, int hd, const float* qw,
+                                                 const float* kw, float eps) {
+    const int lane = threadIdx.x & 63, h = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (h >= n_heads + n_kv) return;  // wave-uniform: the last workgroup's spare waves
+    float* row = qkv + (size_t)blockIdx.y * ldqkv + (size_t)h * hd;
+    const float* w = h < n_heads ? qw : kw;
+    float v[2];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = lane + 64 * j;
+        v[j] = i < hd ? row[i] : 0.f;
+        ss = __builtin_fmaf(v[j], v[j], ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float s = 1.f / sqrtf(ss / (float)hd + eps);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = lane + 64 * j;
+        if (i < hd) row[i] = (v[j] * s) * w[i];
+    }
+}
+
 // ── RoPE on q,k + KV store. One workgroup per token. ─────────────────────────
 // rope table: [pos][half] of (cos, sin); KV cache per layer: [n_kv][ctx][hd].
 // The first position is *d_pos + pos_off (d_pos may be null): with a device
@@ -1412,6 +1442,20 @@ extern "C" int orc_rmsnorm(float* d_out, const float* d_x, const float* d_w, int
         return set_error(ORC_E_INVALID, "rmsnorm: pointers must be 16-byte aligned when n is a multiple of 4");
     if (!n_rows) return ORC_OK;
     hipLaunchKernelGGL(k_rmsnorm, dim3(n_rows), dim3(256), 0, resolve_stream(s), d_out, d_x, d_w, n, eps);
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_qk_norm(float* d_qkv, int ldqkv, int n_tok, int n_heads, int n_kv, int head_dim, const float* d_qw,
+                           const float* d_kw, float eps, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (n_tok < 0 || n_heads <= 0 || n_kv <= 0 || head_dim <= 0 || head_dim > 128 ||
+        ldqkv < (n_heads + 2 * n_kv) * head_dim || !d_qkv || !d_qw || !d_kw)
+        return set_error(ORC_E_INVALID, "qk_norm: bad args (1 <= head_dim <= 128, ldqkv covers q | k | v)");
+    if (!n_tok) return ORC_OK;
+    if (n_tok > 65535) return set_error(ORC_E_INVALID, "qk_norm: at most 65535 tokens per call");
+    hipLaunchKernelGGL(k_qk_norm, dim3((n_heads + n_kv + 3) / 4, n_tok), dim3(256), 0, resolve_stream(s), d_qkv, ldqkv,
+                       n_heads, n_kv, head_dim, d_qw, d_kw, eps);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

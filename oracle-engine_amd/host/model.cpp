@@ -54,7 +54,6 @@ bool Model::load(const std::string& path, int ctx_len) {
         uint64_t a = sh.size() > 0 ? sh[0] : 0, b = sh.size() > 1 ? sh[1] : 0;
         cfg.n_vocab = (uint32_t)std::max(a, b);
     }
-    if (cfg.qk_norm) return fail("per-head QK-norm (Qwen3) is not supported by this build");
     if (cfg.n_kv_heads == 0 || cfg.n_heads % cfg.n_kv_heads) return fail("bad head counts");
     if (cfg.head_dim != 64 && cfg.head_dim != 128) return fail("head_dim must be 64 or 128");
 
@@ -115,6 +114,10 @@ bool Model::load(const std::string& path, int ctx_len) {
                 !(L.bv = vec(b + "attn_v.bias", NKV, true)))
                 return false;
         }
+        // QK-norm weights, head_dim raw floats each (core/model.cpp:129-137)
+        if (cfg.qk_norm && (!(L.q_norm = vec(b + "attn_q_norm.weight", (int)cfg.head_dim, true)) ||
+                            !(L.k_norm = vec(b + "attn_k_norm.weight", (int)cfg.head_dim, true))))
+            return false;
     }
 
     // Q8_0 matrices whose rows hold a multiple of 256 values are regrouped
@@ -254,6 +257,11 @@ int Model::chunk_dev(const int32_t* d_ids, int n, const int32_t* d_pos, int sp, 
         // pre-norm + Q|K|V (+bias) -> qkv rows [q | k | v]   (model.cpp:366-388)
         CK(gemm_segs({{&L.q, {d_qkv_, L.bq}}, {&L.k, {d_qkv_ + NQ, L.bk}}, {&L.v, {d_qkv_ + NQ + NKV, L.bv}}}, n,
                      d_x_, D, QKV, L.attn_norm, ORC_EPI_STORE, s));
+        // QK-norm (Qwen3): per-head RMSNorm of q and k, after the bias and
+        // before RoPE, with the model's epsilon (model.cpp:390-399, 584-593)
+        if (cfg.qk_norm)
+            CK(orc_qk_norm(d_qkv_, QKV, n, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, L.q_norm, L.k_norm, cfg.rms_eps,
+                           s));
         // RoPE + KV store (model.cpp:401-408), attention (model.cpp:410-435).
         // Prefill passes of kPrefillAttnMin tokens or more (host positions):
         // one launch over the pass (query blocks, online softmax; the
@@ -523,19 +531,23 @@ bool Model::load_state(const std::string& path, int& pos) {  // model.cpp:184-23
     return true;
 }
 
-bool Model::test_norm_cache_matches() {  // core/model.hpp:119-121
+bool Model::test_norm_cache_matches() {  // core/model.hpp:119-121, core/model.cpp:296-313
     if (!loaded_) return false;
-    const int D = cfg.embed_dim;
-    std::vector<float> dev((size_t)D);
-    auto same = [&](const std::string& name, const float* d) {
+    const int D = cfg.embed_dim, Hd = cfg.head_dim;
+    std::vector<float> dev((size_t)std::max(D, Hd));
+    auto same = [&](const std::string& name, const float* d, int n) {
         const uint8_t* raw = gguf_.tensor_raw(name);
-        return raw && d && orc_memcpy_d2h(dev.data(), d, (size_t)D * 4, nullptr) == 0 &&
-               std::memcmp(dev.data(), raw, (size_t)D * 4) == 0;
+        return raw && d && orc_memcpy_d2h(dev.data(), d, (size_t)n * 4, nullptr) == 0 &&
+               std::memcmp(dev.data(), raw, (size_t)n * 4) == 0;
     };
-    if (!same("output_norm.weight", out_norm_)) return false;
+    if (!same("output_norm.weight", out_norm_, D)) return false;
     for (uint32_t l = 0; l < cfg.n_layers; ++l) {
         const std::string b = "blk." + std::to_string(l) + ".";
-        if (!same(b + "attn_norm.weight", layers_[l].attn_norm) || !same(b + "ffn_norm.weight", layers_[l].ffn_norm))
+        if (!same(b + "attn_norm.weight", layers_[l].attn_norm, D) ||
+            !same(b + "ffn_norm.weight", layers_[l].ffn_norm, D))
+            return false;
+        if (cfg.qk_norm && (!same(b + "attn_q_norm.weight", layers_[l].q_norm, Hd) ||
+                            !same(b + "attn_k_norm.weight", layers_[l].k_norm, Hd)))
             return false;
     }
     return true;

@@ -135,6 +135,7 @@ private:
     struct Layer {
         Mat q, k, v, o, gate, up, down;
         const float *attn_norm = nullptr, *ffn_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+        const float *q_norm = nullptr, *k_norm = nullptr;  // QK-norm weights (head_dim each)
     };
     GGUFParser gguf_;
     bool loaded_ = false;

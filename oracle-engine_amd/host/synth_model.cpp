@@ -113,6 +113,12 @@ bool synth_preset(const std::string& name, SynthSpec& s) {
         s.t_embd = T::F16; s.t_output = T::BF16; s.f32_layer = 0; s.raw_norm_layer = 1;
         return true;
     }
+    if (name == "t-qwen3") {  // qwen3 arch: per-head QK-norm, head_dim 128 (q width 1024 > d_model 512), no bias
+        s = tiny(name); s.arch = "qwen3"; s.qk_norm = true; s.tied = false; s.rope_theta = 1000000.f;
+        s.head_dim = 128; s.n_heads = 8; s.n_kv_heads = 2; s.rms_eps = 1e-6f; s.seed = 13;
+        s.t_default = T::Q4_K; s.t_attn_v = T::Q6_K; s.t_ffn_down = T::Q6_K;
+        s.t_embd = T::Q4_K; s.t_output = T::Q6_K; return true;
+    }
     if (name == "t-qwen-d") {  // independent 1-layer Q8_0 draft for t-qwen (stochastic spec tests)
         s = tiny(name); s.arch = "qwen2"; s.qkv_bias = true; s.tied = true; s.rope_theta = 1000000.f;
         s.n_layers = 1; s.d_model = 256; s.n_heads = 4; s.n_kv_heads = 2; s.ffn = 512; s.seed = 9;
@@ -123,7 +129,7 @@ bool synth_preset(const std::string& name, SynthSpec& s) {
 
 std::vector<std::string> synth_preset_names() {
     return {"c1", "c2", "c3d", "c4", "c4d", "c5", "t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen",
-            "t-qwen-d", "t-dense", "t-q8-a64"};
+            "t-qwen-d", "t-dense", "t-q8-a64", "t-qwen3"};
 }
 
 // ── tokenizer stub ──────────────────────────────────────────────────────────
@@ -302,6 +308,15 @@ bool synth_write(const SynthSpec& s, const std::string& path, bool verbose) {
         });
     };
 
+    // per-head QK-norm weights (Qwen3): head_dim F32 values 1 + N(0, 0.1^2),
+    // so the norm's weights matter
+    auto head_norm = [&](const std::string& name, int n) {
+        w.add_tensor(name, {(uint64_t)n}, GGMLType::F32, [seed, name, n](int64_t, int64_t, uint8_t* dst) {
+            const uint64_t key = tensor_key(seed, name);
+            for (int i = 0; i < n; ++i) { float v = 1.f + normal_at(key, (uint64_t)i, 0.1f); std::memcpy(dst + 4 * i, &v, 4); }
+        });
+    };
+
     // norm weights 1 + N(0, 0.1^2) stored as F32 bytes under a declared F16
     // type of 2n values (the same byte count)
     auto raw_norm = [&](const std::string& name, int n) {
@@ -326,6 +341,10 @@ bool synth_write(const SynthSpec& s, const std::string& path, bool verbose) {
             bias(b + "attn_q.bias", NQ);
             bias(b + "attn_k.bias", NKV);
             bias(b + "attn_v.bias", NKV);
+        }
+        if (s.qk_norm) {
+            head_norm(b + "attn_q_norm.weight", s.head_dim);
+            head_norm(b + "attn_k_norm.weight", s.head_dim);
         }
         matrix(b + "attn_output.weight", b + "attn_output.weight", NQ, D, td);
         ones(b + "ffn_norm.weight", D);

@@ -1,10 +1,10 @@
-// Synthetic random-init Llama/Qwen2-shaped GGUF models.
+// Synthetic random-init Llama/Qwen2/Qwen3-shaped GGUF models.
 //
 // Every linear weight is i.i.d. N(0, 0.02^2) drawn from a counter-based
 // generator keyed by (seed, tensor name, element index), so any tensor can be
 // regenerated independently and in parallel, and a draft model can reuse the
-// exact float weights of its target's layers. Norm weights are 1.0 and Qwen2
-// QKV biases are N(0, 0.02^2) in F32. The tensor names and metadata keys are
+// exact float weights of its target's layers. Norm weights are 1.0, Qwen2
+// QKV biases are N(0, 0.02^2) and Qwen3 QK-norm weights 1 + N(0, 0.1^2), in F32. The tensor names and metadata keys are
 // the ones the reference reads (core/model.cpp:48-80, 99-154).
 #pragma once
 #include "gguf_types.hpp"
@@ -16,12 +16,13 @@ namespace orc {
 
 struct SynthSpec {
     std::string name;
-    std::string arch = "llama";     // "llama" or "qwen2"
+    std::string arch = "llama";     // "llama", "qwen2" or "qwen3"
     int n_layers = 2, d_model = 512, n_heads = 8, n_kv_heads = 2, head_dim = 64;
     int ffn = 1024, vocab = 2048;
     float rope_theta = 500000.f, rms_eps = 1e-5f;
     bool tied = true;               // no output.weight: the LM head is token_embd
     bool qkv_bias = false;
+    bool qk_norm = false;           // Qwen3 per-head attn_q_norm / attn_k_norm (head_dim F32 each)
     GGMLType t_default = GGMLType::Q8_0;   // attn_q/k/output, ffn_gate/up
     GGMLType t_attn_v = GGMLType::Q8_0;
     GGMLType t_ffn_down = GGMLType::Q8_0;

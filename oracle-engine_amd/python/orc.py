@@ -67,6 +67,7 @@ ABI = [
     ("orc_gemm_fused_mixed", C.c_int, [_ip, C.POINTER(Seg), C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
                                        C.c_float, C.c_int, _vp]),
     ("orc_rmsnorm", C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_float, _vp]),
+    ("orc_qk_norm", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_float, _vp]),
     ("orc_rope_kv_store", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp,
                                     C.c_int, _vp]),
     ("orc_rope_kv_store_at", C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp,

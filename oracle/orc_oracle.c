@@ -310,10 +310,10 @@ struct orco_model {
     uint8_t* map; size_t size; const uint8_t* data;
     otensor* t; int nt;
     char arch[64];
-    int V, L, H, KVH, D, FF, HD, CTX, NQ, NKV, bias, tied;
-    float rope;
+    int V, L, H, KVH, D, FF, HD, CTX, NQ, NKV, bias, tied, qkn;
+    float rope, eps;  /* eps: attention.layer_norm_rms_epsilon, used by the QK-norm only */
     omat embd, head, *wq, *wk, *wv, *wo, *wg, *wu, *wd;
-    const float **attn_norm, **ffn_norm, *out_norm, **bq, **bk, **bv;
+    const float **attn_norm, **ffn_norm, *out_norm, **bq, **bk, **bv, **qn, **kn;
     float *kc, *vc, *x, *xb, *xb2, *hb, *hb2, *q, *k, *v, *att;
 };
 
@@ -424,6 +424,12 @@ orco_model* orco_model_load(const char* path, int ctx_len) {
         snprintf(kk, sizeof kk, "%s.rope.freq_base", m->arch);
         for (uint64_t i = 0; i < nkv; i++) if (!strcmp(kvs[i].key, kk) && (kvs[i].kind == 6 || kvs[i].kind == 12)) m->rope = kvs[i].f;
     }
+    m->eps = 1e-5f;
+    {
+        char kk[200];
+        snprintf(kk, sizeof kk, "%s.attention.layer_norm_rms_epsilon", m->arch);
+        for (uint64_t i = 0; i < nkv; i++) if (!strcmp(kvs[i].key, kk) && (kvs[i].kind == 6 || kvs[i].kind == 12)) m->eps = kvs[i].f;
+    }
 #undef META_U
     free(kvs);
     m->CTX = ctx_len;
@@ -441,11 +447,13 @@ orco_model* orco_model_load(const char* path, int ctx_len) {
     get_mat(m, to ? "output.weight" : "token_embd.weight", &m->head);
     m->out_norm = get_vec(m, "output_norm.weight");
     m->bias = find_t(m, "blk.0.attn_q.bias") != NULL;
+    m->qkn = find_t(m, "blk.0.attn_q_norm.weight") != NULL; /* Qwen3 QK-norm, model.cpp:63 */
 #define ALLOCL(p, T) p = (T*)calloc((size_t)m->L, sizeof(T))
     ALLOCL(m->wq, omat); ALLOCL(m->wk, omat); ALLOCL(m->wv, omat); ALLOCL(m->wo, omat);
     ALLOCL(m->wg, omat); ALLOCL(m->wu, omat); ALLOCL(m->wd, omat);
     ALLOCL(m->attn_norm, const float*); ALLOCL(m->ffn_norm, const float*);
     ALLOCL(m->bq, const float*); ALLOCL(m->bk, const float*); ALLOCL(m->bv, const float*);
+    ALLOCL(m->qn, const float*); ALLOCL(m->kn, const float*);
 #undef ALLOCL
     for (int l = 0; l < m->L; l++) {
         char nm[128];
@@ -456,6 +464,8 @@ orco_model* orco_model_load(const char* path, int ctx_len) {
 #define VEC(field, suffix) snprintf(nm, sizeof nm, "blk.%d.%s", l, suffix); m->field[l] = get_vec(m, nm)
         VEC(attn_norm, "attn_norm.weight"); VEC(ffn_norm, "ffn_norm.weight");
         VEC(bq, "attn_q.bias"); VEC(bk, "attn_k.bias"); VEC(bv, "attn_v.bias");
+        VEC(qn, "attn_q_norm.weight"); VEC(kn, "attn_k_norm.weight");
+        if (m->qkn && (!m->qn[l] || !m->kn[l])) goto fail;
 #undef VEC
     }
     {
@@ -482,7 +492,7 @@ void orco_model_free(orco_model* m) {
     if (!m) return;
     if (m->map) munmap(m->map, m->size);
     free(m->t); free(m->wq); free(m->wk); free(m->wv); free(m->wo); free(m->wg); free(m->wu); free(m->wd);
-    free(m->attn_norm); free(m->ffn_norm); free(m->bq); free(m->bk); free(m->bv);
+    free(m->attn_norm); free(m->ffn_norm); free(m->bq); free(m->bk); free(m->bv); free(m->qn); free(m->kn);
     free(m->kc); free(m->vc); free(m->x); free(m->xb); free(m->xb2); free(m->hb); free(m->hb2);
     free(m->q); free(m->k); free(m->v);
     free(m);
@@ -511,6 +521,15 @@ static void embed_row(orco_model* m, int32_t tok, float* out) { /* model.cpp:352
 static void gemv_m(const omat* w, const float* x, float* y) { orco_gemv(w->type, w->p, w->n_out, w->n_in, x, y); }
 static void addv(float* a, const float* b, int n) { for (int i = 0; i < n; i++) a[i] += b[i]; }
 
+/* QK-norm (Qwen3): ops::rmsnorm over each q head and each k head of one
+ * token, with the model's epsilon, after the bias and before RoPE
+ * (model.cpp:390-399, 584-593) */
+static void qk_norm(const orco_model* m, int l, float* q, float* k) {
+    if (!m->qkn) return;
+    for (int h = 0; h < m->H; h++) orco_rmsnorm(q + h * m->HD, q + h * m->HD, m->qn[l], m->HD, m->eps);
+    for (int h = 0; h < m->KVH; h++) orco_rmsnorm(k + h * m->HD, k + h * m->HD, m->kn[l], m->HD, m->eps);
+}
+
 int orco_model_forward(orco_model* m, int32_t token, int pos, float* logits) { /* model.cpp:340-495 */
     if (pos < 0 || pos >= m->CTX) return -1;
     const int D = m->D, NQ = m->NQ, NKV = m->NKV, FF = m->FF;
@@ -521,6 +540,7 @@ int orco_model_forward(orco_model* m, int32_t token, int pos, float* logits) { /
         gemv_m(&m->wk[l], m->xb, m->k);
         gemv_m(&m->wv[l], m->xb, m->v);
         if (m->bias) { addv(m->q, m->bq[l], NQ); addv(m->k, m->bk[l], NKV); addv(m->v, m->bv[l], NKV); }
+        qk_norm(m, l, m->q, m->k);
         orco_rope(m->q, m->k, m->H, m->KVH, m->HD, pos, m->rope);
         float* kcl = m->kc + (size_t)l * m->CTX * NKV;
         float* vcl = m->vc + (size_t)l * m->CTX * NKV;
@@ -572,6 +592,7 @@ int orco_model_forward_batch(orco_model* m, const int32_t* toks, int n, int sp, 
         float* kcl = m->kc + (size_t)l * m->CTX * NKV;
         float* vcl = m->vc + (size_t)l * m->CTX * NKV;
         for (int t = 0; t < n; t++) {
+            qk_norm(m, l, Q + (size_t)t * NQ, K + (size_t)t * NKV);
             orco_rope(Q + (size_t)t * NQ, K + (size_t)t * NKV, m->H, m->KVH, m->HD, sp + t, m->rope);
             memcpy(kcl + (size_t)(sp + t) * NKV, K + (size_t)t * NKV, sizeof(float) * NKV);
             memcpy(vcl + (size_t)(sp + t) * NKV, Vv + (size_t)t * NKV, sizeof(float) * NKV);

@@ -37,7 +37,8 @@ def models_dir(tmp_path_factory):
     if not os.path.exists(SYNTH):
         pytest.fail(f"{SYNTH} missing: run __graft_entry__.build()")
     d = tmp_path_factory.mktemp("models")
-    for name in ("t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen", "t-qwen-d", "t-dense", "t-q8-a64"):
+    for name in ("t-q8", "t-q40", "t-q4k", "t-q4k-d", "t-q6k", "t-qwen", "t-qwen-d", "t-dense", "t-q8-a64",
+                 "t-qwen3"):
         subprocess.run([SYNTH, name, str(d / f"{name}.gguf")], check=True, capture_output=True)
     return d
 

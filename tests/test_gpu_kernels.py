@@ -392,6 +392,38 @@ def test_rmsnorm(dev, oracle):
             assert np.allclose(got[r], oracle.rmsnorm(x[r], w), rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("H,KVH,hd,nt", [(8, 2, 128, 3), (32, 8, 128, 5), (14, 2, 64, 2), (5, 1, 96, 1)])
+def test_qk_norm(dev, H, KVH, hd, nt):
+    """orc_qk_norm (Qwen3, core/model.cpp:390-399): every q head and every k
+    head of each token's QKV row is RMS-normalised over head_dim with its own
+    weight vector (q heads qw, k heads kw), in place; v and the row padding
+    stay untouched. Checked against the float64 closed form; half the heads
+    are tiny (mean square ~1e-6), so an epsilon of 1e-5 instead of the 1e-6
+    passed would move them by ~2x."""
+    print(f"[gpu] qk_norm H={H} KVH={KVH} hd={hd} nt={nt}", flush=True)
+    rng = np.random.default_rng(H * 100 + hd)
+    ld = (H + 2 * KVH) * hd + 7  # row stride past the q | k | v columns
+    qkv = rng.normal(0, 1, (nt, ld)).astype(np.float32)
+    for h in range(0, H + KVH, 2):  # tiny heads: the epsilon matters
+        qkv[:, h * hd:(h + 1) * hd] *= 1e-3
+    qw = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    d, dq, dk = dev.upload(qkv), dev.upload(qw), dev.upload(kw)
+    eps = 1e-6
+    dev.check(dev.L.orc_qk_norm(d.ptr, ld, nt, H, KVH, hd, dq.ptr, dk.ptr, C.c_float(eps), None))
+    got = d.read(np.float32).reshape(nt, ld)
+    x = qkv.astype(np.float64)
+    for t in range(nt):
+        for h in range(H + KVH):
+            v = x[t, h * hd:(h + 1) * hd]
+            want = v / np.sqrt((v * v).mean() + eps) * (qw if h < H else kw)
+            assert np.allclose(got[t, h * hd:(h + 1) * hd], want, rtol=2e-6, atol=1e-30), (t, h)
+        assert np.array_equal(got[t, (H + KVH) * hd:], qkv[t, (H + KVH) * hd:])  # v and padding untouched
+    # argument checks
+    assert dev.L.orc_qk_norm(d.ptr, (H + 2 * KVH) * hd - 1, nt, H, KVH, hd, dq.ptr, dk.ptr, C.c_float(eps), None) != 0
+    assert dev.L.orc_qk_norm(d.ptr, ld, nt, H, KVH, 256, dq.ptr, dk.ptr, C.c_float(eps), None) != 0
+
+
 @pytest.mark.parametrize("H,KVH,hd,base", [(24, 8, 128, 500000.0), (28, 4, 128, 1e6), (14, 2, 64, 1e6)])
 def test_rope_kv_store(dev, oracle, H, KVH, hd, base):
     print(f"[gpu] rope H={H} KVH={KVH} hd={hd}", flush=True)
