@@ -413,8 +413,14 @@ def main():
         cpu = cpu_baseline(tgt_path, dft_path, prompt, k, n_gen, a.workload.upper())
         if cpu:  # the same workload on both sides: the reference's stream checksum against this run's
             cpu["checksum_equal"] = cpu["checksum"] == checksum
-    metric = ({"c1": "greedy decode tok/s (1B Q8_0)", "c2": "greedy decode tok/s (3B Q4_K_M)"}[a.workload] if plain else
-              "spec-decode tok/s (3B Q4_K, k=4); quant-GEMV HBM GB/s vs peak")
+    metric = {  # c3 carries BASELINE.json's metric; the others name their own configuration
+        "c1": "greedy decode tok/s (1B Q8_0)",
+        "c2": "greedy decode tok/s (3B Q4_K_M)",
+        "c3": "spec-decode tok/s (3B Q4_K, k=4); quant-GEMV HBM GB/s vs peak",
+        "c4": "Engine stochastic spec-decode tok/s per call, prefill included (7B Q4_K_M + 0.5B Q8_0, k=6)",
+        "c4s": "speculative-sampling tok/s per call, prefill included (7B Q4_K_M + 0.5B Q8_0, k=6)",
+        "c5": "spec-decode tok/s after an 8191-id prefill (7B Q6_K + 0.5B Q8_0, k=8, 16384 cache)",
+    }[a.workload]
     out = {
         "metric": metric,
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
