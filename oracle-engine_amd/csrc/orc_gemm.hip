@@ -863,6 +863,17 @@ static int launch_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) 
         }
         if (per_lane == 1) return launch_shape<QT, NT, 1, 1, 4>(p, s, ev);
         if (per_lane == 2) return launch_shape<QT, NT, 1, 2, 4>(p, s, ev);
+        // long rows (4+ units per lane): byte-code types take four units per
+        // batch, Q4_K two rows of two (16384 x 8192 over rotating weights:
+        // Q8_0_X8 28.2 -> 26.7 us, Q4_K 26.0 -> 24.5, Q4_0 24.0 -> 23.3; the
+        // C1-C3 streams and rates unchanged); Q6_K keeps three (four: 27.6 ->
+        // 35.9 us)
+        if constexpr (QT == ORC_Q8_0 || QT == ORC_Q8_0_X8 || QT == ORC_Q4_0) {
+            if (per_lane >= 4) return launch_shape<QT, NT, 1, 4, 4>(p, s, ev);
+        }
+        if constexpr (QT == ORC_Q4_K) {
+            if (per_lane >= 4) return launch_shape<QT, NT, 2, 2, 4>(p, s, ev);
+        }
         return launch_shape<QT, NT, 1, 3, 4>(p, s, ev);
     } else {
         if (pair || tall) return launch_shape<QT, NT, 2, 1, 2>(p, s, ev);
