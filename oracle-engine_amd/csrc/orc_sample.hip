@@ -97,6 +97,86 @@ struct SampScratch {
     unsigned long long cand[kCandMax];
 };
 
+typedef const __attribute__((address_space(1))) float* g_cfp;
+
+// f(i, x[i]) for the row elements this thread owns (i = tid, tid + kST, ...)
+// in increasing i, as a plain strided loop would visit them, with the loads
+// of kRowBatch elements issued together (indices clamped into the row): a
+// pass over a 152K-entry row keeps eight loads in flight per thread instead
+// of waiting on each. x is device memory.
+constexpr int kRowBatch = 8;
+template <class F> __device__ __forceinline__ void row_pass(const float* x, int n, F&& f) {
+    const g_cfp gx = (g_cfp)x;
+    for (int i0 = threadIdx.x; i0 < n; i0 += kRowBatch * kST) {
+        float v[kRowBatch];
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j) v[j] = gx[min(i0 + j * kST, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j)
+            if (i0 + j * kST < n) f(i0 + j * kST, v[j]);
+    }
+}
+
+// row_pass with a wave-uniform trip count: every lane calls f(i, x[i], in)
+// for each of its slots, in = false past the row, so f may use wave-wide
+// operations (ballots).
+template <class F> __device__ __forceinline__ void row_pass_uniform(const float* x, int n, F&& f) {
+    const g_cfp gx = (g_cfp)x;
+    for (int b0 = 0; b0 < n; b0 += kRowBatch * kST) {
+        const int i0 = b0 + (int)threadIdx.x;
+        float v[kRowBatch];
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j) v[j] = gx[min(i0 + j * kST, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j) f(i0 + j * kST, v[j], i0 + j * kST < n);
+    }
+}
+
+// hist[bin] += 1 for every active lane, one LDS atomic per distinct bin of
+// the wave (a wave's probabilities share few leading bytes, and 64 atomics
+// on one address serialise). Whole wave.
+__device__ __forceinline__ void wave_hist_add(unsigned int* hist, unsigned int bin, bool active) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long pending = __ballot(active);
+    while (pending) {
+        const int leader = __builtin_ctzll(pending);
+        const unsigned int b = __shfl(bin, leader, 64);
+        const unsigned long long same = __ballot(active && bin == b);
+        if (lane == leader) atomicAdd(&hist[b], (unsigned int)__builtin_popcountll(same));
+        pending &= ~same;
+    }
+}
+
+// row_pass over two rows at once: f(i, x[i], y[i])
+template <class F> __device__ __forceinline__ void row_pass2(const float* x, const float* y, int n, F&& f) {
+    const g_cfp gx = (g_cfp)x, gy = (g_cfp)y;
+    for (int i0 = threadIdx.x; i0 < n; i0 += kRowBatch * kST) {
+        float u[kRowBatch], v[kRowBatch];
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j) {
+            const int i = min(i0 + j * kST, n - 1);
+            u[j] = gx[i];
+            v[j] = gy[i];
+        }
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j)
+            if (i0 + j * kST < n) f(i0 + j * kST, u[j], v[j]);
+    }
+}
+
+// f(i, w(i)) for i = b .. e-1 in order, the values of kRowBatch consecutive
+// indices computed (loaded) together; f returns false to stop.
+template <class W, class F> __device__ __forceinline__ void chunk_pass(int b, int e, W&& w, F&& f) {
+    for (int i0 = b; i0 < e; i0 += kRowBatch) {
+        float v[kRowBatch];
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j) v[j] = w(min(i0 + j, e - 1));
+#pragma unroll
+        for (int j = 0; j < kRowBatch; ++j)
+            if (i0 + j < e && !f(i0 + j, v[j])) return;
+    }
+}
+
 __device__ float block_max(float v, SampScratch& sh) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -123,13 +203,12 @@ __device__ float block_sum(float v, SampScratch& sh) {
 __device__ int block_argmax(const float* x, int n, SampScratch& sh) {
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += kST) {
-        const float v = x[i];
+    row_pass(x, n, [&](int i, float v) {
         if (v > bv || (v == bv && i < bi)) {
             bv = v;
             bi = i;
         }
-    }
+    });
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
@@ -177,18 +256,68 @@ __device__ void bitonic_sort(SampScratch& sh, int m) {
 
 // Repeat penalty (sampler.cpp:15-27) over the last repeat_last entries of
 // history + extra (extra: proposals not yet recorded), one entry at a time so
-// repeated ids compound. One lane; the caller synchronises.
-__device__ void penalize(const DevSampler* s, float* lg, int n, const int32_t* extra, int n_extra) {
-    if (threadIdx.x != 0 || !(s->pen > 1.f)) return;
+// repeated ids compound. Up to kPenPar entries: each entry's logit is loaded
+// by its own thread, lane 0 applies the penalties in entry order in LDS (an
+// entry updates the value held at its id's first occurrence), and the first
+// occurrences write the results back; the same operations in the same order
+// as one lane walking the entries over the row, without a dependent global
+// load per entry. More entries: that one-lane walk. Whole workgroup (sh.cand
+// and sh.dscan serve as scratch).
+constexpr int kPenPar = 256;
+__device__ void penalize(const DevSampler* s, float* lg, int n, const int32_t* extra, int n_extra,
+                         SampScratch& sh) {
+    if (!(s->pen > 1.f)) return;
     const int L = s->nh + n_extra;
     const int start = L - s->last > 0 ? L - s->last : 0;
-    for (int i = start; i < L; ++i) {
-        const int32_t id = i < s->nh ? s->hist[i] : extra[i - s->nh];
-        if (id < 0 || id >= n) continue;
-        const float l = lg[id];
-        lg[id] = l > 0.f ? l / s->pen : l * s->pen;
+    const int m = L - start;
+    const int tid = threadIdx.x;
+    auto entry = [&](int i) { return i < s->nh ? s->hist[i] : extra[i - s->nh]; };
+    if (m > kPenPar) {
+        if (tid == 0)
+            for (int i = start; i < L; ++i) {
+                const int32_t id = entry(i);
+                if (id < 0 || id >= n) continue;
+                const float l = lg[id];
+                lg[id] = l > 0.f ? l / s->pen : l * s->pen;
+            }
+        __syncthreads();
+        return;
     }
+    int* first = (int*)sh.dscan;  // first occurrence of each entry's id
+    int32_t id = -1;
+    if (tid < m) {
+        id = entry(start + tid);
+        const bool ok = id >= 0 && id < n;
+        const float v = ok ? lg[id] : 0.f;
+        sh.cand[tid] = ((unsigned long long)(uint32_t)(ok ? id : -1) << 32) | __builtin_bit_cast(uint32_t, v);
+    }
+    __syncthreads();
+    if (tid < m) {
+        int f = tid;
+        for (int j = 0; j < tid; ++j)
+            if ((int32_t)(sh.cand[j] >> 32) == (int32_t)(sh.cand[tid] >> 32)) {
+                f = j;
+                break;
+            }
+        first[tid] = f;
+    }
+    __syncthreads();
+    if (tid == 0)
+        for (int i = 0; i < m; ++i) {
+            if ((int32_t)(sh.cand[i] >> 32) < 0) continue;
+            const int f = first[i];
+            const unsigned long long c = sh.cand[f];
+            const float l = __builtin_bit_cast(float, (uint32_t)c);
+            const float r = l > 0.f ? l / s->pen : l * s->pen;
+            sh.cand[f] = (c & 0xFFFFFFFF00000000ull) | __builtin_bit_cast(uint32_t, r);
+        }
+    __syncthreads();
+    if (tid < m && first[tid] == tid && id >= 0 && id < n) lg[id] = __builtin_bit_cast(float, (uint32_t)sh.cand[tid]);
+    __syncthreads();
 }
+
+// probability held in a candidate key (~bits(p) << 32 | index)
+__device__ __forceinline__ float cand_p(unsigned long long c) { return __builtin_bit_cast(float, ~(uint32_t)(c >> 32)); }
 
 // Temperature, softmax (p written over lg) and the top-k candidates sorted by
 // (p desc, index asc) into sh.cand[0 .. k) (sampler.cpp:35-64). T > 0 only.
@@ -200,25 +329,24 @@ __device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& s
     const bool scale = T != 1.f;
     const float inv_t = 1.f / T;
     float mx = -INFINITY;
-    for (int i = tid; i < n; i += kST) {
-        float l = lg[i];
+    row_pass(lg, n, [&](int i, float l) {
         if (scale) {
             l *= inv_t;
             lg[i] = l;
         }
         mx = fmaxf(mx, l);
-    }
+    });
     mx = block_max(mx, sh);
     // softmax (ops::softmax: e = exp(l - max), p = e * (1/sum))
     float sum = 0.f;
-    for (int i = tid; i < n; i += kST) {
-        const float e = expf(lg[i] - mx);
+    row_pass(lg, n, [&](int i, float l) {
+        const float e = expf(l - mx);
         lg[i] = e;
         sum += e;
-    }
+    });
     sum = block_sum(sum, sh);
     const float inv_s = 1.f / sum;
-    for (int i = tid; i < n; i += kST) lg[i] = lg[i] * inv_s;
+    row_pass(lg, n, [&](int i, float e) { lg[i] = e * inv_s; });
     __syncthreads();
     // top-k threshold: exact radix select of the k-th largest p
     const int k = min(s->top_k > 0 ? s->top_k : n, min(n, kCandMax));
@@ -227,10 +355,10 @@ __device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& s
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (int b = tid; b < 256; b += kST) sh.hist[b] = 0;
         __syncthreads();
-        for (int i = tid; i < n; i += kST) {
-            const unsigned int key = __builtin_bit_cast(unsigned int, lg[i]);
-            if ((key & mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
-        }
+        row_pass_uniform(lg, n, [&](int, float p, bool in) {
+            const unsigned int key = __builtin_bit_cast(unsigned int, p);
+            wave_hist_add(sh.hist, (key >> shift) & 255u, in && (key & mask) == prefix);
+        });
         __syncthreads();
         if (tid == 0) {
             int cum = 0, sel = 0;
@@ -255,13 +383,13 @@ __device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& s
     // candidates: every p >= thr (key = ~bits(p) : index sorts p desc, index asc)
     if (tid == 0) sh.bcast[2] = 0;
     __syncthreads();
-    for (int i = tid; i < n; i += kST) {
-        const unsigned int key = __builtin_bit_cast(unsigned int, lg[i]);
+    row_pass(lg, n, [&](int i, float p) {
+        const unsigned int key = __builtin_bit_cast(unsigned int, p);
         if (key >= thr) {
             const int slot = atomicAdd(&sh.bcast[2], 1);
             if (slot < kCandMax) sh.cand[slot] = ((unsigned long long)(~key) << 32) | (unsigned int)i;
         }
-    }
+    });
     __syncthreads();
     int nc = sh.bcast[2];
     if (nc > kCandMax) {
@@ -270,13 +398,13 @@ __device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& s
         __syncthreads();
         if (tid == 0) sh.bcast[2] = 0;
         __syncthreads();
-        for (int i = tid; i < n; i += kST) {
-            const unsigned int key = __builtin_bit_cast(unsigned int, lg[i]);
+        row_pass(lg, n, [&](int i, float p) {
+            const unsigned int key = __builtin_bit_cast(unsigned int, p);
             if (key > thr) {
                 const int slot = atomicAdd(&sh.bcast[2], 1);
                 sh.cand[slot] = ((unsigned long long)(~key) << 32) | (unsigned int)i;
             }
-        }
+        });
         __syncthreads();
         if (tid == 0) {
             int c = sh.bcast[2];
@@ -305,14 +433,14 @@ __device__ void topp_cut(const DevSampler* s, const float* lg, int k, SampScratc
     float cum = 0.f;
     int cut = k;
     for (int i = 0; i < k; ++i) {
-        cum += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
+        cum += cand_p(sh.cand[i]);
         if (cum >= s->top_p) {
             cut = i + 1;
             break;
         }
     }
     float total = 0.f;
-    for (int i = 0; i < cut; ++i) total += lg[(int)(sh.cand[i] & 0xFFFFFFFFu)];
+    for (int i = 0; i < cut; ++i) total += cand_p(sh.cand[i]);
     sh.bcast[4] = cut;
     sh.fb[0] = total;
 }
@@ -321,7 +449,7 @@ __device__ void topp_cut(const DevSampler* s, const float* lg, int k, SampScratc
 // Whole workgroup.
 __device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) {
     const int tid = threadIdx.x;
-    penalize(s, lg, n, nullptr, 0);
+    penalize(s, lg, n, nullptr, 0, sh);
     __syncthreads();
     if (s->temp <= 0.f) return block_argmax(lg, n, sh);  // sampler.cpp:50
     const int k = topk_sorted(s, lg, n, sh);
@@ -333,7 +461,7 @@ __device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) 
         int32_t tok = (int32_t)(sh.cand[0] & 0xFFFFFFFFu);
         for (int i = 0; i < cut; ++i) {
             const int32_t id = (int32_t)(sh.cand[i] & 0xFFFFFFFFu);
-            r -= lg[id];
+            r -= cand_p(sh.cand[i]);  // lg[id]
             if (r <= 0.f) {
                 tok = id;
                 break;
@@ -353,7 +481,7 @@ __device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) 
 __device__ void transform_row(const DevSampler* s, float* lg, int n, const int32_t* extra, int n_extra, float* p_out,
                               SampScratch& sh) {
     const int tid = threadIdx.x;
-    penalize(s, lg, n, extra, n_extra);
+    penalize(s, lg, n, extra, n_extra, sh);
     __syncthreads();
     if (s->temp <= 0.f) {
         const int a = block_argmax(lg, n, sh);
@@ -369,7 +497,7 @@ __device__ void transform_row(const DevSampler* s, float* lg, int n, const int32
     const float total = sh.fb[0];
     for (int i = tid; i < cut; i += kST) {
         const int id = (int)(sh.cand[i] & 0xFFFFFFFFu);
-        p_out[id] = lg[id] / total;
+        p_out[id] = cand_p(sh.cand[i]) / total;  // lg[id] / total
     }
     __syncthreads();
 }
@@ -385,13 +513,13 @@ __device__ int block_pick(int n, W w, double target, SampScratch& sh) {
     const int b = min(n, tid * chunk), e = min(n, b + chunk);
     double loc = 0.0;
     int last = -1;
-    for (int i = b; i < e; ++i) {
-        const float d = w(i);
+    chunk_pass(b, e, w, [&](int i, float d) {
         if (d > 0.f) {
             loc += (double)d;
             last = i;
         }
-    }
+        return true;
+    });
     sh.dscan[tid] = loc;
     if (tid == 0) {
         sh.bcast[5] = 0x7FFFFFFF;
@@ -413,15 +541,15 @@ __device__ int block_pick(int n, W w, double target, SampScratch& sh) {
         if (prefix < target && target <= prefix + loc) {
             double r = target - prefix;
             int got = last;  // rounding left r > 0: the chunk's last positive
-            for (int i = b; i < e; ++i) {
-                const float d = w(i);
-                if (!(d > 0.f)) continue;
+            chunk_pass(b, e, w, [&](int i, float d) {
+                if (!(d > 0.f)) return true;
                 r -= (double)d;
                 if (r <= 0.0) {
                     got = i;
-                    break;
+                    return false;
                 }
-            }
+                return true;
+            });
             atomicMin(&sh.bcast[5], got);
         } else if (target <= 0.0 && prefix == 0.0) {
             for (int i = b; i < e; ++i)
@@ -452,10 +580,10 @@ __device__ int32_t accept_resample(const float* p, const float* q, int n, int32_
     auto resid = [&](int i) { return p[i] - q[i]; };
     // total of the positive residual (double), then the draw
     double loc = 0.0;
-    for (int i = threadIdx.x; i < n; i += kST) {
-        const float d = p[i] - q[i];
+    row_pass2(p, q, n, [&](int, float pv, float qv) {
+        const float d = pv - qv;
         if (d > 0.f) loc += (double)d;
-    }
+    });
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) loc += __shfl_xor(loc, o, 64);
     if ((threadIdx.x & 63) == 0) sh.dscan[threadIdx.x >> 6] = loc;
@@ -579,8 +707,9 @@ __device__ float lane0_uniform(DevSampler* s, SampScratch& sh) {
 
 __device__ double block_total(const float* p, int n, SampScratch& sh) {
     double loc = 0.0;
-    for (int i = threadIdx.x; i < n; i += kST)
-        if (p[i] > 0.f) loc += (double)p[i];
+    row_pass(p, n, [&](int, float v) {
+        if (v > 0.f) loc += (double)v;
+    });
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) loc += __shfl_xor(loc, o, 64);
     if ((threadIdx.x & 63) == 0) sh.dscan[threadIdx.x >> 6] = loc;
