@@ -117,36 +117,6 @@ template <class F> __device__ __forceinline__ void row_pass(const float* x, int 
     }
 }
 
-// row_pass with a wave-uniform trip count: every lane calls f(i, x[i], in)
-// for each of its slots, in = false past the row, so f may use wave-wide
-// operations (ballots).
-template <class F> __device__ __forceinline__ void row_pass_uniform(const float* x, int n, F&& f) {
-    const g_cfp gx = (g_cfp)x;
-    for (int b0 = 0; b0 < n; b0 += kRowBatch * kST) {
-        const int i0 = b0 + (int)threadIdx.x;
-        float v[kRowBatch];
-#pragma unroll
-        for (int j = 0; j < kRowBatch; ++j) v[j] = gx[min(i0 + j * kST, n - 1)];
-#pragma unroll
-        for (int j = 0; j < kRowBatch; ++j) f(i0 + j * kST, v[j], i0 + j * kST < n);
-    }
-}
-
-// hist[bin] += 1 for every active lane, one LDS atomic per distinct bin of
-// the wave (a wave's probabilities share few leading bytes, and 64 atomics
-// on one address serialise). Whole wave.
-__device__ __forceinline__ void wave_hist_add(unsigned int* hist, unsigned int bin, bool active) {
-    const int lane = threadIdx.x & 63;
-    unsigned long long pending = __ballot(active);
-    while (pending) {
-        const int leader = __builtin_ctzll(pending);
-        const unsigned int b = __shfl(bin, leader, 64);
-        const unsigned long long same = __ballot(active && bin == b);
-        if (lane == leader) atomicAdd(&hist[b], (unsigned int)__builtin_popcountll(same));
-        pending &= ~same;
-    }
-}
-
 // row_pass over two rows at once: f(i, x[i], y[i])
 template <class F> __device__ __forceinline__ void row_pass2(const float* x, const float* y, int n, F&& f) {
     const g_cfp gx = (g_cfp)x, gy = (g_cfp)y;
@@ -352,17 +322,34 @@ __device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& s
     const int k = min(s->top_k > 0 ? s->top_k : n, min(n, kCandMax));
     unsigned int prefix = 0, mask = 0;
     int krem = k;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = tid; b < 256; b += kST) sh.hist[b] = 0;
-        __syncthreads();
-        row_pass_uniform(lg, n, [&](int, float p, bool in) {
+    // Four bits per pass (eight passes): each thread counts its own elements
+    // into its own column of 16 counters (the candidate buffer serves as
+    // scratch, [digit][thread]), so no two lanes ever add to one address;
+    // wave d then adds up digit d's column sums.
+    unsigned int* const cnt = (unsigned int*)sh.cand;
+    static_assert(16 * kST * sizeof(unsigned int) <= sizeof(sh.cand), "digit counters fit the candidate buffer");
+    static_assert(kST / 64 == 16, "one wave per digit");
+    for (int shift = 28; shift >= 0; shift -= 4) {
+#pragma unroll
+        for (int d = 0; d < 16; ++d) cnt[d * kST + tid] = 0;
+        row_pass(lg, n, [&](int, float p) {
             const unsigned int key = __builtin_bit_cast(unsigned int, p);
-            wave_hist_add(sh.hist, (key >> shift) & 255u, in && (key & mask) == prefix);
+            if ((key & mask) == prefix) atomicAdd(&cnt[((key >> shift) & 15u) * kST + tid], 1u);
         });
+        __syncthreads();
+        {
+            const int d = tid >> 6, l = tid & 63;
+            unsigned int c = 0;
+#pragma unroll
+            for (int i = 0; i < kST / 64; ++i) c += cnt[d * kST + l * (kST / 64) + i];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+            if (l == 0) sh.hist[d] = c;
+        }
         __syncthreads();
         if (tid == 0) {
             int cum = 0, sel = 0;
-            for (int b = 255; b >= 0; --b) {
+            for (int b = 15; b >= 0; --b) {
                 const int c = (int)sh.hist[b];
                 if (cum + c >= krem) {
                     sel = b;
@@ -375,7 +362,7 @@ __device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& s
         }
         __syncthreads();
         prefix |= (unsigned int)sh.bcast[0] << shift;
-        mask |= 255u << shift;
+        mask |= 15u << shift;
         krem = sh.bcast[1];
         __syncthreads();
     }
