@@ -370,13 +370,24 @@ int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, int n_vocab, 
  * d_extra[0 .. extra_base + r) for row r, temperature, softmax, top-k, top-p,
  * kept set renormalised into d_p (zeros elsewhere); T <= 0 puts all mass on
  * the argmax. The logits rows are rewritten (sampler.cpp:15-85 does the same
- * steps on one row). Nothing is recorded and no random number is drawn. */
+ * steps on one row). Nothing is recorded and no random number is drawn.
+ * Up to 17 rows of up to 196608 logits, T > 0 and 1 <= top_k <= 128 run split
+ * over many workgroups, with per-slice partial results kept in the state's
+ * scratch area: calls on one state must not overlap. */
 int orc_transform_probs(const void* d_state, float* d_logits, int ld, int n_vocab, int rows, const int32_t* d_extra,
                         int extra_base, float* d_p, int ldp, orc_stream_t stream);
 /* One draw from the distribution d_p (one mt19937 uniform u; first index
  * where the running sum of p reaches u * sum(p)); the id goes to d_out[0] and,
  * if given, d_out2[0]. Not recorded. */
 int orc_draw(void* d_state, const float* d_p, int n_vocab, int32_t* d_out, int32_t* d_out2, orc_stream_t stream);
+/* orc_transform_probs of one row (pending proposals d_extra[0 .. n_extra))
+ * followed by orc_draw from it, in one call: the draft step of a speculative
+ * sampling round (the draft's q and its proposal). The draw reads the kept set
+ * instead of the whole row; same uniform, same sums in index order. Like
+ * orc_transform_probs it uses the state's scratch: calls on one state must not
+ * overlap. */
+int orc_transform_draw(void* d_state, float* d_logits, int n_vocab, const int32_t* d_extra, int n_extra, float* d_p,
+                       int32_t* d_out, int32_t* d_out2, orc_stream_t stream);
 /* The acceptance test of proposal x with explicit uniforms: accept when
  * q[x] > 0 and u_acc * q[x] < p[x]; otherwise draw from norm(max(0, p - q))
  * with u_res (argmax of p if that is empty). d_out = [id, accepted]. */

@@ -38,6 +38,24 @@ constexpr int kST = 1024;          // threads of a sampling workgroup
 constexpr int kSampHist = 4096;    // history capacity (repeat_last <= kSampHist - 1)
 constexpr int kCandMax = 16384;    // candidates sorted in LDS (largest top_k; top_k = 0 means this many)
 
+// The transform of a row split over workgroups (k_tx_*): each workgroup owns
+// a slice of kTxSlice logits, passes on at most kTxCand candidates, and the
+// state holds the per-slice partial results between the launches.
+constexpr int kTxSlice = 4 * kST;  // logits per workgroup, four per thread
+constexpr int kTxMaxG = 48;        // slices per row (vocabularies up to 196608)
+constexpr int kTxRows = 17;        // rows per call (a verify pass of 16 proposals + the bonus row)
+constexpr int kTxCand = 192;       // candidates one slice passes on
+constexpr int kTxStop = 128;       // a slice's threshold search stops at this many candidates (or top_k)
+constexpr int kTxK = 128;          // largest top_k of the split path
+
+struct TxWork {
+    float mx[kTxRows][kTxMaxG];   // slice maxima of the scaled logits
+    float sum[kTxRows][kTxMaxG];  // slice sums of exp(l - max)
+    int nc[kTxRows][kTxMaxG];     // candidates per slice
+    int ovf[kTxRows];             // a slice had more than kTxCand candidates
+    uint2 cand[kTxRows][kTxMaxG][kTxCand];  // (bits of exp(l - max), index)
+};
+
 struct DevSampler {
     uint32_t mt[624];
     int mti;
@@ -45,6 +63,7 @@ struct DevSampler {
     int top_k, last;
     int nh;
     int32_t hist[kSampHist];
+    TxWork tx;  // scratch of the split transform (calls on one state must not overlap)
 };
 
 __device__ uint32_t mt_next(DevSampler* s) {
@@ -290,13 +309,13 @@ __device__ void penalize(const DevSampler* s, float* lg, int n, const int32_t* e
 __device__ __forceinline__ float cand_p(unsigned long long c) { return __builtin_bit_cast(float, ~(uint32_t)(c >> 32)); }
 
 // Temperature, softmax (p written over lg) and the top-k candidates sorted by
-// (p desc, index asc) into sh.cand[0 .. k) (sampler.cpp:35-64). T > 0 only.
-// Returns k.
-__device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& sh) {
+// (p desc, index asc) into sh.cand[0 .. k) (sampler.cpp:35-64). T > 0 only;
+// scaled: lg already holds the logits divided by T. Returns k.
+__device__ int topk_sorted(const DevSampler* s, float* lg, int n, SampScratch& sh, bool scaled = false) {
     const int tid = threadIdx.x;
     const float T = s->temp;
     // temperature (sampler.cpp:35-39) and the maximum in one pass
-    const bool scale = T != 1.f;
+    const bool scale = T != 1.f && !scaled;
     const float inv_t = 1.f / T;
     float mx = -INFINITY;
     row_pass(lg, n, [&](int i, float l) {
@@ -462,6 +481,24 @@ __device__ int32_t sample_row(DevSampler* s, float* lg, int n, SampScratch& sh) 
     return tok;
 }
 
+// Top-p cut over the k sorted candidates in sh.cand, then p_out[id] = p / kept
+// mass for the kept ones (zeros elsewhere when zero is set; the caller has
+// cleared p_out otherwise). Whole workgroup.
+__device__ void write_kept(const DevSampler* s, int k, float* p_out, int n, bool zero, SampScratch& sh) {
+    const int tid = threadIdx.x;
+    topp_cut(s, nullptr, k, sh);
+    if (zero)
+        for (int i = tid; i < n; i += kST) p_out[i] = 0.f;
+    __syncthreads();
+    const int cut = sh.bcast[4];
+    const float total = sh.fb[0];
+    for (int i = tid; i < cut; i += kST) {
+        const int id = (int)(sh.cand[i] & 0xFFFFFFFFu);
+        p_out[id] = cand_p(sh.cand[i]) / total;  // lg[id] / total
+    }
+    __syncthreads();
+}
+
 // The same transform as sampling, written out as a distribution: p_out holds
 // the kept set renormalised (zeros elsewhere); T <= 0 puts all mass on the
 // argmax. Whole workgroup.
@@ -477,16 +514,7 @@ __device__ void transform_row(const DevSampler* s, float* lg, int n, const int32
         return;
     }
     const int k = topk_sorted(s, lg, n, sh);
-    topp_cut(s, lg, k, sh);
-    for (int i = tid; i < n; i += kST) p_out[i] = 0.f;
-    __syncthreads();
-    const int cut = sh.bcast[4];
-    const float total = sh.fb[0];
-    for (int i = tid; i < cut; i += kST) {
-        const int id = (int)(sh.cand[i] & 0xFFFFFFFFu);
-        p_out[id] = cand_p(sh.cand[i]) / total;  // lg[id] / total
-    }
-    __syncthreads();
+    write_kept(s, k, p_out, n, true, sh);
 }
 
 // First index whose running sum of the positive parts of w(i) reaches
@@ -719,6 +747,380 @@ __global__ __launch_bounds__(kST) void k_draw(DevSampler* s, const float* p, int
     }
 }
 
+// ── the transform split over workgroups ─────────────────────────────────────
+// Same results as transform_row (same kept set; the softmax sum is added in
+// another order, so p may differ in its last bit) for T > 0 and
+// 1 <= top_k <= kTxK, in three launches:
+//  k_tx_max   (slice x row): repeat penalty of the ids in the slice, 1/T,
+//             slice maximum;
+//  k_tx_exp   (slice x row): e = expf(l - row max) as the one-workgroup
+//             softmax forms it, slice sum, and the slice's candidates: every
+//             e >= t (1 - 2^-20), t found by a radix search on the bits of e
+//             such that at least min(top_k, positives) of the slice's e are
+//             >= t. Any e below that bound has top_k others in its slice whose
+//             p = e / sum is strictly larger, since both products are normal
+//             floats rounded once and differ by more than two roundings, so
+//             the row's top_k by (p desc, index asc) are all candidates;
+//  k_tx_final (row): p = e * (1 / sum of the slice sums), the k-th largest p
+//             by radix select over the candidates, the ones >= it sorted,
+//             top-p cut, p_out written; optionally one draw from it.
+// Zero e (exp underflow) never enters: zero-probability candidates change
+// neither the kept mass nor a draw. Other parameters (T <= 0, top_k 0 or
+// above kTxK) take the one-workgroup transform in k_tx_max's first
+// workgroup of each row, and a row with a slice of more than kTxCand
+// candidates (ties) is redone by that transform in k_tx_final from the
+// scaled logits the first launch left in the row.
+
+__device__ __forceinline__ bool tx_split(const DevSampler* s) {
+    return s->temp > 0.f && s->top_k >= 1 && s->top_k <= kTxK;
+}
+
+__global__ __launch_bounds__(kST) void k_tx_max(DevSampler* s, float* lg, int ld, int n, const int32_t* extra,
+                                                 int extra_base, float* p, int ldp) {
+    __shared__ SampScratch sh;
+    const int r = blockIdx.y, g = blockIdx.x, tid = threadIdx.x;
+    float* row = lg + (size_t)r * ld;
+    if (!tx_split(s)) {
+        if (g == 0) transform_row(s, row, n, extra, extra_base + r, p + (size_t)r * ldp, sh);
+        return;
+    }
+    const int b = g * kTxSlice, e = min(n, b + kTxSlice);
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = b + tid + j * kST;
+        v[j] = i < e ? row[i] : -INFINITY;
+    }
+    if (s->pen > 1.f) {
+        // sampler.cpp:15-27: each occurrence of an id in the window divides
+        // (l > 0) or multiplies its logit by the penalty, in window order; an
+        // id's value sees only its own occurrences, so applying them c times
+        // in a row is the same sequence of operations.
+        int* hits = (int*)sh.cand;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hits[tid + j * kST] = 0;
+        __syncthreads();
+        const int L = s->nh + extra_base + r;
+        const int start = L - s->last > 0 ? L - s->last : 0;
+        for (int q = start + tid; q < L; q += kST) {
+            const int32_t id = q < s->nh ? s->hist[q] : extra[q - s->nh];
+            if (id >= b && id < e) atomicAdd(&hits[id - b], 1);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            for (int c = hits[tid + j * kST]; c > 0; --c) v[j] = v[j] > 0.f ? v[j] / s->pen : v[j] * s->pen;
+    }
+    const float T = s->temp;
+    if (T != 1.f) {
+        const float inv_t = 1.f / T;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] *= inv_t;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = b + tid + j * kST;
+        if (i < e) {
+            row[i] = v[j];
+            mx = fmaxf(mx, v[j]);
+        }
+    }
+    mx = block_max(mx, sh);
+    if (tid == 0) {
+        s->tx.mx[r][g] = mx;
+        if (g == 0) s->tx.ovf[r] = 0;
+    }
+}
+
+// Adds to c[d] the number of this wave's keys with (key & mask) == prefix and
+// digit (key >> shift) & 15 == d.
+__device__ __forceinline__ void wave_digits(unsigned int key, bool valid, unsigned int mask, unsigned int prefix,
+                                            int shift, unsigned int (&c)[16]) {
+    const bool m = valid && (key & mask) == prefix;
+    const unsigned int d = (key >> shift) & 15u;
+#pragma unroll
+    for (int b = 0; b < 16; ++b) c[b] += (unsigned int)__popcll(__ballot(m && d == (unsigned int)b));
+}
+
+// One radix step over the workgroup: the waves' digit counts c (wave-uniform)
+// are added up, and the digit of the want-th largest key among those matching
+// the prefix is chosen. *above: keys above the chosen digit's range (counting
+// the ones already above the prefix); returns the keys >= the new prefix.
+// wc: 16 x 16 LDS counters, tot: 16.
+__device__ int radix_step(const unsigned int (&c)[16], int want, int& above, unsigned int& prefix, unsigned int& mask,
+                          int shift, unsigned int* wc, unsigned int* tot) {
+    const int tid = threadIdx.x, w = tid >> 6;
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int b = 0; b < 16; ++b) wc[w * 16 + b] = c[b];
+    __syncthreads();
+    if (tid < 16) {
+        unsigned int t = 0;
+        for (int i = 0; i < kST / 64; ++i) t += wc[i * 16 + tid];
+        tot[tid] = t;
+    }
+    __syncthreads();
+    int cum = 0, sel = 0;
+    for (int b = 15; b >= 0; --b) {
+        const int cb = (int)tot[b];
+        if (above + cum + cb >= want) {
+            sel = b;
+            break;
+        }
+        cum += cb;
+    }
+    const int ge = above + cum + (int)tot[sel];
+    above += cum;
+    prefix |= (unsigned int)sel << shift;
+    mask |= 15u << shift;
+    return ge;
+}
+
+__global__ __launch_bounds__(kST) void k_tx_exp(DevSampler* s, const float* lg, int ld, int n, float* p, int ldp) {
+    if (!tx_split(s)) return;
+    __shared__ unsigned int wc[16 * 16], tot[16];
+    __shared__ float red[kST / 64];
+    __shared__ int ired[kST / 64], slots;
+    const int r = blockIdx.y, g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, G = gridDim.x;
+    TxWork& w = s->tx;
+    float mx = lane < G ? w.mx[r][lane] : -INFINITY;  // G <= 64: one slice maximum per lane
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const int b = g * kTxSlice, e = min(n, b + kTxSlice);
+    const float* row = lg + (size_t)r * ld;
+    float* prow = p + (size_t)r * ldp;
+    float ev[4];
+    float sum = 0.f;
+    int npos = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = b + tid + j * kST;
+        ev[j] = 0.f;
+        if (i < e) {
+            ev[j] = expf(row[i] - mx);
+            prow[i] = 0.f;
+            sum += ev[j];
+            npos += ev[j] > 0.f;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        sum += __shfl_xor(sum, o, 64);
+        npos += __shfl_xor(npos, o, 64);
+    }
+    if (lane == 0) {
+        red[tid >> 6] = sum;
+        ired[tid >> 6] = npos;
+    }
+    if (tid == 0) slots = 0;
+    __syncthreads();
+    npos = 0;
+    for (int i = 0; i < kST / 64; ++i) npos += ired[i];
+    if (tid == 0) {
+        float t = red[0];
+        for (int i = 1; i < kST / 64; ++i) t += red[i];  // fixed order
+        w.sum[r][g] = t;
+    }
+    const int want = min(s->top_k, npos);
+    unsigned int prefix = 0, mask = 0;
+    if (want > 0) {
+        const int stop = max(want, kTxStop);  // candidates the slice may pass on
+        int above = 0;
+        for (int shift = 28; shift >= 0; shift -= 4) {
+            unsigned int c[16] = {};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wave_digits(__builtin_bit_cast(unsigned int, ev[j]), ev[j] > 0.f, mask, prefix, shift, c);
+            if (radix_step(c, want, above, prefix, mask, shift, wc, tot) <= stop) break;
+        }
+        // bound: 2^-20 below the threshold; below 2^-100 every positive e
+        // (p = e / sum could then be subnormal, where rounding is not relative)
+        const float t = __builtin_bit_cast(float, prefix);
+        const float tm = t < 0x1p-100f ? 0.f : t * (1.f - 0x1p-20f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (ev[j] > 0.f && ev[j] >= tm) {
+                const int slot = atomicAdd(&slots, 1);
+                if (slot < kTxCand)
+                    w.cand[r][g][slot] = make_uint2(__builtin_bit_cast(unsigned int, ev[j]), (unsigned int)(b + tid + j * kST));
+            }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        w.nc[r][g] = min(slots, kTxCand);
+        if (slots > kTxCand) w.ovf[r] = 1;
+    }
+}
+
+// Sorts the m <= kST distinct keys src[0 .. m) ascending into dst by rank
+// (each key's count of smaller keys). Whole workgroup; src and dst distinct.
+__device__ void rank_sort(const unsigned long long* src, unsigned long long* dst, int m) {
+    const int tid = threadIdx.x;
+    if (tid < m) {
+        const unsigned long long k = src[tid];
+        int rank = 0;
+        for (int j = 0; j < m; ++j) rank += src[j] < k;
+        dst[rank] = k;
+    }
+    __syncthreads();
+}
+
+// One draw from the kept set sh.cand[0 .. cut) (p_out[id] = p / total), as
+// k_draw does over the whole row: u * (sum of p_out in index order, double),
+// first index where the running sum reaches it, the last one if rounding
+// leaves it short. The set is put in index order first. Whole workgroup.
+__device__ int32_t draw_kept(DevSampler* s, int cut, float total, SampScratch& sh) {
+    const int tid = threadIdx.x;
+    unsigned long long* byid = (unsigned long long*)sh.dscan;  // (index, p_out bits), kST entries
+    unsigned long long* src = byid + kST / 2;
+    static_assert(kTxK <= kST / 2, "kept set fits half of the scan buffer");
+    if (tid < cut) {
+        const unsigned long long c = sh.cand[tid];
+        const float pv = cand_p(c) / total;
+        src[tid] = ((c & 0xFFFFFFFFull) << 32) | __builtin_bit_cast(unsigned int, pv);
+    }
+    __syncthreads();
+    rank_sort(src, byid, cut);
+    if (tid == 0) {
+        const float u = mt_canonical(s);
+        double tot = 0.0;
+        for (int i = 0; i < cut; ++i) {
+            const float pv = __builtin_bit_cast(float, (unsigned int)byid[i]);
+            if (pv > 0.f) tot += (double)pv;
+        }
+        double rr = (double)u * tot;
+        int tok = -1, last = -1;
+        for (int i = 0; i < cut; ++i) {
+            const float pv = __builtin_bit_cast(float, (unsigned int)byid[i]);
+            if (!(pv > 0.f)) continue;
+            last = (int)(byid[i] >> 32);
+            rr -= (double)pv;
+            if (rr <= 0.0) {
+                tok = last;
+                break;
+            }
+        }
+        sh.bcast[3] = tok >= 0 ? tok : max(last, 0);
+    }
+    __syncthreads();
+    const int32_t tok = sh.bcast[3];
+    __syncthreads();
+    return tok;
+}
+
+// The split transform's last step for row blockIdx.x; with DRAW one draw from
+// the row's distribution into out[0] (and out2[0]).
+template <bool DRAW>
+__global__ __launch_bounds__(kST) void k_tx_final(DevSampler* s, float* lg, int ld, int n, float* p, int ldp,
+                                                   int32_t* out, int32_t* out2) {
+    __shared__ SampScratch sh;
+    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    float* prow = p + (size_t)r * ldp;
+    int32_t tok = -1;
+    if (tx_split(s)) {
+        TxWork& w = s->tx;
+        if (w.ovf[r]) {
+            const int k = topk_sorted(s, lg + (size_t)r * ld, n, sh, true);
+            write_kept(s, k, prow, n, false, sh);
+        } else {
+            const int G = (n + kTxSlice - 1) / kTxSlice;
+            // the row sum over the slice sums (fixed order), as every wave forms it
+            float sum = lane < G ? w.sum[r][lane] : 0.f;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+            const float inv_s = 1.f / sum;
+            int* off = (int*)sh.dscan;  // off[0 .. G]: exclusive prefix of the slice counts
+            if (tid < 64) {
+                const int c = tid < G ? w.nc[r][tid] : 0;
+                int inc = c;  // inclusive scan over the wave
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int t = __shfl_up(inc, o, 64);
+                    if (tid >= o) inc += t;
+                }
+                if (tid <= G) off[tid] = inc - c;
+            }
+            __syncthreads();
+            const int N = off[G];
+            // gather, wave w taking slices w, w + 16, ...: key = ~bits(p) << 32 |
+            // index (p desc, index asc)
+            for (int g = tid >> 6; g < G; g += kST / 64) {
+                const int c0 = off[g], nc = off[g + 1] - c0;
+#pragma unroll
+                for (int j = lane; j < kTxCand; j += 64)
+                    if (j < nc) {
+                        const uint2 c = w.cand[r][g][j];
+                        const float pv = __builtin_bit_cast(float, c.x) * inv_s;
+                        sh.cand[c0 + j] = ((unsigned long long)(~__builtin_bit_cast(unsigned int, pv)) << 32) | c.y;
+                    }
+            }
+            __syncthreads();
+            // a prefix of p bits that the k-th largest p has and at most kRank
+            // candidates reach (the k-th largest itself when ties leave more)
+            const int k = min(s->top_k, n);
+            const int want = min(k, N);
+            constexpr int kRank = 256;
+            unsigned int prefix = 0, mask = 0;
+            int above = 0;
+            unsigned int* wc = sh.hist;
+            unsigned int* tot = (unsigned int*)sh.ired;
+            if (N > kRank)
+                for (int shift = 28; shift >= 0; shift -= 4) {
+                    unsigned int c[16] = {};
+                    for (int i0 = 0; i0 < N; i0 += kST) {
+                        const int i = i0 + tid;
+                        const unsigned int pk = i < N ? ~(unsigned int)(sh.cand[i] >> 32) : 0u;
+                        wave_digits(pk, i < N, mask, prefix, shift, c);
+                    }
+                    if (radix_step(c, want, above, prefix, mask, shift, wc, tot) <= kRank) break;
+                }
+            // every candidate of the row's top k has p >= thr; sorted, the first
+            // k of them are the ones the one-workgroup transform sorts first
+            const unsigned int thr = prefix;
+            if (tid == 0) sh.bcast[2] = 0;
+            __syncthreads();
+            unsigned long long* sel = (unsigned long long*)sh.dscan + 32;  // after off[]
+            constexpr int kSel = kST - 32;
+            static_assert((kTxMaxG + 1) * sizeof(int) <= 32 * sizeof(double), "offsets before the selection");
+            for (int i = tid; i < N; i += kST) {
+                const unsigned long long c = sh.cand[i];
+                if (~(unsigned int)(c >> 32) >= thr) {
+                    const int slot = atomicAdd(&sh.bcast[2], 1);
+                    if (slot < kSel) sel[slot] = c;
+                }
+            }
+            __syncthreads();
+            const int m0 = sh.bcast[2];
+            if (m0 <= kSel) {
+                rank_sort(sel, sh.cand, m0);
+            } else {  // many ties at the threshold: sort the whole candidate list
+                for (int i = tid; i < N; i += kST)
+                    if (~(unsigned int)(sh.cand[i] >> 32) < thr) sh.cand[i] = ~0ull;
+                int mp = 1;
+                while (mp < N) mp <<= 1;
+                for (int i = N + tid; i < mp; i += kST) sh.cand[i] = ~0ull;
+                __syncthreads();
+                bitonic_sort(sh, mp);
+            }
+            const int kk = min(k, m0);
+            write_kept(s, kk, prow, n, false, sh);
+            if (DRAW) tok = draw_kept(s, sh.bcast[4], sh.fb[0], sh);
+        }
+    }
+    if (DRAW) {
+        if (tok < 0) {  // the transform was the one-workgroup one: draw over the row as k_draw does
+            const float u = lane0_uniform(s, sh);
+            const double tt = block_total(prow, n, sh);
+            tok = block_pick(n, [&](int i) { return prow[i]; }, (double)u * tt, sh);
+        }
+        if (tid == 0) {
+            out[0] = tok;
+            if (out2) out2[0] = tok;
+        }
+    }
+}
+
 __global__ __launch_bounds__(kST) void k_accept_resample(const float* p, const float* q, int n, int32_t x,
                                                           float u_acc, float u_res, int32_t* out) {
     __shared__ SampScratch sh;
@@ -815,6 +1217,20 @@ static int check_vocab(const void* d_state, int n_vocab, const char* who) {
 
 extern "C" size_t orc_sampler_state_bytes(void) { return sizeof(DevSampler); }
 
+// Rows the split transform takes: at most kTxRows of at most kTxMaxG slices.
+static bool tx_shape(int n, int rows) { return rows <= kTxRows && n <= kTxMaxG * kTxSlice; }
+
+static void launch_tx(DevSampler* st, float* lg, int ld, int n, int rows, const int32_t* extra, int extra_base,
+                      float* p, int ldp, int32_t* out, int32_t* out2, hipStream_t s) {
+    const dim3 grid((n + kTxSlice - 1) / kTxSlice, rows);
+    hipLaunchKernelGGL(k_tx_max, grid, dim3(kST), 0, s, st, lg, ld, n, extra, extra_base, p, ldp);
+    hipLaunchKernelGGL(k_tx_exp, grid, dim3(kST), 0, s, st, (const float*)lg, ld, n, p, ldp);
+    if (out)
+        hipLaunchKernelGGL(k_tx_final<true>, dim3(rows), dim3(kST), 0, s, st, lg, ld, n, p, ldp, out, out2);
+    else
+        hipLaunchKernelGGL(k_tx_final<false>, dim3(rows), dim3(kST), 0, s, st, lg, ld, n, p, ldp, out, out2);
+}
+
 extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty,
                                 int repeat_last, uint64_t seed, const int32_t* d_hist, int n_hist,
                                 orc_stream_t s) {
@@ -907,8 +1323,33 @@ extern "C" int orc_transform_probs(const void* d_state, float* d_logits, int ld,
         extra_base < 0 || ((extra_base + rows > 1) && !d_extra))
         return set_error(ORC_E_INVALID, "transform_probs: bad args");
     if (int rc = check_vocab(d_state, n_vocab, "transform_probs")) return rc;
-    hipLaunchKernelGGL(k_transform, dim3(rows), dim3(kST), 0, resolve_stream(s), (const DevSampler*)d_state,
-                       d_logits, ld, n_vocab, d_extra, extra_base, d_p, ldp);
+    if (tx_shape(n_vocab, rows)) {
+        launch_tx((DevSampler*)const_cast<void*>(d_state), d_logits, ld, n_vocab, rows, d_extra, extra_base, d_p, ldp,
+                  nullptr, nullptr, resolve_stream(s));
+    } else {
+        hipLaunchKernelGGL(k_transform, dim3(rows), dim3(kST), 0, resolve_stream(s), (const DevSampler*)d_state,
+                           d_logits, ld, n_vocab, d_extra, extra_base, d_p, ldp);
+    }
+    ORC_LAUNCH_CHECK();
+    return ORC_OK;
+}
+
+extern "C" int orc_transform_draw(void* d_state, float* d_logits, int n_vocab, const int32_t* d_extra, int n_extra,
+                                  float* d_p, int32_t* d_out, int32_t* d_out2, orc_stream_t s) {
+    if (!initialized()) return set_error(ORC_E_NOINIT, "orc_init not called");
+    if (!d_state || !d_logits || !d_p || !d_out || n_vocab <= 0 || n_extra < 0 || (n_extra && !d_extra))
+        return set_error(ORC_E_INVALID, "transform_draw: bad args");
+    if (int rc = check_vocab(d_state, n_vocab, "transform_draw")) return rc;
+    const hipStream_t st = resolve_stream(s);
+    if (tx_shape(n_vocab, 1)) {
+        launch_tx((DevSampler*)d_state, d_logits, n_vocab, n_vocab, 1, d_extra, n_extra, d_p, n_vocab, d_out, d_out2,
+                  st);
+    } else {
+        hipLaunchKernelGGL(k_transform, dim3(1), dim3(kST), 0, st, (const DevSampler*)d_state, d_logits, n_vocab,
+                           n_vocab, d_extra, n_extra, d_p, n_vocab);
+        hipLaunchKernelGGL(k_draw, dim3(1), dim3(kST), 0, st, (DevSampler*)d_state, (const float*)d_p, n_vocab, d_out,
+                           d_out2);
+    }
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

@@ -422,8 +422,8 @@ int DecodeSession::sampled_round(Model& tgt, Model& dft, int k, int V) {
     for (int i = 0; i < k; ++i) {
         float* q = d_q_ + (size_t)i * V;
         if (int rc = dft.forward_dev_at(d_vin_ + i, 1, d_pos_, i, true, nullptr)) return rc;
-        if (int rc = orc_transform_probs(d_samp_, dft.d_logits(), V, V, 1, d_vin_ + 1, i, q, V, nullptr)) return rc;
-        if (int rc = orc_draw(d_samp_, q, V, d_vin_ + i + 1, nullptr, nullptr)) return rc;
+        if (int rc = orc_transform_draw(d_samp_, dft.d_logits(), V, d_vin_ + 1, i, q, d_vin_ + i + 1, nullptr, nullptr))
+            return rc;
     }
     if (int rc = tgt.forward_dev_at(d_vin_, k + 1, d_pos_, 0, true, nullptr)) return rc;
     if (int rc = orc_transform_probs(d_samp_, tgt.d_logits(), V, V, k + 1, d_vin_ + 1, 0, d_p_, V, nullptr)) return rc;

@@ -99,6 +99,7 @@ ABI = [
                                          _vp]),
     ("orc_transform_probs", C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int, _vp]),
     ("orc_draw", C.c_int, [_vp, _vp, C.c_int, _vp, _vp, _vp]),
+    ("orc_transform_draw", C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, _vp, _vp, _vp, _vp]),
     ("orc_accept_resample", C.c_int, [_vp, _vp, C.c_int, C.c_int32, C.c_float, C.c_float, _vp, _vp]),
     ("orc_spec_accept_stochastic", C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
                                              _vp, _vp, _vp, _vp]),

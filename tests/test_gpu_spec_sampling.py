@@ -56,21 +56,11 @@ CASES = [  # (V, T, top_p, top_k, penalty, repeat_last)
 ]
 
 
-@pytest.mark.parametrize("case", CASES)
-def test_transform_probs_matches_oracle(dev, oracle, case):
-    """orc_transform_probs over several rows, each with its own pending
-    proposals in the penalty window, equals the oracle's transform."""
-    V, T, P, K, pen, last = case
-    print(f"[gpu] transform V={V} T={T} top_p={P} top_k={K}", flush=True)
+def _check_transform(dev, oracle, lg, T, P, K, pen, last, hist, extra, base):
+    """orc_transform_probs over the rows of lg against the oracle's transform
+    of each row (row r's window: hist + extra[:base + r])."""
     L = dev.L
-    rng = np.random.default_rng(V + K)
-    rows = 4
-    lg = rng.normal(0, 3, (rows, V)).astype(np.float32)
-    hist = rng.integers(0, V, 150).astype(np.int32)
-    hist[:40] = rng.integers(0, 50, 40)  # repeats compound
-    extra = rng.integers(0, 60, rows + 2).astype(np.int32)
-    lg[:, :60] += 4.0  # the penalised ids matter to the kept set
-    base = 2
+    rows, V = lg.shape
     state = dev.alloc(L.orc_sampler_state_bytes())
     dh, dx = dev.upload(hist), dev.upload(extra)
     dl, dp = dev.upload(lg), dev.alloc(lg.nbytes)
@@ -84,6 +74,108 @@ def test_transform_probs_matches_oracle(dev, oracle, case):
         ref = _oracle_probs(oracle, lg[r], T, P, K, pen, _window(oracle, s, extra[:base + r], last))
         assert np.array_equal(got[r] > 0, ref > 0), r
         assert np.abs(got[r] - ref).max() <= 2e-6, (r, np.abs(got[r] - ref).max())
+    oracle.L.orco_sampler_free(s)
+
+
+def _penalty_rows(V, rows, n_hist, seed):
+    rng = np.random.default_rng(seed)
+    lg = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    hist = rng.integers(0, V, n_hist).astype(np.int32)
+    hist[:40] = rng.integers(0, 50, 40)  # repeats compound
+    extra = rng.integers(0, 60, rows + 2).astype(np.int32)
+    lg[:, :60] += 4.0  # the penalised ids matter to the kept set
+    return lg, hist, extra
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_transform_probs_matches_oracle(dev, oracle, case):
+    """orc_transform_probs over several rows, each with its own pending
+    proposals in the penalty window, equals the oracle's transform."""
+    V, T, P, K, pen, last = case
+    print(f"[gpu] transform V={V} T={T} top_p={P} top_k={K}", flush=True)
+    lg, hist, extra = _penalty_rows(V, 4, 150, V + K)
+    _check_transform(dev, oracle, lg, T, P, K, pen, last, hist, extra, 2)
+
+
+# The split transform (T > 0, 1 <= top_k <= 128, up to 17 rows of up to
+# 196608 logits in slices of 4096): a partial last slice, the largest
+# vocabulary, top_k 1 and 128, a peaked distribution whose tail underflows
+# to zero, a penalty window longer than 256 entries.
+SPLIT_CASES = [  # (V, T, top_p, top_k, penalty, repeat_last, history)
+    (16385, 0.8, 0.95, 40, 1.1, 64, 150),
+    (151936, 0.3, 0.5, 1, 1.3, 256, 150),
+    (151936, 1.0, 0.99, 128, 1.0, 64, 150),
+    (196608, 1.7, 0.9, 100, 1.2, 16, 150),
+    (128256, 0.05, 0.95, 40, 1.1, 64, 150),
+    (151936, 0.8, 0.95, 40, 1.1, 3000, 2900),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_transform_split_matches_oracle(dev, oracle, case):
+    V, T, P, K, pen, last, n_hist = case
+    print(f"[gpu] split transform V={V} T={T} top_p={P} top_k={K} window={last}", flush=True)
+    lg, hist, extra = _penalty_rows(V, 3, n_hist, V + K + n_hist)
+    _check_transform(dev, oracle, lg, T, P, K, pen, last, hist, extra, 2)
+
+
+@pytest.mark.parametrize("rows", [1, 17, 18])
+def test_transform_ties_and_row_counts(dev, oracle, rows):
+    """Rows of tied logits: 9000 equal maxima (slices with thousands of tied
+    candidates: the row is redone by the one-workgroup transform), logits on
+    a 0.5 grid (~1900 ties at the top value spread over every slice), and a
+    plain row; 17 rows (the most the split path takes) and 18 (the
+    one-workgroup kernel)."""
+    print(f"[gpu] transform ties rows={rows}", flush=True)
+    V = 151936
+    rng = np.random.default_rng(rows)
+    lg = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    for r in range(rows):
+        if r % 3 == 0:
+            lg[r, 5000:14000] = lg[r].max() + 1.0
+        elif r % 3 == 1:
+            lg[r] = rng.integers(-20, 20, V) * 0.5
+    hist = rng.integers(0, V, 100).astype(np.int32)
+    extra = rng.integers(0, V, rows + 1).astype(np.int32)
+    _check_transform(dev, oracle, lg, 0.9, 0.95, 40, 1.1, 64, hist, extra, 1)
+
+
+@pytest.mark.parametrize("V,K", [(2048, 40), (2048, 0), (151936, 40), (151936, 0)])
+def test_transform_draw_matches_oracle(dev, oracle, V, K):
+    """orc_transform_draw: the distribution as orc_transform_probs writes it
+    and, call after call, the oracle's draw (orco_pick with the oracle's
+    mt19937 uniform) from that distribution; top_k 0 takes the
+    one-workgroup transform and draw. top_k 0 at V > 16384 is refused as
+    orc_transform_probs refuses it."""
+    print(f"[gpu] transform_draw V={V} top_k={K}", flush=True)
+    L = dev.L
+    rng = np.random.default_rng(V + 11)
+    T, P, pen, last = 0.8, 0.95, 1.1, 64
+    state = dev.alloc(L.orc_sampler_state_bytes())
+    hist = rng.integers(0, V, 80).astype(np.int32)
+    dh = dev.upload(hist)
+    dev.check(L.orc_sampler_init(state.ptr, T, P, K, pen, last, 31, dh.ptr, hist.size, None))
+    dp, do = dev.alloc(V * 4), dev.alloc(8)
+    if K == 0 and V > 16384:
+        dl = dev.upload(rng.normal(0, 2, V).astype(np.float32))
+        assert L.orc_transform_draw(state.ptr, dl.ptr, V, None, 0, dp.ptr, do.ptr, None, None) != 0
+        return
+    s = oracle.L.orco_sampler_new(T, P, K, pen, last, 31)
+    for h in hist:
+        oracle.L.orco_sampler_record(s, int(h))
+    extra = rng.integers(0, 100, 8).astype(np.int32)
+    dx = dev.upload(extra)
+    for call in range(8):
+        lg = rng.normal(0, 2, V).astype(np.float32)
+        lg[:100] += 2.0
+        dl = dev.upload(lg)
+        dev.check(L.orc_transform_draw(state.ptr, dl.ptr, V, dx.ptr, call, dp.ptr, do.ptr, do.ptr + 4, None))
+        got = dp.read(np.float32)
+        ref = _oracle_probs(oracle, lg, T, P, K, pen, _window(oracle, s, extra[:call], last))
+        assert np.array_equal(got > 0, ref > 0), call
+        assert np.abs(got - ref).max() <= 2e-6, call
+        tok = oracle.L.orco_pick(ol.fptr(got), V, _uniform(oracle, s))
+        assert list(do.read(np.int32, 2)) == [tok, tok], call
     oracle.L.orco_sampler_free(s)
 
 
