@@ -109,9 +109,9 @@ __device__ void record_tok(DevSampler* s, int32_t tok) {
 struct SampScratch {
     float red[kST / 64];
     int ired[kST / 64];
-    unsigned int hist[256];
+    unsigned int hist[512];
     int bcast[8];
-    float fb[2];
+    float fb[4];  // [2]: the split transform's uniform, [3]: its top_p
     double dscan[kST];
     unsigned long long cand[kCandMax];
 };
@@ -833,45 +833,50 @@ __global__ __launch_bounds__(kST) void k_tx_max(DevSampler* s, float* lg, int ld
     }
 }
 
-// Adds to c[d] the number of this wave's keys with (key & mask) == prefix and
-// digit (key >> shift) & 15 == d.
-__device__ __forceinline__ void wave_digits(unsigned int key, bool valid, unsigned int mask, unsigned int prefix,
-                                            int shift, unsigned int (&c)[16]) {
-    const bool m = valid && (key & mask) == prefix;
-    const unsigned int d = (key >> shift) & 15u;
-#pragma unroll
-    for (int b = 0; b < 16; ++b) c[b] += (unsigned int)__popcll(__ballot(m && d == (unsigned int)b));
+// Radix steps over a workgroup, 4-bit digits: each wave counts its keys'
+// digits into its own 16 counters of one half of wc (2 x 16 x 16 LDS
+// counters, the half by pass parity, so one barrier per pass).
+// radix_buf clears this wave's counters of the pass (before its radix_count
+// calls: a wave's LDS operations complete in order).
+__device__ __forceinline__ unsigned int* radix_buf(unsigned int* wc, int shift) {
+    unsigned int* buf = wc + ((shift >> 2) & 1) * 256 + (threadIdx.x >> 6) * 16;
+    if ((threadIdx.x & 63) < 16) buf[threadIdx.x & 63] = 0;
+    return buf;
+}
+__device__ __forceinline__ void radix_count(unsigned int key, bool valid, unsigned int mask, unsigned int prefix,
+                                            int shift, unsigned int* buf) {
+    if (valid && (key & mask) == prefix) atomicAdd(&buf[(key >> shift) & 15u], 1u);
 }
 
-// One radix step over the workgroup: the waves' digit counts c (wave-uniform)
-// are added up, and the digit of the want-th largest key among those matching
-// the prefix is chosen. *above: keys above the chosen digit's range (counting
-// the ones already above the prefix); returns the keys >= the new prefix.
-// wc: 16 x 16 LDS counters, tot: 16.
-__device__ int radix_step(const unsigned int (&c)[16], int want, int& above, unsigned int& prefix, unsigned int& mask,
-                          int shift, unsigned int* wc, unsigned int* tot) {
-    const int tid = threadIdx.x, w = tid >> 6;
-    if ((tid & 63) == 0)
+// The counters are added up and the digit of the want-th largest key among
+// those matching the prefix is chosen (want >= 1). above: keys above the
+// chosen digit's range (counting the ones already above the prefix); returns
+// the keys >= the new prefix. Every wave adds the counters up and selects by
+// itself.
+__device__ int radix_step(int want, int& above, unsigned int& prefix, unsigned int& mask, int shift,
+                          const unsigned int* wc) {
+    const int lane = threadIdx.x & 63;
+    static_assert(kST / 64 == 16, "sixteen waves");
+    const unsigned int* buf = wc + ((shift >> 2) & 1) * 256;
+    __syncthreads();
+    // lane l: digit l & 15 over waves l >> 4, + 4, + 8, + 12, then over the
+    // four lane groups: every lane holds the count of its digit
+    const int d = lane & 15, g = lane >> 4;
+    unsigned int t = buf[g * 16 + d] + buf[(g + 4) * 16 + d] + buf[(g + 8) * 16 + d] + buf[(g + 12) * 16 + d];
+    t += __shfl_xor(t, 16, 64);
+    t += __shfl_xor(t, 32, 64);
+    // count of digits d .. 15
+    unsigned int sfx = t;
 #pragma unroll
-        for (int b = 0; b < 16; ++b) wc[w * 16 + b] = c[b];
-    __syncthreads();
-    if (tid < 16) {
-        unsigned int t = 0;
-        for (int i = 0; i < kST / 64; ++i) t += wc[i * 16 + tid];
-        tot[tid] = t;
+    for (int o = 1; o < 16; o <<= 1) {
+        const unsigned int v = __shfl_down(sfx, o, 16);
+        if (d + o < 16) sfx += v;
     }
-    __syncthreads();
-    int cum = 0, sel = 0;
-    for (int b = 15; b >= 0; --b) {
-        const int cb = (int)tot[b];
-        if (above + cum + cb >= want) {
-            sel = b;
-            break;
-        }
-        cum += cb;
-    }
-    const int ge = above + cum + (int)tot[sel];
-    above += cum;
+    // digits 0 .. sel reach want (the suffix counts fall with d)
+    const int sel = max(__popcll(__ballot(lane < 16 && above + (int)sfx >= want)) - 1, 0);
+    const int s_sel = (int)__shfl(sfx, sel, 64), t_sel = (int)__shfl(t, sel, 64);
+    const int ge = above + s_sel;
+    above += s_sel - t_sel;
     prefix |= (unsigned int)sel << shift;
     mask |= 15u << shift;
     return ge;
@@ -879,7 +884,7 @@ __device__ int radix_step(const unsigned int (&c)[16], int want, int& above, uns
 
 __global__ __launch_bounds__(kST) void k_tx_exp(DevSampler* s, const float* lg, int ld, int n, float* p, int ldp) {
     if (!tx_split(s)) return;
-    __shared__ unsigned int wc[16 * 16], tot[16];
+    __shared__ unsigned int wc[2 * 16 * 16];
     __shared__ float red[kST / 64];
     __shared__ int ired[kST / 64], slots;
     const int r = blockIdx.y, g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, G = gridDim.x;
@@ -892,7 +897,7 @@ __global__ __launch_bounds__(kST) void k_tx_exp(DevSampler* s, const float* lg, 
     float* prow = p + (size_t)r * ldp;
     float ev[4];
     float sum = 0.f;
-    int npos = 0;
+    int npos = 0;  // positive e, + 2^16 x those below 2^-31 (top key nibble under 3)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = b + tid + j * kST;
@@ -901,7 +906,7 @@ __global__ __launch_bounds__(kST) void k_tx_exp(DevSampler* s, const float* lg, 
             ev[j] = expf(row[i] - mx);
             prow[i] = 0.f;
             sum += ev[j];
-            npos += ev[j] > 0.f;
+            npos += ev[j] > 0.f ? (ev[j] < 0x1p-31f ? 0x10001 : 1) : 0;
         }
     }
 #pragma unroll
@@ -917,6 +922,8 @@ __global__ __launch_bounds__(kST) void k_tx_exp(DevSampler* s, const float* lg, 
     __syncthreads();
     npos = 0;
     for (int i = 0; i < kST / 64; ++i) npos += ired[i];
+    const bool nib3 = (npos >> 16) == 0;  // every positive e has key nibble 3 (2^-31 <= e <= 1)
+    npos &= 0xFFFF;
     if (tid == 0) {
         float t = red[0];
         for (int i = 1; i < kST / 64; ++i) t += red[i];  // fixed order
@@ -927,12 +934,16 @@ __global__ __launch_bounds__(kST) void k_tx_exp(DevSampler* s, const float* lg, 
     if (want > 0) {
         const int stop = max(want, kTxStop);  // candidates the slice may pass on
         int above = 0;
-        for (int shift = 28; shift >= 0; shift -= 4) {
-            unsigned int c[16] = {};
+        if (nib3) {
+            prefix = 0x30000000u;
+            mask = 0xF0000000u;
+        }
+        for (int shift = nib3 ? 24 : 28; shift >= 0; shift -= 4) {
+            unsigned int* buf = radix_buf(wc, shift);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                wave_digits(__builtin_bit_cast(unsigned int, ev[j]), ev[j] > 0.f, mask, prefix, shift, c);
-            if (radix_step(c, want, above, prefix, mask, shift, wc, tot) <= stop) break;
+                radix_count(__builtin_bit_cast(unsigned int, ev[j]), ev[j] > 0.f, mask, prefix, shift, buf);
+            if (radix_step(want, above, prefix, mask, shift, wc) <= stop) break;
         }
         // bound: 2^-20 below the threshold; below 2^-100 every positive e
         // (p = e / sum could then be subnormal, where rounding is not relative)
@@ -966,11 +977,46 @@ __device__ void rank_sort(const unsigned long long* src, unsigned long long* dst
     __syncthreads();
 }
 
+// lane i's value of v (i uniform over the wave)
+__device__ __forceinline__ float rdlane(float v, int i) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), i));
+}
+__device__ __forceinline__ unsigned long long rdlane(unsigned long long v, int i) {
+    const unsigned int lo = (unsigned int)__builtin_amdgcn_readlane((int)(unsigned int)v, i);
+    const unsigned int hi = (unsigned int)__builtin_amdgcn_readlane((int)(unsigned int)(v >> 32), i);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// topp_cut on wave 0 for k <= 128 candidates: the same running float sum in
+// candidate order, the values read from the lanes instead of one at a time
+// from LDS. Ends with a workgroup barrier.
+__device__ void topp_cut_wave(float top_p, int k, SampScratch& sh) {
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const float a = tid < k ? cand_p(sh.cand[tid]) : 0.f;
+        const float b = tid + 64 < k ? cand_p(sh.cand[tid + 64]) : 0.f;
+        float cum = 0.f;
+        int cut = k;
+        for (int i = 0; i < k; ++i) {
+            cum += i < 64 ? rdlane(a, i) : rdlane(b, i - 64);
+            if (cum >= top_p) {
+                cut = i + 1;
+                break;
+            }
+        }
+        if (tid == 0) {
+            sh.bcast[4] = cut;
+            sh.fb[0] = cum;  // the kept mass: the same sum over the first cut
+        }
+    }
+    __syncthreads();
+}
+
 // One draw from the kept set sh.cand[0 .. cut) (p_out[id] = p / total), as
 // k_draw does over the whole row: u * (sum of p_out in index order, double),
 // first index where the running sum reaches it, the last one if rounding
 // leaves it short. The set is put in index order first. Whole workgroup.
-__device__ int32_t draw_kept(DevSampler* s, int cut, float total, SampScratch& sh) {
+__device__ int32_t draw_kept(float u, int cut, float total, SampScratch& sh) {
     const int tid = threadIdx.x;
     unsigned long long* byid = (unsigned long long*)sh.dscan;  // (index, p_out bits), kST entries
     unsigned long long* src = byid + kST / 2;
@@ -982,26 +1028,28 @@ __device__ int32_t draw_kept(DevSampler* s, int cut, float total, SampScratch& s
     }
     __syncthreads();
     rank_sort(src, byid, cut);
-    if (tid == 0) {
-        const float u = mt_canonical(s);
+    if (tid < 64) {  // wave 0, the entries passed between lanes
+        const unsigned long long ea = tid < cut ? byid[tid] : 0ull, eb = tid + 64 < cut ? byid[tid + 64] : 0ull;
+        auto entry = [&](int i) { return i < 64 ? rdlane(ea, i) : rdlane(eb, i - 64); };
         double tot = 0.0;
         for (int i = 0; i < cut; ++i) {
-            const float pv = __builtin_bit_cast(float, (unsigned int)byid[i]);
+            const float pv = __builtin_bit_cast(float, (unsigned int)entry(i));
             if (pv > 0.f) tot += (double)pv;
         }
         double rr = (double)u * tot;
         int tok = -1, last = -1;
         for (int i = 0; i < cut; ++i) {
-            const float pv = __builtin_bit_cast(float, (unsigned int)byid[i]);
+            const unsigned long long c = entry(i);
+            const float pv = __builtin_bit_cast(float, (unsigned int)c);
             if (!(pv > 0.f)) continue;
-            last = (int)(byid[i] >> 32);
+            last = (int)(c >> 32);
             rr -= (double)pv;
             if (rr <= 0.0) {
                 tok = last;
                 break;
             }
         }
-        sh.bcast[3] = tok >= 0 ? tok : max(last, 0);
+        if (tid == 0) sh.bcast[3] = tok >= 0 ? tok : max(last, 0);
     }
     __syncthreads();
     const int32_t tok = sh.bcast[3];
@@ -1020,19 +1068,27 @@ __global__ __launch_bounds__(kST) void k_tx_final(DevSampler* s, float* lg, int 
     int32_t tok = -1;
     if (tx_split(s)) {
         TxWork& w = s->tx;
-        if (w.ovf[r]) {
+        const int G = (n + kTxSlice - 1) / kTxSlice;
+        const float sv = lane < G ? w.sum[r][lane] : 0.f;  // loads issued together
+        const int ncv = lane < G ? w.nc[r][lane] : 0;
+        const bool ovf = w.ovf[r] != 0;
+        if (tid == 0 && !ovf) {  // through LDS, so both are read before the merge's first barrier
+            sh.fb[2] = DRAW ? mt_canonical(s) : 0.f;
+            sh.fb[3] = s->top_p;
+        }
+        if (ovf) {
             const int k = topk_sorted(s, lg + (size_t)r * ld, n, sh, true);
             write_kept(s, k, prow, n, false, sh);
         } else {
-            const int G = (n + kTxSlice - 1) / kTxSlice;
             // the row sum over the slice sums (fixed order), as every wave forms it
-            float sum = lane < G ? w.sum[r][lane] : 0.f;
+            float sum = sv;
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
             const float inv_s = 1.f / sum;
             int* off = (int*)sh.dscan;  // off[0 .. G]: exclusive prefix of the slice counts
+            if (tid == 0) sh.bcast[6] = 0;  // set when a candidate's p is below 2^-31
             if (tid < 64) {
-                const int c = tid < G ? w.nc[r][tid] : 0;
+                const int c = ncv;
                 int inc = c;  // inclusive scan over the wave
 #pragma unroll
                 for (int o = 1; o < 64; o <<= 1) {
@@ -1052,29 +1108,32 @@ __global__ __launch_bounds__(kST) void k_tx_final(DevSampler* s, float* lg, int 
                     if (j < nc) {
                         const uint2 c = w.cand[r][g][j];
                         const float pv = __builtin_bit_cast(float, c.x) * inv_s;
+                        if (pv < 0x1p-31f) sh.bcast[6] = 1;
                         sh.cand[c0 + j] = ((unsigned long long)(~__builtin_bit_cast(unsigned int, pv)) << 32) | c.y;
                     }
             }
             __syncthreads();
-            // a prefix of p bits that the k-th largest p has and at most kRank
-            // candidates reach (the k-th largest itself when ties leave more)
+            // a prefix of p bits that the k-th largest p has and at most
+            // max(k, kRank) candidates reach (the k-th largest itself when ties
+            // leave more)
             const int k = min(s->top_k, n);
             const int want = min(k, N);
-            constexpr int kRank = 256;
+            constexpr int kRank = 64;
             unsigned int prefix = 0, mask = 0;
             int above = 0;
-            unsigned int* wc = sh.hist;
-            unsigned int* tot = (unsigned int*)sh.ired;
-            if (N > kRank)
-                for (int shift = 28; shift >= 0; shift -= 4) {
-                    unsigned int c[16] = {};
-                    for (int i0 = 0; i0 < N; i0 += kST) {
-                        const int i = i0 + tid;
-                        const unsigned int pk = i < N ? ~(unsigned int)(sh.cand[i] >> 32) : 0u;
-                        wave_digits(pk, i < N, mask, prefix, shift, c);
-                    }
-                    if (radix_step(c, want, above, prefix, mask, shift, wc, tot) <= kRank) break;
+            if (N > max(want, kRank)) {
+                const bool nib3 = sh.bcast[6] == 0;  // p <= 1: key nibble 3 unless p < 2^-31
+                if (nib3) {
+                    prefix = 0x30000000u;
+                    mask = 0xF0000000u;
                 }
+                for (int shift = nib3 ? 24 : 28; shift >= 0; shift -= 4) {
+                    unsigned int* buf = radix_buf(sh.hist, shift);
+                    for (int i = tid; i < N; i += kST)
+                        radix_count(~(unsigned int)(sh.cand[i] >> 32), true, mask, prefix, shift, buf);
+                    if (radix_step(want, above, prefix, mask, shift, sh.hist) <= max(want, kRank)) break;
+                }
+            }
             // every candidate of the row's top k has p >= thr; sorted, the first
             // k of them are the ones the one-workgroup transform sorts first
             const unsigned int thr = prefix;
@@ -1104,8 +1163,14 @@ __global__ __launch_bounds__(kST) void k_tx_final(DevSampler* s, float* lg, int 
                 bitonic_sort(sh, mp);
             }
             const int kk = min(k, m0);
-            write_kept(s, kk, prow, n, false, sh);
-            if (DRAW) tok = draw_kept(s, sh.bcast[4], sh.fb[0], sh);
+            topp_cut_wave(sh.fb[3], kk, sh);
+            const int cut = sh.bcast[4];
+            const float total = sh.fb[0];
+            for (int i = tid; i < cut; i += kST) {
+                const int id = (int)(sh.cand[i] & 0xFFFFFFFFu);
+                prow[id] = cand_p(sh.cand[i]) / total;
+            }
+            if (DRAW) tok = draw_kept(sh.fb[2], cut, total, sh);
         }
     }
     if (DRAW) {
