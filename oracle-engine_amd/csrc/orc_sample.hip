@@ -53,6 +53,9 @@ struct TxWork {
     float sum[kTxRows][kTxMaxG];  // slice sums of exp(l - max)
     int nc[kTxRows][kTxMaxG];     // candidates per slice
     int ovf[kTxRows];             // a slice had more than kTxCand candidates
+    int cut[kTxRows];             // kept set of each row (list mode)
+    float total[kTxRows];         // its mass
+    uint2 kept[kTxRows][kTxK];    // (index, bits of p), sorted by (p desc, index asc)
     uint2 cand[kTxRows][kTxMaxG][kTxCand];  // (bits of exp(l - max), index)
 };
 
@@ -303,6 +306,21 @@ __device__ void penalize(const DevSampler* s, float* lg, int n, const int32_t* e
     __syncthreads();
     if (tid < m && first[tid] == tid && id >= 0 && id < n) lg[id] = __builtin_bit_cast(float, (uint32_t)sh.cand[tid]);
     __syncthreads();
+}
+
+// lane i's value of v (i uniform over the wave)
+__device__ __forceinline__ float rdlane(float v, int i) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), i));
+}
+__device__ __forceinline__ unsigned long long rdlane(unsigned long long v, int i) {
+    const unsigned int lo = (unsigned int)__builtin_amdgcn_readlane((int)(unsigned int)v, i);
+    const unsigned int hi = (unsigned int)__builtin_amdgcn_readlane((int)(unsigned int)(v >> 32), i);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// The parameters the split transform takes (T > 0, 1 <= top_k <= kTxK).
+__device__ __forceinline__ bool tx_split(const DevSampler* s) {
+    return s->temp > 0.f && s->top_k >= 1 && s->top_k <= kTxK;
 }
 
 // probability held in a candidate key (~bits(p) << 32 | index)
@@ -664,11 +682,71 @@ __global__ void k_sampler_record(DevSampler* s, const int32_t* tok, int n) {
 // out: [0] emitted, [1] accepted, [2] rows sampled (target forwards of the
 // reference loop), [3] 1 if all drafts were accepted and the bonus emitted,
 // [4 ..] the emitted ids. With d_pos / d_next the device round state advances.
+// With split set and the split transform's parameters, the rows' kept sets
+// were written by k_tx_max<true> / k_tx_exp / k_tx_final<2> (row i's window
+// assumes proposals 0 .. i-1 accepted, the only case in which row i is
+// sampled) and wave 0 draws from them: r = u * mass, r -= p down the sorted
+// set, the first candidate if rounding leaves r > 0 (sampler.cpp:78-85).
 __global__ __launch_bounds__(kST) void k_accept_engine(DevSampler* s, float* logits, int ld, int n_vocab,
                                                         const int32_t* draft, int n_draft, int max_emit,
                                                         int32_t* d_budget, int32_t* out, int32_t* d_pos,
-                                                        int32_t* d_next) {
+                                                        int32_t* d_next, int split) {
     __shared__ SampScratch sh;
+    if (split && tx_split(s)) {
+        if (threadIdx.x >= 64) return;
+        const int lane = threadIdx.x;
+        const TxWork& w = s->tx;
+        if (d_budget) max_emit = *d_budget;
+        int emitted = 0, accepted = 0, rows = 0, all = 0;
+        int32_t last_tok = 0;
+        for (int i = 0; i <= n_draft && emitted < max_emit; ++i) {
+            const int cut = w.cut[i];
+            const float total = w.total[i];
+            const uint2 ea = lane < cut ? w.kept[i][lane] : make_uint2(0u, 0u);
+            const uint2 eb = lane + 64 < cut ? w.kept[i][lane + 64] : make_uint2(0u, 0u);
+            float u = 0.f;
+            if (lane == 0) u = mt_canonical(s);
+            float rr = rdlane(u, 0) * total;
+            int32_t tok = cut > 0 ? (int32_t)__builtin_amdgcn_readlane((int)ea.x, 0) : 0;
+            for (int j = 0; j < cut; ++j) {
+                const uint2 c = j < 64 ? make_uint2((unsigned int)__builtin_amdgcn_readlane((int)ea.x, j),
+                                                    (unsigned int)__builtin_amdgcn_readlane((int)ea.y, j))
+                                       : make_uint2((unsigned int)__builtin_amdgcn_readlane((int)eb.x, j - 64),
+                                                    (unsigned int)__builtin_amdgcn_readlane((int)eb.y, j - 64));
+                rr -= __builtin_bit_cast(float, c.y);
+                if (rr <= 0.f) {
+                    tok = (int32_t)c.x;
+                    break;
+                }
+            }
+            ++rows;
+            if (lane == 0) {
+                record_tok(s, tok);  // Sampler::sample's own record
+                record_tok(s, tok);  // the Engine's second record
+                out[4 + emitted] = tok;
+            }
+            ++emitted;
+            last_tok = tok;
+            if (i == n_draft) {
+                all = 1;
+                break;
+            }
+            if (tok != draft[i]) break;
+            ++accepted;
+        }
+        if (lane == 0) {
+            out[0] = emitted;
+            out[1] = accepted;
+            out[2] = rows;
+            out[3] = all;
+            if (d_pos) {
+                *d_pos += emitted;
+                *d_next = last_tok;
+            }
+            if (d_budget) *d_budget -= emitted;
+        }
+        return;
+    }
     if (d_budget) max_emit = *d_budget;
     int emitted = 0, accepted = 0, rows = 0, all = 0;
     int32_t last_tok = 0;
@@ -771,17 +849,18 @@ __global__ __launch_bounds__(kST) void k_draw(DevSampler* s, const float* p, int
 // candidates (ties) is redone by that transform in k_tx_final from the
 // scaled logits the first launch left in the row.
 
-__device__ __forceinline__ bool tx_split(const DevSampler* s) {
-    return s->temp > 0.f && s->top_k >= 1 && s->top_k <= kTxK;
-}
-
+// ENG (the Engine rule's rows, list mode): row r's window is the history
+// plus extra[0], extra[0], ..., extra[r-1], extra[r-1] (the proposals an
+// accepted prefix records twice each); other parameters are left to the
+// one-workgroup acceptance kernel.
+template <bool ENG>
 __global__ __launch_bounds__(kST) void k_tx_max(DevSampler* s, float* lg, int ld, int n, const int32_t* extra,
                                                  int extra_base, float* p, int ldp) {
     __shared__ SampScratch sh;
     const int r = blockIdx.y, g = blockIdx.x, tid = threadIdx.x;
     float* row = lg + (size_t)r * ld;
     if (!tx_split(s)) {
-        if (g == 0) transform_row(s, row, n, extra, extra_base + r, p + (size_t)r * ldp, sh);
+        if (!ENG && g == 0) transform_row(s, row, n, extra, extra_base + r, p + (size_t)r * ldp, sh);
         return;
     }
     const int b = g * kTxSlice, e = min(n, b + kTxSlice);
@@ -800,10 +879,10 @@ __global__ __launch_bounds__(kST) void k_tx_max(DevSampler* s, float* lg, int ld
 #pragma unroll
         for (int j = 0; j < 4; ++j) hits[tid + j * kST] = 0;
         __syncthreads();
-        const int L = s->nh + extra_base + r;
+        const int L = s->nh + (ENG ? 2 * r : extra_base + r);
         const int start = L - s->last > 0 ? L - s->last : 0;
         for (int q = start + tid; q < L; q += kST) {
-            const int32_t id = q < s->nh ? s->hist[q] : extra[q - s->nh];
+            const int32_t id = q < s->nh ? s->hist[q] : extra[(q - s->nh) >> (ENG ? 1 : 0)];
             if (id >= b && id < e) atomicAdd(&hits[id - b], 1);
         }
         __syncthreads();
@@ -904,7 +983,7 @@ __global__ __launch_bounds__(kST) void k_tx_exp(DevSampler* s, const float* lg, 
         ev[j] = 0.f;
         if (i < e) {
             ev[j] = expf(row[i] - mx);
-            prow[i] = 0.f;
+            if (p) prow[i] = 0.f;
             sum += ev[j];
             npos += ev[j] > 0.f ? (ev[j] < 0x1p-31f ? 0x10001 : 1) : 0;
         }
@@ -977,16 +1056,6 @@ __device__ void rank_sort(const unsigned long long* src, unsigned long long* dst
     __syncthreads();
 }
 
-// lane i's value of v (i uniform over the wave)
-__device__ __forceinline__ float rdlane(float v, int i) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), i));
-}
-__device__ __forceinline__ unsigned long long rdlane(unsigned long long v, int i) {
-    const unsigned int lo = (unsigned int)__builtin_amdgcn_readlane((int)(unsigned int)v, i);
-    const unsigned int hi = (unsigned int)__builtin_amdgcn_readlane((int)(unsigned int)(v >> 32), i);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
 // topp_cut on wave 0 for k <= 128 candidates: the same running float sum in
 // candidate order, the values read from the lanes instead of one at a time
 // from LDS. Ends with a workgroup barrier.
@@ -1057,11 +1126,28 @@ __device__ int32_t draw_kept(float u, int cut, float total, SampScratch& sh) {
     return tok;
 }
 
-// The split transform's last step for row blockIdx.x; with DRAW one draw from
-// the row's distribution into out[0] (and out2[0]).
-template <bool DRAW>
+// The kept set sh.cand[0 .. sh.bcast[4]) (at most kTxK) and its mass
+// sh.fb[0] into the state's list of row r.
+__device__ void keep_list(TxWork& w, int r, SampScratch& sh) {
+    const int cut = sh.bcast[4];
+    for (int i = threadIdx.x; i < cut; i += kST) {
+        const unsigned long long c = sh.cand[i];
+        w.kept[r][i] = make_uint2((unsigned int)(c & 0xFFFFFFFFu), __builtin_bit_cast(unsigned int, cand_p(c)));
+    }
+    if (threadIdx.x == 0) {
+        w.cut[r] = cut;
+        w.total[r] = sh.fb[0];
+    }
+}
+
+// The split transform's last step for row blockIdx.x. MODE 0: p written;
+// 1: p written and one draw from it into out[0] (and out2[0]); 2 (list): the
+// kept set, its mass and size go to the state's scratch for
+// k_accept_engine, p is not written.
+template <int MODE>
 __global__ __launch_bounds__(kST) void k_tx_final(DevSampler* s, float* lg, int ld, int n, float* p, int ldp,
                                                    int32_t* out, int32_t* out2) {
+    constexpr bool DRAW = MODE == 1, LIST = MODE == 2;
     __shared__ SampScratch sh;
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     float* prow = p + (size_t)r * ldp;
@@ -1078,7 +1164,13 @@ __global__ __launch_bounds__(kST) void k_tx_final(DevSampler* s, float* lg, int 
         }
         if (ovf) {
             const int k = topk_sorted(s, lg + (size_t)r * ld, n, sh, true);
-            write_kept(s, k, prow, n, false, sh);
+            if (LIST) {
+                topp_cut(s, nullptr, k, sh);
+                __syncthreads();
+                keep_list(w, r, sh);
+            } else {
+                write_kept(s, k, prow, n, false, sh);
+            }
         } else {
             // the row sum over the slice sums (fixed order), as every wave forms it
             float sum = sv;
@@ -1166,9 +1258,13 @@ __global__ __launch_bounds__(kST) void k_tx_final(DevSampler* s, float* lg, int 
             topp_cut_wave(sh.fb[3], kk, sh);
             const int cut = sh.bcast[4];
             const float total = sh.fb[0];
-            for (int i = tid; i < cut; i += kST) {
-                const int id = (int)(sh.cand[i] & 0xFFFFFFFFu);
-                prow[id] = cand_p(sh.cand[i]) / total;
+            if (LIST) {
+                keep_list(w, r, sh);
+            } else {
+                for (int i = tid; i < cut; i += kST) {
+                    const int id = (int)(sh.cand[i] & 0xFFFFFFFFu);
+                    prow[id] = cand_p(sh.cand[i]) / total;
+                }
             }
             if (DRAW) tok = draw_kept(sh.fb[2], cut, total, sh);
         }
@@ -1285,15 +1381,22 @@ extern "C" size_t orc_sampler_state_bytes(void) { return sizeof(DevSampler); }
 // Rows the split transform takes: at most kTxRows of at most kTxMaxG slices.
 static bool tx_shape(int n, int rows) { return rows <= kTxRows && n <= kTxMaxG * kTxSlice; }
 
+// The split transform: p (and, with out, one draw) or, without p, the kept
+// lists of the Engine rule's rows (extra = the proposals).
 static void launch_tx(DevSampler* st, float* lg, int ld, int n, int rows, const int32_t* extra, int extra_base,
                       float* p, int ldp, int32_t* out, int32_t* out2, hipStream_t s) {
     const dim3 grid((n + kTxSlice - 1) / kTxSlice, rows);
-    hipLaunchKernelGGL(k_tx_max, grid, dim3(kST), 0, s, st, lg, ld, n, extra, extra_base, p, ldp);
-    hipLaunchKernelGGL(k_tx_exp, grid, dim3(kST), 0, s, st, (const float*)lg, ld, n, p, ldp);
-    if (out)
-        hipLaunchKernelGGL(k_tx_final<true>, dim3(rows), dim3(kST), 0, s, st, lg, ld, n, p, ldp, out, out2);
+    if (p)
+        hipLaunchKernelGGL(k_tx_max<false>, grid, dim3(kST), 0, s, st, lg, ld, n, extra, extra_base, p, ldp);
     else
-        hipLaunchKernelGGL(k_tx_final<false>, dim3(rows), dim3(kST), 0, s, st, lg, ld, n, p, ldp, out, out2);
+        hipLaunchKernelGGL(k_tx_max<true>, grid, dim3(kST), 0, s, st, lg, ld, n, extra, 0, p, ldp);
+    hipLaunchKernelGGL(k_tx_exp, grid, dim3(kST), 0, s, st, (const float*)lg, ld, n, p, ldp);
+    if (!p)
+        hipLaunchKernelGGL(k_tx_final<2>, dim3(rows), dim3(kST), 0, s, st, lg, ld, n, p, ldp, out, out2);
+    else if (out)
+        hipLaunchKernelGGL(k_tx_final<1>, dim3(rows), dim3(kST), 0, s, st, lg, ld, n, p, ldp, out, out2);
+    else
+        hipLaunchKernelGGL(k_tx_final<0>, dim3(rows), dim3(kST), 0, s, st, lg, ld, n, p, ldp, out, out2);
 }
 
 extern "C" int orc_sampler_init(void* d_state, float temperature, float top_p, int top_k, float repeat_penalty,
@@ -1375,8 +1478,12 @@ extern "C" int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, in
         (max_emit < 1 && !d_budget) || (!d_pos) != (!d_next))
         return set_error(ORC_E_INVALID, "accept_engine: bad args");
     if (int rc = check_vocab(d_state, n_vocab, "accept_engine")) return rc;
+    const int split = tx_shape(n_vocab, n_draft + 1);
+    if (split)
+        launch_tx((DevSampler*)d_state, d_logits, ld, n_vocab, n_draft + 1, d_draft, 0, nullptr, 0, nullptr, nullptr,
+                  resolve_stream(s));
     hipLaunchKernelGGL(k_accept_engine, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_logits,
-                       ld, n_vocab, d_draft, n_draft, max_emit, d_budget, d_out, d_pos, d_next);
+                       ld, n_vocab, d_draft, n_draft, max_emit, d_budget, d_out, d_pos, d_next, split);
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }
