@@ -56,6 +56,11 @@ struct TxWork {
     int cut[kTxRows];             // kept set of each row (list mode)
     float total[kTxRows];         // its mass
     uint2 kept[kTxRows][kTxK];    // (index, bits of p), sorted by (p desc, index asc)
+    // the acceptance chain split over workgroups (k_chain_*)
+    int ch_mode, ch_row, ch_emitted, ch_accepted, ch_max;  // mode 0: no draw, 1: residual, 2: bonus
+    float ch_u;
+    double ch_sum[kTxMaxG];  // slice sums of the draw's weights
+    int ch_last[kTxMaxG];    // last positive weight of each slice (-1: none)
     uint2 cand[kTxRows][kTxMaxG][kTxCand];  // (bits of exp(l - max), index)
 };
 
@@ -1350,6 +1355,222 @@ __global__ __launch_bounds__(kST) void k_accept_chain(DevSampler* s, const float
     }
 }
 
+// ── the acceptance chain split over workgroups ──────────────────────────────
+// k_accept_chain's rule in three launches: k_chain_scan walks the
+// acceptance tests in order on one wave (the uniforms in the same order,
+// accepted ids recorded); it ends at the first rejection (residual draw from
+// max(0, p_i - q_i)), after k acceptances (bonus draw from p_k) or at the
+// emission limit (no draw). k_chain_part sums the draw's weights per slice of
+// kTxSlice entries (double; contiguous runs of four per thread, then the
+// threads in order); k_chain_pick finds the slice and then the entry where
+// the running sum reaches u * total (first entry whose cumulative sum is
+// >= the target; the last positive one when rounding leaves the target
+// unreached; argmax of p_i when the residual is empty), records it and
+// writes the outputs. The sums associate differently from the one-workgroup
+// kernel's chunks; both are double sums of the same float weights.
+__global__ __launch_bounds__(64) void k_chain_scan(DevSampler* s, const float* p, int ldp, const float* q, int ldq,
+                                                   const int32_t* x, int k, int max_emit, const int32_t* d_budget,
+                                                   int32_t* out) {
+    const int lane = threadIdx.x;
+    TxWork& w = s->tx;
+    if (d_budget) max_emit = *d_budget;
+    int emitted = 0, accepted = 0, mode = 0, row = -1;
+    float u = 0.f;
+    for (int i = 0; i <= k && emitted < max_emit; ++i) {
+        float ua = 0.f;
+        if (lane == 0) ua = mt_canonical(s);
+        ua = rdlane(ua, 0);
+        if (i == k) {
+            mode = 2;
+            row = k;
+            u = ua;
+            break;
+        }
+        const int32_t xi = x[i];
+        const float qx = q[(size_t)i * ldq + xi], px = p[(size_t)i * ldp + xi];
+        if (qx > 0.f && ua * qx < px) {
+            if (lane == 0) {
+                record_tok(s, xi);
+                out[4 + emitted] = xi;
+            }
+            ++emitted;
+            ++accepted;
+            continue;
+        }
+        float ur = 0.f;
+        if (lane == 0) ur = mt_canonical(s);
+        mode = 1;
+        row = i;
+        u = rdlane(ur, 0);
+        break;
+    }
+    if (lane == 0) {
+        w.ch_mode = mode;
+        w.ch_row = row;
+        w.ch_u = u;
+        w.ch_emitted = emitted;
+        w.ch_accepted = accepted;
+        w.ch_max = max_emit;
+    }
+}
+
+// the draw's weight of entry j: positive part of p_i - q_i (residual) or p_k
+__device__ __forceinline__ float chain_w(int mode, const float* pr, const float* qr, int j) {
+    const float d = mode == 1 ? pr[j] - qr[j] : pr[j];
+    return d > 0.f ? d : 0.f;
+}
+
+__global__ __launch_bounds__(kST) void k_chain_part(DevSampler* s, const float* p, int ldp, const float* q, int ldq,
+                                                    int n) {
+    TxWork& w = s->tx;
+    const int mode = w.ch_mode;
+    if (mode == 0) return;
+    __shared__ double red[kST / 64];
+    __shared__ int lred[kST / 64];
+    const int g = blockIdx.x, tid = threadIdx.x, row = w.ch_row;
+    const float* pr = p + (size_t)row * ldp;
+    const float* qr = mode == 1 ? q + (size_t)row * ldq : nullptr;
+    const int b = g * kTxSlice + 4 * tid;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = b + j < n ? chain_w(mode, pr, qr, b + j) : 0.f;
+    double loc = 0.0;
+    int last = -1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (v[j] > 0.f) {
+            loc += (double)v[j];
+            last = b + j;
+        }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        loc += __shfl_xor(loc, o, 64);
+        last = max(last, __shfl_xor(last, o, 64));
+    }
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = loc;
+        lred[tid >> 6] = last;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double t = 0.0;
+        int l = -1;
+        for (int i = 0; i < kST / 64; ++i) {  // waves in order
+            t += red[i];
+            l = max(l, lred[i]);
+        }
+        w.ch_sum[g] = t;
+        w.ch_last[g] = l;
+    }
+}
+
+__global__ __launch_bounds__(kST) void k_chain_pick(DevSampler* s, const float* p, int ldp, const float* q, int ldq,
+                                                    int n, int k, int32_t* d_budget, int32_t* out, int32_t* d_pos,
+                                                    int32_t* d_next) {
+    __shared__ SampScratch sh;
+    TxWork& w = s->tx;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int mode = w.ch_mode, row = w.ch_row;
+    int emitted = w.ch_emitted;
+    const int accepted = w.ch_accepted;
+    int32_t tok = -1;
+    if (mode != 0) {
+        const float* pr = p + (size_t)row * ldp;
+        const float* qr = mode == 1 ? q + (size_t)row * ldq : nullptr;
+        const int G = (n + kTxSlice - 1) / kTxSlice;
+        // slice sums: exclusive prefix in slice order, total (every wave alike)
+        const double sg = lane < G ? w.ch_sum[lane] : 0.0;
+        const int lg_ = lane < G ? w.ch_last[lane] : -1;
+        double inc = sg;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const double t = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += t;
+        }
+        const double pre = inc - sg;
+        const double total = __shfl(inc, 63, 64);
+        int lastpos = lg_;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) lastpos = max(lastpos, __shfl_xor(lastpos, o, 64));
+        if (mode == 1 && !(total > 0.0)) {
+            tok = block_argmax(pr, n, sh);  // empty residual
+        } else {
+            const double target = (double)w.ch_u * total;
+            // the slice holding the target: first one with weight whose range
+            // (pre, pre + sum] contains it (target <= 0: the first with weight)
+            const bool hit = lane < G && sg > 0.0 && (target <= 0.0 ? pre == 0.0 : (pre < target && target <= inc));
+            const unsigned long long hb = __ballot(hit);
+            if (hb == 0) {
+                tok = max(lastpos, 0);  // rounding left the target unreached
+            } else {
+                const int gs = __ffsll((long long)hb) - 1;
+                const double r0 = target - __shfl(pre, gs, 64);
+                // inside the slice: runs of four per thread, prefix in thread order
+                const int b = gs * kTxSlice + 4 * tid;
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = b + j < n ? chain_w(mode, pr, qr, b + j) : 0.f;
+                double loc = 0.0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) loc += (double)v[j];
+                sh.dscan[tid] = loc;
+                if (tid == 0) sh.bcast[5] = 0x7FFFFFFF;
+                __syncthreads();
+                if (tid < 64) {  // exclusive prefix over the threads, 16 per lane
+                    double run = 0.0;
+                    for (int i = 0; i < kST / 64; ++i) run += sh.dscan[tid * (kST / 64) + i];
+                    double sc = run;
+#pragma unroll
+                    for (int o = 1; o < 64; o <<= 1) {
+                        const double t = __shfl_up(sc, o, 64);
+                        if (tid >= o) sc += t;
+                    }
+                    double at = sc - run;
+                    for (int i = 0; i < kST / 64; ++i) {
+                        const double c = sh.dscan[tid * (kST / 64) + i];
+                        sh.dscan[tid * (kST / 64) + i] = at;
+                        at += c;
+                    }
+                }
+                __syncthreads();
+                const double tp = sh.dscan[tid];
+                if (loc > 0.0 && (r0 <= 0.0 ? tp == 0.0 : (tp < r0 && r0 <= tp + loc))) {
+                    double rr = r0 - tp;
+                    int got = -1, lastp = -1;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (v[j] > 0.f) {
+                            lastp = b + j;
+                            rr -= (double)v[j];
+                            if (rr <= 0.0 && got < 0) got = b + j;
+                        }
+                    atomicMin(&sh.bcast[5], got >= 0 ? got : lastp);
+                }
+                __syncthreads();
+                tok = sh.bcast[5] != 0x7FFFFFFF ? sh.bcast[5] : max(w.ch_last[gs], 0);
+            }
+        }
+    }
+    if (tid == 0) {
+        int all = 0;
+        if (mode != 0) {
+            record_tok(s, tok);
+            out[4 + emitted] = tok;
+            ++emitted;
+            all = mode == 2;
+        }
+        out[0] = emitted;
+        out[1] = accepted;
+        out[2] = emitted;
+        out[3] = all;
+        if (d_pos) {
+            *d_pos += emitted;
+            *d_next = emitted > 0 ? out[4 + emitted - 1] : 0;  // the last emitted id
+        }
+        if (d_budget) *d_budget -= emitted;
+    }
+}
+
 __global__ void k_sampler_history(const DevSampler* s, int32_t* out, int cap, int32_t* n_out) {
     if (threadIdx.x != 0) return;
     const int n = s->nh < cap ? s->nh : cap;
@@ -1554,8 +1775,19 @@ extern "C" int orc_spec_accept_stochastic(void* d_state, const float* d_p, int l
     if (!d_state || !d_p || !d_out || n_vocab <= 0 || ldp < n_vocab || k < 0 || (k && (!d_q || !d_x || ldq < n_vocab)) ||
         (max_emit < 1 && !d_budget) || (!d_pos) != (!d_next))
         return set_error(ORC_E_INVALID, "accept_stochastic: bad args");
-    hipLaunchKernelGGL(k_accept_chain, dim3(1), dim3(kST), 0, resolve_stream(s), (DevSampler*)d_state, d_p, ldp, d_q,
-                       ldq, n_vocab, d_x, k, max_emit, d_budget, d_out, d_pos, d_next);
+    const hipStream_t st = resolve_stream(s);
+    DevSampler* ds = (DevSampler*)d_state;
+    if (n_vocab <= kTxMaxG * kTxSlice) {
+        hipLaunchKernelGGL(k_chain_scan, dim3(1), dim3(64), 0, st, ds, d_p, ldp, d_q, ldq, d_x, k, max_emit,
+                           (const int32_t*)d_budget, d_out);
+        hipLaunchKernelGGL(k_chain_part, dim3((n_vocab + kTxSlice - 1) / kTxSlice), dim3(kST), 0, st, ds, d_p, ldp,
+                           d_q, ldq, n_vocab);
+        hipLaunchKernelGGL(k_chain_pick, dim3(1), dim3(kST), 0, st, ds, d_p, ldp, d_q, ldq, n_vocab, k, d_budget,
+                           d_out, d_pos, d_next);
+    } else {
+        hipLaunchKernelGGL(k_accept_chain, dim3(1), dim3(kST), 0, st, ds, d_p, ldp, d_q, ldq, n_vocab, d_x, k,
+                           max_emit, d_budget, d_out, d_pos, d_next);
+    }
     ORC_LAUNCH_CHECK();
     return ORC_OK;
 }

@@ -207,21 +207,23 @@ def test_draw_and_accept_resample_match_oracle(dev, oracle):
     oracle.L.orco_sampler_free(s)
 
 
-@pytest.mark.parametrize("k", [1, 3, 6])
-def test_accept_chain_matches_oracle(dev, oracle, k):
+@pytest.mark.parametrize("k,V", [(1, 1024), (3, 1024), (6, 1024), (3, 151936), (6, 196608)])
+def test_accept_chain_matches_oracle(dev, oracle, k, V):
     """orc_spec_accept_stochastic over many rounds (accepts, rejections,
     bonus draws, budget cuts) equals the oracle's chain: emitted ids,
-    counts, the round state and the sampler history."""
+    counts, the round state and the sampler history. The draw's weights are
+    summed per slice of 4096 entries; the large vocabularies put the kept
+    sets in many slices."""
     L = dev.L
-    rng = np.random.default_rng(k)
-    V = 1024
+    rng = np.random.default_rng(k + V)
+    print(f"[gpu] accept chain k={k} V={V}", flush=True)
     state = dev.alloc(L.orc_sampler_state_bytes())
     dev.check(L.orc_sampler_init(state.ptr, 0.8, 0.95, 40, 1.1, 64, 1234, None, 0, None))
     s = oracle.L.orco_sampler_new(0.8, 0.95, 40, 1.1, 64, 1234)
     dout, dpos = dev.alloc((k + 8) * 4), dev.alloc(8)
     budget = dev.alloc(4)
     paths = {"accept": 0, "reject": 0, "bonus": 0}
-    for rnd in range(40):
+    for rnd in range(40 if V <= 4096 else 12):
         base = rng.normal(0, 2, V)
         # target and draft close enough that every path occurs
         p = np.stack([_oracle_probs(oracle, base + rng.normal(0, 0.3 + 0.1 * (rnd % 5), V), 1.0, 0.99, 30, 1.0, [])
@@ -251,7 +253,7 @@ def test_accept_chain_matches_oracle(dev, oracle, k):
         paths["accept"] += acc.value
         paths["bonus"] += al.value
         paths["reject"] += n - acc.value - al.value
-    assert min(paths.values()) > 0, paths
+    assert min(paths.values()) > 0 if V <= 4096 else paths["reject"] > 0, paths
     hn, hd = dev.alloc(4), dev.alloc(4 * 512)
     dev.check(L.orc_sampler_history(state.ptr, hd.ptr, 512, hn.ptr, None))
     nh = int(hn.read(np.int32, 1)[0])
