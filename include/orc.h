@@ -356,7 +356,12 @@ int orc_sampler_clear_history(void* d_state, orc_stream_t stream);
  * decremented). d_out: [0] emitted, [1] accepted, [2] rows sampled (the
  * reference's target forwards), [3] 1 if all drafts matched (the caller then
  * refills the draft's KV), [4..] the emitted ids (k+5 ints). With d_pos and
- * d_next the round state advances: *d_pos += emitted, *d_next = last id. */
+ * d_next the round state advances: *d_pos += emitted, *d_next = last id.
+ * Up to 16 proposals, vocabularies up to 196608, T > 0 and
+ * 1 <= top_k <= 128: every row's kept set is computed up front (row i's
+ * penalty window is the history plus proposals 0 .. i-1 twice each, the only
+ * case in which it is sampled) into the state's scratch, then drawn from in
+ * row order; calls on one state must not overlap. */
 int orc_spec_accept_engine(void* d_state, float* d_logits, int ld, int n_vocab, const int32_t* d_draft, int n_draft,
                            int max_emit, int32_t* d_budget, int32_t* d_out, int32_t* d_pos, int32_t* d_next,
                            orc_stream_t stream);
@@ -398,7 +403,9 @@ int orc_accept_resample(const float* d_p, const float* d_q, int n_vocab, int32_t
  * emits a residual draw and ends the round; when all k are accepted a bonus
  * id is drawn from p_k. Uniforms come from the state's mt19937 (acceptance,
  * then the residual or bonus draw); each emitted id is recorded once.
- * d_out layout, budget and round state as orc_spec_accept_engine. */
+ * d_out layout, budget and round state as orc_spec_accept_engine. Rows of up
+ * to 196608 entries keep the draw's partial sums in the state's scratch:
+ * calls on one state must not overlap. */
 int orc_spec_accept_stochastic(void* d_state, const float* d_p, int ldp, const float* d_q, int ldq, int n_vocab,
                                const int32_t* d_x, int k, int max_emit, int32_t* d_budget, int32_t* d_out,
                                int32_t* d_pos, int32_t* d_next, orc_stream_t stream);
