@@ -1258,35 +1258,53 @@ __global__ __launch_bounds__(wg_waves<HD>() * 64) void k_attn_wg(const float* qk
 #pragma unroll
         for (int k = 0; k < DPL; ++k) O[r][k] = 0.f;
     }
-    // V of a pass's positions (this lane's DPL dims) and its K rows
-    float vv[16][DPL];
-    float4 k[FL];
-    auto load_pass = [&](int b0, int nb) {
+    // V of a pass's positions (this lane's DPL dims) and its K rows; head_dim
+    // 64 (at most two passes: 16 waves, 512 positions) holds both passes'
+    // rows, so the second pass's loads are in flight with the first
+    constexpr bool PF = HD == 64;
+    static_assert(!PF || kWGMax <= 2 * 16 * kWW, "head_dim 64: at most two passes per wave");
+    float vv[16][DPL], vv2[PF ? 16 : 1][DPL];
+    float4 k[FL], k2[PF ? FL : 1];
+    auto load_pass = [&](auto& vb, auto& kb, int b0, int nb) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int p = b0 + j;
             const float* src = p < start ? vg + (size_t)p * HD : qkv + (size_t)(p - start) * ldqkv + vvh;
 #pragma unroll
-            for (int kk = 0; kk < DPL; ++kk) vv[j][kk] = 0.f;
+            for (int kk = 0; kk < DPL; ++kk) vb[j][kk] = 0.f;
             if (j < nb) {
                 if constexpr (DPL == 2) {
                     const float2 v2 = *(const float2*)(src + 2 * lane);
-                    vv[j][0] = v2.x;
-                    vv[j][1] = v2.y;
+                    vb[j][0] = v2.x;
+                    vb[j][1] = v2.y;
                 } else {
-                    vv[j][0] = src[lane];
+                    vb[j][0] = src[lane];
                 }
             }
         }
-        load_k(k, b0 + sp, sp < nb);
+        load_k(kb, b0 + sp, sp < nb);
     };
     // the first pass's loads are in flight while the query heads are rotated
-    if (p0 < p1) load_pass(p0, min(16, p1 - p0));
+    if (p0 < p1) load_pass(vv, k, p0, min(16, p1 - p0));
+    if constexpr (PF) {
+        if (p0 + 16 < p1) load_pass(vv2, k2, p0 + 16, min(16, p1 - p0 - 16));
+    }
     qrot.store(Qs, tid);
     __syncthreads();  // Qs written
     for (int b0 = p0; b0 < p1; b0 += 16) {
         const int nb = min(16, p1 - b0);
-        if (b0 != p0) load_pass(b0, nb);
+        if (b0 != p0) {
+            if constexpr (PF) {  // the second pass (the last one at head_dim 64): its rows are loaded
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+#pragma unroll
+                    for (int kk = 0; kk < DPL; ++kk) vv[j][kk] = vv2[j][kk];
+#pragma unroll
+                for (int j = 0; j < FL; ++j) k[j] = k2[j];
+            } else {
+                load_pass(vv, k, b0, nb);
+            }
+        }
 #pragma unroll
         for (int r = 0; r < RM; ++r) {
             if (r >= RH) break;
