@@ -76,6 +76,15 @@ struct XCtx {
 };
 
 // Bytes of two dwords as 8 floats: byte k of a -> w[k], of b -> w[4+k].
+// v unchanged, but opaque to the optimiser: a nibble word masked with
+// 0x0F0F0F0F then converted byte by byte stays one AND per word and one
+// v_cvt_f32_ubyteN per value, instead of the mask folded into a v_bfe_u32
+// per value in front of a v_cvt_f32_ubyte0 (twice the conversion work).
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
 __device__ __forceinline__ void to_f8(uint32_t a, uint32_t b, float* w) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -133,16 +142,21 @@ template <int ROWS> struct Unit<ORC_Q4_K, ROWS> {
             q[r] = ld16(blk + 16 + 16 * ch);
         }
     }
+    // the nibbles of the chunk words at bit sh (0: low, 4: high), masked right
+    // before their conversion
     template <int NT>
-    __device__ __forceinline__ void half(const uint32_t (&m)[ROWS][4], int e, const float (&dd)[ROWS],
-                                         const float (&mm)[ROWS], const XCtx& c, float (&acc)[ROWS][NT]) const {
+    __device__ __forceinline__ void half(int sh, int e, const float (&dd)[ROWS], const float (&mm)[ROWS],
+                                         const XCtx& c, float (&acc)[ROWS][NT]) const {
         float S[ROWS][NT];
         zero(S);
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             float w[ROWS][8];
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) to_f8(m[r][2 * k], m[r][2 * k + 1], w[r]);
+            for (int r = 0; r < ROWS; ++r) {
+                const uint32_t a = k ? q[r].z : q[r].x, b = k ? q[r].w : q[r].y;
+                to_f8(opaque((a >> sh) & 0x0F0F0F0Fu), opaque((b >> sh) & 0x0F0F0F0Fu), w[r]);
+            }
             dot8(w, c, padx<64>(e + 8 * k), S);
         }
 #pragma unroll
@@ -160,7 +174,6 @@ template <int ROWS> struct Unit<ORC_Q4_K, ROWS> {
         const int b = u >> 3, ch = u & 7, j = ch >> 1, h = ch & 1;
         const int eA = b * 256 + 64 * j + 16 * h - c.k0;
         float dA[ROWS], mA[ROWS], dB[ROWS], mB[ROWS];
-        uint32_t lo[ROWS][4], hi[ROWS][4];
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
             const float d = h2f(hdr[r].x & 0xFFFFu), dmin = h2f(hdr[r].x >> 16);
@@ -171,15 +184,9 @@ template <int ROWS> struct Unit<ORC_Q4_K, ROWS> {
             mA[r] = dmin * (float)m0;
             dB[r] = d * (float)s1;
             mB[r] = dmin * (float)m1;
-            const uint32_t qq[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                lo[r][i] = qq[i] & 0x0F0F0F0Fu;
-                hi[r][i] = (qq[i] >> 4) & 0x0F0F0F0Fu;
-            }
         }
-        half<NT>(lo, eA, dA, mA, c, acc);
-        half<NT>(hi, eA + 32, dB, mB, c, acc);
+        half<NT>(0, eA, dA, mA, c, acc);
+        half<NT>(4, eA + 32, dB, mB, c, acc);
     }
 };
 
@@ -335,8 +342,8 @@ template <int ROWS> struct Unit<ORC_Q4_0, ROWS> {
             for (int r = 0; r < ROWS; ++r) {
                 const uint32_t qq[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
                 const uint32_t a = qq[2 * (k & 1)], b = qq[2 * (k & 1) + 1];
-                if (k < 2) to_f8(a & 0x0F0F0F0Fu, b & 0x0F0F0F0Fu, w[r]);
-                else to_f8((a >> 4) & 0x0F0F0F0Fu, (b >> 4) & 0x0F0F0F0Fu, w[r]);
+                if (k < 2) to_f8(opaque(a & 0x0F0F0F0Fu), opaque(b & 0x0F0F0F0Fu), w[r]);
+                else to_f8(opaque((a >> 4) & 0x0F0F0F0Fu), opaque((b >> 4) & 0x0F0F0F0Fu), w[r]);
             }
             dot8(w, c, p0 + 8 * k, S);
         }
