@@ -8,14 +8,16 @@
 // residual resampling (no reference counterpart).
 //
 // One 1024-thread workgroup samples one row of logits, in place as the
-// reference does (the row ends up holding the probabilities):
+// reference does (the row ends up holding the probabilities); the transform
+// and the acceptance chain also run split over many workgroups (below):
 //  * repeat penalty over the device-resident history, one entry at a time
 //    (repeated ids compound), then temperature (skipped for T <= 0 or 1);
 //  * T <= 0: first index of the maximum;
 //  * otherwise softmax: block max, block sum of expf(l - max), p = e * (1/sum);
-//  * top-k by an exact 4-pass radix select on the bits of p (p >= 0, so the
-//    bit patterns order like the values), then the candidates (p >= the k-th
-//    value) are sorted by (p desc, index asc) with a bitonic sort in LDS;
+//  * top-k by an exact radix select on the bits of p (eight 4-bit digits;
+//    p >= 0, so the bit patterns order like the values), then the candidates
+//    (p >= the k-th value) are sorted by (p desc, index asc) with a bitonic
+//    sort in LDS;
 //    at most 16384 candidates (top_k = 0, "all tokens" in the reference, is
 //    exact for vocabularies up to that size; the entry points refuse a
 //    larger vocabulary with ORC_E_UNSUPPORTED for a state initialised with
@@ -844,9 +846,12 @@ __global__ __launch_bounds__(kST) void k_draw(DevSampler* s, const float* p, int
 //             p = e / sum is strictly larger, since both products are normal
 //             floats rounded once and differ by more than two roundings, so
 //             the row's top_k by (p desc, index asc) are all candidates;
-//  k_tx_final (row): p = e * (1 / sum of the slice sums), the k-th largest p
-//             by radix select over the candidates, the ones >= it sorted,
-//             top-p cut, p_out written; optionally one draw from it.
+//  k_tx_final (row): p = e * (1 / sum of the slice sums); a radix search
+//             over the candidates' p down to a prefix the k-th largest p has
+//             and at most max(k, 64) candidates reach; those sorted by (p
+//             desc, index asc), the first k kept, top-p cut, p_out written;
+//             optionally one draw from it. (Below t = 2^-100 the slice passes
+//             every positive e on: p could then be subnormal.)
 // Zero e (exp underflow) never enters: zero-probability candidates change
 // neither the kept mass nor a draw. Other parameters (T <= 0, top_k 0 or
 // above kTxK) take the one-workgroup transform in k_tx_max's first
