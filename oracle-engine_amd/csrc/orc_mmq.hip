@@ -62,14 +62,17 @@ __device__ __forceinline__ h8v q4k_slice_b(const MUnit& M, int i, uint32_t sc4) 
 __device__ __forceinline__ void q6k_slice_b(const MUnit& M, int i, int c, h8v& bhi, h8v& blo) {
     const u32x2 src = (i & 1) ? M.b : M.a;
     const int sh = 4 * (i >> 1);
-    const uint32_t q0 = ((src.x >> sh) & 0x0F0F0F0Fu) | (((M.c.x >> (2 * i)) & 0x03030303u) << 4);
-    const uint32_t q1 = ((src.y >> sh) & 0x0F0F0F0Fu) | (((M.c.y >> (2 * i)) & 0x03030303u) << 4);
+    uint32_t r[4];
+    switch (i) {  // the slice index as a constant of the helper
+        case 0: q6k_magic<0>(src.x, M.c.x, sh, r[0], r[1]), q6k_magic<0>(src.y, M.c.y, sh, r[2], r[3]); break;
+        case 1: q6k_magic<1>(src.x, M.c.x, sh, r[0], r[1]), q6k_magic<1>(src.y, M.c.y, sh, r[2], r[3]); break;
+        case 2: q6k_magic<2>(src.x, M.c.x, sh, r[0], r[1]), q6k_magic<2>(src.y, M.c.y, sh, r[2], r[3]); break;
+        default: q6k_magic<3>(src.x, M.c.x, sh, r[0], r[1]), q6k_magic<3>(src.y, M.c.y, sh, r[2], r[3]); break;
+    }
     const int si = 2 * i + (c >> 1);
     const uint32_t sw = si < 4 ? M.d.x : M.d.y;
     const _Float16 sf = (_Float16)(float)(int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
     const h2v sc2{sf, sf}, off{(_Float16)-1056.f, (_Float16)-1056.f};
-    const uint32_t r[4] = {(q0 & 0x00FF00FFu) | 0x64006400u, ((q0 >> 8) & 0x00FF00FFu) | 0x64006400u,
-                           (q1 & 0x00FF00FFu) | 0x64006400u, ((q1 >> 8) & 0x00FF00FFu) | 0x64006400u};
     u32x4 bh, bl;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {

@@ -96,6 +96,21 @@ __device__ __forceinline__ uint32_t vreg(uint32_t c) {
     return r;
 }
 
+// Four 6-bit Q6_K codes (low nibbles at bit sh of the bytes of lw, the two
+// high bits at bit 2i of the bytes of hw, i a compile-time slice index) as
+// two words of fp16 pairs 1024 + q in the A entries' element order: bytes 0
+// and 2 into r0, 1 and 3 into r1 (each code in the low byte of a half whose
+// high byte is 0x64). One AND-OR and one shift-and build the clean codes,
+// one byte permute per word places them.
+template <int I>
+__device__ __forceinline__ void q6k_magic(uint32_t lw, uint32_t hw, int sh, uint32_t& r0, uint32_t& r1) {
+    const uint32_t h = (I < 2 ? hw << (4 - 2 * I) : hw >> (2 * I - 4)) & 0x30303030u;  // bits 4, 5 of each byte
+    const uint32_t q = ((sh ? lw >> 4 : lw) & 0x0F0F0F0Fu) | h;
+    const uint32_t mg = vreg(0x64646464u);
+    r0 = __builtin_amdgcn_perm(mg, q, sreg(0x04020400u));  // [q0, 0x64, q2, 0x64]
+    r1 = __builtin_amdgcn_perm(mg, q, sreg(0x04030401u));  // [q1, 0x64, q3, 0x64]
+}
+
 // Q4_K 6-bit scales and minimums of sub-blocks 4h .. 4h + 3 (h = 0, 1), one
 // per byte of sc4 / mn4, from the 12 scale bytes s0 | s1 | s2
 // (core/gguf_parser.cpp:1085-1093); branch-free, h selects by mask.
@@ -298,15 +313,18 @@ __device__ __forceinline__ void mmq_core_q6k(const MUnit (&M)[TR], int lane, con
             // 6-bit codes of the lane's 8 values of slice i (stored + 32)
             const u32x2 src = (i & 1) ? M[tr].b : M[tr].a;
             const int sh = 4 * (i >> 1);
-            const uint32_t q0 = ((src.x >> sh) & 0x0F0F0F0Fu) | (((M[tr].c.x >> (2 * i)) & 0x03030303u) << 4);
-            const uint32_t q1 = ((src.y >> sh) & 0x0F0F0F0Fu) | (((M[tr].c.y >> (2 * i)) & 0x03030303u) << 4);
+            uint32_t r[4];
+            switch (i) {  // the slice index as a constant of the helper
+                case 0: q6k_magic<0>(src.x, M[tr].c.x, sh, r[0], r[1]), q6k_magic<0>(src.y, M[tr].c.y, sh, r[2], r[3]); break;
+                case 1: q6k_magic<1>(src.x, M[tr].c.x, sh, r[0], r[1]), q6k_magic<1>(src.y, M[tr].c.y, sh, r[2], r[3]); break;
+                case 2: q6k_magic<2>(src.x, M[tr].c.x, sh, r[0], r[1]), q6k_magic<2>(src.y, M[tr].c.y, sh, r[2], r[3]); break;
+                default: q6k_magic<3>(src.x, M[tr].c.x, sh, r[0], r[1]), q6k_magic<3>(src.y, M[tr].c.y, sh, r[2], r[3]); break;
+            }
             // scale of the lane's 16-value sub-block 2i + c/2
             const int si = 2 * i + (c >> 1);
             const uint32_t sw = si < 4 ? M[tr].d.x : M[tr].d.y;
             const _Float16 sf = (_Float16)(float)(int8_t)((sw >> (8 * (si & 3))) & 0xFFu);
             const h2v sc2{sf, sf}, off{(_Float16)-1056.f, (_Float16)-1056.f};  // 1024 + 32
-            const uint32_t r[4] = {(q0 & 0x00FF00FFu) | 0x64006400u, ((q0 >> 8) & 0x00FF00FFu) | 0x64006400u,
-                                   (q1 & 0x00FF00FFu) | 0x64006400u, ((q1 >> 8) & 0x00FF00FFu) | 0x64006400u};
             u32x4 bh, bl;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
