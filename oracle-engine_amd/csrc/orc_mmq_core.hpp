@@ -104,7 +104,9 @@ __device__ __forceinline__ uint32_t vreg(uint32_t c) {
 // one byte permute per word places them.
 template <int I>
 __device__ __forceinline__ void q6k_magic(uint32_t lw, uint32_t hw, int sh, uint32_t& r0, uint32_t& r1) {
-    const uint32_t h = (I < 2 ? hw << (4 - 2 * I) : hw >> (2 * I - 4)) & 0x30303030u;  // bits 4, 5 of each byte
+    uint32_t h;  // bits 4, 5 of each byte
+    if constexpr (I < 2) h = (hw << (4 - 2 * I)) & 0x30303030u;
+    else h = (hw >> (2 * I - 4)) & 0x30303030u;
     const uint32_t q = ((sh ? lw >> 4 : lw) & 0x0F0F0F0Fu) | h;
     const uint32_t mg = vreg(0x64646464u);
     r0 = __builtin_amdgcn_perm(mg, q, sreg(0x04020400u));  // [q0, 0x64, q2, 0x64]
