@@ -392,15 +392,16 @@ __global__ __launch_bounds__(kPfWG) void k_mmq_pf(QmvParams p) {
 
 bool mmq_type(int type) { return type == ORC_Q4_K || type == ORC_Q6_K || type == kMixK; }
 
-// tokens per launch: up to kMmqMaxNT (kMmqTallNT in whole-tile mode) as long
-// as the smallest staging window (one four-unit pass per wave) fits, with the
-// launch's tiles per wave (two for SwiGLU pairs and tall Q4_K matrices)
+// tokens per launch: up to kMmqMaxNT as long as the activations fit: the
+// smallest staging window (one four-unit pass per wave) in split-tile mode,
+// every unit of the row in whole-tile mode, with the launch's tiles per wave
+// (two for SwiGLU pairs and tall Q4_K matrices)
 int mmq_max_tokens(int type, const QmvParams& p) {
     const int per_wave = (p.n_in / 128 + kMW - 1) / kMW;
-    const int hs = std::min(per_wave, 4);
+    const int hs = mmq_tall(type, p) ? 0 : std::min(per_wave, 4);
     const bool two = type != kMixK && (p.epi == ORC_EPI_SWIGLU || (type == ORC_Q4_K && p.n_rows >= 32 * g_n_cu));
     const int tr = two ? 2 : 1;
-    int nt = mmq_tall(type, p) ? kMmqTallNT : kMmqMaxNT;
+    int nt = kMmqMaxNT;
     while (nt > 1 && mmq_lds(type, nt, p.n_in, tr, hs) > g_lds_max) --nt;
     return mmq_lds(type, nt, p.n_in, tr, hs) <= g_lds_max ? nt : 0;
 }

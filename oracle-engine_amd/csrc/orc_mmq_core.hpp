@@ -844,11 +844,12 @@ static int mmq_nt(const QmvParams& p, hipStream_t s, const LaunchEvents& ev) {
     // (ring depth and staging width change no result; two-tile and wide-batch
     // shapes keep them small enough that nothing spills)
     if constexpr (QT != kMixK) {
-        if constexpr (NT <= kMmqTallNT) {
+        if constexpr (!mmq_wide<NT>()) {
             if (tall)
                 return two ? mmq_shape<MW, QT, NT, 2, 4, 4, true>(p, s, ev) : mmq_shape<MW, QT, NT, 1, 6, 4, true>(p, s, ev);
-        } else if (tall) {
-            return set_error(ORC_E_INVALID, "gemm: more than 8 tokens in a whole-tile launch");
+        } else {  // the lo tile's registers: a shorter ring
+            if (tall)
+                return two ? mmq_shape<MW, QT, NT, 2, 2, 4, true>(p, s, ev) : mmq_shape<MW, QT, NT, 1, 6, 4, true>(p, s, ev);
         }
         if constexpr (mmq_wide<NT>()) {  // the lo tile's registers leave room for a ring of two
             if (two) return mmq_shape<MW, QT, NT, 2, 2, 4, false>(p, s, ev);
