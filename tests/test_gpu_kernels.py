@@ -92,7 +92,8 @@ def test_gemv_vs_exact(dev, oracle, qt, n_out, n_in):
 
 @pytest.mark.parametrize("qt,n_out,n_in", [(ol.Q4_K, 200, 3072), (ol.Q6_K, 77, 8192), (ol.Q8_0, 90, 896),
                                            (ol.Q4_0, 33, 2048), (ol.Q6_K, 24, 18944), (ol.Q8_0, 40000, 896),
-                                           (ol.Q4_K, 8192, 3072), (ol.Q6_K, 70000, 1024)])
+                                           (ol.Q4_K, 8192, 3072), (ol.Q6_K, 70000, 1024),
+                                           (ol.Q4_K, 140000, 512)])
 def test_gemm_batch_invariant(dev, oracle, qt, n_out, n_in):
     """Tokens of a launch are independent: verify(n)[t] is bit-identical for
     every n. Q8_0 / Q4_0 run one kernel family for all n, so verify(n)[t] also
@@ -100,7 +101,9 @@ def test_gemm_batch_invariant(dev, oracle, qt, n_out, n_in):
     token on the vector ALUs and verify 2..16 on the matrix cores (up to 8
     tokens as stacked hi / lo rows, 9-16 as two tiles), like the reference,
     whose gemv_q and gemm_q round differently: decode and verify then agree
-    within 4e-6 of sum |w x|."""
+    within 4e-6 of sum |w x|. The 70000- and 140000-row matrices take the
+    whole-tile kernels (LM-head shapes; the Q4_K one with two tiles per
+    wave), whose launches hold up to 16 tokens when the staged row fits."""
     print(f"[gpu] gemm invariance type={qt} {n_out}x{n_in}", flush=True)
     rng = np.random.default_rng(3)
     raw = rand_blocks(qt, n_out * n_in, rng)
