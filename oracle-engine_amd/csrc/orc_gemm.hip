@@ -303,13 +303,18 @@ template <int ROWS> struct Unit<ORC_Q8_0, ROWS> {
 // ORC_Q8_0_X8: block u is code run u % 8 of the 272-byte group u / 8 (8
 // fp16 scales, then 8 x 32 codes): the same values as Q8_0, loaded with
 // aligned 16-byte reads; the arithmetic is Q8_0's.
+// Loads through the global address space (not flat), so the x staging's LDS
+// waits (lgkmcnt) never wait for them: this type's first batch is in flight
+// during the staging.
 template <int ROWS> struct Unit<ORC_Q8_0_X8, ROWS> : Unit<ORC_Q8_0, ROWS> {
+    typedef const __attribute__((address_space(1))) u32x4* g16;
+    typedef const __attribute__((address_space(1))) uint16_t* g2;
     __device__ __forceinline__ void load(const uint8_t* const (&rp)[ROWS], int u) {
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
             const uint8_t* grp = rp[r] + (size_t)(u >> 3) * 272;
-            this->dh[r] = *(const uint16_t*)(grp + 2 * (u & 7));
-            const u32x4* q = (const u32x4*)(grp + 16 + 32 * (u & 7));
+            this->dh[r] = *(g2)(grp + 2 * (u & 7));
+            const g16 q = (g16)(grp + 16 + 32 * (u & 7));
             this->q0[r] = q[0];
             this->q1[r] = q[1];
         }
@@ -534,6 +539,15 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
     // queued behind it (measured: 0.4-1.3 us per launch on 1-30 MB
     // matrices); or (large matrices, row-group pipelining) right after the
     // first pass of x loads, in flight while x is stored.
+    // the regrouped Q8_0 layout: the first batch goes out with the x loads,
+    // before x is stored, at every size. Its loads are global (the staging's
+    // LDS waits skip them) and unconditional (the waits for x count past
+    // them instead of draining them at a branch's join); measured against
+    // the late order below: C3 269.2 -> 271.2 tok/s. The other types keep
+    // the late order for launches under 40 MB: issued early, their weights
+    // delay x (C2 greedy 693 -> 663, C4 113.6 -> 111.4 tok/s with the same
+    // exact waits)
+    constexpr bool kEarly = QT == ORC_Q8_0_X8;
     const bool norm = p.norm_w != nullptr;
     float ss[NT];
 #pragma unroll
@@ -584,7 +598,14 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
     {
         float4 v[NT][4], gw[4];
         load_pass(0, v, gw);
-        if (!p.late_w && g < p.n_groups) {  // first batch of the first row group
+        if constexpr (kEarly) {  // every wave, no branch: idle waves load group 0's rows
+            map_rows<ROWS, RG>(p, g < p.n_groups ? g : 0, slot, R);
+#pragma unroll
+            for (int i = 0; i < UPL; ++i) {
+                const int u = li + LPR * i;
+                U[i].load(R.rp, u < p.units ? u : 0);
+            }
+        } else if (!p.late_w && g < p.n_groups) {  // first batch of the first row group
             map_rows<ROWS, RG>(p, g, slot, R);
 #pragma unroll
             for (int i = 0; i < UPL; ++i) {
@@ -608,7 +629,7 @@ __global__ __launch_bounds__(kQWG) __attribute__((amdgpu_waves_per_eu(WPE))) voi
         }
     }
     __syncthreads();
-    if (QT != kMixK && p.late_w && g < p.n_groups) {
+    if (QT != kMixK && !kEarly && p.late_w && g < p.n_groups) {
         map_rows<ROWS, RG>(p, g, slot, R);
 #pragma unroll
         for (int i = 0; i < UPL; ++i) {
